@@ -1,0 +1,632 @@
+/*
+ * ferrum_oracle.c — CPU restatement of ferrum_core's Q8_0 decode hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP path and the timed CPU
+ * baseline ("port") of bench.py.  Nothing in the product library links or calls
+ * this file.  Build: oracle/Makefile (-O3 -ffp-contract=off, no fast-math, the
+ * default x86-64 ISA like a default `cargo build --release`).
+ *
+ * Each function follows the reference file:line given in ferrum_oracle.h.  The
+ * reference is pure Rust and cannot be built here (no Rust toolchain), so this
+ * restatement is pinned by the reference's own known-answer tests, re-encoded
+ * under tests/, and by library/closed-form checks (numpy's IEEE half cast,
+ * numpy's sequential float32 cumsum, brute force on small inputs).
+ */
+#define _GNU_SOURCE
+#include "ferrum_oracle.h"
+
+#include <float.h>
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* IEEE half codec                                                           */
+/* ------------------------------------------------------------------------ */
+
+static uint32_t f32_bits(float v) {
+    uint32_t u;
+    memcpy(&u, &v, 4);
+    return u;
+}
+
+static float bits_f32(uint32_t u) {
+    float v;
+    memcpy(&v, &u, 4);
+    return v;
+}
+
+/* gguf_write/blocks.rs:12-61 */
+uint16_t fo_f32_to_f16(float value) {
+    uint32_t x = f32_bits(value);
+    uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+    int32_t exp32 = (int32_t)((x >> 23) & 0xFFu);
+    uint32_t mant32 = x & 0x007FFFFFu;
+    if (exp32 == 0xFF) return mant32 != 0 ? (uint16_t)(sign | 0x7E00u) : (uint16_t)(sign | 0x7C00u);
+    int32_t exp16 = exp32 - 127 + 15;
+    if (exp16 >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+    if (exp16 <= 0) {
+        if (exp16 < -10) return sign;
+        uint32_t mant = mant32 | 0x00800000u;
+        uint32_t shift = (uint32_t)(14 - exp16); /* 14..24 */
+        uint32_t half = mant >> shift;
+        uint32_t rem = mant & ((1u << shift) - 1u);
+        uint32_t halfway = 1u << (shift - 1u);
+        if (rem > halfway || (rem == halfway && (half & 1u) == 1u)) half += 1u;
+        return (uint16_t)(sign | (uint16_t)half);
+    }
+    uint16_t mant16 = (uint16_t)(mant32 >> 13);
+    uint32_t rem = mant32 & 0x1FFFu;
+    if (rem > 0x1000u || (rem == 0x1000u && (mant16 & 1u) == 1u)) {
+        mant16 = (uint16_t)(mant16 + 1u);
+        if (mant16 == 0x0400u) {
+            mant16 = 0;
+            exp16 += 1;
+            if (exp16 >= 0x1F) return (uint16_t)(sign | 0x7C00u);
+        }
+    }
+    return (uint16_t)(sign | (uint16_t)((uint32_t)exp16 << 10) | mant16);
+}
+
+/* gguf/dequant.rs:7-35 */
+float fo_f16_to_f32(uint16_t h) {
+    uint32_t sign = (uint32_t)((h >> 15) & 1u);
+    int32_t exp = (int32_t)((h >> 10) & 0x1Fu);
+    uint32_t mant = (uint32_t)(h & 0x3FFu);
+    uint32_t bits;
+    if (exp == 0) {
+        if (mant == 0) {
+            bits = sign << 31;
+        } else {
+            uint32_t m = mant;
+            int32_t e = -14;
+            while ((m & 0x400u) == 0) {
+                m <<= 1;
+                e -= 1;
+            }
+            m &= 0x3FFu;
+            bits = (sign << 31) | ((uint32_t)(e + 127) << 23) | (m << 13);
+        }
+    } else if (exp == 0x1F) {
+        bits = (sign << 31) | (0xFFu << 23) | (mant << 13);
+    } else {
+        bits = (sign << 31) | ((uint32_t)(exp - 15 + 127) << 23) | (mant << 13);
+    }
+    return bits_f32(bits);
+}
+
+void fo_f32_to_f16_n(const float* x, size_t n, uint16_t* out) {
+    for (size_t i = 0; i < n; i++) out[i] = fo_f32_to_f16(x[i]);
+}
+
+void fo_f16_to_f32_n(const uint16_t* h, size_t n, float* out) {
+    for (size_t i = 0; i < n; i++) out[i] = fo_f16_to_f32(h[i]);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Q8_0                                                                       */
+/* ------------------------------------------------------------------------ */
+
+/* Rust `f32::round(v) as i8`: half away from zero, saturating, NaN -> 0. */
+static int8_t round_sat_i8(float v) {
+    float r = roundf(v);
+    if (isnan(r)) return 0;
+    if (r >= 127.0f) return 127;
+    if (r <= -128.0f) return -128;
+    return (int8_t)r;
+}
+
+/* quant.rs:271-280 */
+void fo_q8_0_block(const float* x, uint16_t* d16, int8_t* q) {
+    float amax = 0.0f;
+    for (int i = 0; i < 32; i++) amax = fmaxf(amax, fabsf(x[i])); /* f32::max ignores NaN */
+    float d = amax / 127.0f;
+    float id = d != 0.0f ? 1.0f / d : 0.0f;
+    for (int i = 0; i < 32; i++) q[i] = round_sat_i8(x[i] * id);
+    *d16 = fo_f32_to_f16(d);
+}
+
+/* gguf_write/blocks.rs:65-92 (length check), 132-140 */
+int fo_q8_0_encode(const float* data, size_t n, uint8_t* out) {
+    if (n % 32 != 0) return -1;
+    for (size_t b = 0; b < n / 32; b++) {
+        uint16_t d16;
+        int8_t q[32];
+        fo_q8_0_block(data + b * 32, &d16, q);
+        out[b * 34 + 0] = (uint8_t)(d16 & 0xFFu);
+        out[b * 34 + 1] = (uint8_t)(d16 >> 8);
+        memcpy(out + b * 34 + 2, q, 32);
+    }
+    return 0;
+}
+
+static float q8_0_weight(const uint8_t* blk, int t) {
+    uint16_t d16 = (uint16_t)(blk[0] | ((uint16_t)blk[1] << 8));
+    return fo_f16_to_f32(d16) * (float)(int8_t)blk[2 + t];
+}
+
+/* gguf/dequant.rs:37-49 */
+int fo_q8_0_dequant(const uint8_t* raw, size_t raw_len, size_t n, float* out) {
+    size_t nb = n / 32;
+    if (raw_len < nb * 34) return -1;
+    for (size_t b = 0; b < nb; b++) {
+        const uint8_t* blk = raw + b * 34;
+        for (int t = 0; t < 32; t++) out[b * 32 + (size_t)t] = q8_0_weight(blk, t);
+    }
+    return 0;
+}
+
+/* quant.rs:283-291 */
+static void snap_block(float* x) {
+    uint16_t d16;
+    int8_t q[32];
+    fo_q8_0_block(x, &d16, q);
+    float d = fo_f16_to_f32(d16);
+    for (int i = 0; i < 32; i++) x[i] = (float)q[i] * d;
+}
+
+/* quant.rs:298-305 */
+void fo_fake_quantize_q8_0_rows(float* data, size_t len, size_t ne0) {
+    if (ne0 == 0 || ne0 % 32 != 0) return;
+    for (size_t b = 0; b + 32 <= len; b += 32) snap_block(data + b);
+}
+
+/* quant.rs:309-325 */
+void fo_fake_quantize_q8_0_cols(float* data, size_t rows_in, size_t cols_out) {
+    if (rows_in == 0 || rows_in % 32 != 0) return;
+    float buf[32];
+    for (size_t j = 0; j < cols_out; j++) {
+        for (size_t i0 = 0; i0 < rows_in; i0 += 32) {
+            for (size_t t = 0; t < 32; t++) buf[t] = data[(i0 + t) * cols_out + j];
+            snap_block(buf);
+            for (size_t t = 0; t < 32; t++) data[(i0 + t) * cols_out + j] = buf[t];
+        }
+    }
+}
+
+/* gguf/tensors.rs:58-87 + gguf/llama.rs:342-350 */
+int fo_q8_0_to_ferrum_weight(const uint8_t* raw, size_t n_rows, size_t k, float* w_kn) {
+    if (k % 32 != 0) return -1;
+    size_t row_bytes = k / 32 * 34;
+    for (size_t r = 0; r < n_rows; r++) {
+        const uint8_t* row = raw + r * row_bytes;
+        for (size_t p = 0; p < k; p++) w_kn[p * n_rows + r] = q8_0_weight(row + (p / 32) * 34, (int)(p % 32));
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Linear layer: ops.rs:29-256 with the parallel.rs row split                 */
+/* ------------------------------------------------------------------------ */
+
+enum { KC = 256, NC = 256, MR = 4, NR = 8 };
+
+/* ops.rs:99-126 */
+static void edge_rows(const float* a, const float* b, size_t k, size_t n, size_t ia, size_t ib,
+                      size_t r0, size_t ja, size_t jb, size_t pp, size_t p1, float* out) {
+    for (size_t i = ia; i < ib; i++) {
+        const float* arow = a + i * k;
+        float* o = out + (i - r0) * n;
+        for (size_t p = pp; p < p1; p++) {
+            float aip = arow[p];
+            const float* brow = b + p * n;
+            for (size_t j = ja; j < jb; j++) o[j] += aip * brow[j];
+        }
+    }
+}
+
+/* ops.rs:63-94 */
+static void micro_tile(const float* a, const float* b, size_t k, size_t n, size_t i, size_t r0,
+                       size_t j, size_t pp, size_t p1, float* out) {
+    float acc[MR][NR];
+    for (int r = 0; r < MR; r++)
+        for (int c = 0; c < NR; c++) acc[r][c] = out[(i + (size_t)r - r0) * n + j + (size_t)c];
+    for (size_t p = pp; p < p1; p++) {
+        const float* bs = b + p * n + j;
+        for (int r = 0; r < MR; r++) {
+            float av = a[(i + (size_t)r) * k + p];
+            for (int c = 0; c < NR; c++) acc[r][c] += av * bs[c];
+        }
+    }
+    for (int r = 0; r < MR; r++)
+        for (int c = 0; c < NR; c++) out[(i + (size_t)r - r0) * n + j + (size_t)c] = acc[r][c];
+}
+
+/* ops.rs:29-55 */
+static void matmul_block(const float* a, const float* b, size_t k, size_t n, size_t r0, size_t r1,
+                         float* out) {
+    for (size_t jj = 0; jj < n;) {
+        size_t j1 = jj + NC < n ? jj + NC : n;
+        for (size_t pp = 0; pp < k;) {
+            size_t p1 = pp + KC < k ? pp + KC : k;
+            size_t i = r0;
+            for (; i + MR <= r1; i += MR) {
+                size_t j = jj;
+                for (; j + NR <= j1; j += NR) micro_tile(a, b, k, n, i, r0, j, pp, p1, out);
+                if (j < j1) edge_rows(a, b, k, n, i, i + MR, r0, j, j1, pp, p1, out);
+            }
+            if (i < r1) edge_rows(a, b, k, n, i, r1, r0, jj, j1, pp, p1, out);
+            pp = p1;
+        }
+        jj = j1;
+    }
+}
+
+/* ops.rs:132-148 */
+static void matmul_bias_block(const float* a, const float* b, const float* bias, size_t k, size_t n,
+                              size_t r0, size_t r1, float* block) {
+    matmul_block(a, b, k, n, r0, r1, block);
+    if (bias && n > 0)
+        for (size_t i = r0; i < r1; i++) {
+            float* row = block + (i - r0) * n;
+            for (size_t j = 0; j < n; j++) row[j] += bias[j];
+        }
+}
+
+typedef struct {
+    const float *a, *b, *bias;
+    size_t k, n, r0, r1;
+    float* out;
+} row_job;
+
+static void* row_job_run(void* arg) {
+    row_job* j = (row_job*)arg;
+    matmul_bias_block(j->a, j->b, j->bias, j->k, j->n, j->r0, j->r1, j->out + j->r0 * j->n);
+    return NULL;
+}
+
+int fo_linear_forward(const float* x, size_t m, size_t k, const float* w_kn, size_t n,
+                      const float* bias, float* y, int threads) {
+    memset(y, 0, m * n * sizeof(float));
+    size_t cost = m * k * n;
+    /* parallel.rs:90-92: rows >= 2 && cost >= 1<<16 && threads > 1 */
+    if (threads <= 1 || m < 2 || cost < (1u << 16)) {
+        matmul_bias_block(x, w_kn, bias, k, n, 0, m, y);
+        return 0;
+    }
+    size_t t = (size_t)threads < m ? (size_t)threads : m;
+    size_t rows_per = (m + t - 1) / t; /* parallel.rs:190, 280 */
+    row_job jobs[256];
+    pthread_t tids[256];
+    size_t nj = 0;
+    for (size_t r0 = 0; r0 < m && nj < 256; r0 += rows_per) {
+        jobs[nj] = (row_job){x, w_kn, bias, k, n, r0, r0 + rows_per < m ? r0 + rows_per : m, y};
+        nj++;
+    }
+    int started[256];
+    for (size_t i = 1; i < nj; i++) started[i] = pthread_create(&tids[i], NULL, row_job_run, &jobs[i]) == 0;
+    row_job_run(&jobs[0]);
+    for (size_t i = 1; i < nj; i++) {
+        if (started[i])
+            pthread_join(tids[i], NULL);
+        else
+            row_job_run(&jobs[i]); /* parallel.rs:285-291: a failed spawn leaves its share to the caller */
+    }
+    return 0;
+}
+
+int fo_q8_0_linear_rows(const float* x, size_t m, size_t k, const uint8_t* raw, size_t n,
+                        const float* bias, float* y) {
+    if (k % 32 != 0) return -1;
+    size_t row_bytes = k / 32 * 34;
+    for (size_t i = 0; i < m; i++) {
+        const float* xr = x + i * k;
+        for (size_t j = 0; j < n; j++) {
+            const uint8_t* row = raw + j * row_bytes;
+            float acc = 0.0f;
+            for (size_t b = 0; b < k / 32; b++) {
+                const uint8_t* blk = row + b * 34;
+                float d = fo_f16_to_f32((uint16_t)(blk[0] | ((uint16_t)blk[1] << 8)));
+                for (int t = 0; t < 32; t++) {
+                    float w = d * (float)(int8_t)blk[2 + t];
+                    acc += xr[b * 32 + (size_t)t] * w;
+                }
+            }
+            if (bias) acc += bias[j];
+            y[i * n + j] = acc;
+        }
+    }
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* W8A8                                                                       */
+/* ------------------------------------------------------------------------ */
+
+void fo_q8_0_quantize_rows(const float* x, size_t m, size_t k, uint16_t* d16, int8_t* q) {
+    size_t kb = k / 32;
+    for (size_t i = 0; i < m; i++)
+        for (size_t b = 0; b < kb; b++) fo_q8_0_block(x + i * k + b * 32, d16 + i * kb + b, q + i * k + b * 32);
+}
+
+void fo_q8_0_block_dots(const int8_t* qx, size_t m, size_t k, const uint8_t* raw, size_t n,
+                        int32_t* dots) {
+    size_t kb = k / 32, row_bytes = kb * 34;
+    for (size_t i = 0; i < m; i++)
+        for (size_t j = 0; j < n; j++)
+            for (size_t b = 0; b < kb; b++) {
+                const uint8_t* blk = raw + j * row_bytes + b * 34;
+                int32_t s = 0;
+                for (int t = 0; t < 32; t++) s += (int32_t)qx[i * k + b * 32 + (size_t)t] * (int32_t)(int8_t)blk[2 + t];
+                dots[(i * n + j) * kb + b] = s;
+            }
+}
+
+int fo_q8_0_linear_w8a8(const float* x, size_t m, size_t k, const uint8_t* raw, size_t n,
+                        const float* bias, float* y) {
+    if (k % 32 != 0) return -1;
+    size_t kb = k / 32, row_bytes = kb * 34;
+    uint16_t* dx = (uint16_t*)malloc((m * kb + 1) * sizeof(uint16_t));
+    int8_t* qx = (int8_t*)malloc(m * k + 1);
+    if (!dx || !qx) {
+        free(dx);
+        free(qx);
+        return -2;
+    }
+    fo_q8_0_quantize_rows(x, m, k, dx, qx);
+    for (size_t i = 0; i < m; i++)
+        for (size_t j = 0; j < n; j++) {
+            float sumf = 0.0f;
+            for (size_t b = 0; b < kb; b++) {
+                const uint8_t* blk = raw + j * row_bytes + b * 34;
+                int32_t s = 0;
+                for (int t = 0; t < 32; t++) s += (int32_t)qx[i * k + b * 32 + (size_t)t] * (int32_t)(int8_t)blk[2 + t];
+                float dw = fo_f16_to_f32((uint16_t)(blk[0] | ((uint16_t)blk[1] << 8)));
+                float dd = dw * fo_f16_to_f32(dx[i * kb + b]);
+                sumf += (float)s * dd;
+            }
+            if (bias) sumf += bias[j];
+            y[i * n + j] = sumf;
+        }
+    free(dx);
+    free(qx);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
+/* softmax + ln bridge                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* ops.rs:478-502 */
+void fo_softmax_rows(const float* z, size_t rows, size_t cols, float* out) {
+    for (size_t r = 0; r < rows; r++) {
+        const float* zr = z + r * cols;
+        float* o = out + r * cols;
+        float mx = -INFINITY;
+        for (size_t c = 0; c < cols; c++) mx = fmaxf(mx, zr[c]);
+        float sum = 0.0f;
+        for (size_t c = 0; c < cols; c++) {
+            float e = expf(zr[c] - mx);
+            o[c] = e;
+            sum += e;
+        }
+        for (size_t c = 0; c < cols; c++) o[c] /= sum;
+    }
+}
+
+/* slm/token_stream.rs:134 */
+void fo_ln_bridge(const float* p, size_t n, float* out) {
+    for (size_t i = 0; i < n; i++) out[i] = logf(fmaxf(p[i], 1e-12f));
+}
+
+/* ------------------------------------------------------------------------ */
+/* RNG                                                                        */
+/* ------------------------------------------------------------------------ */
+
+uint64_t fo_rng_new(uint64_t seed) { return seed == 0 ? 0x9E3779B97F4A7C15ull : seed; }
+
+uint64_t fo_rng_next_u64(uint64_t* state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return x * 0x2545F4914F6CDD1Dull;
+}
+
+float fo_draw_to_f32(uint64_t draw) { return (float)(draw >> 40) / (float)(1u << 24); }
+
+float fo_rng_next_f32(uint64_t* state) { return fo_draw_to_f32(fo_rng_next_u64(state)); }
+
+/* ------------------------------------------------------------------------ */
+/* Sampler: slm/sampling.rs:96-210                                            */
+/* ------------------------------------------------------------------------ */
+
+/* f32::total_cmp as a signed integer key. */
+static int32_t total_key(float v) {
+    int32_t b;
+    memcpy(&b, &v, 4);
+    return b ^ (int32_t)(((uint32_t)(b >> 31)) >> 1);
+}
+
+/* sampling.rs:96-104 */
+static size_t argmax_first(const float* xs, size_t n) {
+    size_t best = 0;
+    for (size_t i = 0; i < n; i++)
+        if (total_key(xs[i]) > total_key(xs[best])) best = i;
+    return best;
+}
+
+size_t fo_argmax_first(const float* xs, size_t n) { return n ? argmax_first(xs, n) : 0; }
+
+/* sampling.rs:109-122 */
+size_t fo_pick_by_mass(const float* probs, size_t n, float r) {
+    float cumsum = 0.0f;
+    size_t last = 0;
+    for (size_t i = 0; i < n; i++)
+        if (probs[i] > 0.0f) {
+            last = i;
+            cumsum += probs[i];
+            if (r <= cumsum) return i;
+        }
+    return last;
+}
+
+static int cmp_desc_f32(const void* a, const void* b) {
+    int32_t ka = total_key(*(const float*)a), kb = total_key(*(const float*)b);
+    return ka < kb ? 1 : (ka > kb ? -1 : 0);
+}
+
+static int cmp_idx_desc(const void* a, const void* b, void* ctx) {
+    const float* probs = (const float*)ctx;
+    uint32_t ia = *(const uint32_t*)a, ib = *(const uint32_t*)b;
+    int32_t ka = total_key(probs[ia]), kb = total_key(probs[ib]);
+    if (ka != kb) return ka < kb ? 1 : -1;
+    return ia < ib ? -1 : (ia > ib ? 1 : 0);
+}
+
+static float rel_gap(float hi, float lo) {
+    float den = fabsf(hi) > 1e-30f ? fabsf(hi) : 1e-30f;
+    return (hi - lo) / den;
+}
+
+uint32_t fo_sample(const float* logits, size_t n, const fo_sampling_params* params,
+                   const uint32_t* recent, size_t n_recent, uint64_t draw, fo_sample_info* info) {
+    fo_sample_info local;
+    if (!info) info = &local;
+    memset(info, 0, sizeof(*info));
+    info->margin = info->greedy_gap = info->topk_gap = info->topp_gap = info->draw_gap = 1.0f;
+    if (n == 0) return 0;
+
+    float* work = (float*)malloc(n * sizeof(float));
+    memcpy(work, logits, n * sizeof(float));
+    float pen = params->repetition_penalty;
+    /* 1. repetition penalty, once per occurrence (sampling.rs:133-144) */
+    if (fabsf(pen - 1.0f) > FLT_EPSILON && pen > 0.0f)
+        for (size_t r = 0; r < n_recent; r++) {
+            uint32_t tok = recent[r];
+            if (tok < n) work[tok] = work[tok] > 0.0f ? work[tok] / pen : work[tok] * pen;
+        }
+
+    /* greedy (sampling.rs:147-149) */
+    if (params->temperature <= 0.0f) {
+        size_t best = argmax_first(work, n);
+        float second = -INFINITY;
+        for (size_t i = 0; i < n; i++)
+            if (i != best && total_key(work[i]) > total_key(second)) second = work[i];
+        info->path = FO_PATH_GREEDY;
+        info->greedy_gap = n > 1 ? rel_gap(work[best], second) : 1.0f;
+        info->margin = info->greedy_gap;
+        free(work);
+        return (uint32_t)best;
+    }
+    float t = fmaxf(params->temperature, 0.01f);
+
+    /* 2. temperature softmax (sampling.rs:150-169) */
+    float mx = -INFINITY;
+    for (size_t i = 0; i < n; i++) mx = fmaxf(mx, work[i]);
+    float* probs = work; /* in place: work is not read again */
+    float sum = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        probs[i] = expf((probs[i] - mx) / t);
+        sum += probs[i];
+    }
+    if (isnan(sum) || sum <= 1e-10f) {
+        info->path = FO_PATH_FALLBACK;
+        free(work);
+        return (uint32_t)(draw % (uint64_t)n);
+    }
+    for (size_t i = 0; i < n; i++) probs[i] /= sum;
+    info->path = FO_PATH_SAMPLED;
+
+    /* 3. top-k (sampling.rs:171-180) */
+    if (params->top_k > 0 && params->top_k < n) {
+        float* sorted = (float*)malloc(n * sizeof(float));
+        memcpy(sorted, probs, n * sizeof(float));
+        qsort(sorted, n, sizeof(float), cmp_desc_f32);
+        float thr = sorted[params->top_k - 1];
+        float below = 0.0f;
+        for (size_t i = params->top_k; i < n; i++)
+            if (sorted[i] < thr) {
+                below = sorted[i];
+                break;
+            }
+        info->topk_gap = thr > 0.0f ? rel_gap(thr, below) : 1.0f;
+        for (size_t i = 0; i < n; i++)
+            if (probs[i] < thr) probs[i] = 0.0f;
+        free(sorted);
+    }
+
+    /* 4. top-p (sampling.rs:183-200) */
+    if (params->top_p < 1.0f) {
+        uint32_t* order = (uint32_t*)malloc(n * sizeof(uint32_t));
+        unsigned char* keep = (unsigned char*)calloc(n, 1);
+        for (size_t i = 0; i < n; i++) order[i] = (uint32_t)i;
+        qsort_r(order, n, sizeof(uint32_t), cmp_idx_desc, probs);
+        float cum = 0.0f, prev = 0.0f;
+        size_t c = 0;
+        int crossed = 0;
+        for (; c < n; c++) {
+            keep[order[c]] = 1;
+            prev = cum;
+            cum += probs[order[c]];
+            if (cum >= params->top_p) {
+                crossed = 1;
+                break;
+            }
+        }
+        float tp = params->top_p;
+        if (crossed) {
+            float g1 = (tp - prev) / tp, g2 = (cum - tp) / tp;
+            info->topp_gap = g1 < g2 ? g1 : g2;
+            if (c + 1 < n) {
+                float pc = probs[order[c]], pn = probs[order[c + 1]];
+                if (pn == pc && pc > 0.0f) info->topp_tie = 1;
+                float g3 = pc > 0.0f ? rel_gap(pc, pn) : 1.0f;
+                if (g3 < info->topp_gap) info->topp_gap = g3;
+            }
+        } else {
+            info->topp_gap = (tp - cum) / tp;
+        }
+        for (size_t i = 0; i < n; i++)
+            if (!keep[i]) probs[i] = 0.0f;
+        free(order);
+        free(keep);
+    }
+
+    /* 5. renormalise and draw (sampling.rs:205-209, 109-122) */
+    float sum2 = 0.0f;
+    for (size_t i = 0; i < n; i++) sum2 += probs[i];
+    for (size_t i = 0; i < n; i++) probs[i] /= sum2;
+    float r = fo_draw_to_f32(draw);
+    float cumsum = 0.0f, before = 0.0f;
+    size_t last = 0, pick = n;
+    int first_survivor = 1, pick_first = 0;
+    uint32_t kept = 0;
+    for (size_t i = 0; i < n; i++) {
+        if (probs[i] > 0.0f) {
+            kept++;
+            last = i;
+            before = cumsum;
+            cumsum += probs[i];
+            if (pick == n && r <= cumsum) {
+                pick = i;
+                pick_first = first_survivor;
+                float g_hi = cumsum - r, g_lo = r - before;
+                info->draw_gap = pick_first ? g_hi : (g_hi < g_lo ? g_hi : g_lo);
+            }
+            first_survivor = 0;
+        }
+    }
+    if (pick == n) {
+        pick = last;
+        info->draw_gap = r - cumsum;
+    }
+    info->n_kept = kept;
+    float m = info->topk_gap;
+    if (info->topp_gap < m) m = info->topp_gap;
+    if (info->draw_gap < m) m = info->draw_gap;
+    if (info->topp_tie) m = 0.0f;
+    info->margin = m;
+    free(work);
+    return (uint32_t)pick;
+}
+
+uint32_t fo_sample_with_params(const float* logits, size_t n, const fo_sampling_params* params,
+                               const uint32_t* recent, size_t n_recent, uint64_t* rng_state,
+                               fo_sample_info* info) {
+    uint64_t draw = 0;
+    if (params->temperature > 0.0f || isnan(params->temperature)) draw = fo_rng_next_u64(rng_state);
+    return fo_sample(logits, n, params, recent, n_recent, draw, info);
+}
