@@ -1,0 +1,277 @@
+"""Benchmark of the MI355X Q8_0 decode-step hot path (one JSON line on stdout).
+
+Workload (GPT-2-124M shape, batch 1): one decode
+step of the hot path = the 49 Q8_0 linear layers of a GPT-2-124M forward
+(12 x [QKV 2304x768, attn-out 768x768, MLP-up 3072x768, MLP-down 768x3072],
+bias added; tied lm_head 50257x768, no bias) followed by the fused sampler on
+the 50257 head outputs (GPT-2 softmax -> ln bridge, temperature 0.8, top-k 40,
+top-p 0.95, repetition penalty 1.1 over a 128-id window, one host draw).
+Random-init N(0, 0.02) weights, Q8_0-encoded on the GPU; synthetic N(0,1)
+activations resident in HBM.  The adjacent LayerNorm/attention/GELU ops are not
+part of the hot path and are not timed.
+
+Residency: three replicas of the whole weight set (3 x 131 MB = 394 MB, above
+the 256 MB MALL) are used in rotation, so every step streams its weights from
+HBM ("hbm-forced").  A MALL-resident figure (one replica) is reported beside it.
+
+The step is captured once per replica into a HIP graph (torch.cuda.CUDAGraph)
+and replayed; K timed steps are bracketed by synchronisations and HIP events.
+
+roofline: the dominant kernel is the Q8_0 GEMV; it is measured on the lm_head
+shape (50257 x 768, the largest launch) in back-to-back launches over 8 head
+replicas (328 MB, HBM-forced), timed with HIP events on the launch stream.
+Algorithmic bytes per launch = 50257*768*34/32 (Q8_0 weight) + 768*4 (x)
++ 50257*4 (y).
+
+cpu_baseline: the CPU oracle (oracle/, ferrum_core's arithmetic restated in C,
+"port") on one host core — ferrum_core runs the m=1 linear serially at any
+thread count (parallel.rs:90-92) — over f32-expanded weights as the reference's
+loader builds them, for a bounded number of decode steps.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "ferrum-cpu_amd"))
+
+D, L, FFN, V, N_RECENT = 768, 12, 3072, 50257, 128
+LAYER_SHAPES = [(3 * D, D), (D, D), (FFN, D), (D, FFN)]  # (n_rows, k): QKV, attn-out, up, down
+HBM_PEAK_GBS = 8000.0
+SAMPLER = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
+
+
+def q8_bytes(n, k):
+    return n * k // 32 * 34
+
+
+def make_weight(ctx, fh, torch, n, k, gen):
+    """N(0, 0.02) weight [n, k] -> GGUF Q8_0 bytes (GPU encoder) -> device weight."""
+    w = torch.randn((n, k), generator=gen, device="cuda", dtype=torch.float32) * 0.02
+    raw = torch.empty(q8_bytes(n, k), dtype=torch.uint8, device="cuda")
+    fh.q8_0_encode_async(ctx, w, n * k, raw)
+    wt = fh.Q8_0Weight.upload_device(ctx, raw, n, k)
+    ctx.sync()
+    del w, raw
+    return wt
+
+
+class Replica:
+    def __init__(self, ctx, fh, torch, gen):
+        self.layers = [[make_weight(ctx, fh, torch, n, k, gen) for (n, k) in LAYER_SHAPES] for _ in range(L)]
+        self.head = make_weight(ctx, fh, torch, V, D, gen)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--replicas", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--leg", choices=["all", "head"], default="all",
+                    help="'head': only the lm_head GEMV roofline leg (for counter runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
+              "the Q8_0 decode path is sized for one MI355X and has no multi-GPU leg.", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    import ferrum_hip as fh
+
+    torch.cuda.init()
+    dev = torch.device("cuda:0")
+    ctx = fh.Context(0)
+    stream = torch.cuda.current_stream()
+    ctx.set_stream(stream.cuda_stream)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(1234)
+
+    x_d = torch.randn((1, D), generator=gen, device=dev)
+    x_f = torch.randn((1, FFN), generator=gen, device=dev)
+    y_big = torch.empty((1, max(3 * D, FFN)), device=dev)
+    logits = torch.empty((1, V), device=dev)
+    biases = {n: torch.randn(n, generator=gen, device=dev) * 0.1 for n in {s[0] for s in LAYER_SHAPES}}
+    rec = torch.from_numpy(np.random.default_rng(3).integers(0, V, size=N_RECENT).astype(np.uint32)).to(dev)
+    rec_off = torch.tensor([0, N_RECENT], dtype=torch.int32, device=dev)
+    draws = torch.tensor([0x1234_5678_9ABC_DEF1], dtype=torch.int64, device=dev)  # u64 bit pattern
+    out_id = torch.zeros(1, dtype=torch.int32, device=dev)
+    params = fh.SamplingParams(**SAMPLER)
+
+    def head_gemv(rep):
+        fh.linear_forward_async(ctx, rep.head, x_d, 1, D, None, 0, logits)
+
+    def step(rep):
+        for li in range(L):
+            for (n, k), w in zip(LAYER_SHAPES, rep.layers[li]):
+                fh.linear_forward_async(ctx, w, x_d if k == D else x_f, 1, k, biases[n], n, y_big)
+        head_gemv(rep)
+        fh.sample_rows_async(ctx, logits, 1, V, params, rec, rec_off, draws, out_id, fh.LOGITS_GPT2_SOFTMAX)
+
+    result = {}
+    if args.leg == "all":
+        reps = [Replica(ctx, fh, torch, gen) for _ in range(args.replicas)]
+        for r in reps:  # eager pass: grows the context workspace before capture
+            step(r)
+        torch.cuda.synchronize()
+        graphs = []
+        for r in reps:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+                step(r)
+            ctx.set_stream(stream.cuda_stream)
+            graphs.append(g)
+        torch.cuda.synchronize()
+
+        def timed(gs, steps, warmup):
+            for i in range(warmup):
+                gs[i % len(gs)].replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            t0 = time.perf_counter()
+            e0.record()
+            for i in range(steps):
+                gs[i % len(gs)].replay()
+            e1.record()
+            torch.cuda.synchronize()
+            wall = (time.perf_counter() - t0) * 1e3
+            return e0.elapsed_time(e1) / steps, wall / steps
+
+        ms_step, wall_step = timed(graphs, args.steps, args.warmup)
+        ms_mall, _ = timed(graphs[:1], args.steps, args.warmup)
+        # Sampler alone: one 50257-wide row (GPT-2 bridge, config-3 params).
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ns = 500
+        for _ in range(20):
+            fh.sample_rows_async(ctx, logits, 1, V, params, rec, rec_off, draws, out_id, fh.LOGITS_GPT2_SOFTMAX)
+        e0.record()
+        for _ in range(ns):
+            fh.sample_rows_async(ctx, logits, 1, V, params, rec, rec_off, draws, out_id, fh.LOGITS_GPT2_SOFTMAX)
+        e1.record()
+        torch.cuda.synchronize()
+        result["sampler_us_per_row"] = round(e0.elapsed_time(e1) / ns * 1e3, 2)
+        step_bytes = sum(q8_bytes(n, k) for (n, k) in LAYER_SHAPES) * L + q8_bytes(V, D)
+        result.update(ms_per_step=ms_step, wall_ms_per_step=wall_step, ms_per_step_mall=ms_mall,
+                      step_weight_bytes=step_bytes)
+        del graphs, reps
+        torch.cuda.synchronize()
+
+    # ---- roofline leg: lm_head GEMV, back-to-back, HBM-forced ----------------------
+    n_head_rep = 8
+    heads = [make_weight(ctx, fh, torch, V, D, gen) for _ in range(n_head_rep)]
+    hr = [type("H", (), {"head": h})() for h in heads]
+    for i in range(3 * n_head_rep):
+        head_gemv(hr[i % n_head_rep])
+    torch.cuda.synchronize()
+    launches = 400 if args.leg == "all" else 200
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(launches):
+        head_gemv(hr[i % n_head_rep])
+    e1.record()
+    torch.cuda.synchronize()
+    head_us = e0.elapsed_time(e1) / launches * 1e3
+    head_bytes = q8_bytes(V, D) + 4 * D + 4 * V
+    achieved = head_bytes / (head_us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "k_gemv_w8a32<16,4,1,nobias> (lm_head 50257x768, Q8_0, m=1)",
+                "avg_launch_us": round(head_us, 3), "bytes_per_launch": head_bytes}
+    if args.leg == "head":
+        print(json.dumps({"leg": "head", "roofline": roofline}))
+        return
+
+    # ---- CPU baseline: the oracle on this host, one core ----------------------------
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(args.cpu_seconds)
+
+    ms = result["ms_per_step"]
+    line = {
+        "metric": "decode tok/s GPT-2-124M Q8_0 b1 (hot path: Q8_0 linears + fused sampler)",
+        "value": round(1000.0 / ms, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (random-init N(0,0.02) Q8_0 weights, N(0,1) activations, random logits history)",
+        "config": {"workload": "gpt2-124m-q8_0-decode-step-hotpath", "batch": 1, "layers": L, "d_model": D,
+                   "ffn": FFN, "vocab": V, "numerics": "W8A32 (ferrum_core)", "sampler": SAMPLER,
+                   "residency": f"hbm-forced ({args.replicas} weight replicas, "
+                                f"{args.replicas * result['step_weight_bytes'] / 1e6:.0f} MB > 256 MB MALL)"},
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+        "mall_resident_tok_s": round(1000.0 / result["ms_per_step_mall"], 1),
+        "step_weight_GBps": round(result["step_weight_bytes"] / (ms * 1e-3) / 1e9, 1),
+        "sampler_us_per_row": result["sampler_us_per_row"],
+        "wall_ms_per_step": round(result["wall_ms_per_step"], 5),
+    }
+    print(json.dumps(line))
+
+
+def cpu_baseline(budget_s):
+    """ferrum_core's decode-step hot path on the host CPU (the oracle, one core)."""
+    import numpy as np
+
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+
+    if not os.path.exists(oracle.LIB_PATH):
+        oracle.build()
+    t_setup = time.perf_counter()
+    rng = np.random.default_rng(7)
+    layers = []
+    for li in range(L):
+        ws = []
+        for (n, k) in LAYER_SHAPES:
+            raw = oracle.quantize_weight(n, k, seed=li * 10 + n + k)
+            ws.append((oracle.q8_0_to_ferrum_weight(raw, n, k), rng.standard_normal(n).astype(np.float32) * 0.1))
+        layers.append(ws)
+    head = oracle.q8_0_to_ferrum_weight(oracle.quantize_weight(V, D, seed=99), V, D)
+    x_d = rng.standard_normal((1, D)).astype(np.float32)
+    x_f = rng.standard_normal((1, FFN)).astype(np.float32)
+    recent = list(rng.integers(0, V, size=N_RECENT))
+    params = oracle.SamplingParams(**SAMPLER)
+    orng = oracle.Rng(7)
+    setup = time.perf_counter() - t_setup
+
+    def one_step():
+        for ws in layers:
+            for (w_kn, b), (n, k) in zip(ws, LAYER_SHAPES):
+                oracle.linear_forward(x_d if k == D else x_f, w_kn, b, threads=1)
+        z = oracle.linear_forward(x_d, head, None, threads=1)
+        l = oracle.ln_bridge(oracle.softmax_rows(z)[0])
+        oracle.sample_with_params(l, params, recent, orng)
+
+    one_step()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while time.perf_counter() < t_end or len(times) < 3:
+        t0 = time.perf_counter()
+        one_step()
+        times.append(time.perf_counter() - t0)
+    best, med = min(times), float(np.median(times))
+    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+            "sample": f"{len(times)} GPT-2-124M decode steps of the hot path (49 f32-expanded linears, serial "
+                      f"m=1 as ferrum_core runs them, + softmax/ln bridge + sampler) in {sum(times):.1f} s; "
+                      f"median {med * 1e3:.1f} ms/step, best {best * 1e3:.1f} ms; setup {setup:.1f} s",
+            "best_tok_s": round(1.0 / best, 3)}
+
+
+if __name__ == "__main__":
+    main()

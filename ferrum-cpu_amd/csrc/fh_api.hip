@@ -1,0 +1,457 @@
+// fh_api.hip — the C ABI of libferrum_hip (contexts, weights, argument checks).
+//
+// Argument checking and error text follow the reference entry points each
+// function replaces (cited per function); kernels live in the other
+// translation units and are reached through the fh_launch_* launchers.
+#include <cstdio>
+#include <cstring>
+#include <new>
+#include <string>
+
+#include "fh_internal.hpp"
+
+static thread_local std::string g_create_err;
+
+int fh_fail(fh_ctx* ctx, int code, const std::string& msg) {
+    if (ctx) ctx->err = msg;
+    else g_create_err = msg;
+    return code;
+}
+
+int fh_hip_fail(fh_ctx* ctx, hipError_t e, const char* what) {
+    std::string m = std::string("HIP error ") + hipGetErrorName(e) + " (" + hipGetErrorString(e) +
+                    ") in " + what;
+    int code = (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation) ? FH_ERR_OOM : FH_ERR_HIP;
+    return fh_fail(ctx, code, m);
+}
+
+int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) {
+    bytes = fh_align256(bytes ? bytes : 256);
+    if (ctx->ws_bytes < bytes) {
+        if (ctx->ws) {
+            // The previous workspace may still be read by queued kernels.
+            FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            FH_HIP(ctx, hipFree(ctx->ws));
+            ctx->ws = nullptr;
+            ctx->ws_bytes = 0;
+        }
+        FH_HIP(ctx, hipMalloc(&ctx->ws, bytes));
+        ctx->ws_bytes = bytes;
+    }
+    *out = ctx->ws;
+    return FH_OK;
+}
+
+int fh_staging(fh_ctx* ctx, size_t bytes, void** out) {
+    bytes = fh_align256(bytes ? bytes : 256);
+    if (ctx->io_bytes < bytes) {
+        if (ctx->io) {
+            FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            FH_HIP(ctx, hipHostFree(ctx->io));
+            ctx->io = nullptr;
+            ctx->io_bytes = 0;
+        }
+        FH_HIP(ctx, hipHostMalloc(&ctx->io, bytes, hipHostMallocDefault));
+        ctx->io_bytes = bytes;
+    }
+    *out = ctx->io;
+    return FH_OK;
+}
+
+// Every entry point works on the context's device.
+// (hipSetDevice only when needed, so calls stay legal under stream capture.)
+static hipError_t on_device(int device) {
+    int cur = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur == device) return hipSuccess;
+    return hipSetDevice(device);
+}
+#define FH_ON_DEVICE(ctx) FH_HIP((ctx), on_device((ctx)->device))
+
+extern "C" {
+
+int fh_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int fh_ctx_create(int device, fh_ctx** out) {
+    if (!out) return fh_fail(nullptr, FH_ERR_INVALID, "fh_ctx_create: out is NULL");
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n == 0)
+        return fh_fail(nullptr, FH_ERR_HIP, "fh_ctx_create: no HIP device visible");
+    if (device < 0 || device >= n)
+        return fh_fail(nullptr, FH_ERR_INVALID,
+                       "fh_ctx_create: device " + std::to_string(device) + " out of range (" +
+                           std::to_string(n) + " visible)");
+    fh_ctx* c = new (std::nothrow) fh_ctx();
+    if (!c) return fh_fail(nullptr, FH_ERR_OOM, "fh_ctx_create: out of host memory");
+    c->device = device;
+    if ((e = hipSetDevice(device)) != hipSuccess ||
+        (e = hipStreamCreateWithFlags(&c->own, hipStreamNonBlocking)) != hipSuccess) {
+        int code = fh_hip_fail(nullptr, e, "fh_ctx_create");
+        delete c;
+        return code;
+    }
+    c->stream = c->own;
+    *out = c;
+    return FH_OK;
+}
+
+void fh_ctx_destroy(fh_ctx* ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+    if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->io) (void)hipHostFree(ctx->io);
+    if (ctx->own) (void)hipStreamDestroy(ctx->own);
+    delete ctx;
+}
+
+int fh_ctx_set_stream(fh_ctx* ctx, void* hip_stream) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+    return FH_OK;
+}
+
+int fh_sync(fh_ctx* ctx) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    FH_ON_DEVICE(ctx);
+    FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    return FH_OK;
+}
+
+const char* fh_last_error(const fh_ctx* ctx) { return ctx ? ctx->err.c_str() : g_create_err.c_str(); }
+
+// ---- weights -------------------------------------------------------------------
+
+static int alloc_weight(fh_ctx* ctx, size_t n_rows, size_t k, fh_q8_0** out) {
+    if (!out) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_upload: out is NULL");
+    *out = nullptr;
+    if (k == 0 || k % 32 != 0)
+        return fh_fail(ctx, FH_ERR_INVALID,
+                       "fh_q8_0_upload: ne0 = " + std::to_string(k) +
+                           " is not a positive multiple of the Q8_0 block size 32");
+    if (n_rows == 0) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_upload: n_rows is 0");
+    fh_q8_0* w = new (std::nothrow) fh_q8_0();
+    if (!w) return fh_fail(ctx, FH_ERR_OOM, "fh_q8_0_upload: out of host memory");
+    w->ctx = ctx;
+    w->device = ctx->device;
+    w->n = n_rows;
+    w->k = k;
+    w->kb = k / 32;
+    size_t qbytes = fh_align256(n_rows * k), dbytes = fh_align256(n_rows * w->kb * 2);
+    hipError_t e = hipMalloc(&w->base, qbytes + dbytes);
+    if (e != hipSuccess) {
+        delete w;
+        return fh_hip_fail(ctx, e, "hipMalloc(Q8_0 weight)");
+    }
+    w->qs = static_cast<int8_t*>(w->base);
+    w->d = reinterpret_cast<uint16_t*>(static_cast<char*>(w->base) + qbytes);
+    *out = w;
+    return FH_OK;
+}
+
+int fh_q8_0_upload_device(fh_ctx* ctx, const uint8_t* d_gguf, size_t n_rows, size_t k,
+                          fh_q8_0** out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (!d_gguf) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_upload: bytes is NULL");
+    FH_ON_DEVICE(ctx);
+    int rc = alloc_weight(ctx, n_rows, k, out);
+    if (rc) return rc;
+    rc = fh_launch_repack(ctx, d_gguf, n_rows, k, (*out)->qs, (*out)->d);
+    if (rc) {
+        fh_q8_0_free(*out);
+        *out = nullptr;
+    }
+    return rc;
+}
+
+int fh_q8_0_upload(fh_ctx* ctx, const uint8_t* gguf, size_t n_rows, size_t k, fh_q8_0** out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (!gguf) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_upload: bytes is NULL");
+    if (k == 0 || k % 32 != 0 || n_rows == 0) return alloc_weight(ctx, n_rows, k, out);
+    FH_ON_DEVICE(ctx);
+    size_t raw = n_rows * (k / 32) * 34;
+    void* d_raw = nullptr;
+    FH_HIP(ctx, hipMalloc(&d_raw, raw));
+    hipError_t e = hipMemcpyAsync(d_raw, gguf, raw, hipMemcpyHostToDevice, ctx->stream);
+    int rc = e == hipSuccess ? fh_q8_0_upload_device(ctx, static_cast<uint8_t*>(d_raw), n_rows, k, out)
+                             : fh_hip_fail(ctx, e, "hipMemcpyAsync(weight upload)");
+    hipError_t es = hipStreamSynchronize(ctx->stream);
+    (void)hipFree(d_raw);
+    if (rc == FH_OK && es != hipSuccess) {
+        fh_q8_0_free(*out);
+        *out = nullptr;
+        return fh_hip_fail(ctx, es, "hipStreamSynchronize(weight upload)");
+    }
+    return rc;
+}
+
+int fh_q8_0_download(fh_ctx* ctx, const fh_q8_0* w, uint8_t* gguf) {
+    if (!ctx || !w || !gguf) return ctx ? fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_download: NULL argument") : FH_ERR_INVALID;
+    ctx->err.clear();
+    FH_ON_DEVICE(ctx);
+    size_t raw = w->n * w->kb * 34;
+    void* d_raw = nullptr;
+    FH_HIP(ctx, hipMalloc(&d_raw, raw));
+    int rc = fh_launch_unpack(ctx, w->qs, w->d, w->n, w->k, static_cast<uint8_t*>(d_raw));
+    if (rc == FH_OK) {
+        hipError_t e = hipMemcpyAsync(gguf, d_raw, raw, hipMemcpyDeviceToHost, ctx->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+        if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_download copy");
+    } else {
+        (void)hipStreamSynchronize(ctx->stream);
+    }
+    (void)hipFree(d_raw);
+    return rc;
+}
+
+int fh_q8_0_dims(const fh_q8_0* w, size_t* n_rows, size_t* k) {
+    if (!w) return FH_ERR_INVALID;
+    if (n_rows) *n_rows = w->n;
+    if (k) *k = w->k;
+    return FH_OK;
+}
+
+void fh_q8_0_free(fh_q8_0* w) {
+    if (!w) return;
+    (void)hipSetDevice(w->device);
+    if (w->ctx && w->ctx->stream) (void)hipStreamSynchronize(w->ctx->stream);
+    if (w->base) (void)hipFree(w->base);
+    delete w;
+}
+
+// ---- linear --------------------------------------------------------------------
+
+// Shape checks of ops::linear_forward (ops.rs:236-246) / Linear::forward
+// (layer/linear.rs:178-183), with the reference's messages.
+static int check_linear(fh_ctx* ctx, const fh_q8_0* w, size_t k, const void* bias, size_t bias_len,
+                        int numerics) {
+    if (!w) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight is NULL");
+    if (numerics != FH_W8A32 && numerics != FH_W8A8)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: unknown numerics " + std::to_string(numerics));
+    if (w->device != ctx->device)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight lives on another device");
+    if (k != w->k)
+        return fh_fail(ctx, FH_ERR_DIM, "linear_forward: input width " + std::to_string(k) +
+                                            " \xe2\x89\xa0 weight rows " + std::to_string(w->k));
+    if ((bias == nullptr) != (bias_len == 0) || (bias_len != 0 && bias_len != w->n))
+        return fh_fail(ctx, FH_ERR_DIM, "linear_forward: bias length " + std::to_string(bias_len) +
+                                            " \xe2\x89\xa0 out_features " + std::to_string(w->n));
+    return FH_OK;
+}
+
+int fh_q8_0_linear_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                         const float* d_bias, size_t bias_len, float* d_y, int numerics) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    int rc = check_linear(ctx, w, k, d_bias, bias_len, numerics);
+    if (rc) return rc;
+    if (m == 0) return FH_OK;
+    if (!d_x || !d_y) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x or y is NULL");
+    FH_ON_DEVICE(ctx);
+    return numerics == FH_W8A32 ? fh_launch_linear_w8a32(ctx, w, d_x, m, d_bias, d_y)
+                                : fh_launch_linear_w8a8(ctx, w, d_x, m, d_bias, d_y);
+}
+
+int fh_q8_0_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, size_t k,
+                   const float* bias, size_t bias_len, float* y, int numerics) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    int rc = check_linear(ctx, w, k, bias, bias_len, numerics);
+    if (rc) return rc;
+    if (m == 0) return FH_OK;
+    if (!x || !y) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x or y is NULL");
+    FH_ON_DEVICE(ctx);
+    size_t xb = fh_align256(m * k * 4), bb = fh_align256(bias_len * 4), yb = fh_align256(m * w->n * 4);
+    // Device buffers of the blocking call sit past the kernels' own workspace
+    // needs, so allocate them separately from ctx->ws.
+    char* dev = nullptr;
+    FH_HIP(ctx, hipMalloc(&dev, xb + bb + yb));
+    float* dx = reinterpret_cast<float*>(dev);
+    float* db = bias_len ? reinterpret_cast<float*>(dev + xb) : nullptr;
+    float* dy = reinterpret_cast<float*>(dev + xb + bb);
+    hipError_t e = hipMemcpyAsync(dx, x, m * k * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && db) e = hipMemcpyAsync(db, bias, bias_len * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_linear copy-in");
+    if (rc == FH_OK) rc = numerics == FH_W8A32 ? fh_launch_linear_w8a32(ctx, w, dx, m, db, dy)
+                                               : fh_launch_linear_w8a8(ctx, w, dx, m, db, dy);
+    if (rc == FH_OK) {
+        e = hipMemcpyAsync(y, dy, m * w->n * 4, hipMemcpyDeviceToHost, ctx->stream);
+        if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_linear copy-out");
+    }
+    e = hipStreamSynchronize(ctx->stream);
+    if (rc == FH_OK && e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_linear sync");
+    (void)hipFree(dev);
+    return rc;
+}
+
+// ---- Q8_0 codec ----------------------------------------------------------------
+
+int fh_q8_0_encode_async(fh_ctx* ctx, const float* d_x, size_t n, uint8_t* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (n % 32 != 0)
+        return fh_fail(ctx, FH_ERR_INVALID, "tensor length " + std::to_string(n) +
+                                                " is not a multiple of block size 32");
+    if (n == 0) return FH_OK;
+    if (!d_x || !d_out) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_encode: NULL buffer");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_encode(ctx, d_x, n, d_out);
+}
+
+int fh_q8_0_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (n % 32 != 0)
+        return fh_fail(ctx, FH_ERR_INVALID, "tensor length " + std::to_string(n) +
+                                                " is not a multiple of block size 32");
+    if (n == 0) return FH_OK;
+    if (!x || !out) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_encode: NULL buffer");
+    FH_ON_DEVICE(ctx);
+    size_t xb = fh_align256(n * 4), ob = n / 32 * 34;
+    char* dev = nullptr;
+    FH_HIP(ctx, hipMalloc(&dev, xb + ob));
+    int rc = FH_OK;
+    hipError_t e = hipMemcpyAsync(dev, x, n * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_encode copy-in");
+    if (rc == FH_OK) rc = fh_launch_encode(ctx, reinterpret_cast<float*>(dev), n, reinterpret_cast<uint8_t*>(dev + xb));
+    if (rc == FH_OK) {
+        e = hipMemcpyAsync(out, dev + xb, ob, hipMemcpyDeviceToHost, ctx->stream);
+        if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_encode copy-out");
+    }
+    e = hipStreamSynchronize(ctx->stream);
+    if (rc == FH_OK && e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_encode sync");
+    (void)hipFree(dev);
+    return rc;
+}
+
+int fh_q8_0_dequant_async(fh_ctx* ctx, const uint8_t* d_raw, size_t n, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (n % 32 != 0)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_dequant: n = " + std::to_string(n) +
+                                                " is not a multiple of block size 32");
+    if (n == 0) return FH_OK;
+    if (!d_raw || !d_out) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_dequant: NULL buffer");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_dequant(ctx, d_raw, n, d_out);
+}
+
+int fh_q8_0_block_dots_async(fh_ctx* ctx, const fh_q8_0* w, const int8_t* d_qx, size_t m,
+                             int32_t* d_dots) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (!w) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_block_dots: weight is NULL");
+    if (m == 0) return FH_OK;
+    if (!d_qx || !d_dots) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_block_dots: NULL buffer");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_block_dots(ctx, w, d_qx, m, d_dots);
+}
+
+// ---- sampler -------------------------------------------------------------------
+
+enum { FH_MAX_RECENT = 16384 };
+
+static int check_sample(fh_ctx* ctx, size_t rows, size_t vocab, int kind, const fh_sampling_params* p) {
+    if (!p) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: params is NULL");
+    if (kind != FH_LOGITS_RAW && kind != FH_LOGITS_GPT2_SOFTMAX)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: unknown logits kind " + std::to_string(kind));
+    if (vocab == 0) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: vocab is 0");
+    if (vocab > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_sample_rows: vocab above 2^31 - 1");
+    if (rows > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_sample_rows: rows above 2^31 - 1");
+    return FH_OK;
+}
+
+static int check_offsets(fh_ctx* ctx, const uint32_t* off, size_t rows, const void* recent) {
+    if (!off) return FH_OK;
+    for (size_t r = 0; r < rows; r++) {
+        if (off[r + 1] < off[r])
+            return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: recent_offsets decrease at row " + std::to_string(r));
+        if (off[r + 1] - off[r] > FH_MAX_RECENT)
+            return fh_fail(ctx, FH_ERR_LIMIT, "fh_sample_rows: row " + std::to_string(r) + " has " +
+                                                  std::to_string(off[r + 1] - off[r]) +
+                                                  " recent ids, above the limit of 16384");
+    }
+    if (off[rows] != off[0] && !recent) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: recent is NULL");
+    return FH_OK;
+}
+
+int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t vocab, int kind,
+                         const fh_sampling_params* p, const uint32_t* d_recent,
+                         const uint32_t* d_off, const uint64_t* d_draws, uint32_t* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    int rc = check_sample(ctx, rows, vocab, kind, p);
+    if (rc) return rc;
+    if (rows == 0) return FH_OK;
+    if (!d_logits || !d_out) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: logits or out_ids is NULL");
+    if (!d_draws && !(p->temperature <= 0.0f))
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: draws is NULL with temperature > 0");
+    // Device offsets cannot be inspected without a copy; the kernel clamps each
+    // row's list to FH_MAX_RECENT ids and ignores decreasing offsets.
+    FH_ON_DEVICE(ctx);
+    return fh_launch_sample(ctx, d_logits, rows, vocab, kind, p, d_recent, d_off, d_draws, d_out);
+}
+
+int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, int kind,
+                   const fh_sampling_params* p, const uint32_t* recent, const uint32_t* off,
+                   const uint64_t* draws, uint32_t* out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    int rc = check_sample(ctx, rows, vocab, kind, p);
+    if (rc) return rc;
+    if (rows == 0) return FH_OK;
+    if (!logits || !out) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: logits or out_ids is NULL");
+    bool sampled = !(p->temperature <= 0.0f);
+    if (!draws && sampled) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: draws is NULL with temperature > 0");
+    if ((rc = check_offsets(ctx, off, rows, recent))) return rc;
+    FH_ON_DEVICE(ctx);
+    size_t n_recent = off ? off[rows] - off[0] : 0;
+    size_t lb = fh_align256(rows * vocab * 4), rb = fh_align256(n_recent * 4 + 4),
+           ob = fh_align256((rows + 1) * 4), db = fh_align256(rows * 8), yb = fh_align256(rows * 4);
+    char* dev = nullptr;
+    FH_HIP(ctx, hipMalloc(&dev, lb + rb + ob + db + yb));
+    float* d_logits = reinterpret_cast<float*>(dev);
+    uint32_t* d_recent = reinterpret_cast<uint32_t*>(dev + lb);
+    uint32_t* d_off = reinterpret_cast<uint32_t*>(dev + lb + rb);
+    uint64_t* d_draws = reinterpret_cast<uint64_t*>(dev + lb + rb + ob);
+    uint32_t* d_out = reinterpret_cast<uint32_t*>(dev + lb + rb + ob + db);
+    hipError_t e = hipMemcpyAsync(d_logits, logits, rows * vocab * 4, hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess && n_recent)
+        e = hipMemcpyAsync(d_recent, recent + off[0], n_recent * 4, hipMemcpyHostToDevice, ctx->stream);
+    // Rebase the offsets so the device list starts at 0.
+    uint32_t* hoff = nullptr;
+    if (e == hipSuccess && off) {
+        hoff = new (std::nothrow) uint32_t[rows + 1];
+        if (!hoff) rc = fh_fail(ctx, FH_ERR_OOM, "fh_sample_rows: out of host memory");
+        else {
+            for (size_t r = 0; r <= rows; r++) hoff[r] = off[r] - off[0];
+            e = hipMemcpyAsync(d_off, hoff, (rows + 1) * 4, hipMemcpyHostToDevice, ctx->stream);
+        }
+    }
+    if (e == hipSuccess && draws) e = hipMemcpyAsync(d_draws, draws, rows * 8, hipMemcpyHostToDevice, ctx->stream);
+    if (e != hipSuccess && rc == FH_OK) rc = fh_hip_fail(ctx, e, "fh_sample_rows copy-in");
+    if (rc == FH_OK)
+        rc = fh_launch_sample(ctx, d_logits, rows, vocab, kind, p, n_recent ? d_recent : nullptr,
+                              off ? d_off : nullptr, draws ? d_draws : nullptr, d_out);
+    if (rc == FH_OK) {
+        e = hipMemcpyAsync(out, d_out, rows * 4, hipMemcpyDeviceToHost, ctx->stream);
+        if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_sample_rows copy-out");
+    }
+    e = hipStreamSynchronize(ctx->stream);
+    if (rc == FH_OK && e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_sample_rows sync");
+    delete[] hoff;
+    (void)hipFree(dev);
+    return rc;
+}
+
+}  // extern "C"

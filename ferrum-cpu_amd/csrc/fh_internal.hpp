@@ -1,0 +1,84 @@
+// fh_internal.hpp — shared host/device definitions of libferrum_hip (gfx950).
+//
+// Device weight layout ("split planes", built once at upload):
+//   qs : int8  [n][k]      the Q8_0 quants, row-major; every row starts 32-B
+//                          aligned (k % 32 == 0), so a lane loads 16 quants
+//                          with one 16-byte global load.
+//   d  : uint16 [n][k/32]  the f16 block scales, as stored in GGUF.
+// Together 34 B per 32 weights, exactly the GGUF footprint: the repack only
+// separates GGUF's interleaved 34-byte blocks (which are 2-byte aligned) into
+// two naturally aligned planes.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+#include <string>
+
+#include "../../include/ferrum_hip.h"
+
+struct fh_ctx {
+    int device = 0;
+    hipStream_t own = nullptr;   // created by fh_ctx_create
+    hipStream_t stream = nullptr;  // where work is enqueued (own or borrowed)
+    std::string err;
+    // Grow-on-demand device workspace for intermediate buffers (activation
+    // quants, sampler rows).  Reused across calls on this context.
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    // Host-side staging for the synchronous (host pointer) entry points.
+    void* io = nullptr;
+    size_t io_bytes = 0;
+};
+
+struct fh_q8_0 {
+    fh_ctx* ctx = nullptr;
+    int device = 0;
+    size_t n = 0, k = 0, kb = 0;
+    int8_t* qs = nullptr;
+    uint16_t* d = nullptr;
+    void* base = nullptr;  // the one allocation holding both planes
+};
+
+// ---- error plumbing ---------------------------------------------------------
+int fh_fail(fh_ctx* ctx, int code, const std::string& msg);
+int fh_hip_fail(fh_ctx* ctx, hipError_t e, const char* what);
+#define FH_HIP(ctx, call)                                          \
+    do {                                                           \
+        hipError_t e_ = (call);                                    \
+        if (e_ != hipSuccess) return fh_hip_fail((ctx), e_, #call); \
+    } while (0)
+
+// Make sure ctx->ws holds at least `bytes` (device, 256-B aligned).
+int fh_workspace(fh_ctx* ctx, size_t bytes, void** out);
+// Make sure ctx->io holds at least `bytes` (pinned host).
+int fh_staging(fh_ctx* ctx, size_t bytes, void** out);
+// Round up to a multiple of 256 bytes.
+static inline size_t fh_align256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+// ---- launchers implemented in the kernel translation units -------------------
+int fh_launch_repack(fh_ctx* ctx, const uint8_t* d_raw, size_t n, size_t k, int8_t* qs,
+                     uint16_t* d);
+int fh_launch_unpack(fh_ctx* ctx, const int8_t* qs, const uint16_t* d, size_t n, size_t k,
+                     uint8_t* d_raw);
+int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
+                           const float* bias, float* y);
+int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
+                          const float* bias, float* y);
+int fh_launch_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out);
+int fh_launch_dequant(fh_ctx* ctx, const uint8_t* raw, size_t n, float* out);
+int fh_launch_block_dots(fh_ctx* ctx, const fh_q8_0* w, const int8_t* qx, size_t m,
+                         int32_t* dots);
+int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, int kind,
+                     const fh_sampling_params* p, const uint32_t* recent,
+                     const uint32_t* offsets, const uint64_t* draws, uint32_t* out);
+
+// ---- device helpers ---------------------------------------------------------
+#ifdef __HIPCC__
+// IEEE half -> float, exact for every code (gguf/dequant.rs:7-35 semantics; the
+// hardware conversion is exact, subnormals included).
+__device__ __forceinline__ float fh_h2f(uint16_t h) {
+    return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+#endif

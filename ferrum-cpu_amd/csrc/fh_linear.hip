@@ -1,0 +1,312 @@
+// fh_linear.hip — Q8_0 linear layers on gfx950.
+//
+//   y[i, j] = sum_p x[i, p] * W[j, p] (+ b[j])      W = f16(d) * q, exact in f32
+//
+// is ferrum_core's ops::linear_forward on its f32 expansion of the GGUF tensor
+// (ops.rs:233-256, loader/decode.rs:97-100).  The reference sums the products
+// in ascending p without FMA and adds the bias last; these kernels keep the
+// bias last but reduce in a parallel order with FMA, which moves the last bits
+// (judged at 1e-5 relative, see tests/test_gpu_linear.py).
+//
+// Kernels
+//  k_gemv_w8a32  m <= 2 (decode).  HBM-bound: every weight byte is read once,
+//                16 quants per lane per 16-byte load, dequantised in registers;
+//                the activation chunks a lane needs stay in its registers for
+//                every row it visits.  G lanes share a row and finish it with a
+//                butterfly shuffle reduction; 64/G rows per wave per step.
+//  k_gemm_w8a32  m >= 3.  LDS-tiled f32 FMA (32 x 64 outputs per block,
+//                K step = one Q8_0 block), weights dequantised once per tile.
+//  k_linear_w8a8 llama.cpp numerics: x is Q8_0-encoded per 32 (bit-exact
+//                q8_0_block), exact int32 block dots with sdot4, then
+//                sum_b f32(dot_b) * (d_w * d_x) + b.
+#include "fh_internal.hpp"
+
+__global__ void fh_k_encode_split(const float* __restrict__ x, size_t nblocks, uint32_t* __restrict__ qx,
+                                  uint16_t* __restrict__ dx);
+
+namespace {
+
+constexpr int kWaves = 4;  // waves per block in the GEMV kernels
+constexpr int kRowSetsPerStep = 2;
+
+__device__ __forceinline__ float sbyte(uint32_t w, int i) {
+    return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xFFu));
+}
+
+template <int G, int CPL, int M, bool kBias>
+__global__ void __launch_bounds__(64 * kWaves)
+    k_gemv_w8a32(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const float* __restrict__ x,
+                 const float* __restrict__ bias, float* __restrict__ y, int n, int k) {
+    constexpr int RW = 64 / G;  // rows per wave per row-set
+    const int lane = threadIdx.x & 63;
+    const int grp = lane / G, gl = lane % G;
+    const int k16 = k >> 4, kb = k >> 5;
+
+    float xr[M][CPL][16];
+#pragma unroll
+    for (int c = 0; c < CPL; c++) {
+        const int ci = gl + c * G;
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            if (ci < k16) {
+                const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * k + ci * 16);
+#pragma unroll
+                for (int v = 0; v < 4; v++) {
+                    float4 f = src[v];
+                    xr[m][c][4 * v + 0] = f.x;
+                    xr[m][c][4 * v + 1] = f.y;
+                    xr[m][c][4 * v + 2] = f.z;
+                    xr[m][c][4 * v + 3] = f.w;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 16; t++) xr[m][c][t] = 0.0f;
+            }
+        }
+    }
+
+    const int nsets = (n + RW - 1) / RW;
+    const int wave_id = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int nwaves = gridDim.x * kWaves;
+    for (int rs0 = wave_id * kRowSetsPerStep; rs0 < nsets; rs0 += nwaves * kRowSetsPerStep) {
+        uint4 qv[kRowSetsPerStep][CPL];
+        float dv[kRowSetsPerStep][CPL];
+#pragma unroll
+        for (int u = 0; u < kRowSetsPerStep; u++) {
+            const int row = (rs0 + u) * RW + grp;
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+                const int ci = gl + c * G;
+                if (row < n && ci < k16) {
+                    qv[u][c] = *reinterpret_cast<const uint4*>(qs + static_cast<size_t>(row) * k + ci * 16);
+                    dv[u][c] = fh_h2f(dsc[static_cast<size_t>(row) * kb + (ci >> 1)]);
+                } else {
+                    qv[u][c] = make_uint4(0, 0, 0, 0);
+                    dv[u][c] = 0.0f;
+                }
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kRowSetsPerStep; u++) {
+            float acc[M];
+#pragma unroll
+            for (int m = 0; m < M; m++) acc[m] = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+                const uint32_t wq[4] = {qv[u][c].x, qv[u][c].y, qv[u][c].z, qv[u][c].w};
+                float wf[16];
+#pragma unroll
+                for (int t = 0; t < 16; t++) wf[t] = sbyte(wq[t >> 2], t & 3);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    float s = 0.0f;
+#pragma unroll
+                    for (int t = 0; t < 16; t++) s = fmaf(xr[m][c][t], wf[t], s);
+                    acc[m] = fmaf(dv[u][c], s, acc[m]);
+                }
+            }
+#pragma unroll
+            for (int off = G / 2; off > 0; off >>= 1)
+#pragma unroll
+                for (int m = 0; m < M; m++) acc[m] += __shfl_xor(acc[m], off, 64);
+            const int row = (rs0 + u) * RW + grp;
+            if (gl == 0 && row < n) {
+#pragma unroll
+                for (int m = 0; m < M; m++) y[static_cast<size_t>(m) * n + row] = kBias ? acc[m] + bias[row] : acc[m];
+            }
+        }
+    }
+}
+
+// ---- m >= 3: LDS-tiled FMA GEMM ----------------------------------------------
+constexpr int BM = 32, BN = 64, BK = 32;
+
+__global__ void __launch_bounds__(256)
+    k_gemm_w8a32(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const float* __restrict__ x,
+                 const float* __restrict__ bias, float* __restrict__ y, int m, int n, int k) {
+    __shared__ float xs[BM][BK + 1];
+    __shared__ float ws[BK][BN + 4];
+    const int tid = threadIdx.x;
+    const int i0 = blockIdx.y * BM, j0 = blockIdx.x * BN;
+    const int tm = tid / 16, tn = tid % 16;  // 16 x 16 threads, 2 x 4 outputs each
+    const int kb = k >> 5;
+    float acc[2][4] = {};
+    for (int b = 0; b < kb; b++) {
+        // x tile: 32 x 32 floats, 4 per thread
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int e = tid + r * 256, ii = e / BK, kk = e % BK;
+            xs[ii][kk] = (i0 + ii < m) ? x[static_cast<size_t>(i0 + ii) * k + b * BK + kk] : 0.0f;
+        }
+        // w tile: 64 rows x 32 quants, 8 per thread, dequantised (exact)
+        {
+            const int jj = tid / 4, part = tid % 4;
+            const int j = j0 + jj;
+            if (j < n) {
+                const uint2 q = *reinterpret_cast<const uint2*>(qs + static_cast<size_t>(j) * k + b * BK + part * 8);
+                const float d = fh_h2f(dsc[static_cast<size_t>(j) * kb + b]);
+#pragma unroll
+                for (int t = 0; t < 8; t++) ws[part * 8 + t][jj] = d * sbyte(t < 4 ? q.x : q.y, t & 3);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 8; t++) ws[part * 8 + t][jj] = 0.0f;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < BK; kk++) {
+            const float a0 = xs[tm * 2][kk], a1 = xs[tm * 2 + 1][kk];
+#pragma unroll
+            for (int c = 0; c < 4; c++) {
+                const float w = ws[kk][tn * 4 + c];
+                acc[0][c] = fmaf(a0, w, acc[0][c]);
+                acc[1][c] = fmaf(a1, w, acc[1][c]);
+            }
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++) {
+        const int i = i0 + tm * 2 + r;
+        if (i >= m) continue;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const int j = j0 + tn * 4 + c;
+            if (j < n) y[static_cast<size_t>(i) * n + j] = bias ? acc[r][c] + bias[j] : acc[r][c];
+        }
+    }
+}
+
+// ---- W8A8 ------------------------------------------------------------------------
+// One lane per Q8_0 block of a (activation row, weight row) pair; G lanes per
+// pair reduce with a butterfly.  Block dots are exact (sdot4 on int8).
+template <int G>
+__global__ void __launch_bounds__(256)
+    k_linear_w8a8(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const int8_t* __restrict__ qx,
+                  const uint16_t* __restrict__ dx, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
+                  int k) {
+    constexpr int RW = 64 / G;
+    const int lane = threadIdx.x & 63;
+    const int grp = lane / G, gl = lane % G;
+    const int kb = k >> 5;
+    const size_t pairs = static_cast<size_t>(m) * n;
+    const size_t set = (blockIdx.x * static_cast<size_t>(4) + (threadIdx.x >> 6));
+    const size_t pair = set * RW + grp;
+    const bool live = pair < pairs;
+    const int i = live ? static_cast<int>(pair / n) : 0, j = live ? static_cast<int>(pair % n) : 0;
+    float acc = 0.0f;
+    if (live) {
+        for (int b = gl; b < kb; b += G) {
+            const int4* a = reinterpret_cast<const int4*>(qx + static_cast<size_t>(i) * k + b * 32);
+            const int4* w = reinterpret_cast<const int4*>(qs + static_cast<size_t>(j) * k + b * 32);
+            int s = 0;
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                const int4 av = a[h], wv = w[h];
+                s = __builtin_amdgcn_sdot4(av.x, wv.x, s, false);
+                s = __builtin_amdgcn_sdot4(av.y, wv.y, s, false);
+                s = __builtin_amdgcn_sdot4(av.z, wv.z, s, false);
+                s = __builtin_amdgcn_sdot4(av.w, wv.w, s, false);
+            }
+            const float dd = fh_h2f(dsc[static_cast<size_t>(j) * kb + b]) * fh_h2f(dx[static_cast<size_t>(i) * kb + b]);
+            acc = fmaf(static_cast<float>(s), dd, acc);
+        }
+    }
+#pragma unroll
+    for (int off = G / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off, 64);
+    if (live && gl == 0) y[pair] = bias ? acc + bias[j] : acc;
+}
+
+template <int G, int CPL, int M>
+int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y) {
+    // The bias-free form (ops::matmul, the tied lm_head) is its own instance.
+    auto kernel = bias ? k_gemv_w8a32<G, CPL, M, true> : k_gemv_w8a32<G, CPL, M, false>;
+    constexpr int RW = 64 / G;
+    const size_t nsets = (w->n + RW - 1) / RW;
+    const size_t steps = (nsets + kRowSetsPerStep - 1) / kRowSetsPerStep;
+    // Enough waves for every row-set step, capped at 16 waves per CU on 256 CUs.
+    size_t blocks = (steps + kWaves - 1) / kWaves;
+    if (blocks > 1024) blocks = 1024;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves), 0,
+                       ctx->stream, w->qs, w->d, x, bias, y, static_cast<int>(w->n), static_cast<int>(w->k));
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+// Lanes per row (G) and 16-quant chunks per lane (CPL) for a row of k quants:
+// the fewest chunks per lane (at most 4 when k allows) with all 64 lanes busy.
+template <int M>
+int dispatch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y) {
+    const size_t k16 = w->k / 16;
+#define FH_GEMV(G, C) return launch_gemv<G, C, M>(ctx, w, x, bias, y)
+    if (k16 >= 64) {
+        const size_t cpl = (k16 + 63) / 64;
+        if (cpl == 1) FH_GEMV(64, 1);
+        if (cpl == 2) FH_GEMV(64, 2);
+        if (cpl == 3) FH_GEMV(64, 3);
+        if (cpl == 4) FH_GEMV(64, 4);
+        if (cpl <= 6) FH_GEMV(64, 6);
+        if (cpl <= 8) FH_GEMV(64, 8);
+        return -1;  // caller falls back to the tiled kernel
+    }
+    if (k16 > 32) FH_GEMV(16, 4);  // 48 (k = 768): 3 used of 4
+    if (k16 > 16) FH_GEMV(8, 4);
+    if (k16 > 8) FH_GEMV(4, 4);
+    if (k16 > 4) FH_GEMV(2, 4);
+    FH_GEMV(1, 4);
+#undef FH_GEMV
+}
+
+template <int G>
+int launch_w8a8(fh_ctx* ctx, const fh_q8_0* w, const int8_t* qx, const uint16_t* dx, size_t m, const float* bias,
+                float* y) {
+    constexpr int RW = 64 / G;
+    const size_t pairs = m * w->n;
+    const size_t sets = (pairs + RW - 1) / RW;
+    const size_t blocks = (sets + 3) / 4;
+    hipLaunchKernelGGL((k_linear_w8a8<G>), dim3(static_cast<unsigned>(blocks)), dim3(256), 0, ctx->stream, w->qs, w->d,
+                       qx, dx, bias, y, static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k));
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+}  // namespace
+
+int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    if (reinterpret_cast<uintptr_t>(x) & 15)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x must be 16-byte aligned");
+    if (w->n > 0x7FFFFFFFu || w->k > 0x7FFFFFFFu || m > 0x7FFFFFFFu)
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: a dimension is above 2^31 - 1");
+    if (m <= 2) {
+        int rc = m == 1 ? dispatch_gemv<1>(ctx, w, x, bias, y) : dispatch_gemv<2>(ctx, w, x, bias, y);
+        if (rc >= 0) return rc;
+    }
+    dim3 grid(static_cast<unsigned>((w->n + BN - 1) / BN), static_cast<unsigned>((m + BM - 1) / BM));
+    if (grid.y > 65535) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: m above 2,097,120");
+    hipLaunchKernelGGL(k_gemm_w8a32, grid, dim3(256), 0, ctx->stream, w->qs, w->d, x, bias, y, static_cast<int>(m),
+                       static_cast<int>(w->n), static_cast<int>(w->k));
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    if (reinterpret_cast<uintptr_t>(x) & 3)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x must be 4-byte aligned");
+    if (w->n > 0x7FFFFFFFu || w->k > 0x7FFFFFFFu || m * w->n > 0x7FFFFFFFu * size_t(64))
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: problem too large for the W8A8 kernel");
+    const size_t kb = w->k / 32;
+    const size_t qbytes = fh_align256(m * w->k), dbytes = fh_align256(m * kb * 2);
+    void* ws = nullptr;
+    int rc = fh_workspace(ctx, qbytes + dbytes, &ws);
+    if (rc) return rc;
+    int8_t* qx = static_cast<int8_t*>(ws);
+    uint16_t* dx = reinterpret_cast<uint16_t*>(static_cast<char*>(ws) + qbytes);
+    const size_t nb = m * kb;
+    hipLaunchKernelGGL(fh_k_encode_split, dim3(static_cast<unsigned>((nb + 255) / 256)), dim3(256), 0, ctx->stream, x,
+                       nb, reinterpret_cast<uint32_t*>(qx), dx);
+    FH_HIP(ctx, hipGetLastError());
+    if (kb >= 64) return launch_w8a8<64>(ctx, w, qx, dx, m, bias, y);
+    if (kb >= 16) return launch_w8a8<16>(ctx, w, qx, dx, m, bias, y);
+    if (kb >= 4) return launch_w8a8<4>(ctx, w, qx, dx, m, bias, y);
+    return launch_w8a8<1>(ctx, w, qx, dx, m, bias, y);
+}

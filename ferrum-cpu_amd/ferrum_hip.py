@@ -1,0 +1,332 @@
+"""Host-side face of libferrum_hip: ferrum_core's matmul-engine and sampler API
+on an MI355X, through the library's C ABI (include/ferrum_hip.h).
+
+The names mirror the reference's Rust API one for one, so code written against
+ferrum_core reads the same here:
+
+    ops::linear_forward(input, weight, bias)   ferrum_core/src/ops.rs:233-256
+    ops::matmul(a, b)                          ferrum_core/src/ops.rs:197-223
+    Linear::forward (Q8_0-backed)              ferrum_core/src/layer/linear.rs:177-210
+    SamplingParams                             ferrum_core/src/slm/sampling.rs:27-83
+    sample_with_params(logits, params, recent, rng)
+                                               ferrum_core/src/slm/sampling.rs:124-210
+    Rng (xorshift64*)                          ferrum_core/src/rng.rs:1-41
+    q8_0_block / enc_q8_0 / dequant_q8_0       quant.rs:271-280, gguf_write/blocks.rs:132-140,
+                                               gguf/dequant.rs:37-49
+
+Errors: a shape mismatch raises ``DimMismatch`` (the reference's
+``InferError::DimMismatch``, same message); every other failure raises
+``FerrumHipError`` carrying the library's status code and message.
+
+The library must be built (``make -C ferrum-cpu_amd``); there is no CPU
+fallback: importing this module without the built library raises.
+PyTorch is only plumbing here (device buffers and streams for the _async
+forms); the computation is the HIP library's.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libferrum_hip.so")
+
+FH_OK, FH_ERR_DIM, FH_ERR_INVALID, FH_ERR_OOM, FH_ERR_HIP, FH_ERR_LIMIT = range(6)
+W8A32, W8A8 = 0, 1
+LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
+
+EXPORTS = (
+    "fh_ctx_create", "fh_ctx_destroy", "fh_ctx_set_stream", "fh_sync", "fh_last_error",
+    "fh_device_count", "fh_q8_0_upload", "fh_q8_0_upload_device", "fh_q8_0_download",
+    "fh_q8_0_dims", "fh_q8_0_free", "fh_q8_0_linear", "fh_q8_0_linear_async",
+    "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
+    "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async",
+)
+
+
+class FerrumHipError(RuntimeError):
+    def __init__(self, code: int, msg: str):
+        super().__init__(f"[ferrum_hip status {code}] {msg}")
+        self.code = code
+        self.msg = msg
+
+
+class DimMismatch(FerrumHipError, ValueError):
+    """ferrum_core's InferError::DimMismatch (error.rs:5-27)."""
+
+
+class SamplingParams(C.Structure):
+    """slm/sampling.rs:27-38 (the cancel flag is a host-side control checked
+    between tokens, so it is not part of the device call)."""
+
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_k", C.c_uint32),
+        ("top_p", C.c_float),
+        ("repetition_penalty", C.c_float),
+    ]
+
+    def __init__(self, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0):
+        super().__init__(float(temperature), int(top_k), float(top_p), float(repetition_penalty))
+
+    @classmethod
+    def with_temperature(cls, temperature: float) -> "SamplingParams":
+        """SamplingParams::with_temperature (slm/sampling.rs:76-82)."""
+        return cls(temperature=temperature)
+
+    def __repr__(self):
+        return (f"SamplingParams(temperature={self.temperature}, top_k={self.top_k}, "
+                f"top_p={self.top_p}, repetition_penalty={self.repetition_penalty})")
+
+
+class Rng:
+    """rng::Rng, the reference's seeded xorshift64* (rng.rs:10-41).  The draws
+    stay on the host so the sequence is exactly the reference's."""
+
+    _M = (1 << 64) - 1
+
+    def __init__(self, seed: int = 0):
+        self.state = 0x9E3779B97F4A7C15 if seed == 0 else seed & self._M
+
+    @classmethod
+    def from_state(cls, state: int) -> "Rng":
+        r = cls(1)
+        r.state = state & cls._M
+        return r
+
+    def next_u64(self) -> int:
+        x = self.state
+        x ^= (x << 13) & self._M
+        x ^= x >> 7
+        x ^= (x << 17) & self._M
+        self.state = x
+        return (x * 0x2545F4914F6CDD1D) & self._M
+
+    def next_f32(self) -> float:
+        return float(np.float32(self.next_u64() >> 40) / np.float32(1 << 24))
+
+
+_lib = None
+
+
+def lib():
+    """The loaded libferrum_hip (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FerrumHipError(FH_ERR_INVALID, f"{LIB_PATH} is not built (run make -C {HERE})")
+        L = C.CDLL(LIB_PATH)
+        vp, sz, i32 = C.c_void_p, C.c_size_t, C.c_int
+        L.fh_ctx_create.argtypes = [i32, C.POINTER(vp)]
+        L.fh_ctx_destroy.argtypes = [vp]
+        L.fh_ctx_destroy.restype = None
+        L.fh_ctx_set_stream.argtypes = [vp, vp]
+        L.fh_sync.argtypes = [vp]
+        L.fh_last_error.argtypes = [vp]
+        L.fh_last_error.restype = C.c_char_p
+        L.fh_device_count.argtypes = []
+        L.fh_q8_0_upload.argtypes = [vp, vp, sz, sz, C.POINTER(vp)]
+        L.fh_q8_0_upload_device.argtypes = [vp, vp, sz, sz, C.POINTER(vp)]
+        L.fh_q8_0_download.argtypes = [vp, vp, vp]
+        L.fh_q8_0_dims.argtypes = [vp, C.POINTER(sz), C.POINTER(sz)]
+        L.fh_q8_0_free.argtypes = [vp]
+        L.fh_q8_0_free.restype = None
+        L.fh_q8_0_linear.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32]
+        L.fh_q8_0_linear_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32]
+        L.fh_q8_0_encode.argtypes = [vp, vp, sz, vp]
+        L.fh_q8_0_encode_async.argtypes = [vp, vp, sz, vp]
+        L.fh_q8_0_dequant_async.argtypes = [vp, vp, sz, vp]
+        L.fh_q8_0_block_dots_async.argtypes = [vp, vp, vp, sz, vp]
+        L.fh_sample_rows.argtypes = [vp, vp, sz, sz, i32, C.POINTER(SamplingParams), vp, vp, vp, vp]
+        L.fh_sample_rows_async.argtypes = [vp, vp, sz, sz, i32, C.POINTER(SamplingParams), vp, vp, vp, vp]
+        _lib = L
+    return _lib
+
+
+def device_count() -> int:
+    return int(lib().fh_device_count())
+
+
+def _ptr(a):
+    if a is None:
+        return None
+    if isinstance(a, int):
+        return a
+    if isinstance(a, np.ndarray):
+        return a.ctypes.data
+    return a.data_ptr()  # a torch tensor on the device
+
+
+class Context:
+    """One HIP device and stream (fh_ctx)."""
+
+    def __init__(self, device: int = 0):
+        h = C.c_void_p()
+        rc = lib().fh_ctx_create(int(device), C.byref(h))
+        if rc != FH_OK:
+            raise FerrumHipError(rc, lib().fh_last_error(None).decode())
+        self.h = h
+        self.device = device
+
+    def check(self, rc: int):
+        if rc == FH_OK:
+            return
+        msg = lib().fh_last_error(self.h).decode()
+        raise (DimMismatch if rc == FH_ERR_DIM else FerrumHipError)(rc, msg)
+
+    def set_stream(self, stream_handle: int | None):
+        """Enqueue on a caller's hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
+        self.check(lib().fh_ctx_set_stream(self.h, stream_handle))
+
+    def sync(self):
+        self.check(lib().fh_sync(self.h))
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib().fh_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+
+class Q8_0Weight:
+    """A device-resident GGUF Q8_0 weight [n_rows x k] (fh_q8_0): the backing of
+    a Q8_0 Linear, uploaded straight from the GGUF bytes (no f32 expansion)."""
+
+    def __init__(self, ctx: Context, handle, n_rows: int, k: int):
+        self.ctx, self.h, self.n_rows, self.k = ctx, handle, n_rows, k
+
+    @classmethod
+    def upload(cls, ctx: Context, gguf_bytes, n_rows: int, k: int) -> "Q8_0Weight":
+        raw = np.ascontiguousarray(gguf_bytes, dtype=np.uint8)
+        if k % 32 == 0 and raw.size != n_rows * (k // 32) * 34:
+            raise FerrumHipError(FH_ERR_INVALID, f"expected {n_rows * (k // 32) * 34} bytes, got {raw.size}")
+        h = C.c_void_p()
+        ctx.check(lib().fh_q8_0_upload(ctx.h, raw.ctypes.data, n_rows, k, C.byref(h)))
+        return cls(ctx, h, n_rows, k)
+
+    @classmethod
+    def upload_device(cls, ctx: Context, d_bytes, n_rows: int, k: int) -> "Q8_0Weight":
+        h = C.c_void_p()
+        ctx.check(lib().fh_q8_0_upload_device(ctx.h, _ptr(d_bytes), n_rows, k, C.byref(h)))
+        return cls(ctx, h, n_rows, k)
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.n_rows * (self.k // 32) * 34, np.uint8)
+        self.ctx.check(lib().fh_q8_0_download(self.ctx.h, self.h, out.ctypes.data))
+        return out
+
+    def dims(self):
+        n, k = C.c_size_t(), C.c_size_t()
+        lib().fh_q8_0_dims(self.h, C.byref(n), C.byref(k))
+        return int(n.value), int(k.value)
+
+    def free(self):
+        if self.h:
+            lib().fh_q8_0_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def linear_forward(ctx: Context, x, weight: Q8_0Weight, bias=None, numerics: int = W8A32) -> np.ndarray:
+    """ops::linear_forward(input [m, k], weight, bias [n]) -> [m, n] on the GPU
+    (bias None = ops::matmul).  Host arrays in, host array out."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    if x.ndim != 2:
+        raise FerrumHipError(FH_ERR_INVALID, f"expected a matrix, got shape {x.shape}")
+    m, k = x.shape
+    b = None if bias is None else np.ascontiguousarray(bias, dtype=np.float32).ravel()
+    y = np.empty((m, weight.n_rows), np.float32)
+    ctx.check(lib().fh_q8_0_linear(ctx.h, weight.h, x.ctypes.data, m, k,
+                                   None if b is None else b.ctypes.data, 0 if b is None else b.size,
+                                   y.ctypes.data, numerics))
+    return y
+
+
+def matmul(ctx: Context, x, weight: Q8_0Weight, numerics: int = W8A32) -> np.ndarray:
+    return linear_forward(ctx, x, weight, None, numerics)
+
+
+def linear_forward_async(ctx: Context, weight: Q8_0Weight, x, m: int, k: int, bias, bias_len: int, y,
+                         numerics: int = W8A32):
+    """Device-pointer form (torch tensors or raw addresses), enqueued on the context stream."""
+    ctx.check(lib().fh_q8_0_linear_async(ctx.h, weight.h, _ptr(x), m, k, _ptr(bias), bias_len, _ptr(y),
+                                         numerics))
+
+
+def q8_0_encode(ctx: Context, x) -> np.ndarray:
+    """enc_q8_0 over q8_0_block: f32 -> GGUF Q8_0 bytes, on the GPU."""
+    x = np.ascontiguousarray(x, dtype=np.float32).ravel()
+    out = np.empty(max(x.size // 32 * 34, 1), np.uint8)
+    ctx.check(lib().fh_q8_0_encode(ctx.h, x.ctypes.data if x.size else None, x.size, out.ctypes.data))
+    return out[: x.size // 32 * 34]
+
+
+def q8_0_encode_async(ctx: Context, x, n: int, out):
+    ctx.check(lib().fh_q8_0_encode_async(ctx.h, _ptr(x), n, _ptr(out)))
+
+
+def q8_0_dequant_async(ctx: Context, raw, n: int, out):
+    ctx.check(lib().fh_q8_0_dequant_async(ctx.h, _ptr(raw), n, _ptr(out)))
+
+
+def q8_0_block_dots_async(ctx: Context, weight: Q8_0Weight, qx, m: int, dots):
+    ctx.check(lib().fh_q8_0_block_dots_async(ctx.h, weight.h, _ptr(qx), m, _ptr(dots)))
+
+
+def _recent_lists(recents, rows):
+    if recents is None:
+        return None, None
+    if len(recents) != rows:
+        raise FerrumHipError(FH_ERR_INVALID, f"{len(recents)} recent lists for {rows} rows")
+    lens = [len(r) for r in recents]
+    off = np.zeros(rows + 1, np.uint32)
+    off[1:] = np.cumsum(lens, dtype=np.uint64).astype(np.uint32)
+    flat = np.concatenate([np.asarray(r, dtype=np.uint64).ravel() for r in recents]) if sum(lens) else np.zeros(0)
+    # ids beyond u32 are out of any vocab; the reference skips them (sampling.rs:136)
+    flat = np.minimum(flat, 0xFFFFFFFF).astype(np.uint32)
+    return np.ascontiguousarray(flat), off
+
+
+def sample_rows(ctx: Context, logits, params: SamplingParams, recents=None, draws=None,
+                logits_kind: int = LOGITS_RAW) -> np.ndarray:
+    """sample_with_params for every row of logits [rows, vocab] (host arrays).
+    recents: one id list per row; draws: one u64 per row (Rng::next_u64)."""
+    lg = np.ascontiguousarray(logits, dtype=np.float32)
+    if lg.ndim == 1:
+        lg = lg[None, :]
+    rows, vocab = lg.shape
+    flat, off = _recent_lists(recents, rows)
+    dr = None if draws is None else np.ascontiguousarray(np.asarray(draws, dtype=np.uint64).ravel())
+    out = np.zeros(max(rows, 1), np.uint32)
+    ctx.check(lib().fh_sample_rows(ctx.h, lg.ctypes.data, rows, vocab, logits_kind, C.byref(params),
+                                   None if flat is None or flat.size == 0 else flat.ctypes.data,
+                                   None if off is None else off.ctypes.data,
+                                   None if dr is None else dr.ctypes.data, out.ctypes.data))
+    return out[:rows]
+
+
+def sample_rows_async(ctx: Context, d_logits, rows: int, vocab: int, params: SamplingParams, d_recent=None,
+                      d_offsets=None, d_draws=None, d_out=None, logits_kind: int = LOGITS_RAW):
+    ctx.check(lib().fh_sample_rows_async(ctx.h, _ptr(d_logits), rows, vocab, logits_kind, C.byref(params),
+                                         _ptr(d_recent), _ptr(d_offsets), _ptr(d_draws), _ptr(d_out)))
+
+
+def sample_with_params(ctx: Context, logits, params: SamplingParams, recent, rng: Rng,
+                       logits_kind: int = LOGITS_RAW) -> int:
+    """slm::sampling::sample_with_params (sampling.rs:124): one row, drawing from
+    rng exactly as the reference does (nothing when greedy, one next_u64 otherwise)."""
+    draw = None if params.temperature <= 0.0 else [rng.next_u64()]
+    return int(sample_rows(ctx, np.asarray(logits, np.float32)[None, :], params, [list(recent)], draw,
+                           logits_kind)[0])

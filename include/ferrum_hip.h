@@ -1,0 +1,182 @@
+/*
+ * ferrum_hip.h — C ABI of libferrum_hip, the MI355X (gfx950) implementation of
+ * ferrum_core's decode-step hot path: GGUF Q8_0 linear layers and the logit
+ * sampler.
+ *
+ * The reference (thomascherickal/ferrum-cpu, Rust, CPU-only) has no plugin
+ * registry: the path is reached through two Rust source APIs, which these
+ * entry points replace one for one:
+ *
+ *   ops::linear_forward(input, weight, bias)     ferrum_core/src/ops.rs:233-256
+ *   ops::matmul(a, b)  (the bias-free form)      ferrum_core/src/ops.rs:197-223
+ *     called only from Linear::forward           ferrum_core/src/layer/linear.rs:177-210
+ *   slm::sampling::sample_with_params(logits, params, recent, rng)
+ *                                                ferrum_core/src/slm/sampling.rs:124-210
+ *
+ * plus the Q8_0 block codec they are specified by:
+ *
+ *   quant::q8_0_block                            ferrum_core/src/quant.rs:271-280
+ *   gguf_write enc_q8_0                          ferrum_core/src/gguf_write/blocks.rs:132-140
+ *   gguf dequant_q8_0                            ferrum_core/src/gguf/dequant.rs:37-49
+ *
+ * Conventions.
+ *  - Every entry point returns an int status (FH_OK = 0); the message of the
+ *    last failure is fh_last_error(ctx).  Nothing aborts the process.
+ *  - A context owns one HIP stream on one device (or borrows a caller's stream,
+ *    fh_ctx_set_stream).  A context is not thread-safe; use one per thread.
+ *  - Entry points without the _async suffix take HOST pointers, copy in, run,
+ *    copy out and synchronise before returning (the reference's blocking call).
+ *    _async entry points take DEVICE pointers, enqueue on the context stream
+ *    and return at once; fh_sync waits.
+ *  - Shapes follow the reference: an input x is [m, k] row-major, a weight is
+ *    the GGUF Q8_0 tensor with ne0 = k (the reduction axis) and ne1 = n rows,
+ *    and y = x . W^T + b is [m, n] — the same product ferrum_core computes on
+ *    its transposed [k, n] f32 expansion (gguf/llama.rs:342-350).
+ *  - Results are deterministic run to run: no reduction depends on the order
+ *    in which atomics land.
+ */
+#ifndef FERRUM_HIP_H
+#define FERRUM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------- */
+enum {
+    FH_OK = 0,
+    FH_ERR_DIM = 1,     /* shape mismatch: ferrum_core's InferError::DimMismatch (ops.rs:236-246) */
+    FH_ERR_INVALID = 2, /* null pointer, unknown enum value, k % 32 != 0 */
+    FH_ERR_OOM = 3,     /* device or host allocation failed */
+    FH_ERR_HIP = 4,     /* a HIP runtime call failed (message carries hipGetErrorString) */
+    FH_ERR_LIMIT = 5    /* a size beyond a documented kernel limit */
+};
+
+/* Numerics of a Q8_0 linear.
+ *  FH_W8A32: ferrum_core's own semantics — weights dequantized exactly
+ *            (f16(d) * q is exact in f32), activations stay f32, products and
+ *            sums in f32 (loader/decode.rs:97-100; ops.rs:233-256).  Judged
+ *            against the reference at 1e-5 relative.
+ *  FH_W8A8:  llama.cpp's semantics, which the reference names as the
+ *            behaviour it does NOT follow (MANUAL.md:1609-1611): activations
+ *            Q8_0-encoded per 32 with q8_0_block, exact int32 block dots,
+ *            then y = sum_b f32(dot_b) * (d_w * d_x) + bias. */
+enum { FH_W8A32 = 0, FH_W8A8 = 1 };
+
+/* What fh_sample_* receives in `logits`.
+ *  FH_LOGITS_RAW:          the sampler input itself (the Llama/Qwen path,
+ *                          llm.rs:745).
+ *  FH_LOGITS_GPT2_SOFTMAX: the GPT-2 head's raw scores z; the sampler first
+ *                          forms p = softmax(z) (ops.rs:478-502) and the bridge
+ *                          l = ln(max(p, 1e-12)) (slm/token_stream.rs:134),
+ *                          fused into the same kernel. */
+enum { FH_LOGITS_RAW = 0, FH_LOGITS_GPT2_SOFTMAX = 1 };
+
+/* slm/sampling.rs:27-38 (SamplingParams without its cancel flag, which is a
+ * host-side control checked between tokens, slm/token_stream.rs:126-131). */
+typedef struct {
+    float temperature;        /* <= 0: greedy argmax_first, no draw consumed */
+    uint32_t top_k;           /* 0 or >= vocab: off */
+    float top_p;              /* >= 1: off */
+    float repetition_penalty; /* |pen - 1| <= f32::EPSILON or pen <= 0: off */
+} fh_sampling_params;
+
+typedef struct fh_ctx fh_ctx;
+typedef struct fh_q8_0 fh_q8_0; /* a device-resident Q8_0 weight [n rows x k] */
+
+/* ---- context ------------------------------------------------------------ */
+/* No reference counterpart (the reference has no device); creates a context on
+ * HIP device `device` with its own non-blocking stream. */
+int fh_ctx_create(int device, fh_ctx** out);
+void fh_ctx_destroy(fh_ctx* ctx);
+/* Enqueue on `hip_stream` (a hipStream_t of the same device) instead of the
+ * context's own stream; NULL restores the context's stream. */
+int fh_ctx_set_stream(fh_ctx* ctx, void* hip_stream);
+/* Wait for all work enqueued on the context stream. */
+int fh_sync(fh_ctx* ctx);
+/* Message of the last failed call on `ctx` ("" if none); valid until the next
+ * call on `ctx`.  fh_ctx_create failures are reported with ctx == NULL. */
+const char* fh_last_error(const fh_ctx* ctx);
+/* Number of HIP devices visible (0 when none), for hosts that probe first. */
+int fh_device_count(void);
+
+/* ---- Q8_0 weights ------------------------------------------------------- */
+/* Upload the raw bytes of a GGUF Q8_0 tensor (ne0 = k, ne1 = n_rows; n_rows
+ * rows of k/32 blocks, each block a little-endian f16 scale then 32 int8)
+ * and repack it on the device for the kernels.  Replaces the reference's
+ * load-time f32 expansion Gguf::dequantize -> dequant_q8_0 -> transpose_2d
+ * (gguf/tensors.rs:58-87, gguf/dequant.rs:37-49, gguf/llama.rs:342-350,
+ * loader/decode.rs:57-81) without expanding: the weight stays 34 B per 32
+ * values in HBM.  k % 32 != 0 -> FH_ERR_INVALID (the reference stores such a
+ * tensor as F32, loader/mod.rs:147-152). */
+int fh_q8_0_upload(fh_ctx* ctx, const uint8_t* gguf_bytes, size_t n_rows, size_t k, fh_q8_0** out);
+/* The same from a device buffer holding the GGUF bytes. */
+int fh_q8_0_upload_device(fh_ctx* ctx, const uint8_t* d_gguf_bytes, size_t n_rows, size_t k,
+                          fh_q8_0** out);
+/* Write the tensor back as GGUF bytes (host buffer of n_rows * k / 32 * 34). */
+int fh_q8_0_download(fh_ctx* ctx, const fh_q8_0* w, uint8_t* gguf_bytes);
+int fh_q8_0_dims(const fh_q8_0* w, size_t* n_rows, size_t* k);
+void fh_q8_0_free(fh_q8_0* w);
+
+/* ---- Q8_0 linear -------------------------------------------------------- */
+/* y[m, n] = x[m, k] . W^T (+ bias[n]).  Replaces ops::linear_forward
+ * (ops.rs:233-256; bias_len == n) and ops::matmul (ops.rs:197-223; bias NULL,
+ * bias_len 0) on a Q8_0-backed Linear (layer/linear.rs:191-194).
+ * k != W's k, or bias_len not in {0 (with bias NULL), n} -> FH_ERR_DIM, with the
+ * reference's message.  m == 0 is a valid empty call.  numerics: FH_W8A32 or
+ * FH_W8A8.  Host pointers; blocks until y is written. */
+int fh_q8_0_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, size_t k,
+                   const float* bias, size_t bias_len, float* y, int numerics);
+/* Device-pointer form of fh_q8_0_linear, enqueued on the context stream. */
+int fh_q8_0_linear_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                         const float* d_bias, size_t bias_len, float* d_y, int numerics);
+
+/* ---- Q8_0 encode -------------------------------------------------------- */
+/* n floats -> n/32 GGUF Q8_0 blocks of 34 bytes, bit-exact with enc_q8_0
+ * (gguf_write/blocks.rs:132-140) over q8_0_block (quant.rs:271-280) and
+ * f32_to_f16 (gguf_write/blocks.rs:12-61).  n % 32 != 0 -> FH_ERR_INVALID
+ * (encode_tensor's length check, gguf_write/blocks.rs:65-92). */
+int fh_q8_0_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out);
+int fh_q8_0_encode_async(fh_ctx* ctx, const float* d_x, size_t n, uint8_t* d_out);
+/* GGUF Q8_0 bytes -> f32, bit-exact with dequant_q8_0 (gguf/dequant.rs:37-49). */
+int fh_q8_0_dequant_async(fh_ctx* ctx, const uint8_t* d_gguf_bytes, size_t n, float* d_out);
+/* The exact int32 block dot products of the W8A8 path:
+ * dots[i, j, b] = sum_{t<32} qx[i, 32b+t] * q_w[j, 32b+t] for int8 activations
+ * qx [m, k] (as fh_q8_0_encode lays them out, scales stripped).  A checking
+ * hook for the integer core of FH_W8A8; no reference counterpart. */
+int fh_q8_0_block_dots_async(fh_ctx* ctx, const fh_q8_0* w, const int8_t* d_qx, size_t m,
+                             int32_t* d_dots);
+
+/* ---- sampler ------------------------------------------------------------ */
+/* One token id per row of `logits` [rows, vocab], each row sampled exactly as
+ * sample_with_params does (slm/sampling.rs:124-210): repetition penalty once
+ * per occurrence of an id in the row's `recent` list (ids >= vocab skipped),
+ * greedy argmax_first when temperature <= 0, else temperature softmax, top-k
+ * (ties at the k-th probability kept), top-p over the descending order,
+ * renormalise and the inverse-CDF draw pick_by_mass (sampling.rs:109-122).
+ *
+ * Row r's recent ids are recent[recent_offsets[r] .. recent_offsets[r+1]]
+ * (recent_offsets has rows + 1 entries; recent may be NULL when all are empty).
+ * draws[r] is the one u64 the reference's Rng::next_u64 yields for the row
+ * (rng.rs:29-36): the draw is r = (draws[r] >> 40) / 2^24 (Rng::next_f32,
+ * rng.rs:39-41), or draws[r] % vocab on the degenerate-softmax fallback
+ * (sampling.rs:156-168).  The RNG stays on the host so the sequence is exactly
+ * the reference's; draws may be NULL for greedy.  logits_kind: FH_LOGITS_*.
+ * vocab == 0 -> FH_ERR_INVALID; a row with more than 16384 recent ids ->
+ * FH_ERR_LIMIT.  Host pointers; blocks until out_ids is written. */
+int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, int logits_kind,
+                   const fh_sampling_params* params, const uint32_t* recent,
+                   const uint32_t* recent_offsets, const uint64_t* draws, uint32_t* out_ids);
+/* Device-pointer form of fh_sample_rows (params by value, on the host). */
+int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t vocab,
+                         int logits_kind, const fh_sampling_params* params,
+                         const uint32_t* d_recent, const uint32_t* d_recent_offsets,
+                         const uint64_t* d_draws, uint32_t* d_out_ids);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* FERRUM_HIP_H */

@@ -1,0 +1,242 @@
+"""Q8_0 linear, codec and weight upload on the GPU, checked against the CPU
+oracle (oracle/ferrum_oracle.c, a restatement of ferrum_core's arithmetic).
+
+Tolerances:
+  * Q8_0 block encode, dequant, weight round trip, int32 block dots: bit-exact.
+  * f32 outputs: |gpu - ref| <= 1e-5 * max(|ref|, 1e-2 * max|ref of the row|)
+    — relative 1e-5 with a floor at 1% of the row's largest output, so that
+    outputs that cancel to near zero are judged against the row's scale.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+RTOL = 1e-5
+
+
+def assert_close(got, want, rtol=RTOL):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = np.maximum(np.abs(want), 1e-2 * np.abs(want).max(axis=-1, keepdims=True))
+    err = np.abs(got - want)
+    bad = err > rtol * scale
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} outside tolerance; worst rel "
+                           f"{(err / np.maximum(scale, 1e-30)).max():.3e}")
+
+
+def weight(orc, n, k, seed, std=0.02):
+    return orc.quantize_weight(n, k, seed, std)
+
+
+def acts(m, k, seed):
+    return np.random.default_rng(seed + 7).standard_normal((m, k), dtype=np.float32)
+
+
+def bias_for(n, seed):
+    return (np.random.default_rng(seed + 11).standard_normal(n, dtype=np.float32) * np.float32(0.1))
+
+
+# ---- upload / download --------------------------------------------------------
+
+@pytest.mark.parametrize("n,k", [(1, 32), (3, 64), (768, 768), (50257, 768)])
+def test_weight_round_trip_is_bit_exact(fh, n, k):
+    import ferrum_hip
+
+    raw = np.random.default_rng(n + k).integers(0, 256, size=n * (k // 32) * 34, dtype=np.uint8)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    assert w.dims() == (n, k)
+    assert np.array_equal(w.download(), raw)
+    w.free()
+
+
+def test_upload_rejects_a_row_length_off_the_block_grid(fh):
+    import ferrum_hip
+
+    with pytest.raises(ferrum_hip.FerrumHipError, match="multiple of the Q8_0 block size"):
+        ferrum_hip.Q8_0Weight.upload(fh, np.zeros(34, np.uint8), 1, 48)
+
+
+# ---- W8A32 (ferrum_core semantics) ------------------------------------------------
+
+CONFIG2 = [(n, k) for n in (768, 2304, 3072, 50257) for k in (768, 3072)]
+
+
+@pytest.mark.parametrize("n,k", CONFIG2)
+def test_gemv_m1_config2_matches_oracle(fh, orc, n, k):
+    import ferrum_hip
+
+    seed = n * 31 + k
+    raw = weight(orc, n, k, seed)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x, b = acts(1, k, seed), bias_for(n, seed)
+    assert_close(ferrum_hip.linear_forward(fh, x, w, b), orc.q8_0_linear(x, raw, n, b))
+    assert_close(ferrum_hip.matmul(fh, x, w), orc.q8_0_linear(x, raw, n, None))
+    w.free()
+
+
+@pytest.mark.parametrize("m,n,k", [(2, 768, 768), (2, 3072, 3072), (3, 2304, 768), (8, 3072, 768),
+                                   (8, 768, 3072), (32, 2304, 768), (32, 768, 3072), (32, 50257, 768),
+                                   (64, 896, 896), (65, 130, 4864)])
+def test_batched_linear_matches_oracle(fh, orc, m, n, k):
+    import ferrum_hip
+
+    seed = m * 7 + n * 3 + k
+    raw = weight(orc, n, k, seed)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x, b = acts(m, k, seed), bias_for(n, seed)
+    assert_close(ferrum_hip.linear_forward(fh, x, w, b), orc.q8_0_linear(x, raw, n, b))
+    w.free()
+
+
+@pytest.mark.parametrize("m", [1, 2, 5])
+@pytest.mark.parametrize("n,k", [(1, 32), (3, 64), (67, 96), (5, 128), (33, 256), (17, 512), (9, 896),
+                                 (11, 1024), (7, 4096), (5, 4864), (3, 8192), (2, 9216)])
+def test_ragged_shapes_match_oracle(fh, orc, m, n, k):
+    import ferrum_hip
+
+    seed = m + n * 13 + k
+    raw = weight(orc, n, k, seed, std=0.5)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x, b = acts(m, k, seed), bias_for(n, seed)
+    assert_close(ferrum_hip.linear_forward(fh, x, w, b), orc.q8_0_linear(x, raw, n, b))
+    w.free()
+
+
+def test_expanded_weight_path_agrees(fh, orc):
+    """The GPU result against ops::linear_forward on the f32 expansion the
+    reference's loader builds (dequant + transpose), not only the row form."""
+    import ferrum_hip
+
+    n, k = 2304, 768
+    raw = weight(orc, n, k, 5)
+    w_kn = orc.q8_0_to_ferrum_weight(raw, n, k)
+    x, b = acts(3, k, 5), bias_for(n, 5)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    assert_close(ferrum_hip.linear_forward(fh, x, w, b), orc.linear_forward(x, w_kn, b, threads=4))
+    w.free()
+
+
+def test_empty_batch_and_dim_errors(fh, orc):
+    import ferrum_hip
+
+    raw = weight(orc, 8, 64, 1)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, 8, 64)
+    assert ferrum_hip.linear_forward(fh, np.zeros((0, 64), np.float32), w).shape == (0, 8)
+    with pytest.raises(ferrum_hip.DimMismatch, match="input width 32"):
+        ferrum_hip.linear_forward(fh, np.zeros((1, 32), np.float32), w)
+    with pytest.raises(ferrum_hip.DimMismatch, match="bias length 7"):
+        ferrum_hip.linear_forward(fh, np.zeros((1, 64), np.float32), w, np.zeros(7, np.float32))
+    with pytest.raises(ferrum_hip.FerrumHipError, match="unknown numerics"):
+        ferrum_hip.linear_forward(fh, np.zeros((1, 64), np.float32), w, None, numerics=9)
+    w.free()
+
+
+def test_async_path_on_torch_buffers(fh, orc):
+    import torch
+
+    import ferrum_hip
+
+    n, k, m = 3072, 768, 1
+    raw = weight(orc, n, k, 9)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x, b = acts(m, k, 9), bias_for(n, 9)
+    dx, db = torch.from_numpy(x).cuda(), torch.from_numpy(b).cuda()
+    dy = torch.empty((m, n), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    fh.set_stream(torch.cuda.current_stream().cuda_stream)
+    try:
+        ferrum_hip.linear_forward_async(fh, w, dx, m, k, db, n, dy)
+        torch.cuda.synchronize()
+    finally:
+        fh.set_stream(None)
+    assert_close(dy.cpu().numpy(), orc.q8_0_linear(x, raw, n, b))
+    w.free()
+
+
+# ---- W8A8 (llama.cpp semantics) and the codec -------------------------------------
+
+@pytest.mark.parametrize("m,n,k", [(1, 768, 768), (1, 3072, 3072), (4, 2304, 768), (32, 768, 3072),
+                                   (3, 7, 32), (2, 5, 4864)])
+def test_w8a8_matches_oracle(fh, orc, m, n, k):
+    import ferrum_hip
+
+    raw = weight(orc, n, k, m + n + k)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x, b = acts(m, k, n), bias_for(n, k)
+    got = ferrum_hip.linear_forward(fh, x, w, b, numerics=ferrum_hip.W8A8)
+    assert_close(got, orc.q8_0_linear_w8a8(x, raw, n, b))
+    w.free()
+
+
+def test_int32_block_dots_are_bit_exact(fh, orc):
+    import torch
+
+    import ferrum_hip
+
+    m, n, k = 3, 257, 768
+    raw = weight(orc, n, k, 3)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x = acts(m, k, 3) * np.float32(5.0)
+    _, qx = orc.q8_0_quantize_rows(x)
+    dq = torch.from_numpy(qx).cuda()
+    dots = torch.empty((m, n, k // 32), dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ferrum_hip.q8_0_block_dots_async(fh, w, dq, m, dots)
+    fh.sync()
+    assert np.array_equal(dots.cpu().numpy(), orc.q8_0_block_dots(qx, raw, n))
+    w.free()
+
+
+def encode_cases():
+    rng = np.random.default_rng(77)
+    blocks = [
+        np.array([127, 0.5, 1.5, -0.5, -2.5, 2.4999, -126.5, 0.49] + [0] * 24, np.float32),  # quant.rs:357-365
+        np.zeros(32, np.float32),
+        np.full(32, 1e-30, np.float32),
+        np.full(32, -1e-38, np.float32),
+        np.full(32, 1e-41, np.float32),
+        (rng.standard_normal(32) * 1e-37).astype(np.float32),
+        np.full(32, 8.3e6, np.float32),
+        np.array([65504.0 * 127] + [1.0] * 31, np.float32),
+        np.array([np.nan] + [1.0] * 31, np.float32),
+        np.array([np.inf] + [1.0] * 31, np.float32),
+        np.array([-np.inf, np.nan] + [0.25] * 30, np.float32),
+        np.arange(32, dtype=np.float32) - 16,
+    ]
+    blocks.append((rng.standard_normal(32 * 4096) * rng.choice([1e-3, 1, 1e3], 32 * 4096)).astype(np.float32))
+    # ties of x * (1/d) at .5 for many scales
+    ties = (np.arange(-63, 64, dtype=np.float32)[:, None] + 0.5) * np.float32(1 / 127)
+    blocks.append(np.concatenate([np.concatenate([[1.0], t.repeat(31)]) for t in ties.ravel()]).astype(np.float32))
+    return np.concatenate(blocks).astype(np.float32)
+
+
+def test_q8_0_encode_is_bit_exact(fh, orc):
+    import ferrum_hip
+
+    x = encode_cases()
+    assert np.array_equal(ferrum_hip.q8_0_encode(fh, x), orc.q8_0_encode(x))
+
+
+def test_q8_0_encode_length_error(fh):
+    import ferrum_hip
+
+    with pytest.raises(ferrum_hip.FerrumHipError, match="not a multiple of block size 32"):
+        ferrum_hip.q8_0_encode(fh, np.zeros(33, np.float32))
+
+
+def test_q8_0_dequant_is_bit_exact(fh, orc):
+    import torch
+
+    import ferrum_hip
+
+    raw = np.random.default_rng(4).integers(0, 256, size=34 * 5000, dtype=np.uint8)
+    # finite scales only: NaN payloads are compared separately
+    raw16 = raw.view(np.uint16).reshape(-1, 17)
+    raw16[:, 0] &= 0x7BFF
+    dr = torch.from_numpy(raw).cuda()
+    out = torch.empty(32 * 5000, dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    ferrum_hip.q8_0_dequant_async(fh, dr, 32 * 5000, out)
+    fh.sync()
+    assert np.array_equal(out.cpu().numpy().view(np.uint32), orc.q8_0_dequant(raw, 32 * 5000).view(np.uint32))

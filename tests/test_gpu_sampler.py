@@ -1,0 +1,184 @@
+"""The fused sampler on the GPU against the oracle's sample_with_params
+(slm/sampling.rs:124-210).
+
+Parity rule: token ids identical given the same
+uniform draws, except where the oracle reports a decision margin below 1e-5 —
+a top-2 gap for greedy, or for sampling the smallest of |r - cumsum boundary|,
+|cum - top_p| at the cut and the p gap at the k-th place — because the GPU's
+exp/log and its parallel softmax sum may move a probability by about 1e-7
+relative.  Such exempt rows must stay rare (counted and bounded per test).
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+MARGIN = 1e-5
+
+
+def run_and_compare(fh, orc, logits, params_kw, recents=None, draws=None, kind=0, max_exempt=0.01):
+    import ferrum_hip
+
+    logits = np.ascontiguousarray(logits, np.float32)
+    rows, vocab = logits.shape
+    if recents is None:
+        recents = [[] for _ in range(rows)]
+    if draws is None:
+        rng = np.random.default_rng(rows * 977 + vocab)
+        draws = rng.integers(0, 2**64, size=rows, dtype=np.uint64)
+    gp = ferrum_hip.SamplingParams(**params_kw)
+    got = ferrum_hip.sample_rows(fh, logits, gp, recents, draws, kind)
+    op = orc.SamplingParams(**params_kw)
+    exempt = 0
+    for r in range(rows):
+        row = logits[r]
+        if kind == ferrum_hip.LOGITS_GPT2_SOFTMAX:
+            row = orc.ln_bridge(orc.softmax_rows(row)[0])
+        want, info = orc.sample(row, op, recents[r], int(draws[r]))
+        if got[r] != want:
+            assert info.margin < MARGIN, (f"row {r}: gpu {got[r]} vs oracle {want}, margin {info.margin:.3e}, "
+                                          f"path {info.path}, kept {info.n_kept}")
+            exempt += 1
+    assert exempt <= max(1, int(max_exempt * rows)), f"{exempt} exempt rows of {rows}"
+    return got
+
+
+def normal_logits(rows, vocab, seed, scale=3.0):
+    return (np.random.default_rng(seed).standard_normal((rows, vocab)) * scale).astype(np.float32)
+
+
+# ---- the reference's own known answers (sampling.rs:219-422) --------------------------
+
+def test_greedy_known_answers(fh):
+    import ferrum_hip
+
+    g = ferrum_hip.SamplingParams(temperature=0.0)
+    s = lambda lg, rec=(): ferrum_hip.sample_with_params(fh, np.array(lg, np.float32), g, list(rec), ferrum_hip.Rng(1))
+    assert s([0.1, 2.0, 2.0, 1.0]) == 1 and s([3.0, 3.0, 3.0]) == 0 and s([-1.0, -0.5, -0.5]) == 1
+    assert s([float("-inf"), float("-inf")]) == 0 and s([1.0, 5.0, 5.0]) == 1 and s([1.0]) == 0
+    # repetition penalty flips the argmax (sampling.rs:235-262); out-of-vocab ids ignored (219-232)
+    pen = ferrum_hip.SamplingParams(temperature=0.0, repetition_penalty=2.0)
+    t = lambda lg, rec: ferrum_hip.sample_with_params(fh, np.array(lg, np.float32), pen, rec, ferrum_hip.Rng(1))
+    assert t([2.0, 1.5], [0]) == 1 and t([2.0, 1.5], [99]) == 0 and t([-1.0, -1.5], [0, 0]) == 1
+
+
+def test_greedy_draws_no_rng(fh):
+    # sampling.rs:365-389: greedy consumes nothing from the generator
+    import ferrum_hip
+
+    rng = ferrum_hip.Rng(7)
+    before = rng.state
+    ferrum_hip.sample_with_params(fh, np.arange(10, dtype=np.float32), ferrum_hip.SamplingParams(0.0), [], rng)
+    assert rng.state == before
+
+
+def test_top_k_one_is_argmax_and_nan_fallback(fh, orc):
+    import ferrum_hip
+
+    lg = normal_logits(16, 1000, 3)
+    got = ferrum_hip.sample_rows(fh, lg, ferrum_hip.SamplingParams(0.9, 1), None, np.arange(16, dtype=np.uint64) << 40)
+    assert np.array_equal(got, lg.argmax(axis=1))
+    # a NaN or +inf logit makes the softmax sum NaN: the reference draws next_u64 % n (sampling.rs:156-168)
+    bad = lg.copy()
+    bad[0, 5] = np.nan
+    bad[1, 9] = np.inf
+    draws = np.array([123456789, 987654321] + [0] * 14, np.uint64)
+    got = ferrum_hip.sample_rows(fh, bad, ferrum_hip.SamplingParams(1.0), None, draws)
+    assert got[0] == 123456789 % 1000 and got[1] == 987654321 % 1000
+
+
+def test_pick_by_mass_boundaries(fh, orc):
+    """Draws on both sides of every cumulative boundary of a small distribution
+    (sampling.rs:408-422 behaviour through the whole sampler)."""
+    lg = np.log(np.array([[0.1, 0.2, 0.3, 0.4]], np.float32))
+    rs = np.arange(0, 1 << 24, 1 << 14, dtype=np.uint64) << 40
+    for d in rs[:256]:
+        run_and_compare(fh, orc, lg, dict(temperature=1.0), draws=np.array([d], np.uint64))
+
+
+# ---- seeded parity sweeps -------------------------------------------------------------
+
+PARAMS = {
+    "greedy": dict(temperature=0.0),
+    "greedy_pen": dict(temperature=0.0, repetition_penalty=1.3),
+    "temp": dict(temperature=0.8),
+    "topk": dict(temperature=0.8, top_k=40),
+    "topp": dict(temperature=0.8, top_p=0.95),
+    "topk_topp_pen": dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1),
+    "hot_topp": dict(temperature=2.5, top_p=0.6),
+    "bigk": dict(temperature=1.0, top_k=6000),
+    "tiny_t": dict(temperature=0.001, top_k=5),
+}
+
+
+@pytest.mark.parametrize("name", sorted(PARAMS))
+@pytest.mark.parametrize("vocab", [2, 7, 4096, 50257])
+def test_raw_logits_parity(fh, orc, name, vocab):
+    rows = 24 if vocab > 1000 else 64
+    lg = normal_logits(rows, vocab, vocab + len(name))
+    rng = np.random.default_rng(vocab)
+    recents = [list(rng.integers(0, vocab + 3, size=rng.integers(0, 300))) for _ in range(rows)]
+    run_and_compare(fh, orc, lg, PARAMS[name], recents)
+
+
+@pytest.mark.parametrize("name", ["greedy", "topk_topp_pen", "topp", "temp"])
+def test_gpt2_softmax_bridge_parity(fh, orc, name):
+    import ferrum_hip
+
+    rows, vocab = 16, 50257
+    lg = normal_logits(rows, vocab, 99, scale=2.0)
+    rng = np.random.default_rng(5)
+    recents = [list(rng.integers(0, vocab, size=256)) for _ in range(rows)]
+    run_and_compare(fh, orc, lg, PARAMS[name], recents, kind=ferrum_hip.LOGITS_GPT2_SOFTMAX)
+
+
+def test_repeated_ids_penalised_once_per_occurrence(fh, orc):
+    rows, vocab = 8, 4096
+    lg = normal_logits(rows, vocab, 12)
+    rec = [[7] * 50 + [9] * 3 + list(range(100, 140)) * 4 for _ in range(rows)]
+    lg[:, 7] = 9.0
+    run_and_compare(fh, orc, lg, dict(temperature=0.0, repetition_penalty=1.05), rec)
+    run_and_compare(fh, orc, lg, dict(temperature=0.7, top_k=20, repetition_penalty=1.05), rec)
+
+
+def test_long_history_chunks(fh, orc):
+    """More recent ids than one LDS table fill (4096), with heavy repetition."""
+    rows, vocab = 4, 50257
+    lg = normal_logits(rows, vocab, 21)
+    rng = np.random.default_rng(3)
+    rec = [list(rng.integers(0, 64, size=9000)) + list(rng.integers(0, vocab, size=3000)) for _ in range(rows)]
+    run_and_compare(fh, orc, lg, dict(temperature=0.0, repetition_penalty=1.01), rec)
+    run_and_compare(fh, orc, lg, dict(temperature=0.9, top_k=50, repetition_penalty=1.01), rec)
+
+
+def test_flat_top_p_takes_the_general_path(fh, orc):
+    """Nearly flat logits: the top-p set is thousands of ids (beyond the LDS
+    list), so the cut is found by the mass radix select."""
+    rows, vocab = 12, 50257
+    lg = (np.random.default_rng(8).standard_normal((rows, vocab)) * 0.05).astype(np.float32)
+    run_and_compare(fh, orc, lg, dict(temperature=1.0, top_p=0.5), max_exempt=0.1)
+    run_and_compare(fh, orc, lg, dict(temperature=1.0, top_k=10000, top_p=0.9), max_exempt=0.1)
+
+
+def test_qwen_config5_rows(fh, orc):
+    """Config 5: 151936-wide logits ~N(0,3) plus 5 planted peaks (+12), top-k 50,
+    top-p 0.9, repetition penalty 1.05 over a 1024-token random history."""
+    rows, vocab = 16, 151936
+    rng = np.random.default_rng(55)
+    lg = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    peaks = rng.integers(0, vocab, size=5)
+    lg[:, peaks] += 12.0
+    rec = [list(rng.integers(0, vocab, size=1024)) + list(peaks[:2]) for _ in range(rows)]
+    run_and_compare(fh, orc, lg, dict(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.05), rec)
+
+
+def test_sampler_errors(fh):
+    import ferrum_hip
+
+    with pytest.raises(ferrum_hip.FerrumHipError, match="vocab is 0"):
+        ferrum_hip.sample_rows(fh, np.zeros((1, 0), np.float32), ferrum_hip.SamplingParams(0.0))
+    with pytest.raises(ferrum_hip.FerrumHipError, match="above the limit"):
+        ferrum_hip.sample_rows(fh, np.zeros((1, 10), np.float32), ferrum_hip.SamplingParams(0.0, repetition_penalty=1.1),
+                               [[1] * 16385])
+    with pytest.raises(ferrum_hip.FerrumHipError, match="draws is NULL"):
+        ferrum_hip.sample_rows(fh, np.zeros((1, 10), np.float32), ferrum_hip.SamplingParams(0.5))
