@@ -18,8 +18,8 @@ The step is captured once per replica into a HIP graph (torch.cuda.CUDAGraph)
 and replayed; K timed steps are bracketed by synchronisations and HIP events.
 
 roofline: the dominant kernel is the Q8_0 GEMV; it is measured on the lm_head
-shape (50257 x 768, the largest launch) in back-to-back launches over 8 head
-replicas (328 MB, HBM-forced), timed with HIP events on the launch stream.
+shape (50257 x 768, the largest launch) in back-to-back launches over 32 head
+replicas (1.3 GB, HBM-forced), timed with HIP events on the launch stream.
 Algorithmic bytes per launch = 50257*768*34/32 (Q8_0 weight) + 768*4 (x)
 + 50257*4 (y).
 
@@ -90,7 +90,8 @@ def main():
     torch.cuda.init()
     dev = torch.device("cuda:0")
     ctx = fh.Context(0)
-    stream = torch.cuda.current_stream()
+    stream = torch.cuda.Stream()  # every launch and event of the run goes on this stream
+    torch.cuda.set_stream(stream)
     ctx.set_stream(stream.cuda_stream)
     gen = torch.Generator(device=dev)
     gen.manual_seed(1234)
@@ -167,7 +168,7 @@ def main():
         torch.cuda.synchronize()
 
     # ---- roofline leg: lm_head GEMV, back-to-back, HBM-forced ----------------------
-    n_head_rep = 8
+    n_head_rep = 32  # 32 x 41 MB = 1.3 GB, five times the MALL
     heads = [make_weight(ctx, fh, torch, V, D, gen) for _ in range(n_head_rep)]
     hr = [type("H", (), {"head": h})() for h in heads]
     for i in range(3 * n_head_rep):

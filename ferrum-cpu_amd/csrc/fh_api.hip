@@ -42,22 +42,6 @@ int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) {
     return FH_OK;
 }
 
-int fh_staging(fh_ctx* ctx, size_t bytes, void** out) {
-    bytes = fh_align256(bytes ? bytes : 256);
-    if (ctx->io_bytes < bytes) {
-        if (ctx->io) {
-            FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
-            FH_HIP(ctx, hipHostFree(ctx->io));
-            ctx->io = nullptr;
-            ctx->io_bytes = 0;
-        }
-        FH_HIP(ctx, hipHostMalloc(&ctx->io, bytes, hipHostMallocDefault));
-        ctx->io_bytes = bytes;
-    }
-    *out = ctx->io;
-    return FH_OK;
-}
-
 // Every entry point works on the context's device.
 // (hipSetDevice only when needed, so calls stay legal under stream capture.)
 static hipError_t on_device(int device) {
@@ -106,7 +90,6 @@ void fh_ctx_destroy(fh_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
-    if (ctx->io) (void)hipHostFree(ctx->io);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
 }
@@ -114,7 +97,14 @@ void fh_ctx_destroy(fh_ctx* ctx) {
 int fh_ctx_set_stream(fh_ctx* ctx, void* hip_stream) {
     if (!ctx) return FH_ERR_INVALID;
     ctx->err.clear();
-    ctx->stream = hip_stream ? static_cast<hipStream_t>(hip_stream) : ctx->own;
+    ctx->stream = static_cast<hipStream_t>(hip_stream);
+    return FH_OK;
+}
+
+int fh_ctx_reset_stream(fh_ctx* ctx) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    ctx->stream = ctx->own;
     return FH_OK;
 }
 
@@ -140,7 +130,6 @@ static int alloc_weight(fh_ctx* ctx, size_t n_rows, size_t k, fh_q8_0** out) {
     if (n_rows == 0) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_upload: n_rows is 0");
     fh_q8_0* w = new (std::nothrow) fh_q8_0();
     if (!w) return fh_fail(ctx, FH_ERR_OOM, "fh_q8_0_upload: out of host memory");
-    w->ctx = ctx;
     w->device = ctx->device;
     w->n = n_rows;
     w->k = k;
@@ -223,8 +212,9 @@ int fh_q8_0_dims(const fh_q8_0* w, size_t* n_rows, size_t* k) {
 
 void fh_q8_0_free(fh_q8_0* w) {
     if (!w) return;
-    (void)hipSetDevice(w->device);
-    if (w->ctx && w->ctx->stream) (void)hipStreamSynchronize(w->ctx->stream);
+    // The weight does not hold its context (which may be gone by now); hipFree
+    // itself waits for the device's outstanding work before releasing memory.
+    (void)on_device(w->device);
     if (w->base) (void)hipFree(w->base);
     delete w;
 }

@@ -21,19 +21,15 @@
 struct fh_ctx {
     int device = 0;
     hipStream_t own = nullptr;   // created by fh_ctx_create
-    hipStream_t stream = nullptr;  // where work is enqueued (own or borrowed)
+    hipStream_t stream = nullptr;  // where work is enqueued (own, borrowed, or NULL = legacy default)
     std::string err;
     // Grow-on-demand device workspace for intermediate buffers (activation
     // quants, sampler rows).  Reused across calls on this context.
     void* ws = nullptr;
     size_t ws_bytes = 0;
-    // Host-side staging for the synchronous (host pointer) entry points.
-    void* io = nullptr;
-    size_t io_bytes = 0;
 };
 
 struct fh_q8_0 {
-    fh_ctx* ctx = nullptr;
     int device = 0;
     size_t n = 0, k = 0, kb = 0;
     int8_t* qs = nullptr;
@@ -52,8 +48,6 @@ int fh_hip_fail(fh_ctx* ctx, hipError_t e, const char* what);
 
 // Make sure ctx->ws holds at least `bytes` (device, 256-B aligned).
 int fh_workspace(fh_ctx* ctx, size_t bytes, void** out);
-// Make sure ctx->io holds at least `bytes` (pinned host).
-int fh_staging(fh_ctx* ctx, size_t bytes, void** out);
 // Round up to a multiple of 256 bytes.
 static inline size_t fh_align256(size_t b) { return (b + 255) & ~(size_t)255; }
 

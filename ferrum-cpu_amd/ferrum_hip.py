@@ -38,7 +38,7 @@ W8A32, W8A8 = 0, 1
 LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
 
 EXPORTS = (
-    "fh_ctx_create", "fh_ctx_destroy", "fh_ctx_set_stream", "fh_sync", "fh_last_error",
+    "fh_ctx_create", "fh_ctx_destroy", "fh_ctx_set_stream", "fh_ctx_reset_stream", "fh_sync", "fh_last_error",
     "fh_device_count", "fh_q8_0_upload", "fh_q8_0_upload_device", "fh_q8_0_download",
     "fh_q8_0_dims", "fh_q8_0_free", "fh_q8_0_linear", "fh_q8_0_linear_async",
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
@@ -111,18 +111,33 @@ class Rng:
 _lib = None
 
 
+def _share_torch_hip_runtime():
+    """PyTorch wheels ship their own libamdhip64.so and load it by that file
+    name, so a process that loads this library (which needs the soname
+    libamdhip64.so.7) before torch ends up with two HIP runtimes, and torch then
+    sees no GPU.  Importing torch first makes both share torch's runtime, and
+    torch streams and device pointers stay valid here.  Without torch, the
+    system ROCm runtime is used."""
+    try:
+        import torch  # noqa: F401
+    except ImportError:
+        pass
+
+
 def lib():
     """The loaded libferrum_hip (raises if it has not been built)."""
     global _lib
     if _lib is None:
         if not os.path.exists(LIB_PATH):
             raise FerrumHipError(FH_ERR_INVALID, f"{LIB_PATH} is not built (run make -C {HERE})")
+        _share_torch_hip_runtime()
         L = C.CDLL(LIB_PATH)
         vp, sz, i32 = C.c_void_p, C.c_size_t, C.c_int
         L.fh_ctx_create.argtypes = [i32, C.POINTER(vp)]
         L.fh_ctx_destroy.argtypes = [vp]
         L.fh_ctx_destroy.restype = None
         L.fh_ctx_set_stream.argtypes = [vp, vp]
+        L.fh_ctx_reset_stream.argtypes = [vp]
         L.fh_sync.argtypes = [vp]
         L.fh_last_error.argtypes = [vp]
         L.fh_last_error.restype = C.c_char_p
@@ -177,8 +192,12 @@ class Context:
         raise (DimMismatch if rc == FH_ERR_DIM else FerrumHipError)(rc, msg)
 
     def set_stream(self, stream_handle: int | None):
-        """Enqueue on a caller's hipStream_t (e.g. torch.cuda.current_stream().cuda_stream)."""
-        self.check(lib().fh_ctx_set_stream(self.h, stream_handle))
+        """Enqueue on a caller's hipStream_t, e.g. torch.cuda.current_stream().cuda_stream
+        (0 is the legacy default stream); None goes back to the context's own stream."""
+        if stream_handle is None:
+            self.check(lib().fh_ctx_reset_stream(self.h))
+        else:
+            self.check(lib().fh_ctx_set_stream(self.h, stream_handle))
 
     def sync(self):
         self.check(lib().fh_sync(self.h))

@@ -92,9 +92,12 @@ typedef struct fh_q8_0 fh_q8_0; /* a device-resident Q8_0 weight [n rows x k] */
  * HIP device `device` with its own non-blocking stream. */
 int fh_ctx_create(int device, fh_ctx** out);
 void fh_ctx_destroy(fh_ctx* ctx);
-/* Enqueue on `hip_stream` (a hipStream_t of the same device) instead of the
- * context's own stream; NULL restores the context's stream. */
+/* Enqueue on `hip_stream`, a hipStream_t of the same device, instead of the
+ * context's own stream.  NULL is HIP's legacy default stream (it is what
+ * PyTorch's default stream handle is).  fh_ctx_reset_stream goes back to the
+ * context's own stream. */
 int fh_ctx_set_stream(fh_ctx* ctx, void* hip_stream);
+int fh_ctx_reset_stream(fh_ctx* ctx);
 /* Wait for all work enqueued on the context stream. */
 int fh_sync(fh_ctx* ctx);
 /* Message of the last failed call on `ctx` ("" if none); valid until the next

@@ -129,7 +129,10 @@ def test_gpt2_softmax_bridge_parity(fh, orc, name):
     lg = normal_logits(rows, vocab, 99, scale=2.0)
     rng = np.random.default_rng(5)
     recents = [list(rng.integers(0, vocab, size=256)) for _ in range(rows)]
-    run_and_compare(fh, orc, lg, PARAMS[name], recents, kind=ferrum_hip.LOGITS_GPT2_SOFTMAX)
+    # GPT-2-bridged rows are flat (|z| ~ 2): the kept set runs to thousands of
+    # ids spaced ~1e-4 apart in cumulative mass, so a draw lands within 1e-5 of
+    # a boundary in a sizeable share of rows; each mismatch must still be one.
+    run_and_compare(fh, orc, lg, PARAMS[name], recents, kind=ferrum_hip.LOGITS_GPT2_SOFTMAX, max_exempt=0.25)
 
 
 def test_repeated_ids_penalised_once_per_occurrence(fh, orc):
