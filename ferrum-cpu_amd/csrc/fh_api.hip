@@ -42,6 +42,29 @@ int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) {
     return FH_OK;
 }
 
+int fh_sync_area(fh_ctx* ctx, size_t bytes, void** out) {
+    bytes = fh_align256(bytes ? bytes : 256);
+    if (ctx->sync_bytes < bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        FH_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fh_fail(ctx, FH_ERR_INVALID,
+                           "the sampler's per-row state must grow, which cannot happen during graph capture: "
+                           "run the same call once outside capture first");
+        FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        if (ctx->sync) {
+            FH_HIP(ctx, hipFree(ctx->sync));
+            ctx->sync = nullptr;
+            ctx->sync_bytes = 0;
+        }
+        FH_HIP(ctx, hipMalloc(&ctx->sync, bytes));
+        FH_HIP(ctx, hipMemset(ctx->sync, 0, bytes));
+        ctx->sync_bytes = bytes;
+    }
+    *out = ctx->sync;
+    return FH_OK;
+}
+
 // Every entry point works on the context's device.
 // (hipSetDevice only when needed, so calls stay legal under stream capture.)
 static hipError_t on_device(int device) {
@@ -81,6 +104,9 @@ int fh_ctx_create(int device, fh_ctx** out) {
         return code;
     }
     c->stream = c->own;
+    if (hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
+        c->num_cus < 1)
+        c->num_cus = 1;
     *out = c;
     return FH_OK;
 }
@@ -90,6 +116,7 @@ void fh_ctx_destroy(fh_ctx* ctx) {
     (void)hipSetDevice(ctx->device);
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
+    if (ctx->sync) (void)hipFree(ctx->sync);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
 }

@@ -20,6 +20,7 @@
 
 struct fh_ctx {
     int device = 0;
+    int num_cus = 1;             // compute units of the device
     hipStream_t own = nullptr;   // created by fh_ctx_create
     hipStream_t stream = nullptr;  // where work is enqueued (own, borrowed, or NULL = legacy default)
     std::string err;
@@ -27,6 +28,10 @@ struct fh_ctx {
     // quants, sampler rows).  Reused across calls on this context.
     void* ws = nullptr;
     size_t ws_bytes = 0;
+    // Zero-initialised device state that kernels leave zeroed again when they
+    // finish (the split sampler's per-row barriers).  Never shares ws.
+    void* sync = nullptr;
+    size_t sync_bytes = 0;
 };
 
 struct fh_q8_0 {
@@ -48,6 +53,9 @@ int fh_hip_fail(fh_ctx* ctx, hipError_t e, const char* what);
 
 // Make sure ctx->ws holds at least `bytes` (device, 256-B aligned).
 int fh_workspace(fh_ctx* ctx, size_t bytes, void** out);
+// Make sure ctx->sync holds at least `bytes`, zeroed when (re)allocated.
+// Growing is refused while the stream is being captured into a graph.
+int fh_sync_area(fh_ctx* ctx, size_t bytes, void** out);
 // Round up to a multiple of 256 bytes.
 static inline size_t fh_align256(size_t b) { return (b + 255) & ~(size_t)255; }
 

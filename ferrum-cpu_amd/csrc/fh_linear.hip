@@ -27,92 +27,131 @@ __global__ void fh_k_encode_split(const float* __restrict__ x, size_t nblocks, u
 namespace {
 
 constexpr int kWaves = 4;  // waves per block in the GEMV kernels
-constexpr int kRowSetsPerStep = 2;
 
 __device__ __forceinline__ float sbyte(uint32_t w, int i) {
     return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xFFu));
 }
 
-template <int G, int CPL, int M, bool kBias>
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float rdlane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over each group of G consecutive lanes (G a power of two <= 16), every
+// lane of the group ending with the same total: quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if (G >= 2) v += dpp<0xB1>(v);
+    if (G >= 4) v += dpp<0x4E>(v);
+    if (G >= 8) v += dpp<0x141>(v);
+    if (G >= 16) v += dpp<0x140>(v);
+    return v;
+}
+
+// Q8_0 GEMV, m = M <= 2.  A wave owns `per_wave` consecutive row-sets (a
+// row-set = 64 / G rows, G lanes per row); it issues the loads of up to U
+// row-sets at once — CPL 16-byte quant chunks and their f16 scales per lane —
+// next to its activation chunks, so a whole batch costs one memory latency.
+// Lane gl of a row holds chunks gl, gl + G, ... (coalesced: the G lanes of a
+// row read G consecutive 16-byte chunks).
+template <int G, int CPL, int M, int U, bool kBias>
 __global__ void __launch_bounds__(64 * kWaves)
     k_gemv_w8a32(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const float* __restrict__ x,
-                 const float* __restrict__ bias, float* __restrict__ y, int n, int k) {
-    constexpr int RW = 64 / G;  // rows per wave per row-set
+                 const float* __restrict__ bias, float* __restrict__ y, int n, int k, int per_wave) {
+    constexpr int RW = 64 / G;  // rows per row-set
     const int lane = threadIdx.x & 63;
     const int grp = lane / G, gl = lane % G;
     const int k16 = k >> 4, kb = k >> 5;
+    const int nsets = (n + RW - 1) / RW;
+    const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
+    const int set0 = wave * per_wave;
+    if (set0 >= nsets) return;
+    const int set1 = min(nsets, set0 + per_wave);
 
+    // Every load below is unconditional, from a clamped (always valid)
+    // address, so the compiler issues them back to back without waits; the
+    // lanes and rows past the end are zeroed when the data is used.
+    // A chunk past the row end (k16 not a multiple of G) re-reads the last one
+    // and gets its activations masked to +0.0 bit-wise, so it adds nothing.
     float xr[M][CPL][16];
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
-        const int ci = gl + c * G;
+        const int ci = min(gl + c * G, k16 - 1);
+        const uint32_t keep = gl + c * G < k16 ? 0xFFFFFFFFu : 0u;
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            if (ci < k16) {
-                const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * k + ci * 16);
+            const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * k + ci * 16);
 #pragma unroll
-                for (int v = 0; v < 4; v++) {
-                    float4 f = src[v];
-                    xr[m][c][4 * v + 0] = f.x;
-                    xr[m][c][4 * v + 1] = f.y;
-                    xr[m][c][4 * v + 2] = f.z;
-                    xr[m][c][4 * v + 3] = f.w;
-                }
-            } else {
+            for (int v = 0; v < 4; v++) {
+                const float4 f = src[v];
+                const float fv[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
-                for (int t = 0; t < 16; t++) xr[m][c][t] = 0.0f;
+                for (int e = 0; e < 4; e++)
+                    xr[m][c][4 * v + e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, fv[e]) & keep);
             }
         }
     }
 
-    const int nsets = (n + RW - 1) / RW;
-    const int wave_id = blockIdx.x * kWaves + (threadIdx.x >> 6);
-    const int nwaves = gridDim.x * kWaves;
-    for (int rs0 = wave_id * kRowSetsPerStep; rs0 < nsets; rs0 += nwaves * kRowSetsPerStep) {
-        uint4 qv[kRowSetsPerStep][CPL];
-        float dv[kRowSetsPerStep][CPL];
+    for (int sb = set0; sb < set1; sb += U) {
+        uint4 qv[U][CPL];
+        uint32_t dh[U][CPL];
 #pragma unroll
-        for (int u = 0; u < kRowSetsPerStep; u++) {
-            const int row = (rs0 + u) * RW + grp;
+        for (int u = 0; u < U; u++) {
+            const int row = min((sb + u) * RW + grp, n - 1);
 #pragma unroll
             for (int c = 0; c < CPL; c++) {
-                const int ci = gl + c * G;
-                if (row < n && ci < k16) {
-                    qv[u][c] = *reinterpret_cast<const uint4*>(qs + static_cast<size_t>(row) * k + ci * 16);
-                    dv[u][c] = fh_h2f(dsc[static_cast<size_t>(row) * kb + (ci >> 1)]);
-                } else {
-                    qv[u][c] = make_uint4(0, 0, 0, 0);
-                    dv[u][c] = 0.0f;
-                }
+                const int ci = min(gl + c * G, k16 - 1);
+                qv[u][c] = *reinterpret_cast<const uint4*>(qs + static_cast<size_t>(row) * k + ci * 16);
+                dh[u][c] = dsc[static_cast<size_t>(row) * kb + (ci >> 1)];
             }
         }
+        // Keep the scheduler from interleaving the batch's loads with its math:
+        // all of them go out before the first wait.
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int u = 0; u < kRowSetsPerStep; u++) {
+        for (int u = 0; u < U; u++) {
+            const bool live = sb + u < set1;  // dead row-sets run on clamped data, unstored
             float acc[M];
 #pragma unroll
             for (int m = 0; m < M; m++) acc[m] = 0.0f;
 #pragma unroll
             for (int c = 0; c < CPL; c++) {
+                const float dvc = fh_h2f(static_cast<uint16_t>(dh[u][c]));
                 const uint32_t wq[4] = {qv[u][c].x, qv[u][c].y, qv[u][c].z, qv[u][c].w};
                 float wf[16];
 #pragma unroll
                 for (int t = 0; t < 16; t++) wf[t] = sbyte(wq[t >> 2], t & 3);
 #pragma unroll
                 for (int m = 0; m < M; m++) {
-                    float s = 0.0f;
+                    float sacc = 0.0f;
 #pragma unroll
-                    for (int t = 0; t < 16; t++) s = fmaf(xr[m][c][t], wf[t], s);
-                    acc[m] = fmaf(dv[u][c], s, acc[m]);
+                    for (int t = 0; t < 16; t++) sacc = fmaf(xr[m][c][t], wf[t], sacc);
+                    acc[m] = fmaf(dvc, sacc, acc[m]);
                 }
             }
+            const int row = (sb + u) * RW + grp;
+            if (G <= 16) {
 #pragma unroll
-            for (int off = G / 2; off > 0; off >>= 1)
+                for (int m = 0; m < M; m++) acc[m] = group_sum<G>(acc[m]);
+                if (live && gl == 0 && row < n) {
 #pragma unroll
-                for (int m = 0; m < M; m++) acc[m] += __shfl_xor(acc[m], off, 64);
-            const int row = (rs0 + u) * RW + grp;
-            if (gl == 0 && row < n) {
+                    for (int m = 0; m < M; m++)
+                        y[static_cast<size_t>(m) * n + row] = kBias ? acc[m] + bias[row] : acc[m];
+                }
+            } else {
+                // G = 32 or 64: 16-lane row totals, then across rows with readlane
 #pragma unroll
-                for (int m = 0; m < M; m++) y[static_cast<size_t>(m) * n + row] = kBias ? acc[m] + bias[row] : acc[m];
+                for (int m = 0; m < M; m++) {
+                    const float r16 = group_sum<16>(acc[m]);
+                    const float lo = rdlane(r16, 0) + rdlane(r16, 16);
+                    const float hi = rdlane(r16, 32) + rdlane(r16, 48);
+                    const float tot = G == 64 ? lo + hi : (grp == 0 ? lo : hi);
+                    if (live && gl == 0 && row < n) y[static_cast<size_t>(m) * n + row] = kBias ? tot + bias[row] : tot;
+                }
             }
         }
     }
@@ -217,42 +256,55 @@ __global__ void __launch_bounds__(256)
     if (live && gl == 0) y[pair] = bias ? acc + bias[j] : acc;
 }
 
-template <int G, int CPL, int M>
+// Row-sets per wave: enough waves to cover the chip (12 per CU on 256 CUs)
+// before a wave takes more than one row-set; beyond U, whole batches of U.
+template <int G, int CPL, int M, int U>
 int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y) {
-    // The bias-free form (ops::matmul, the tied lm_head) is its own instance.
-    auto kernel = bias ? k_gemv_w8a32<G, CPL, M, true> : k_gemv_w8a32<G, CPL, M, false>;
     constexpr int RW = 64 / G;
     const size_t nsets = (w->n + RW - 1) / RW;
-    const size_t steps = (nsets + kRowSetsPerStep - 1) / kRowSetsPerStep;
-    // Enough waves for every row-set step, capped at 16 waves per CU on 256 CUs.
-    size_t blocks = (steps + kWaves - 1) / kWaves;
-    if (blocks > 1024) blocks = 1024;
-    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves), 0,
-                       ctx->stream, w->qs, w->d, x, bias, y, static_cast<int>(w->n), static_cast<int>(w->k));
+    size_t per_wave = (nsets + 3071) / 3072;
+    if (per_wave < 1) per_wave = 1;
+    if (per_wave > static_cast<size_t>(U)) per_wave = ((per_wave + U - 1) / U) * U;
+    const size_t waves = (nsets + per_wave - 1) / per_wave;
+    const size_t blocks = (waves + kWaves - 1) / kWaves;
+    // The bias-free form (ops::matmul, the tied lm_head) is its own instance.
+    auto kernel = bias ? k_gemv_w8a32<G, CPL, M, U, true> : k_gemv_w8a32<G, CPL, M, U, false>;
+    hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves), 0, ctx->stream, w->qs, w->d,
+                       x, bias, y, static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(per_wave));
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
 
 // Lanes per row (G) and 16-quant chunks per lane (CPL) for a row of k quants:
-// the fewest chunks per lane (at most 4 when k allows) with all 64 lanes busy.
+// G = 64 with CPL = ceil(k/16/64) for long rows; shorter rows take the
+// smallest power-of-two G with at most 4 chunks per lane.  U keeps about 12
+// quant loads in flight per lane.
 template <int M>
 int dispatch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y) {
     const size_t k16 = w->k / 16;
-#define FH_GEMV(G, C) return launch_gemv<G, C, M>(ctx, w, x, bias, y)
+#define FH_GEMV(G, C) return launch_gemv<G, C, M, (12 / C > 0 ? 12 / C : 1)>(ctx, w, x, bias, y)
     if (k16 >= 64) {
-        const size_t cpl = (k16 + 63) / 64;
-        if (cpl == 1) FH_GEMV(64, 1);
-        if (cpl == 2) FH_GEMV(64, 2);
-        if (cpl == 3) FH_GEMV(64, 3);
-        if (cpl == 4) FH_GEMV(64, 4);
-        if (cpl <= 6) FH_GEMV(64, 6);
-        if (cpl <= 8) FH_GEMV(64, 8);
-        return -1;  // caller falls back to the tiled kernel
+        switch ((k16 + 63) / 64) {
+            case 1: FH_GEMV(64, 1);
+            case 2: FH_GEMV(64, 2);
+            case 3: FH_GEMV(64, 3);
+            case 4: FH_GEMV(64, 4);
+            case 5: FH_GEMV(64, 5);
+            case 6: FH_GEMV(64, 6);
+            case 7:
+            case 8: FH_GEMV(64, 8);
+            default: return -1;  // caller falls back to the tiled kernel
+        }
     }
-    if (k16 > 32) FH_GEMV(16, 4);  // 48 (k = 768): 3 used of 4
-    if (k16 > 16) FH_GEMV(8, 4);
-    if (k16 > 8) FH_GEMV(4, 4);
-    if (k16 > 4) FH_GEMV(2, 4);
+    const size_t g = (k16 + 3) / 4;  // lanes needed at 4 chunks per lane
+    const size_t cpl16 = (k16 + 15) / 16;
+    if (g > 8) {  // G = 16
+        if (cpl16 == 3) FH_GEMV(16, 3);
+        FH_GEMV(16, 4);
+    }
+    if (g > 4) FH_GEMV(8, 4);
+    if (g > 2) FH_GEMV(4, 4);
+    if (g > 1) FH_GEMV(2, 4);
     FH_GEMV(1, 4);
 #undef FH_GEMV
 }

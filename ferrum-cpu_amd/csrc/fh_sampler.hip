@@ -63,6 +63,8 @@ struct Shared {
     uint32_t rhist[256];
     unsigned long long rmass[256];
     float slab[kW][kMaxItems];
+    float pa[256], pb[256];  // other workgroups' partials of the split kernel
+    int qa[256], qb[256];
     float redf[kW];
     int redi[kW];
     int bi[8];
@@ -202,16 +204,18 @@ __device__ __forceinline__ float block_exclusive_scan(Shared& s, float v, float*
 
 // ---- row storage ---------------------------------------------------------------------
 
-// Register-resident row: thread t holds ids t + j * kT, j < ITEMS.
+// Register-resident row (or row segment): thread t holds ids
+// base + t + j * kT < n, j < ITEMS (n is the end of the ids held here).
 template <int ITEMS>
 struct RegRow {
     static constexpr bool kRegs = true;
     float v[ITEMS];
     int n;
+    int base = 0;
     __device__ __forceinline__ void load(const float* __restrict__ src) {
 #pragma unroll
         for (int j = 0; j < ITEMS; j++) {
-            const int i = threadIdx.x + j * kT;
+            const int i = base + threadIdx.x + j * kT;
             v[j] = i < n ? src[i] : 0.0f;
         }
     }
@@ -219,7 +223,7 @@ struct RegRow {
     __device__ __forceinline__ void map(F f) {
 #pragma unroll
         for (int j = 0; j < ITEMS; j++) {
-            const int i = threadIdx.x + j * kT;
+            const int i = base + threadIdx.x + j * kT;
             if (i < n) v[j] = f(v[j], i);
         }
     }
@@ -227,7 +231,7 @@ struct RegRow {
     __device__ __forceinline__ void visit(F f) const {
 #pragma unroll
         for (int j = 0; j < ITEMS; j++) {
-            const int i = threadIdx.x + j * kT;
+            const int i = base + threadIdx.x + j * kT;
             if (i < n) f(v[j], i);
         }
     }
@@ -477,23 +481,23 @@ __device__ __forceinline__ void topp_by_mass(Shared& s, Row& row, float top_p) {
     __syncthreads();
 }
 
-// The first id in index order whose running mass of p / sum2 reaches r (the
-// last id with mass if none does): register rows scan slab by slab (slab j =
-// ids [j * kT, (j + 1) * kT)), global rows by contiguous per-thread segments.
+// The first id in index order whose running mass cum0 + sum of p / sum2
+// reaches r, or INT_MAX.  Slab j = the kT ids base + [j * kT, (j + 1) * kT):
+// slab totals (wave sums, then waves in order) find the slab, one block scan
+// finds the id.
 template <int ITEMS>
-__device__ __forceinline__ int draw_scan(Shared& s, const RegRow<ITEMS>& row, float sum2, float r) {
+__device__ __forceinline__ int draw_scan_from(Shared& s, const RegRow<ITEMS>& row, float sum2, float r, float cum0) {
     const int lane = lane_id(), wv = wave_id();
-    // per-slab totals: wave sums, then over waves in wave order
 #pragma unroll
     for (int j = 0; j < ITEMS; j++) {
-        const int i = threadIdx.x + j * kT;
+        const int i = row.base + threadIdx.x + j * kT;
         const float q = (i < row.n && row.v[j] > 0.0f) ? row.v[j] / sum2 : 0.0f;
         const float t = wave_sum(q);
         if (lane == 0) s.slab[wv][j] = t;
     }
     __syncthreads();
     if (threadIdx.x == 0) {
-        float cum = 0.0f;
+        float cum = cum0;
         int js = -1;
         for (int j = 0; j < ITEMS; j++) {
             float t = 0.0f;
@@ -510,24 +514,30 @@ __device__ __forceinline__ int draw_scan(Shared& s, const RegRow<ITEMS>& row, fl
     const int js = s.bi[0];
     const float base = s.redf[0];
     __syncthreads();
-    if (js >= 0) {
-        float q = 0.0f;
-        int mine = -1;
+    if (js < 0) return INT_MAX;
+    float q = 0.0f;
+    int mine = -1;
 #pragma unroll
-        for (int j = 0; j < ITEMS; j++)
-            if (j == js) {
-                const int i = threadIdx.x + j * kT;
-                if (i < row.n && row.v[j] > 0.0f) {
-                    q = row.v[j] / sum2;
-                    mine = i;
-                }
+    for (int j = 0; j < ITEMS; j++)
+        if (j == js) {
+            const int i = row.base + threadIdx.x + j * kT;
+            if (i < row.n && row.v[j] > 0.0f) {
+                q = row.v[j] / sum2;
+                mine = i;
             }
-        float total;
-        const float before = block_exclusive_scan(s, q, &total);
-        const bool hit = mine >= 0 && r <= base + before + q;
-        const int first = block_min_i(s, hit ? mine : INT_MAX);
-        if (first != INT_MAX) return first;
-    }
+        }
+    float total;
+    const float before = block_exclusive_scan(s, q, &total);
+    const bool hit = mine >= 0 && r <= base + before + q;
+    return block_min_i(s, hit ? mine : INT_MAX);
+}
+
+// The first id in index order whose running mass of p / sum2 reaches r, else
+// the last id with mass (pick_by_mass, sampling.rs:109-122).
+template <int ITEMS>
+__device__ __forceinline__ int draw_scan(Shared& s, const RegRow<ITEMS>& row, float sum2, float r) {
+    const int first = draw_scan_from(s, row, sum2, r, 0.0f);
+    if (first != INT_MAX) return first;
     int last = -1;
     row.visit([&](float p, int i) {
         if (p > 0.0f) last = i;
@@ -564,6 +574,217 @@ __device__ __forceinline__ int draw_scan(Shared& s, const GlobalRow& row, float 
     const int first = block_min_i(s, pick);
     const int lastg = block_max_i(s, last);
     return first != INT_MAX ? first : (lastg >= 0 ? lastg : 0);
+}
+
+__device__ __forceinline__ unsigned long long shfl_xor64(unsigned long long v, int m) {
+    const unsigned lo = __shfl_xor(static_cast<unsigned>(v), m, 64);
+    const unsigned hi = __shfl_xor(static_cast<unsigned>(v >> 32), m, 64);
+    return (static_cast<unsigned long long>(hi) << 32) | lo;
+}
+__device__ __forceinline__ unsigned rlu(unsigned v, int lane) {
+    return static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(v), lane));
+}
+
+__device__ __forceinline__ unsigned long long rl64(unsigned long long v, int lane) {
+    return (static_cast<unsigned long long>(rlu(static_cast<unsigned>(v >> 32), lane)) << 32) |
+           rlu(static_cast<unsigned>(v), lane);
+}
+
+// Sort one wave's keys (lanes < nc, distinct) descending: each lane counts the
+// keys above its own (readlane broadcasts, no LDS round trips), then the keys
+// are scattered to their ranks through `tmp` (64 entries of LDS).
+__device__ __forceinline__ unsigned long long wave_sort_desc(unsigned long long k, int nc, unsigned long long* tmp) {
+    const int lane = lane_id();
+    // lanes >= nc hold key 0, which is above no key: all 64 steps, no branches
+    k = lane < nc ? k : 0ull;
+    int rank = 0;
+#pragma unroll
+    for (int j = 0; j < 64; j++) rank += rl64(k, j) > k;
+    if (lane < nc) tmp[rank] = k;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const unsigned long long r = lane < nc ? tmp[lane] : 0ull;
+    __builtin_amdgcn_wave_barrier();
+    return r;
+}
+
+// Running f32 sum over lanes 0..len-1 in lane order (the reference's
+// sequential order): lane c gets the sum of lanes 0..c.  Each step is one
+// readlane and one dependent add; no branches.
+__device__ __forceinline__ float lane_running_sum(float v, int len) {
+    const int lane = lane_id();
+    // lanes >= len add +0.0, which leaves a non-negative sum unchanged: all
+    // 64 steps, unrolled, no branches
+    const unsigned vb = __builtin_bit_cast(unsigned, lane < len ? v : 0.0f);
+    float cum = 0.0f, mine = 0.0f;
+#pragma unroll
+    for (int c = 0; c < 64; c++) {
+        cum += __builtin_bit_cast(float, rlu(vb, c));
+        mine = lane == c ? cum : mine;
+    }
+    return mine;
+}
+
+// Steps 4-6 for at most 64 gathered ids, in one wave and in registers: sort
+// by (p desc, index asc), the reference's top-k threshold and sequential
+// top-p walk, back to index order, sequential sum2 and pick_by_mass
+// (sampling.rs:171-209, 109-122).  Every lane of the wave calls with the same
+// arguments; lane 0 writes *out.  Returns false, writing nothing, when the
+// top-p cut lies below the gathered ids.
+__device__ __forceinline__ bool wave_tail(unsigned long long key, int nc, int top_k, float top_p, bool use_k,
+                                          bool use_p, float r, uint32_t* __restrict__ out, unsigned long long* tmp) {
+    const int lane = lane_id();
+    unsigned long long k = lane < nc ? key : 0ull;
+    k = wave_sort_desc(k, nc, tmp);
+    int len = nc;
+    if (use_k) {
+        const float thr = __builtin_bit_cast(float, rlu(static_cast<unsigned>(k >> 32), top_k - 1));
+        len = __popcll(__ballot(lane < nc && key_p(k) >= thr));  // a prefix: the keys are sorted
+    }
+    if (use_p) {
+        // cum after each survivor in descending order; keep up to the first >= top_p
+        const float cum = lane_running_sum(lane < len ? key_p(k) : 0.0f, len);
+        const unsigned long long crossed = __ballot(lane < len && cum >= top_p);
+        if (crossed) len = __ffsll(static_cast<long long>(crossed));
+        else if (!use_k) return false;
+    }
+    unsigned long long k2 =
+        lane < len ? (static_cast<unsigned long long>(~static_cast<uint32_t>(key_i(k))) << 32) | (k >> 32) : 0ull;
+    k2 = wave_sort_desc(k2, len, tmp);  // descending ~index = ascending index
+    const float pl = lane < len ? __builtin_bit_cast(float, static_cast<unsigned>(k2)) : 0.0f;
+    const int idx = static_cast<int>(~static_cast<unsigned>(k2 >> 32));
+    // sum2 in index order, sequentially
+    const unsigned pb = __builtin_bit_cast(unsigned, pl);
+    float sum2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 64; i++) sum2 += __builtin_bit_cast(float, rlu(pb, i));  // lanes >= len hold +0.0
+    // p / sum2 per lane, the running cumsum in index order, then the first
+    // id with mass whose cumsum reaches r, else the last id with mass
+    const float q = pl / sum2;
+    const float cumsum = lane_running_sum(q, len);
+    const unsigned long long live = __ballot(lane < len && q > 0.0f);
+    const unsigned long long hit = __ballot(lane < len && q > 0.0f && r <= cumsum);
+    const int pick_lane = hit ? __ffsll(static_cast<long long>(hit)) - 1 : (live ? 63 - __clzll(live) : 0);
+    const int pick = __builtin_amdgcn_readlane(idx, pick_lane);
+    if (lane == 0) *out = static_cast<uint32_t>(live ? pick : 0);
+    return true;
+}
+
+// The shallowest bucket depth whose cumulative count reaches k (top-k) or
+// whose fixed-point mass reaches top_p, plus one bucket of margin (top-p
+// only); -1 when not found or when more than kCap ids would be gathered.
+__device__ __forceinline__ int bucket_depth(const uint32_t* hist, const unsigned long long* mass, int top_k,
+                                            float top_p, bool use_k, bool use_p) {
+    int depth = -1, cnt = 0;
+    unsigned long long acc = 0;
+    const unsigned long long target = use_p ? fix40(top_p) : 0;
+    for (int b = 0; b < kBuckets; b++) {
+        cnt += static_cast<int>(hist[b]);
+        acc += mass[b];
+        if (use_k ? cnt >= top_k : acc >= target) {
+            depth = b;
+            break;
+        }
+    }
+    if (depth >= 0 && !use_k && depth + 1 < kBuckets) {
+        depth++;
+        cnt += static_cast<int>(hist[depth]);
+    }
+    return (depth >= 0 && cnt <= kCap) ? depth : -1;
+}
+
+// Sort s.u.cand[0..nc) by (p desc, index asc) and replay top-k then top-p in
+// the reference's order (sampling.rs:171-200).  Returns the survivor count,
+// or -1 when the top-p cut lies below the gathered ids.  Every thread calls.
+__device__ __forceinline__ int replay_list(Shared& s, int nc, int top_k, float top_p, bool use_k, bool use_p) {
+    const int tid = threadIdx.x;
+    int n2 = 1;
+    while (n2 < nc) n2 <<= 1;
+    for (int i = nc + tid; i < n2; i += kT) s.u.cand[i] = 0ull;  // p = 0 sorts last
+    sort_desc(s, n2);
+    if (tid < 64) {  // wave 0, every lane the same
+        int len = nc;
+        bool ok = true;
+        if (use_k) {
+            const float thr = key_p(s.u.cand[top_k - 1]);
+            len = top_k;
+            while (len < nc && key_p(s.u.cand[len]) >= thr) len++;
+        }
+        if (use_p) {
+            float cum = 0.0f;
+            bool crossed = false;
+            int c = 0;
+            for (; c < len; c++) {
+                cum += key_p(s.u.cand[c]);
+                if (cum >= top_p) {
+                    crossed = true;
+                    break;
+                }
+            }
+            if (crossed) len = c + 1;
+            else if (!use_k) ok = false;
+        }
+        if (tid == 0) s.bi[1] = ok ? len : -1;
+    }
+    __syncthreads();
+    const int n_list = s.bi[1];
+    __syncthreads();
+    return n_list;
+}
+
+// Renormalise the survivors s.u.cand[0..n_list) (p-descending on entry) and
+// draw: back into index order, then one wave replays sum2 and pick_by_mass
+// sequentially (sampling.rs:205-209, 109-122).  Every thread calls; thread 0
+// writes *out.
+__device__ __forceinline__ void finish_list(Shared& s, int n_list, float r, uint32_t* __restrict__ out) {
+    const int tid = threadIdx.x;
+    for (int i = tid; i < n_list; i += kT) {  // key (~index << 32) | bits(p)
+        const unsigned long long k = s.u.cand[i];
+        s.u.cand[i] = (static_cast<unsigned long long>(~static_cast<uint32_t>(key_i(k))) << 32) | (k >> 32);
+    }
+    int n2 = 1;
+    while (n2 < n_list) n2 <<= 1;
+    for (int i = n_list + tid; i < n2; i += kT) s.u.cand[i] = 0ull;
+    sort_desc(s, n2);  // descending ~index = ascending index
+    if (tid < 64) {
+        float sum2 = 0.0f;
+        for (int i = 0; i < n_list; i++) sum2 += __builtin_bit_cast(float, static_cast<uint32_t>(s.u.cand[i]));
+        float cumsum = 0.0f;
+        int pick = -1, last = 0;
+        for (int i = 0; i < n_list; i++) {
+            const unsigned long long k = s.u.cand[i];
+            const float p = __builtin_bit_cast(float, static_cast<uint32_t>(k)) / sum2;
+            const int idx = static_cast<int>(~static_cast<uint32_t>(k >> 32));
+            if (p > 0.0f) {
+                last = idx;
+                cumsum += p;
+                if (r <= cumsum) {
+                    pick = idx;
+                    break;
+                }
+            }
+        }
+        if (tid == 0) *out = static_cast<uint32_t>(pick >= 0 ? pick : last);
+    }
+}
+
+// The general path over a whole row: exact top-k threshold, top-p cut by mass,
+// then the block-wide draw.  Every thread calls; thread 0 writes *out.
+template <class Row>
+__device__ __forceinline__ void general_tail(Shared& s, Row& row, int top_k, float top_p, bool use_k, bool use_p,
+                                             float r, uint32_t* __restrict__ out) {
+    if (use_k) {
+        const float thr = radix_kth_largest(s, row, top_k);
+        row.map([&](float p, int) { return p < thr ? 0.0f : p; });
+        __syncthreads();
+    }
+    if (use_p) topp_by_mass(s, row, top_p);
+    float s2 = 0.0f;
+    row.visit([&](float p, int) { s2 += p; });
+    const float sum2 = block_sum(s, s2);
+    const int pick = draw_scan(s, row, sum2, r);
+    if (threadIdx.x == 0) *out = static_cast<uint32_t>(pick);
 }
 
 struct Params {
@@ -676,10 +897,9 @@ __device__ __forceinline__ void sample_row(Shared& s, Row& row, const Params& P,
     const float pmax = block_max(s, pm);
     const float r = static_cast<float>(draw_u64 >> 40) / static_cast<float>(1u << 24);
 
-    // ---- 4./5. top-k and top-p ------------------------------------------------------------
+    // ---- 4./5./6. top-k, top-p, renormalise and draw --------------------------------------
     const bool use_k = P.top_k > 0 && P.top_k < n;
     const bool use_p = P.top_p < 1.0f;
-    int n_list = -1;  // >= 0: the survivors are s.u.cand[0..n_list), p descending
     if (use_k || use_p) {
         const int ktop = key12(pmax);
         const int copy = tid & (kCopies - 1);
@@ -708,114 +928,34 @@ __device__ __forceinline__ void sample_row(Shared& s, Row& row, const Params& P,
         }
         __syncthreads();
         if (tid == 0) {
-            // The shallowest bucket depth whose cumulative count reaches k (top-k)
-            // or whose mass reaches top_p, plus one bucket of margin (top-p only).
-            int depth = -1, cnt = 0;
-            unsigned long long acc = 0;
-            const unsigned long long target = use_p ? fix40(P.top_p) : 0;
-            for (int b = 0; b < kBuckets; b++) {
-                cnt += static_cast<int>(s.hist[0][b]);
-                acc += s.mass[0][b];
-                if (use_k ? cnt >= P.top_k : acc >= target) {
-                    depth = b;
-                    break;
-                }
-            }
-            if (depth >= 0 && !use_k && depth + 1 < kBuckets) {
-                depth++;
-                cnt += static_cast<int>(s.hist[0][depth]);
-            }
-            s.bi[0] = (depth >= 0 && cnt <= kCap) ? depth : -1;
+            s.bi[0] = bucket_depth(s.hist[0], s.mass[0], P.top_k, P.top_p, use_k, use_p);
             s.n_cand = 0;
         }
         __syncthreads();
         const int depth = s.bi[0];
+        int n_list = -1;
         if (depth >= 0) {
             row.visit([&](float p, int i) { append(s, p > 0.0f && ktop - key12(p) <= depth, cand_key(p, i)); });
-            // RegRow::visit skips ids >= n per item, so append's ballot may run
-            // with some lanes inactive; the list is complete after the barrier.
             __syncthreads();
             const int nc = static_cast<int>(s.n_cand);
-            int n2 = 1;
-            while (n2 < nc) n2 <<= 1;
-            for (int i = nc + tid; i < n2; i += kT) s.u.cand[i] = 0ull;  // p = 0 sorts last
-            sort_desc(s, n2);
-            if (tid < 64) {  // wave 0 replays top-k / top-p in the reference's order
-                int len = nc;
-                bool ok = true;
-                if (use_k) {
-                    const float thr = key_p(s.u.cand[P.top_k - 1]);
-                    len = P.top_k;
-                    while (len < nc && key_p(s.u.cand[len]) >= thr) len++;
+            if (nc <= 64) {
+                if (tid < 64) {
+                    const bool ok = wave_tail(s.u.cand[tid < nc ? tid : 0], nc, P.top_k, P.top_p, use_k, use_p, r, out,
+                                              reinterpret_cast<unsigned long long*>(&s.slab[0][0]));
+                    if (tid == 0) s.bi[2] = ok;
                 }
-                if (use_p) {
-                    float cum = 0.0f;
-                    bool crossed = false;
-                    int c = 0;
-                    for (; c < len; c++) {
-                        cum += key_p(s.u.cand[c]);
-                        if (cum >= P.top_p) {
-                            crossed = true;
-                            break;
-                        }
-                    }
-                    if (crossed) len = c + 1;
-                    else if (!use_k) ok = false;  // the cut lies below the gathered set
-                }
-                if (tid == 0) s.bi[1] = ok ? len : -1;
-            }
-            __syncthreads();
-            n_list = s.bi[1];
-            __syncthreads();
-        }
-        if (n_list < 0) {
-            if (use_k) {
-                const float thr = radix_kth_largest(s, row, P.top_k);
-                row.map([&](float p, int) { return p < thr ? 0.0f : p; });
                 __syncthreads();
+                if (s.bi[2]) return;
+            } else {
+                n_list = replay_list(s, nc, P.top_k, P.top_p, use_k, use_p);
             }
-            if (use_p) topp_by_mass(s, row, P.top_p);
+        }
+        if (n_list >= 0) {
+            finish_list(s, n_list, r, out);
+            return;
         }
     }
-
-    // ---- 6. renormalise and draw -------------------------------------------------------
-    if (n_list >= 0) {
-        // survivors back into index order: key (~index << 32) | bits(p), descending
-        for (int i = tid; i < n_list; i += kT) {
-            const unsigned long long k = s.u.cand[i];
-            s.u.cand[i] = (static_cast<unsigned long long>(~static_cast<uint32_t>(key_i(k))) << 32) | (k >> 32);
-        }
-        int n2 = 1;
-        while (n2 < n_list) n2 <<= 1;
-        for (int i = n_list + tid; i < n2; i += kT) s.u.cand[i] = 0ull;
-        sort_desc(s, n2);
-        if (tid < 64) {  // wave 0: sum2, then pick_by_mass, sequentially in index order
-            float sum2 = 0.0f;
-            for (int i = 0; i < n_list; i++) sum2 += __builtin_bit_cast(float, static_cast<uint32_t>(s.u.cand[i]));
-            float cumsum = 0.0f;
-            int pick = -1, last = 0;
-            for (int i = 0; i < n_list; i++) {
-                const unsigned long long k = s.u.cand[i];
-                const float p = __builtin_bit_cast(float, static_cast<uint32_t>(k)) / sum2;
-                const int idx = static_cast<int>(~static_cast<uint32_t>(k >> 32));
-                if (p > 0.0f) {
-                    last = idx;
-                    cumsum += p;
-                    if (r <= cumsum) {
-                        pick = idx;
-                        break;
-                    }
-                }
-            }
-            if (tid == 0) *out = static_cast<uint32_t>(pick >= 0 ? pick : last);
-        }
-        return;
-    }
-    float s2 = 0.0f;
-    row.visit([&](float p, int) { s2 += p; });
-    const float sum2 = block_sum(s, s2);
-    const int pick = draw_scan(s, row, sum2, r);
-    if (tid == 0) *out = static_cast<uint32_t>(pick);
+    general_tail(s, row, P.top_k, P.top_p, use_k, use_p, r, out);
 }
 
 template <int ITEMS>
@@ -860,6 +1000,460 @@ __global__ void __launch_bounds__(kT)
                has_draw, out + row);
 }
 
+// ---- one row over several workgroups ---------------------------------------------------
+//
+// Vocabulary rows split into S segments of kT * ITEMS ids, one workgroup each,
+// so the per-id exp/log/divide work of steps 0-3 spreads over S CUs.  The
+// workgroups of a row exchange small per-segment results (softmax max/sum
+// pairs, bucket histograms, segment masses) and workgroup 0 finishes the row
+// (sorting the gathered survivors, or the general path over the row's p values
+// in `pbuf`).  Partial results are combined in segment order, so the result
+// does not depend on timing.
+//
+// Exchange.  Every value crosses workgroups in a 64-bit slot (32-bit payload,
+// 32-bit tag) written with one device-coherent store (a relaxed agent-scope
+// atomic: it bypasses the XCD-private L2, so no cache write-back or invalidate
+// is needed); a reader polls the slots until each carries this launch's tag,
+// so one memory round trip both synchronises and delivers the data.  The tag
+// is the row's generation + 1: every workgroup reads `gen` at its start and
+// workgroup 0 bumps it when the row is done, so no slot is ever cleared and a
+// stale slot (the previous launch's tag) is never taken for a fresh one — which
+// keeps the state valid across HIP graph replays.  The launcher keeps rows * S
+// <= the number of CUs with one workgroup per CU (the kernel's LDS allows no
+// more), so every workgroup of a row is resident together; every poll is
+// bounded: a slot still stale after kSpinLimit polls records an error and the
+// workgroup goes on.
+
+constexpr int kSMax = 64;
+constexpr unsigned kSpinLimit = 1u << 20;
+enum { kPhGpt2 = 0, kPhTemp = 1, kPhGreedy = 2, kPhSeg = 3, kPhDone = 4, kPhases = 5 };
+
+struct RowSync {
+    unsigned gen;
+    unsigned err;
+    unsigned n_cand;  // survivors appended so far (workgroup 0 zeroes it when done)
+    unsigned pad[13];
+    unsigned long long a[kPhases][kSMax];  // payload A | tag
+    unsigned long long b[kPhases][kSMax];  // payload B | tag
+    unsigned long long hist[kSMax][kBuckets];  // bucket count | tag
+    unsigned long long mass[kSMax][kBuckets];  // bucket mass, stored before its count
+    unsigned long long cand[kCap];
+};
+
+template <class T>
+__device__ __forceinline__ void cstore(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T cload(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wait until this thread's own earlier stores are complete (so a later store
+// of a tag cannot overtake them).
+__device__ __forceinline__ void stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ unsigned long long tagf(float v, unsigned tag) {
+    return (static_cast<unsigned long long>(tag) << 32) | __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ unsigned long long tagi(int v, unsigned tag) {
+    return (static_cast<unsigned long long>(tag) << 32) | static_cast<uint32_t>(v);
+}
+__device__ __forceinline__ float untagf(unsigned long long x) { return __builtin_bit_cast(float, static_cast<uint32_t>(x)); }
+__device__ __forceinline__ int untagi(unsigned long long x) { return static_cast<int>(static_cast<uint32_t>(x)); }
+
+// Poll one slot until it carries `tag` (bounded).
+__device__ __forceinline__ unsigned long long poll(RowSync* rs, const unsigned long long* slot, unsigned tag) {
+    unsigned spins = 0;
+    while (true) {
+        const unsigned long long x = cload(slot);
+        if (static_cast<unsigned>(x >> 32) == tag) return x;
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins == kSpinLimit) {
+            atomicOr(&rs->err, 1u);
+            return x;
+        }
+    }
+}
+// Poll two slots at once (both loads in flight per round).
+__device__ __forceinline__ void poll2(RowSync* rs, const unsigned long long* p, const unsigned long long* q,
+                                      unsigned tag, unsigned long long* x, unsigned long long* y) {
+    unsigned spins = 0;
+    while (true) {
+        *x = cload(p);
+        *y = cload(q);
+        if (static_cast<unsigned>(*x >> 32) == tag && static_cast<unsigned>(*y >> 32) == tag) return;
+        __builtin_amdgcn_s_sleep(1);
+        if (++spins == kSpinLimit) {
+            atomicOr(&rs->err, 1u);
+            return;
+        }
+    }
+}
+
+// Thread 0 publishes this workgroup's pair for `phase`.
+__device__ __forceinline__ void publish(RowSync* rs, int phase, int w, unsigned long long a, unsigned long long b) {
+    if (threadIdx.x == 0) {
+        cstore(&rs->a[phase][w], a);
+        cstore(&rs->b[phase][w], b);
+    }
+}
+
+// Every workgroup's pair for `phase` into s.pa / s.pb (float view) and
+// s.qa / s.qb (int view); whole-workgroup call.
+__device__ __forceinline__ void gather(Shared& s, RowSync* rs, int phase, int S, unsigned tag) {
+    const int tid = threadIdx.x;
+    if (tid < S) {
+        unsigned long long x, y;
+        poll2(rs, &rs->a[phase][tid], &rs->b[phase][tid], tag, &x, &y);
+        s.pa[tid] = untagf(x);
+        s.pb[tid] = untagf(y);
+        s.qa[tid] = untagi(x);
+        s.qb[tid] = untagi(y);
+    }
+    __syncthreads();
+}
+
+// Softmax statistics of one segment: its max m and sum of exp((x - m) / t),
+// two block reductions.  The reference's NaN and -inf behaviour is kept: a
+// NaN term makes the sum NaN; a segment whose max is -inf adds nothing (or
+// NaN, if it holds a NaN) once merged.
+template <class Row>
+__device__ __forceinline__ void block_softmax_stats(Shared& s, const Row& row, float t, bool divide, float* m_out,
+                                                    float* s_out) {
+    float m = -INFINITY;
+    row.visit([&](float x, int) { m = fmaxf(m, x); });
+    m = block_max(s, m);
+    float sum = 0.0f;
+    if (m != -INFINITY) row.visit([&](float x, int) { sum += expf(divide ? (x - m) / t : x - m); });
+    else row.visit([&](float x, int) { sum += x != x ? NAN : 0.0f; });
+    *m_out = m;
+    *s_out = block_sum(s, sum);
+}
+
+// The gathered per-segment pairs (s.pa = max, s.pb = sum) merged: the row max
+// M, then Z = sum_w s_w exp((m_w - M) / t), one segment per lane of every wave
+// (a fixed reduction pattern, so every wave gets the same M and Z).
+__device__ __forceinline__ void merge_segments(const Shared& s, int S, float t, bool divide, float* M, float* Z) {
+    const int lane = lane_id();
+    const float mw = lane < S ? s.pa[lane] : -INFINITY;
+    const float sw = lane < S ? s.pb[lane] : 0.0f;
+    const float m = wave_max(mw);
+    float term = 0.0f;
+    if (lane < S) term = mw == -INFINITY ? sw * 0.0f : sw * expf(divide ? (mw - m) / t : mw - m);
+    *M = m;
+    *Z = wave_sum(term);
+}
+
+template <int ITEMS>
+__global__ void __launch_bounds__(kT)
+    k_sample_split(const float* __restrict__ logits, Params P, const uint32_t* __restrict__ recent,
+                   const uint32_t* __restrict__ offsets, const uint64_t* __restrict__ draws,
+                   uint32_t* __restrict__ out, RowSync* __restrict__ sync, float* __restrict__ pbuf, int S) {
+    __shared__ Shared s;
+    const int tid = threadIdx.x;
+    const int row = blockIdx.x / S, w = blockIdx.x % S;
+    const int n = P.n;
+    RowSync* rs = sync + row;
+    const unsigned gen = cload(&rs->gen);
+    const unsigned tag = gen + 1;
+    const float* z = logits + static_cast<size_t>(row) * n;
+    uint32_t* o = out + row;
+    RegRow<ITEMS> st;
+    st.base = w * kT * ITEMS;
+    st.n = min(n, st.base + kT * ITEMS);
+    st.load(z);
+    // workgroup 0 finishes the row: zero the survivor count, bump the generation
+    auto finish = [&]() __attribute__((always_inline)) {
+        __syncthreads();
+        if (tid == 0) {
+            cstore(&rs->n_cand, 0u);
+            cstore(&rs->gen, tag);
+        }
+    };
+
+    // ---- 1. repetition penalty on this segment's ids: the table of (id, count)
+    // is built before the first exchange so its loads overlap the wait; it is
+    // applied after the GPT-2 bridge, as the reference orders them.
+    const float pen = P.pen;
+    int nrec = 0;
+    const uint32_t* rec = nullptr;
+    if (offsets && recent) {
+        const uint32_t r0 = offsets[row], r1 = offsets[row + 1];
+        nrec = r1 > r0 ? static_cast<int>(min(r1 - r0, static_cast<uint32_t>(kMaxRecent))) : 0;
+        rec = recent + r0;
+    }
+    const bool use_pen = fabsf(pen - 1.0f) > FLT_EPSILON && pen > 0.0f && nrec > 0;
+    auto fill = [&](int b0) __attribute__((always_inline)) {
+        for (int i = tid; i < kSlots; i += kT) {
+            s.u.pen.key[i] = kEmpty;
+            s.u.pen.cnt[i] = 0;
+        }
+        __syncthreads();
+        const int end = min(nrec, b0 + kChunk);
+        for (int r = b0 + tid; r < end; r += kT) {
+            const uint32_t tok = rec[r];
+            if (tok < static_cast<uint32_t>(st.base) || tok >= static_cast<uint32_t>(st.n)) continue;
+            uint32_t h = (tok * 2654435761u) & (kSlots - 1);
+            while (true) {
+                const uint32_t prev = atomicCAS(&s.u.pen.key[h], kEmpty, tok);
+                if (prev == kEmpty || prev == tok) {
+                    atomicAdd(&s.u.pen.cnt[h], 1u);
+                    break;
+                }
+                h = (h + 1) & (kSlots - 1);
+            }
+        }
+        __syncthreads();
+    };
+    auto apply = [&]() __attribute__((always_inline)) {
+        st.map([&](float l, int i) {
+            uint32_t h = (static_cast<uint32_t>(i) * 2654435761u) & (kSlots - 1);
+            while (true) {
+                const uint32_t key = s.u.pen.key[h];
+                if (key == kEmpty) return l;
+                if (key == static_cast<uint32_t>(i)) {
+                    for (uint32_t c = s.u.pen.cnt[h]; c > 0; c--) l = l > 0.0f ? l / pen : l * pen;
+                    return l;
+                }
+                h = (h + 1) & (kSlots - 1);
+            }
+        });
+        __syncthreads();
+    };
+    if (use_pen) fill(0);
+
+    // ---- 0. GPT-2 bridge, with the row's softmax max and sum --------------------------
+    if (P.kind == FH_LOGITS_GPT2_SOFTMAX) {
+        float m, sm;
+        block_softmax_stats(s, st, 1.0f, false, &m, &sm);
+        publish(rs, kPhGpt2, w, tagf(m, tag), tagf(sm, tag));
+        gather(s, rs, kPhGpt2, S, tag);
+        float M, Z;
+        merge_segments(s, S, 1.0f, false, &M, &Z);
+        st.map([&](float x, int) { return logf(fmaxf(expf(x - M) / Z, 1e-12f)); });
+    }
+    if (use_pen) {
+        apply();
+        for (int b0 = kChunk; b0 < nrec; b0 += kChunk) {
+            fill(b0);
+            apply();
+        }
+    }
+
+    // ---- 2. greedy ---------------------------------------------------------------------
+    if (P.temperature <= 0.0f) {
+        int bk = INT_MIN, bi = INT_MAX;
+        st.visit([&](float x, int i) {
+            const int k = total_key(x);
+            if (k > bk || (k == bk && i < bi)) {
+                bk = k;
+                bi = i;
+            }
+        });
+        const int best = block_max_i(s, bk);
+        const int first = block_min_i(s, bk == best ? bi : INT_MAX);
+        publish(rs, kPhGreedy, w, tagi(best, tag), tagi(first, tag));
+        if (w != 0) return;
+        gather(s, rs, kPhGreedy, S, tag);
+        if (tid == 0) {
+            int gk = INT_MIN, gi = INT_MAX;
+            for (int v = 0; v < S; v++) {  // segments in index order: strict '>' keeps the first
+                const int k = s.qa[v], i = s.qb[v];
+                if (i != INT_MAX && (gi == INT_MAX || k > gk)) {
+                    gk = k;
+                    gi = i;
+                }
+            }
+            *o = static_cast<uint32_t>(gi == INT_MAX ? 0 : gi);
+        }
+        finish();
+        return;
+    }
+    const float t = fmaxf(P.temperature, 0.01f);
+    const uint64_t draw = draws[row];
+    const float r = static_cast<float>(draw >> 40) / static_cast<float>(1u << 24);
+
+    // ---- 3. temperature softmax over the row --------------------------------------------
+    {
+        float m, sm;
+        block_softmax_stats(s, st, t, true, &m, &sm);
+        publish(rs, kPhTemp, w, tagf(m, tag), tagf(sm, tag));
+    }
+    gather(s, rs, kPhTemp, S, tag);
+    float mx, sum;
+    merge_segments(s, S, t, true, &mx, &sum);
+    if (sum != sum || sum <= 1e-10f) {
+        if (w == 0) {
+            if (tid == 0) *o = static_cast<uint32_t>(draw % static_cast<uint64_t>(n));
+            finish();
+        }
+        return;
+    }
+    st.map([&](float l, int) { return expf((l - mx) / t) / sum; });
+    const float pmax = 1.0f / sum;  // the max id has e = exp(0) = 1
+    float* prow = pbuf + static_cast<size_t>(row) * n;
+
+    const bool use_k = P.top_k > 0 && P.top_k < n;
+    const bool use_p = P.top_p < 1.0f;
+    if (use_k || use_p) {
+        // ---- 4./5. bucket histograms, then the gathered survivors --------------------
+        st.visit([&](float p, int i) { cstore(&prow[i], p); });  // for the general path
+        const int ktop = key12(pmax);
+        const int copy = tid & (kCopies - 1);
+        for (int i = tid; i < kCopies * kBuckets; i += kT) {
+            (&s.hist[0][0])[i] = 0;
+            (&s.mass[0][0])[i] = 0;
+        }
+        __syncthreads();
+        st.visit([&](float p, int) {
+            const int b = ktop - key12(p);
+            if (p > 0.0f && b < kBuckets) {
+                atomicAdd(&s.hist[copy][b], 1u);
+                if (!use_k) atomicAdd(&s.mass[copy][b], fix40(p));
+            }
+        });
+        __syncthreads();
+        if (tid < kBuckets) {
+            uint32_t c = 0;
+            unsigned long long ms = 0;
+            for (int k = 0; k < kCopies; k++) {
+                c += s.hist[k][tid];
+                ms += s.mass[k][tid];
+            }
+            if (!use_k) {
+                cstore(&rs->mass[w][tid], ms);
+                stores_done();
+            }
+            cstore(&rs->hist[w][tid], tagi(static_cast<int>(c), tag));
+        }
+        // every segment's histogram, summed in segment order
+        uint32_t* hc = reinterpret_cast<uint32_t*>(s.u.cand);                     // [S][kBuckets]
+        unsigned long long* hm = s.u.cand + (kSMax * kBuckets) / 2;                 // [S][kBuckets]
+        for (int i = tid; i < S * kBuckets; i += kT) {
+            const int v = i / kBuckets, b = i % kBuckets;
+            hc[i] = static_cast<uint32_t>(poll(rs, &rs->hist[v][b], tag));
+            if (!use_k) hm[i] = cload(&rs->mass[v][b]);
+        }
+        __syncthreads();
+        if (tid < kBuckets) {
+            uint32_t c = 0;
+            unsigned long long ms = 0;
+            for (int v = 0; v < S; v++) {
+                c += hc[v * kBuckets + tid];
+                if (!use_k) ms += hm[v * kBuckets + tid];
+            }
+            s.hist[0][tid] = c;
+            s.mass[0][tid] = ms;
+        }
+        __syncthreads();
+        if (tid == 0) s.bi[0] = bucket_depth(s.hist[0], s.mass[0], P.top_k, P.top_p, use_k, use_p);
+        __syncthreads();
+        const int depth = s.bi[0];
+        if (depth >= 0) {
+            // append this segment's survivors to the row's list, one atomic per wave
+            st.visit([&](float p, int i) {
+                const bool take = p > 0.0f && ktop - key12(p) <= depth;
+                const unsigned long long mask = __ballot(take);
+                if (mask == 0) return;
+                const int lane = lane_id();
+                const int leader = __ffsll(static_cast<long long>(mask)) - 1;
+                unsigned base = 0;
+                if (lane == leader) base = atomicAdd(&rs->n_cand, static_cast<unsigned>(__popcll(mask)));
+                base = __builtin_amdgcn_readlane(base, leader);
+                if (take) cstore(&rs->cand[base + __popcll(mask & ((1ull << lane) - 1ull))], cand_key(p, i));
+            });
+        }
+        stores_done();
+        __syncthreads();
+        publish(rs, kPhDone, w, tagi(0, tag), tagi(0, tag));
+        if (w != 0) return;
+        gather(s, rs, kPhDone, S, tag);
+        int n_list = -1;
+        bool done = false;
+        if (depth >= 0) {
+            // the count and the first 64 keys in one round trip
+            unsigned long long key = 0;
+            if (tid < 64) key = cload(&rs->cand[tid]);
+            const int nc = static_cast<int>(cload(&rs->n_cand));
+            if (nc <= 64) {
+                if (tid < 64) {
+                    const bool ok = wave_tail(key, nc, P.top_k, P.top_p, use_k, use_p, r, o,
+                                              reinterpret_cast<unsigned long long*>(&s.slab[0][0]));
+                    if (tid == 0) s.bi[2] = ok;
+                }
+                __syncthreads();
+                done = s.bi[2];
+            } else {
+                for (int i = tid; i < nc; i += kT) s.u.cand[i] = cload(&rs->cand[i]);
+                __syncthreads();
+                n_list = replay_list(s, nc, P.top_k, P.top_p, use_k, use_p);
+            }
+        }
+        if (!done) {
+            if (n_list >= 0) {
+                finish_list(s, n_list, r, o);
+            } else {
+                __threadfence();  // the general path reads prow with ordinary loads
+                GlobalRow g;
+                g.w = prow;
+                g.n = n;
+                general_tail(s, g, P.top_k, P.top_p, use_k, use_p, r, o);
+            }
+        }
+        finish();
+        return;
+    }
+
+    // ---- 6. no top-k / top-p: segment masses, then the segment holding r ------------------
+    {
+        float loc = 0.0f;
+        int lastid = -1;
+        st.visit([&](float p, int i) {
+            loc += p;
+            if (p > 0.0f) lastid = i;
+        });
+        loc = block_sum(s, loc);
+        lastid = block_max_i(s, lastid);
+        publish(rs, kPhSeg, w, tagf(loc, tag), tagi(lastid, tag));
+    }
+    gather(s, rs, kPhSeg, S, tag);
+    float sum2 = 0.0f, before = 0.0f;
+    for (int v = 0; v < S; v++) {
+        if (v == w) before = sum2;
+        sum2 += s.pa[v];
+    }
+    // Every segment at or past the crossing scans itself; the smallest id found
+    // wins.  (A crossing that rounding pushes past a segment's end is then
+    // taken by the next segment's first id with mass; past the row's end, by
+    // the last id with mass, as pick_by_mass does.)
+    const float cum0 = before / sum2;
+    const float mine = s.pa[w] / sum2;
+    int first = INT_MAX;
+    if (r <= cum0 + mine || w == S - 1) first = draw_scan_from(s, st, sum2, r, cum0);
+    publish(rs, kPhDone, w, tagi(first, tag), tagi(0, tag));
+    if (w != 0) return;
+    // s.qb still holds every segment's last id with mass (gathered above)
+    int lastg = -1;
+    for (int v = 0; v < S; v++) lastg = max(lastg, s.qb[v]);
+    __syncthreads();
+    gather(s, rs, kPhDone, S, tag);
+    if (tid == 0) {
+        int pick = INT_MAX;
+        for (int v = 0; v < S; v++) pick = min(pick, s.qa[v]);
+        *o = static_cast<uint32_t>(pick != INT_MAX ? pick : (lastg >= 0 ? lastg : 0));
+    }
+    finish();
+}
+
+template <int ITEMS>
+int launch_split(fh_ctx* ctx, size_t rows, int S, const float* logits, const Params& P, const uint32_t* recent,
+                 const uint32_t* offsets, const uint64_t* draws, uint32_t* out, void* sync, float* pbuf) {
+    hipLaunchKernelGGL(k_sample_split<ITEMS>, dim3(static_cast<unsigned>(rows * S)), dim3(kT), 0, ctx->stream,
+                       logits, P, recent, offsets, draws, out, static_cast<RowSync*>(sync), pbuf, S);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
 template <int ITEMS>
 int launch_regs(fh_ctx* ctx, size_t rows, const float* logits, const Params& P, const uint32_t* recent,
                 const uint32_t* offsets, const uint64_t* draws, uint32_t* out) {
@@ -882,7 +1476,32 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
     P.pen = p->repetition_penalty;
     P.kind = kind;
     P.n = static_cast<int>(vocab);
+    // Split rows over S workgroups while rows * S fits one workgroup per CU
+    // (the kernel's LDS allows one per CU, so all of a row's workgroups are
+    // resident together): the fewest ids per thread that fits, for rows of at
+    // least 8192 ids.
     const size_t items = (vocab + kT - 1) / kT;
+    if (vocab >= 8192 && rows <= 128) {
+        static const int kOpts[] = {4, 8, 16, 32};
+        for (int it : kOpts) {
+            const size_t S = (vocab + static_cast<size_t>(kT) * it - 1) / (static_cast<size_t>(kT) * it);
+            if (S < 2 || rows * S > static_cast<size_t>(ctx->num_cus) || S > static_cast<size_t>(kSMax)) continue;
+            void* sync = nullptr;
+            int rc = fh_sync_area(ctx, rows * sizeof(RowSync), &sync);
+            if (rc) return rc;
+            void* ws = nullptr;
+            rc = fh_workspace(ctx, rows * vocab * sizeof(float), &ws);
+            if (rc) return rc;
+            float* pbuf = static_cast<float*>(ws);
+            const int s32 = static_cast<int>(S);
+            switch (it) {
+                case 4: return launch_split<4>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
+                case 8: return launch_split<8>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
+                case 16: return launch_split<16>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
+                default: return launch_split<32>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
+            }
+        }
+    }
     if (items <= 1) return launch_regs<1>(ctx, rows, logits, P, recent, offsets, draws, out);
     if (items <= 4) return launch_regs<4>(ctx, rows, logits, P, recent, offsets, draws, out);
     if (items <= 16) return launch_regs<16>(ctx, rows, logits, P, recent, offsets, draws, out);

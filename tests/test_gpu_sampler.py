@@ -185,3 +185,50 @@ def test_sampler_errors(fh):
                                [[1] * 16385])
     with pytest.raises(ferrum_hip.FerrumHipError, match="draws is NULL"):
         ferrum_hip.sample_rows(fh, np.zeros((1, 10), np.float32), ferrum_hip.SamplingParams(0.5))
+
+
+def test_split_rows_replay_in_a_graph(fh, orc):
+    """The multi-workgroup sampler keeps per-row barrier state on the device and
+    zeroes it when a row finishes, so back-to-back launches and HIP graph
+    replays must give the same ids as the first eager call."""
+    import torch
+
+    import ferrum_hip
+
+    rows, vocab = 3, 50257
+    lg = normal_logits(rows, vocab, 31)
+    rng = np.random.default_rng(2)
+    recents = [list(rng.integers(0, vocab, size=128)) for _ in range(rows)]
+    flat, off = ferrum_hip._recent_lists(recents, rows)
+    draws = rng.integers(0, 2**63, size=rows, dtype=np.uint64)
+    cases = [dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1), dict(temperature=0.0),
+             dict(temperature=0.9), dict(temperature=1.0, top_p=0.5)]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        d_lg = torch.from_numpy(lg).cuda()
+        d_rec = torch.from_numpy(flat.astype(np.int32)).cuda()
+        d_off = torch.from_numpy(off.astype(np.int32)).cuda()
+        d_dr = torch.from_numpy(draws.view(np.int64)).cuda()
+        d_out = torch.zeros(rows, dtype=torch.int32, device="cuda")
+        for kind in (ferrum_hip.LOGITS_RAW, ferrum_hip.LOGITS_GPT2_SOFTMAX):
+            for kw in cases:
+                params = ferrum_hip.SamplingParams(**kw)
+                want = ferrum_hip.sample_rows(fh, lg, params, recents, draws, kind)
+                fh.set_stream(s.cuda_stream)
+                try:
+                    ferrum_hip.sample_rows_async(fh, d_lg, rows, vocab, params, d_rec, d_off, d_dr, d_out, kind)
+                    s.synchronize()
+                    assert np.array_equal(d_out.cpu().numpy().astype(np.uint32), want), (kind, kw)
+                    g = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(g, stream=s):
+                        fh.set_stream(torch.cuda.current_stream().cuda_stream)
+                        ferrum_hip.sample_rows_async(fh, d_lg, rows, vocab, params, d_rec, d_off, d_dr, d_out, kind)
+                    fh.set_stream(s.cuda_stream)
+                    for rep in range(4):
+                        d_out.zero_()
+                        g.replay()
+                        s.synchronize()
+                        assert np.array_equal(d_out.cpu().numpy().astype(np.uint32), want), (kind, kw, rep)
+                        ferrum_hip.sample_rows(fh, lg, params, recents, draws, kind)  # eager work between replays
+                finally:
+                    fh.set_stream(None)
