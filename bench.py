@@ -45,8 +45,23 @@ HBM_PEAK_GBS = 8000.0
 SAMPLER = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
 
 
+COPY_BYTES = 256 << 20
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q8_0_lm_head_pmc.json")
+
+
 def q8_bytes(n, k):
     return n * k // 32 * 34
+
+
+def measured_traffic():
+    """HBM bytes per lm_head GEMV launch from the committed counter runs
+    (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size); None when
+    that summary is absent."""
+    try:
+        with open(PMC_SUMMARY) as f:
+            return json.load(f)["traffic_bytes_per_launch"]
+    except (OSError, KeyError, ValueError):
+        return None
 
 
 def make_weight(ctx, fh, torch, n, k, gen):
@@ -193,11 +208,18 @@ def main():
     head_bytes = q8_bytes(V, D) + 4 * D + 4 * V
     achieved = head_bytes / (head_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "k_gemv_w8a32<16,4,1,nobias> (lm_head 50257x768, Q8_0, m=1)",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+                "kernel": "k_gemv_w8a32<16,3,1,4,false> (lm_head 50257x768, Q8_0, m=1)",
                 "avg_launch_us": round(head_us, 3), "bytes_per_launch": head_bytes}
     if args.leg == "head":
-        print(json.dumps({"leg": "head", "roofline": roofline}))
+        # A plain device copy of known size, for scaling the PMC byte counters
+        # (FETCH_SIZE / WRITE_SIZE) of the same run.
+        src = torch.empty(COPY_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"leg": "head", "roofline": roofline, "copy_bytes_per_launch": COPY_BYTES}))
         return
 
     # ---- CPU baseline: the oracle on this host, one core ----------------------------
