@@ -1,0 +1,309 @@
+// fh_gemm.hip — Q8_0 W8A32 linear for m >= 3 on the gfx950 matrix cores.
+//
+//   y[i, j] = sum_b d_jb * sum_{p in block b} x[i, p] * q[j, p]  (+ bias[j])
+//
+// is ferrum_core's ops::linear_forward on the f32 expansion W = f16(d) * q of a
+// GGUF Q8_0 tensor (ops.rs:233-256, gguf/dequant.rs:37-49).  The quants are
+// integers in [-127, 127], exact in f16, so the inner block sums run on
+// v_mfma_f32_32x32x16_f16 once the activations are in f16 too.  An f32
+// activation keeps its 24-bit significand as two f16 terms:
+//
+//   x[i, p] * 2^e_i = h + l,   h = f16(x * 2^e_i),   l = f16(x * 2^e_i - h)
+//
+// with one power-of-two scale per row (the row's largest finite |x| lands in
+// [2^14, 2^15), so neither term overflows and l stays normal for every value
+// that matters).  h + l carries 22 significant bits; the products h*q and l*q
+// are exact and the matrix core sums them in f32.  Each Q8_0 block's partial
+// sum (four MFMAs: h and l, two K halves) is scaled by the block's weight
+// scale with one FMA per output into the running f32 sum; the row scale 2^-e_i
+// is applied exactly at the end, and the bias is added last, as the reference
+// does.  Non-finite activations keep l = 0, so inf and NaN propagate as they
+// do in the reference's products (inf * 0 = NaN, inf * q = inf).
+//
+// Work split: k_split_rows writes the h/l terms once per call into a panel
+// laid out for the GEMM's staging ([row tile][block][row][h 32 | l 32], 128 B
+// per row and block, so a stage is one contiguous read).  k_gemm_mfma stages
+// KW Q8_0 blocks of the activation panel and of the weight rows per step into
+// LDS (double buffered, one barrier per step), converting the int8 quants to
+// f16 on the way in; each wave owns TM x TN 32x32 output tiles, and with
+// KW > 1 the waves split the K blocks and add their sums in wave order (a
+// fixed order: results do not depend on timing).
+#include "fh_internal.hpp"
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+
+// Staged rows, in f16 elements.  Activations: 32 h, 32 l, 8 pad (144 B);
+// weights: 32 quants, 8 pad (80 B).  Both strides keep the 16 lanes of a
+// ds_read_b128 phase (16 consecutive rows) on disjoint banks.
+constexpr int kArow = 72;
+constexpr int kBrow = 40;
+
+// Four int8 quants to four f16, exactly: bias the bytes to unsigned, place each
+// in the mantissa of 1024.0 (0x6400 | u == 1024 + u), subtract 1152.
+__device__ __forceinline__ uint2 quants_to_f16(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);
+    const h2 off = {static_cast<_Float16>(1152.0f), static_cast<_Float16>(1152.0f)};
+    const h2 a = __builtin_bit_cast(h2, lo) - off;
+    const h2 b = __builtin_bit_cast(h2, hi) - off;
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+
+__device__ __forceinline__ bool finite(float v) { return (__builtin_bit_cast(uint32_t, v) & 0x7F800000u) != 0x7F800000u; }
+
+}  // namespace
+
+// One wave per activation row (rows m .. m_pad - 1 are written as zeros).
+__global__ void __launch_bounds__(256)
+    k_split_rows(const float* __restrict__ x, int m, int m_pad, int k, int bm, uint4* __restrict__ panel,
+                 float* __restrict__ xinv) {
+    const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= m_pad) return;
+    const int kb = k >> 5, chunks = k >> 3;
+    const bool live = row < m;
+    const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(live ? row : 0) * k);
+    float mx = 0.0f;
+    if (live) {
+        for (int c = lane; c < chunks; c += 64) {
+            const float4 a = xr[2 * c], b = xr[2 * c + 1];
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int t = 0; t < 8; t++)
+                if (finite(v[t])) mx = fmaxf(mx, fabsf(v[t]));
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    // mx = f * 2^E with f in [0.5, 1): scale by 2^(15 - E).  A subnormal
+    // maximum reads E = -126 and clamps like any tiny row.
+    int e = 0;
+    if (mx > 0.0f) {
+        const int E = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 126;
+        e = min(max(15 - E, -126), 126);
+    }
+    const float sc = __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23);
+    if (lane == 0) xinv[row] = __builtin_bit_cast(float, static_cast<uint32_t>(127 - e) << 23);
+    uint4* dst_row = panel + (static_cast<size_t>(row / bm) * kb * bm + row % bm) * 8;
+    for (int c = lane; c < chunks; c += 64) {
+        float v[8] = {};
+        if (live) {
+            const float4 a = xr[2 * c], b = xr[2 * c + 1];
+            v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+            v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+        }
+        h8 hv, lv;
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const float s = v[t] * sc;
+            const _Float16 h = static_cast<_Float16>(s);
+            hv[t] = h;
+            lv[t] = finite(s) ? static_cast<_Float16>(s - static_cast<float>(h)) : static_cast<_Float16>(0.0f);
+        }
+        uint4* dst = dst_row + static_cast<size_t>(c >> 2) * bm * 8;
+        dst[c & 3] = __builtin_bit_cast(uint4, hv);
+        dst[4 + (c & 3)] = __builtin_bit_cast(uint4, lv);
+    }
+}
+
+// CTA tile BM x BN; 4 waves = WM x WN output sub-tiles x KW K-slices.
+template <int BM, int BN, int WM, int WN, int KW>
+__global__ void __launch_bounds__(256)
+    k_gemm_mfma(const uint4* __restrict__ panel, const float* __restrict__ xinv, const int8_t* __restrict__ qs,
+                const uint16_t* __restrict__ dsc, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
+                int k, int tiles_n) {
+    static_assert(WM * WN * KW == 4, "four waves");
+    constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
+    static_assert(TM >= 1 && TN >= 1 && TM * 32 * WM == BM && TN * 32 * WN == BN, "tile shape");
+    constexpr int A_BYTES = KW * BM * kArow * 2, B_BYTES = KW * BN * kBrow * 2, S_BYTES = KW * BN * 4;
+    constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
+    // 16-byte pieces per thread (the last weight round may leave threads idle)
+    constexpr int AP = KW * BM * 8 / 256, BPN = KW * BN * 2, BP = (BPN + 255) / 256;
+    static_assert(AP * 256 == KW * BM * 8 && KW * BN <= 256, "staging split");
+    constexpr int RED = (KW - 1) * WM * WN * TM * TN * 16 * 64 * 4;
+    static_assert(RED <= 2 * STAGE, "reduction fits the stage buffers");
+    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int kw = wave / (WM * WN), wm = (wave % (WM * WN)) / WN, wn = wave % WN;
+    const int tile_m = static_cast<int>(blockIdx.x) / tiles_n, tile_n = static_cast<int>(blockIdx.x) % tiles_n;
+    const int j0 = tile_n * BN;
+    const int kb = k >> 5, steps = (kb + KW - 1) / KW;
+    const uint4* pan = panel + static_cast<size_t>(tile_m) * kb * BM * 8;
+
+    uint4 ra[AP], rb[BP];
+    float rs = 0.0f;
+    auto load = [&](int st) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < AP; p++) {
+            const int piece = tid + 256 * p, blk = piece / (BM * 8), rem = piece % (BM * 8);
+            const int b = st * KW + blk;
+            ra[p] = b < kb ? pan[static_cast<size_t>(b) * BM * 8 + rem] : make_uint4(0, 0, 0, 0);
+        }
+#pragma unroll
+        for (int p = 0; p < BP; p++) {
+            const int piece = tid + 256 * p, blk = piece / (BN * 2), rem = piece % (BN * 2);
+            const int b = st * KW + blk, j = j0 + rem / 2;
+            rb[p] = (piece < BPN && b < kb && j < n)
+                        ? *reinterpret_cast<const uint4*>(qs + static_cast<size_t>(j) * k + b * 32 + (rem & 1) * 16)
+                        : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < KW * BN) {
+            const int b = st * KW + tid / BN, j = j0 + tid % BN;
+            rs = (b < kb && j < n) ? fh_h2f(dsc[static_cast<size_t>(j) * kb + b]) : 0.0f;
+        }
+    };
+    auto store = [&](int buf) __attribute__((always_inline)) {
+        char* st = lds + buf * STAGE;
+#pragma unroll
+        for (int p = 0; p < AP; p++) {
+            const int piece = tid + 256 * p, blk = piece / (BM * 8), rem = piece % (BM * 8);
+            *reinterpret_cast<uint4*>(st + ((blk * BM + rem / 8) * kArow) * 2 + (rem % 8) * 16) = ra[p];
+        }
+#pragma unroll
+        for (int p = 0; p < BP; p++) {
+            const int piece = tid + 256 * p, blk = piece / (BN * 2), rem = piece % (BN * 2);
+            if (BPN % 256 != 0 && piece >= BPN) break;
+            char* dst = st + A_BYTES + ((blk * BN + rem / 2) * kBrow) * 2 + (rem & 1) * 32;
+            const uint2 a = quants_to_f16(rb[p].x), b = quants_to_f16(rb[p].y);
+            const uint2 c = quants_to_f16(rb[p].z), d = quants_to_f16(rb[p].w);
+            *reinterpret_cast<uint4*>(dst) = make_uint4(a.x, a.y, b.x, b.y);
+            *reinterpret_cast<uint4*>(dst + 16) = make_uint4(c.x, c.y, d.x, d.y);
+        }
+        if (tid < KW * BN) reinterpret_cast<float*>(st + A_BYTES + B_BYTES)[tid] = rs;
+    };
+
+    f16x acc[TM][TN];
+#pragma unroll
+    for (int r = 0; r < TM; r++)
+#pragma unroll
+        for (int c = 0; c < TN; c++) acc[r][c] = f16x{};
+    const f16x zero = {};
+
+    load(0);
+    store(0);
+    __syncthreads();
+    const int arow = lane % 32, koff = (lane / 32) * 8;
+    for (int st = 0; st < steps; st++) {
+        const int buf = st & 1;
+        if (st + 1 < steps) load(st + 1);
+        const char* sb = lds + buf * STAGE;
+        const _Float16* As = reinterpret_cast<const _Float16*>(sb) + kw * BM * kArow;
+        const _Float16* Bs = reinterpret_cast<const _Float16*>(sb + A_BYTES) + kw * BN * kBrow;
+        const float* Ss = reinterpret_cast<const float*>(sb + A_BYTES + B_BYTES) + kw * BN;
+        h8 ah[TM][2], al[TM][2], bq[TN][2];
+        float dw[TN];
+#pragma unroll
+        for (int r = 0; r < TM; r++) {
+            const _Float16* a = As + ((wm * TM + r) * 32 + arow) * kArow + koff;
+            ah[r][0] = *reinterpret_cast<const h8*>(a);
+            ah[r][1] = *reinterpret_cast<const h8*>(a + 16);
+            al[r][0] = *reinterpret_cast<const h8*>(a + 32);
+            al[r][1] = *reinterpret_cast<const h8*>(a + 48);
+        }
+#pragma unroll
+        for (int c = 0; c < TN; c++) {
+            const int col = (wn * TN + c) * 32 + arow;
+            const _Float16* b = Bs + col * kBrow + koff;
+            bq[c][0] = *reinterpret_cast<const h8*>(b);
+            bq[c][1] = *reinterpret_cast<const h8*>(b + 16);
+            dw[c] = Ss[col];
+        }
+#pragma unroll
+        for (int r = 0; r < TM; r++)
+#pragma unroll
+            for (int c = 0; c < TN; c++) {
+                f16x p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[r][0], bq[c][0], zero, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[r][0], bq[c][0], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[r][1], bq[c][1], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[r][1], bq[c][1], p, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) acc[r][c][v] = fmaf(dw[c], p[v], acc[r][c][v]);
+            }
+        if (st + 1 < steps) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    if (KW > 1) {
+        // K-slices 1..KW-1 hand their sums to slice 0 through LDS; slice 0 adds
+        // them in slice order.
+        float* red = reinterpret_cast<float*>(lds);
+        const int sub = wave % (WM * WN);
+        if (kw > 0) {
+#pragma unroll
+            for (int r = 0; r < TM; r++)
+#pragma unroll
+                for (int c = 0; c < TN; c++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        red[((((kw - 1) * WM * WN + sub) * TM + r) * TN + c) * 1024 + v * 64 + lane] = acc[r][c][v];
+        }
+        __syncthreads();
+        if (kw > 0) return;
+#pragma unroll
+        for (int s = 1; s < KW; s++)
+#pragma unroll
+            for (int r = 0; r < TM; r++)
+#pragma unroll
+                for (int c = 0; c < TN; c++)
+#pragma unroll
+                    for (int v = 0; v < 16; v++)
+                        acc[r][c][v] += red[((((s - 1) * WM * WN + sub) * TM + r) * TN + c) * 1024 + v * 64 + lane];
+    }
+
+    const int i0 = tile_m * BM;
+#pragma unroll
+    for (int c = 0; c < TN; c++) {
+        const int j = j0 + (wn * TN + c) * 32 + arow;
+        if (j >= n) continue;
+        const float bj = bias ? bias[j] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < TM; r++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int i = i0 + (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4);
+                if (i >= m) continue;
+                const float s = acc[r][c][v] * xinv[i];
+                y[static_cast<size_t>(i) * n + j] = bias ? s + bj : s;
+            }
+    }
+}
+
+namespace {
+
+template <int BM, int BN, int WM, int WN, int KW>
+int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    const size_t m_pad = (m + BM - 1) / BM * BM;
+    const size_t pbytes = fh_align256(m_pad * w->k * 4), ibytes = fh_align256(m_pad * 4);
+    void* ws = nullptr;
+    int rc = fh_workspace(ctx, pbytes + ibytes, &ws);
+    if (rc) return rc;
+    uint4* panel = static_cast<uint4*>(ws);
+    float* xinv = reinterpret_cast<float*>(static_cast<char*>(ws) + pbytes);
+    hipLaunchKernelGGL(k_split_rows, dim3(static_cast<unsigned>((m_pad + 3) / 4)), dim3(256), 0, ctx->stream, x,
+                       static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(w->k), BM, panel, xinv);
+    FH_HIP(ctx, hipGetLastError());
+    const size_t tiles_n = (w->n + BN - 1) / BN, tiles = tiles_n * (m_pad / BM);
+    if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
+    hipLaunchKernelGGL((k_gemm_mfma<BM, BN, WM, WN, KW>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0,
+                       ctx->stream, panel, xinv, w->qs, w->d, bias, y, static_cast<int>(m), static_cast<int>(w->n),
+                       static_cast<int>(w->k), static_cast<int>(tiles_n));
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+}  // namespace
+
+// Tile choice: the 128 x 128 tile once it still yields two tiles per CU,
+// else 64 x 64, else 32 x 32 outputs with the four waves splitting K.
+int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    const size_t cus = static_cast<size_t>(ctx->num_cus);
+    if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) return launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
+    if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) return launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
+    return launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);
+}

@@ -14,8 +14,8 @@
 //                the activation chunks a lane needs stay in its registers for
 //                every row it visits.  G lanes share a row and finish it with a
 //                butterfly shuffle reduction; 64/G rows per wave per step.
-//  k_gemm_w8a32  m >= 3.  LDS-tiled f32 FMA (32 x 64 outputs per block,
-//                K step = one Q8_0 block), weights dequantised once per tile.
+//  m >= 3 (and rows too long for the GEMV) go to the matrix-core GEMM in
+//                fh_gemm.hip.
 //  k_linear_w8a8 llama.cpp numerics: x is Q8_0-encoded per 32 (bit-exact
 //                q8_0_block), exact int32 block dots with sdot4, then
 //                sum_b f32(dot_b) * (d_w * d_x) + b.
@@ -157,65 +157,6 @@ __global__ void __launch_bounds__(64 * kWaves)
     }
 }
 
-// ---- m >= 3: LDS-tiled FMA GEMM ----------------------------------------------
-constexpr int BM = 32, BN = 64, BK = 32;
-
-__global__ void __launch_bounds__(256)
-    k_gemm_w8a32(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const float* __restrict__ x,
-                 const float* __restrict__ bias, float* __restrict__ y, int m, int n, int k) {
-    __shared__ float xs[BM][BK + 1];
-    __shared__ float ws[BK][BN + 4];
-    const int tid = threadIdx.x;
-    const int i0 = blockIdx.y * BM, j0 = blockIdx.x * BN;
-    const int tm = tid / 16, tn = tid % 16;  // 16 x 16 threads, 2 x 4 outputs each
-    const int kb = k >> 5;
-    float acc[2][4] = {};
-    for (int b = 0; b < kb; b++) {
-        // x tile: 32 x 32 floats, 4 per thread
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const int e = tid + r * 256, ii = e / BK, kk = e % BK;
-            xs[ii][kk] = (i0 + ii < m) ? x[static_cast<size_t>(i0 + ii) * k + b * BK + kk] : 0.0f;
-        }
-        // w tile: 64 rows x 32 quants, 8 per thread, dequantised (exact)
-        {
-            const int jj = tid / 4, part = tid % 4;
-            const int j = j0 + jj;
-            if (j < n) {
-                const uint2 q = *reinterpret_cast<const uint2*>(qs + static_cast<size_t>(j) * k + b * BK + part * 8);
-                const float d = fh_h2f(dsc[static_cast<size_t>(j) * kb + b]);
-#pragma unroll
-                for (int t = 0; t < 8; t++) ws[part * 8 + t][jj] = d * sbyte(t < 4 ? q.x : q.y, t & 3);
-            } else {
-#pragma unroll
-                for (int t = 0; t < 8; t++) ws[part * 8 + t][jj] = 0.0f;
-            }
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < BK; kk++) {
-            const float a0 = xs[tm * 2][kk], a1 = xs[tm * 2 + 1][kk];
-#pragma unroll
-            for (int c = 0; c < 4; c++) {
-                const float w = ws[kk][tn * 4 + c];
-                acc[0][c] = fmaf(a0, w, acc[0][c]);
-                acc[1][c] = fmaf(a1, w, acc[1][c]);
-            }
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int r = 0; r < 2; r++) {
-        const int i = i0 + tm * 2 + r;
-        if (i >= m) continue;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-            const int j = j0 + tn * 4 + c;
-            if (j < n) y[static_cast<size_t>(i) * n + j] = bias ? acc[r][c] + bias[j] : acc[r][c];
-        }
-    }
-}
-
 // ---- W8A8 ------------------------------------------------------------------------
 // One lane per Q8_0 block of a (activation row, weight row) pair; G lanes per
 // pair reduce with a butterfly.  Block dots are exact (sdot4 on int8).
@@ -333,12 +274,7 @@ int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t
         int rc = m == 1 ? dispatch_gemv<1>(ctx, w, x, bias, y) : dispatch_gemv<2>(ctx, w, x, bias, y);
         if (rc >= 0) return rc;
     }
-    dim3 grid(static_cast<unsigned>((w->n + BN - 1) / BN), static_cast<unsigned>((m + BM - 1) / BM));
-    if (grid.y > 65535) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: m above 2,097,120");
-    hipLaunchKernelGGL(k_gemm_w8a32, grid, dim3(256), 0, ctx->stream, w->qs, w->d, x, bias, y, static_cast<int>(m),
-                       static_cast<int>(w->n), static_cast<int>(w->k));
-    FH_HIP(ctx, hipGetLastError());
-    return FH_OK;
+    return fh_launch_gemm_w8a32(ctx, w, x, m, bias, y);
 }
 
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {

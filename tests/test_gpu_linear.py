@@ -142,6 +142,93 @@ def test_ragged_shapes_match_oracle(fh, orc, m, n, k):
     assert_close(got, orc.q8_0_linear(x, raw, n, b), term_mass(orc, x, raw, n, k))
 
 
+# ---- m >= 3: the matrix-core GEMM ---------------------------------------------------
+# Tile edges of all three tilings (32 x 32 with the waves splitting K, 64 x 64,
+# 128 x 128), K-block counts that do not fill the last K step, and m, n one off
+# a tile boundary.
+
+@pytest.mark.parametrize("m,n,k", [(3, 33, 32), (31, 65, 96), (33, 31, 160), (95, 130, 64), (129, 257, 224),
+                                   (257, 97, 1024), (64, 1024, 768), (600, 1000, 128)])
+def test_gemm_tile_edges_match_oracle(fh, orc, m, n, k):
+    import ferrum_hip
+
+    seed = 3 * m + 5 * n + k
+    raw = weight(orc, n, k, seed, std=0.3)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x, b = acts(m, k, seed), bias_for(n, seed)
+    got = ferrum_hip.linear_forward(fh, x, w, b)
+    got_nb = ferrum_hip.matmul(fh, x, w)
+    w.free()
+    mass = term_mass(orc, x, raw, n, k)
+    assert_close(got, orc.q8_0_linear(x, raw, n, b), mass)
+    assert_close(got_nb, orc.q8_0_linear(x, raw, n, None), mass)
+    assert_as_accurate(got, orc.q8_0_linear(x, raw, n, b), exact_linear(orc, x, raw, n, k, b))
+
+
+def test_gemm_large_tiles_against_exact_product(fh, orc):
+    """A shape that takes the 128 x 128 tiling on 256 CUs (>= 512 tiles),
+    against the float64 product of the same weights at the same tolerance."""
+    import ferrum_hip
+
+    m, n, k = 2048, 4096, 256
+    raw = weight(orc, n, k, 41)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x, b = acts(m, k, 41), bias_for(n, 41)
+    got = ferrum_hip.linear_forward(fh, x, w, b)
+    w.free()
+    assert_close(got, exact_linear(orc, x, raw, n, k, b), term_mass(orc, x, raw, n, k))
+
+
+def test_gemm_rows_of_any_magnitude(fh, orc):
+    """Each row carries its own power-of-two scale: rows near the f32 range
+    ends, a row with one large outlier, and an all-zero row."""
+    import ferrum_hip
+
+    n, k = 70, 256
+    raw = weight(orc, n, k, 8)
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((8, k)).astype(np.float32)
+    x[0] *= np.float32(1e-30)
+    x[1] *= np.float32(1e30)
+    x[2] *= np.float32(1e-40)           # subnormal activations
+    x[3, 17] = np.float32(3e4)          # one outlier next to O(1) values
+    x[4] = 0.0
+    x[5] *= np.float32(65504.0 * 4)     # beyond the f16 range
+    x[6] *= np.float32(1e-6)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    got = ferrum_hip.linear_forward(fh, x, w, None)
+    w.free()
+    ref = orc.q8_0_linear(x, raw, n, None)
+    mass = term_mass(orc, x, raw, n, k)
+    ok = np.ones(8, bool)
+    ok[2] = False                       # checked separately below
+    assert_close(got[ok], ref[ok], mass[ok])
+    # Subnormal inputs: f16 terms lose the bits below 2^-149 * 2^126; the
+    # error stays below 1e-5 of the row's own term mass plus one f32 subnormal step.
+    assert np.all(np.abs(got[2].astype(np.float64) - ref[2]) <= 1e-5 * mass[2] + 1.5e-45 * k)
+    assert np.all(got[4] == 0.0)
+
+
+def test_gemm_propagates_inf_and_nan_like_the_reference(fh, orc):
+    import ferrum_hip
+
+    n, k = 40, 128
+    raw = weight(orc, n, k, 12)
+    x = acts(5, k, 12)
+    x[0, 3] = np.inf
+    x[1, 100] = -np.inf
+    x[2, 5] = np.nan
+    x[3, 0], x[3, 64] = np.inf, -np.inf
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    got = ferrum_hip.linear_forward(fh, x, w, bias_for(n, 12))
+    w.free()
+    ref = orc.q8_0_linear(x, raw, n, bias_for(n, 12))
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)) and np.array_equal(np.isneginf(got), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert_close(got[fin], ref[fin], term_mass(orc, x, raw, n, k)[fin])
+
+
 def test_expanded_weight_path_agrees(fh, orc):
     """The GPU result against ops::linear_forward on the f32 expansion the
     reference's loader builds (dequant + transpose), not only the row form."""
