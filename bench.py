@@ -45,6 +45,13 @@ HBM_PEAK_GBS = 8000.0
 SAMPLER = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
 
 
+B32 = 32
+# GPT-2-medium: 24 layers, d 1024, MLP 4096; prefill
+# of 32 prompts x 512 tokens = 16,384 activation rows per linear.
+MED_D, MED_L, MED_FFN, MED_M = 1024, 24, 4096, 32 * 512
+MED_SHAPES = [(3 * MED_D, MED_D), (MED_D, MED_D), (MED_FFN, MED_D), (MED_D, MED_FFN)]
+F16_DENSE_TFLOPS, I8_DENSE_TOPS = 2500.0, 5000.0
+
 COPY_BYTES = 256 << 20
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q8_0_lm_head_pmc.json")
 
@@ -89,8 +96,10 @@ def main():
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--leg", choices=["all", "head"], default="all",
-                    help="'head': only the lm_head GEMV roofline leg (for counter runs)")
+    ap.add_argument("--leg", choices=["all", "head", "prefill"], default="all",
+                    help="'head': only the lm_head GEMV roofline leg (for counter runs); "
+                         "'prefill': only the GPT-2-medium prefill GEMMs")
+    ap.add_argument("--prefill-steps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -187,8 +196,51 @@ def main():
         step_bytes = sum(q8_bytes(n, k) for (n, k) in LAYER_SHAPES) * L + q8_bytes(V, D)
         result.update(ms_per_step=ms_step, wall_ms_per_step=wall_step, ms_per_step_mall=ms_mall,
                       step_weight_bytes=step_bytes)
-        del graphs, reps
+        del graphs
         torch.cuda.synchronize()
+
+        # ---- batch 32: the same step for 32 sequences (BASELINE's b32 decode) ----
+        B = B32
+        xb_d = torch.randn((B, D), generator=gen, device=dev)
+        xb_f = torch.randn((B, FFN), generator=gen, device=dev)
+        yb = torch.empty((B, max(3 * D, FFN)), device=dev)
+        logits_b = torch.empty((B, V), device=dev)
+        rec_b = torch.from_numpy(np.random.default_rng(4).integers(0, V, size=B * N_RECENT).astype(np.uint32)).to(dev)
+        off_b = torch.arange(0, (B + 1) * N_RECENT, N_RECENT, dtype=torch.int32, device=dev)
+        draws_b = torch.from_numpy(np.random.default_rng(5).integers(0, 2**63, size=B, dtype=np.int64)).to(dev)
+        out_b = torch.zeros(B, dtype=torch.int32, device=dev)
+
+        def step_b(rep):
+            for li in range(L):
+                for (n, k), w in zip(LAYER_SHAPES, rep.layers[li]):
+                    fh.linear_forward_async(ctx, w, xb_d if k == D else xb_f, B, k, biases[n], n, yb)
+            fh.linear_forward_async(ctx, rep.head, xb_d, B, D, None, 0, logits_b)
+            fh.sample_rows_async(ctx, logits_b, B, V, params, rec_b, off_b, draws_b, out_b, fh.LOGITS_GPT2_SOFTMAX)
+
+        for r in reps:
+            step_b(r)
+        torch.cuda.synchronize()
+        graphs_b = []
+        for r in reps:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+                step_b(r)
+            ctx.set_stream(stream.cuda_stream)
+            graphs_b.append(g)
+        torch.cuda.synchronize()
+        ms_b, _ = timed(graphs_b, max(args.steps // 4, 10), args.warmup)
+        result["b32"] = {"tok_s": round(B * 1000.0 / ms_b, 1), "ms_per_step": round(ms_b, 5), "batch": B,
+                         "sampler_rows": B, "residency": f"hbm-forced ({args.replicas} weight replicas)"}
+        del graphs_b, reps
+        torch.cuda.synchronize()
+
+    if args.leg in ("all", "prefill"):
+        result["prefill"] = prefill_leg(ctx, fh, torch, gen, dev, args.prefill_steps)
+
+    if args.leg == "prefill":
+        print(json.dumps({"leg": "prefill", "prefill": result["prefill"]}))
+        return
 
     # ---- roofline leg: lm_head GEMV, back-to-back, HBM-forced ----------------------
     n_head_rep = 32  # 32 x 41 MB = 1.3 GB, five times the MALL
@@ -251,8 +303,52 @@ def main():
         "step_weight_GBps": round(result["step_weight_bytes"] / (ms * 1e-3) / 1e9, 1),
         "sampler_us_per_row": result["sampler_us_per_row"],
         "wall_ms_per_step": round(result["wall_ms_per_step"], 5),
+        "b32": result["b32"],
+        "prefill": result["prefill"],
     }
     print(json.dumps(line))
+
+
+def prefill_leg(ctx, fh, torch, gen, dev, steps):
+    """GPT-2-medium prefill linears: 24 x [QKV, attn-out, up, down] at m = 16,384
+    (32 prompts x 512 tokens), W8A32 on the f16 matrix cores.  One step = the 96
+    GEMMs (bias added), captured into one graph; FLOPs = 2 m n k per GEMM."""
+    layers = [[make_weight(ctx, fh, torch, n, k, gen) for (n, k) in MED_SHAPES] for _ in range(MED_L)]
+    biases = {n: torch.randn(n, generator=gen, device=dev) * 0.1 for n in {s[0] for s in MED_SHAPES}}
+    x = {k: torch.randn((MED_M, k), generator=gen, device=dev) for k in {s[1] for s in MED_SHAPES}}
+    y = torch.empty((MED_M, max(s[0] for s in MED_SHAPES)), device=dev)
+
+    def step():
+        for li in range(MED_L):
+            for (n, k), w in zip(MED_SHAPES, layers[li]):
+                fh.linear_forward_async(ctx, w, x[k], MED_M, k, biases[n], n, y)
+
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        step()
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    flops = sum(2.0 * MED_M * n * k for (n, k) in MED_SHAPES) * MED_L
+    tflops = flops / (ms * 1e-3) / 1e12
+    del g
+    for lw in layers:
+        for w in lw:
+            w.free()
+    return {"workload": "gpt2-medium prefill linears, 32 x 512 tokens (m = 16384), W8A32 f16-MFMA",
+            "ms": round(ms, 3), "tflops": round(tflops, 1),
+            "frac_f16_dense_peak": round(tflops / F16_DENSE_TFLOPS, 4),
+            "frac_i8_dense_peak": round(tflops / I8_DENSE_TOPS, 4)}
 
 
 def cpu_baseline(budget_s):

@@ -28,6 +28,12 @@ int fh_hip_fail(fh_ctx* ctx, hipError_t e, const char* what) {
 int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) {
     bytes = fh_align256(bytes ? bytes : 256);
     if (ctx->ws_bytes < bytes) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        FH_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
+        if (cs != hipStreamCaptureStatusNone)
+            return fh_fail(ctx, FH_ERR_INVALID,
+                           "the context workspace must grow, which cannot happen during graph capture: "
+                           "run the same call once outside capture first");
         if (ctx->ws) {
             // The previous workspace may still be read by queued kernels.
             FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
@@ -42,27 +48,37 @@ int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) {
     return FH_OK;
 }
 
-int fh_sync_area(fh_ctx* ctx, size_t bytes, void** out) {
+// Grow a zero-initialised area (kernels leave it zeroed again).  Growing
+// synchronises the stream and is refused under graph capture.
+static int zeroed_area(fh_ctx* ctx, void** area, size_t* area_bytes, size_t bytes, const char* who, void** out) {
     bytes = fh_align256(bytes ? bytes : 256);
-    if (ctx->sync_bytes < bytes) {
+    if (*area_bytes < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         FH_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
         if (cs != hipStreamCaptureStatusNone)
             return fh_fail(ctx, FH_ERR_INVALID,
-                           "the sampler's per-row state must grow, which cannot happen during graph capture: "
+                           std::string(who) + " must grow, which cannot happen during graph capture: "
                            "run the same call once outside capture first");
         FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
-        if (ctx->sync) {
-            FH_HIP(ctx, hipFree(ctx->sync));
-            ctx->sync = nullptr;
-            ctx->sync_bytes = 0;
+        if (*area) {
+            FH_HIP(ctx, hipFree(*area));
+            *area = nullptr;
+            *area_bytes = 0;
         }
-        FH_HIP(ctx, hipMalloc(&ctx->sync, bytes));
-        FH_HIP(ctx, hipMemset(ctx->sync, 0, bytes));
-        ctx->sync_bytes = bytes;
+        FH_HIP(ctx, hipMalloc(area, bytes));
+        FH_HIP(ctx, hipMemset(*area, 0, bytes));
+        *area_bytes = bytes;
     }
-    *out = ctx->sync;
+    *out = *area;
     return FH_OK;
+}
+
+int fh_sync_area(fh_ctx* ctx, size_t bytes, void** out) {
+    return zeroed_area(ctx, &ctx->sync, &ctx->sync_bytes, bytes, "the sampler's per-row state", out);
+}
+
+int fh_counter_area(fh_ctx* ctx, size_t bytes, void** out) {
+    return zeroed_area(ctx, &ctx->counters, &ctx->counters_bytes, bytes, "the GEMM's per-tile counters", out);
 }
 
 // Every entry point works on the context's device.
@@ -117,6 +133,7 @@ void fh_ctx_destroy(fh_ctx* ctx) {
     if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->sync) (void)hipFree(ctx->sync);
+    if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
 }

@@ -274,6 +274,236 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// ---- skinny m (batched decode): m <= 32 * MT ------------------------------------
+// Grid: 32-wide weight-row tiles x S splits of the Q8_0 blocks.  A workgroup's
+// waves divide its split's blocks and issue every load of a batch of up to BPW
+// blocks at once (weights straight into registers: each weight byte is used by
+// one workgroup).  Activations are split per (row, block) instead of per row,
+// so no pre-pass is needed: the two lanes holding a row's block agree on the
+// block's power-of-two scale through one lane swap, and the block partial is
+// unscaled exactly (t = P * 2^-e) before the weight-scale FMA.  Inside a block
+// the K order is permuted (lane half h holds elements 16h .. 16h + 15; MFMA 0
+// takes the first 8 of each half, MFMA 1 the rest) identically for activations
+// and weights, so every product still pairs x[i, p] with q[j, p].
+// Sums: over the waves in wave order (LDS), then over the splits in split
+// order by whichever workgroup of the tile finishes last (a counter per tile,
+// left at zero for the next launch) -- a fixed order either way.
+namespace {
+
+typedef float f2 __attribute__((ext_vector_type(2)));
+constexpr int kMaxSplits = 8;  // K splits of the skinny GEMM
+
+// 16 activations (one lane's half of a row's block) times 2^e as h + l; the
+// caller has handled blocks whose maximum is not finite (SAFE keeps l = 0 for
+// inf and NaN inputs).
+template <bool SAFE>
+__device__ __forceinline__ void split16(const float* v, float sc, h8& ah0, h8& ah1, h8& al0, h8& al1) {
+#pragma unroll
+    for (int q = 0; q < 16; q += 2) {
+        const f2 s = {v[q] * sc, v[q + 1] * sc};
+        const h2 h = __builtin_convertvector(s, h2);
+        f2 r = {s.x - static_cast<float>(h.x), s.y - static_cast<float>(h.y)};
+        if (SAFE) {
+            r.x = finite(s.x) ? r.x : 0.0f;
+            r.y = finite(s.y) ? r.y : 0.0f;
+        }
+        const h2 l = __builtin_convertvector(r, h2);
+        if (q < 8) {
+            ah0[q] = h.x; ah0[q + 1] = h.y; al0[q] = l.x; al0[q + 1] = l.y;
+        } else {
+            ah1[q - 8] = h.x; ah1[q - 7] = h.y; al1[q - 8] = l.x; al1[q - 7] = l.y;
+        }
+    }
+}
+
+__device__ __forceinline__ int block_exponent(float mx) {
+    if (!(mx > 0.0f)) return 0;
+    const int E = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 126;
+    return min(max(15 - E, -126), 126);
+}
+
+}  // namespace
+
+template <int MT, int NT, int BPW>
+__global__ void __launch_bounds__(512)
+    k_gemm_skinny(const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
+                  const float* __restrict__ bias, float* __restrict__ y, int m, int n, int k, int bps,
+                  float* __restrict__ part, unsigned* __restrict__ counters) {
+    constexpr int OUT = MT * NT * 1024;  // outputs of one workgroup
+    // [KW][OUT] wave sums, then [KW][MT][BPW][32] row scales
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    __shared__ int last;
+    float* sums = lds;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, kw = blockDim.x >> 6;
+    const int kb = k >> 5, half = lane >> 5, r32 = lane & 31;
+    const int tile = blockIdx.x, split = blockIdx.y, splits = gridDim.y;
+    const int b_begin = split * bps, b_end = min(kb, b_begin + bps);
+    const int8_t* wrow[NT];
+    const uint16_t* drow[NT];
+#pragma unroll
+    for (int c = 0; c < NT; c++) {
+        const int j = min((tile * NT + c) * 32 + r32, n - 1);
+        wrow[c] = qs + static_cast<size_t>(j) * k + half * 16;
+        drow[c] = dsc + static_cast<size_t>(j) * kb;
+    }
+    float* inv_lds = lds + kw * OUT + wave * (MT * BPW * 32);  // this wave's row scales
+    f16x acc[MT][NT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int c = 0; c < NT; c++) acc[t][c] = f16x{};
+    const f16x zero = {};
+
+    for (int b0 = b_begin + wave * BPW; b0 < b_end; b0 += kw * BPW) {
+        // Every load is unconditional (clamped to a block of this split and a
+        // valid row) so the batch is in flight at once.  Rows past m compute
+        // garbage that is never stored (an MFMA output row depends only on its
+        // own activation row); blocks past the split are skipped whole.
+        uint4 wq[NT][BPW];
+        uint16_t wd[NT][BPW];
+        float4 xv[MT][BPW][4];
+#pragma unroll
+        for (int u = 0; u < BPW; u++) {
+            const int b = min(b0 + u, b_end - 1);
+#pragma unroll
+            for (int c = 0; c < NT; c++) {
+                wq[c][u] = *reinterpret_cast<const uint4*>(wrow[c] + b * 32);
+                wd[c][u] = drow[c][b];
+            }
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const int i = min(t * 32 + r32, m - 1);
+                const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(i) * k + b * 32 + half * 16);
+#pragma unroll
+                for (int q = 0; q < 4; q++) xv[t][u][q] = src[q];
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < BPW; u++) {
+            if (b0 + u >= b_end) break;  // wave-uniform
+            h8 bq0[NT], bq1[NT];
+            float dw[NT];
+#pragma unroll
+            for (int c = 0; c < NT; c++) {
+                const uint2 c0 = quants_to_f16(wq[c][u].x), c1 = quants_to_f16(wq[c][u].y);
+                const uint2 c2 = quants_to_f16(wq[c][u].z), c3 = quants_to_f16(wq[c][u].w);
+                bq0[c] = __builtin_bit_cast(h8, make_uint4(c0.x, c0.y, c1.x, c1.y));
+                bq1[c] = __builtin_bit_cast(h8, make_uint4(c2.x, c2.y, c3.x, c3.y));
+                dw[c] = fh_h2f(wd[c][u]);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                const float v[16] = {xv[t][u][0].x, xv[t][u][0].y, xv[t][u][0].z, xv[t][u][0].w,
+                                     xv[t][u][1].x, xv[t][u][1].y, xv[t][u][1].z, xv[t][u][1].w,
+                                     xv[t][u][2].x, xv[t][u][2].y, xv[t][u][2].z, xv[t][u][2].w,
+                                     xv[t][u][3].x, xv[t][u][3].y, xv[t][u][3].z, xv[t][u][3].w};
+                // fmaxf skips NaN; an infinite maximum takes the rare safe path.
+                float mx = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 16; q++) mx = fmaxf(mx, fabsf(v[q]));
+                mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+                h8 ah0, ah1, al0, al1;
+                int e;
+                if (__builtin_expect(__ballot(!finite(mx)) != 0, 0)) {
+                    float fm = 0.0f;
+#pragma unroll
+                    for (int q = 0; q < 16; q++)
+                        if (finite(v[q])) fm = fmaxf(fm, fabsf(v[q]));
+                    fm = fmaxf(fm, __shfl_xor(fm, 32, 64));
+                    e = block_exponent(fm);
+                    split16<true>(v, __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23), ah0, ah1, al0, al1);
+                } else {
+                    e = block_exponent(mx);
+                    split16<false>(v, __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23), ah0, ah1, al0, al1);
+                }
+                // The output rows this lane holds are not the row it split:
+                // publish 2^-e per row, read back the four groups of four.
+                float* sl = inv_lds + (t * BPW + u) * 32;
+                if (half == 0) sl[r32] = __builtin_bit_cast(float, static_cast<uint32_t>(127 - e) << 23);
+                __builtin_amdgcn_wave_barrier();
+                float4 iv[4];
+#pragma unroll
+                for (int g = 0; g < 4; g++) iv[g] = *reinterpret_cast<const float4*>(sl + g * 8 + half * 4);
+#pragma unroll
+                for (int c = 0; c < NT; c++) {
+                    f16x p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, bq0[c], zero, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, bq0[c], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, bq1[c], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, bq1[c], p, 0, 0, 0);
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        acc[t][c][4 * g + 0] = fmaf(dw[c], p[4 * g + 0] * iv[g].x, acc[t][c][4 * g + 0]);
+                        acc[t][c][4 * g + 1] = fmaf(dw[c], p[4 * g + 1] * iv[g].y, acc[t][c][4 * g + 1]);
+                        acc[t][c][4 * g + 2] = fmaf(dw[c], p[4 * g + 2] * iv[g].z, acc[t][c][4 * g + 2]);
+                        acc[t][c][4 * g + 3] = fmaf(dw[c], p[4 * g + 3] * iv[g].w, acc[t][c][4 * g + 3]);
+                    }
+                }
+                __builtin_amdgcn_wave_barrier();
+            }
+        }
+    }
+    // Wave sums: every wave stores its own, then each output is added over the
+    // waves in wave order.
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int c = 0; c < NT; c++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) sums[wave * OUT + ((t * NT + c) * 16 + v) * 64 + lane] = acc[t][c][v];
+    __syncthreads();
+    // Output o = ((t * NT + c) * 16 + v) * 64 + l  ->  row, column.
+    auto row_of = [](int o) { const int t = o / (NT * 1024), v = (o / 64) % 16, l = o % 64;
+                              return t * 32 + (v / 4) * 8 + (l / 32) * 4 + (v % 4); };
+    auto col_of = [&](int o) { return (tile * NT + (o / 1024) % NT) * 32 + (o & 31); };
+    const size_t tiles = gridDim.x;
+    for (int o = threadIdx.x; o < OUT; o += blockDim.x) {
+        float s = sums[o];
+        for (int w = 1; w < kw; w++) s += sums[w * OUT + o];
+        if (splits == 1) {
+            const int i = row_of(o), jj = col_of(o);
+            if (i < m && jj < n) y[static_cast<size_t>(i) * n + jj] = bias ? s + bias[jj] : s;
+        } else {
+            __hip_atomic_store(part + (split * tiles + tile) * OUT + o, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    }
+    if (splits == 1) return;
+    // Publish this split; the tile's last workgroup adds all splits in order.
+    // The partials go out as device-coherent stores and every thread waits for
+    // its own to complete before the arrival count is bumped, so whoever sees
+    // the final count reads complete partials (device-coherent loads).  This
+    // avoids a release fence, which writes back the whole L2.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (threadIdx.x == 0) last = atomicAdd(counters + tile, 1u) == static_cast<unsigned>(splits - 1);
+    __syncthreads();
+    if (!last) return;
+    // All splits of two outputs per thread are loaded at once (clamped
+    // addresses, unused values skipped in the sum), then added in split order.
+    for (int o0 = threadIdx.x; o0 < OUT; o0 += 2 * blockDim.x) {
+        float pv[2][kMaxSplits];
+#pragma unroll
+        for (int q = 0; q < 2; q++)
+#pragma unroll
+            for (int sp = 0; sp < kMaxSplits; sp++) {
+                const int o = min(o0 + q * static_cast<int>(blockDim.x), OUT - 1);
+                pv[q][sp] = __hip_atomic_load(part + (min(sp, splits - 1) * tiles + tile) * OUT + o, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+            }
+#pragma unroll
+        for (int q = 0; q < 2; q++) {
+            const int o = o0 + q * static_cast<int>(blockDim.x);
+            float s = pv[q][0];
+#pragma unroll
+            for (int sp = 1; sp < kMaxSplits; sp++) s = sp < splits ? s + pv[q][sp] : s;
+            if (o >= OUT) continue;
+            const int i = row_of(o), jj = col_of(o);
+            if (i < m && jj < n) y[static_cast<size_t>(i) * n + jj] = bias ? s + bias[jj] : s;
+        }
+    }
+    if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 namespace {
 
 template <int BM, int BN, int WM, int WN, int KW>
@@ -297,12 +527,63 @@ int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const f
     return FH_OK;
 }
 
+// Splits of K only while the column tiles alone leave half the CUs idle, and
+// then as few as let one batch of BPW blocks per wave cover a split (each split
+// costs a round of partial stores and reloads).  Waves: at most 16 / (MT * NT)
+// (their sums fit 64 KiB of LDS) and 8 (256 VGPRs per lane).  Column tiles per
+// wave (NT): up to 4 while that still leaves >= 256 workgroups, so wide
+// outputs split each activation block once per 128 columns.
+template <int MT, int NT, int BPW>
+int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    constexpr size_t kMaxWaves = 16 / (MT * NT) < 8 ? 16 / (MT * NT) : 8;
+    const size_t kb = w->k / 32, tiles = (w->n + 32 * NT - 1) / (32 * NT);
+    size_t splits = 1;
+    if (tiles < static_cast<size_t>(ctx->num_cus) / 2) splits = (kb + kMaxWaves * BPW - 1) / (kMaxWaves * BPW);
+    if (splits > static_cast<size_t>(kMaxSplits)) splits = kMaxSplits;
+    const size_t bps = (kb + splits - 1) / splits;
+    splits = (kb + bps - 1) / bps;  // no empty split
+    size_t kw = (bps + BPW - 1) / BPW;
+    if (kw > kMaxWaves) kw = kMaxWaves;
+    const size_t lds = kw * (static_cast<size_t>(MT * NT * 1024) + MT * BPW * 32) * sizeof(float);
+    float* part = nullptr;
+    unsigned* counters = nullptr;
+    if (splits > 1) {
+        void* ws = nullptr;
+        int rc = fh_workspace(ctx, splits * tiles * MT * NT * 1024 * sizeof(float), &ws);
+        if (rc) return rc;
+        part = static_cast<float*>(ws);
+        void* cnt = nullptr;
+        rc = fh_counter_area(ctx, tiles * sizeof(unsigned), &cnt);
+        if (rc) return rc;
+        counters = static_cast<unsigned*>(cnt);
+    }
+    if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: too many output columns");
+    const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), block(static_cast<unsigned>(64 * kw));
+    hipLaunchKernelGGL((k_gemm_skinny<MT, NT, BPW>), grid, block, lds, ctx->stream, x, w->qs, w->d, bias, y,
+                       static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(bps), part,
+                       counters);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    const size_t t32 = (w->n + 31) / 32;
+    if (m <= 32) {
+        if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y);
+        if (t32 >= 2 * 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y);
+        return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y);
+    }
+    if (t32 >= 2 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y);
+    return launch_skinny_t<2, 1, 3>(ctx, w, x, m, bias, y);
+}
+
 }  // namespace
 
 // Tile choice: the 128 x 128 tile once it still yields two tiles per CU,
 // else 64 x 64, else 32 x 32 outputs with the four waves splitting K.
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
     const size_t cus = static_cast<size_t>(ctx->num_cus);
+    if (m <= 64) return launch_skinny(ctx, w, x, m, bias, y);
     if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) return launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
     if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) return launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
     return launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);

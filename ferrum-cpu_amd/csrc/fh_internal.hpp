@@ -32,6 +32,11 @@ struct fh_ctx {
     // finish (the split sampler's per-row barriers).  Never shares ws.
     void* sync = nullptr;
     size_t sync_bytes = 0;
+    // Zero-initialised counters that kernels leave at zero (the split-K
+    // GEMM's per-tile arrival counts).  Separate from sync: the sampler's
+    // generation tags there must never be reset behind its back.
+    void* counters = nullptr;
+    size_t counters_bytes = 0;
 };
 
 struct fh_q8_0 {
@@ -56,6 +61,8 @@ int fh_workspace(fh_ctx* ctx, size_t bytes, void** out);
 // Make sure ctx->sync holds at least `bytes`, zeroed when (re)allocated.
 // Growing is refused while the stream is being captured into a graph.
 int fh_sync_area(fh_ctx* ctx, size_t bytes, void** out);
+// The same for ctx->counters.
+int fh_counter_area(fh_ctx* ctx, size_t bytes, void** out);
 // Round up to a multiple of 256 bytes.
 static inline size_t fh_align256(size_t b) { return (b + 255) & ~(size_t)255; }
 
