@@ -178,14 +178,15 @@ static int alloc_weight(fh_ctx* ctx, size_t n_rows, size_t k, fh_q8_0** out) {
     w->n = n_rows;
     w->k = k;
     w->kb = k / 32;
-    size_t qbytes = fh_align256(n_rows * k), dbytes = fh_align256(n_rows * w->kb * 2);
-    hipError_t e = hipMalloc(&w->base, qbytes + dbytes);
+    size_t qbytes = fh_align256(n_rows * k), dbytes = fh_align256(n_rows * w->kb * 2), ebytes = fh_align256(n_rows);
+    hipError_t e = hipMalloc(&w->base, qbytes + dbytes + ebytes);
     if (e != hipSuccess) {
         delete w;
         return fh_hip_fail(ctx, e, "hipMalloc(Q8_0 weight)");
     }
     w->qs = static_cast<int8_t*>(w->base);
     w->d = reinterpret_cast<uint16_t*>(static_cast<char*>(w->base) + qbytes);
+    w->rexp = reinterpret_cast<int8_t*>(static_cast<char*>(w->base) + qbytes + dbytes);
     *out = w;
     return FH_OK;
 }
@@ -199,6 +200,7 @@ int fh_q8_0_upload_device(fh_ctx* ctx, const uint8_t* d_gguf, size_t n_rows, siz
     int rc = alloc_weight(ctx, n_rows, k, out);
     if (rc) return rc;
     rc = fh_launch_repack(ctx, d_gguf, n_rows, k, (*out)->qs, (*out)->d);
+    if (rc == FH_OK) rc = fh_launch_row_exponents(ctx, (*out)->d, n_rows, k / 32, (*out)->rexp);
     if (rc) {
         fh_q8_0_free(*out);
         *out = nullptr;

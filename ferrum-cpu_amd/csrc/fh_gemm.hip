@@ -35,6 +35,8 @@ namespace {
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16x __attribute__((ext_vector_type(16)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));  // staging registers (a struct copy would go through scratch)
 
 // Staged rows, in f16 elements.  Activations: 32 h, 32 l, 8 pad (144 B);
 // weights: 32 quants, 8 pad (80 B).  Both strides keep the 16 lanes of a
@@ -56,12 +58,28 @@ __device__ __forceinline__ uint2 quants_to_f16(uint32_t w) {
 
 __device__ __forceinline__ bool finite(float v) { return (__builtin_bit_cast(uint32_t, v) & 0x7F800000u) != 0x7F800000u; }
 
+// Outputs whose activation row holds inf/NaN (large-m kernel) or whose weight
+// row has a non-finite block scale (every kernel) are recomputed this way: the
+// reference's own arithmetic (ops.rs:29-126 on the f32 expansion), products
+// and sums rounded separately in ascending p, so the inf/NaN pattern (inf * 0
+// = NaN, inf - inf = NaN) and the value are the reference's bit for bit.
+__device__ __attribute__((noinline)) float exact_dot(const float* __restrict__ x, int k, const int8_t* __restrict__ q,
+                                                   const uint16_t* __restrict__ d) {
+    float s = 0.0f;
+    for (int b = 0; b < (k >> 5); b++) {
+        const float ds = fh_h2f(d[b]);
+        for (int t = 0; t < 32; t++)
+            s = __fadd_rn(s, __fmul_rn(x[b * 32 + t], ds * static_cast<float>(q[b * 32 + t])));
+    }
+    return s;
+}
+
 }  // namespace
 
 // One wave per activation row (rows m .. m_pad - 1 are written as zeros).
 __global__ void __launch_bounds__(256)
     k_split_rows(const float* __restrict__ x, int m, int m_pad, int k, int bm, uint4* __restrict__ panel,
-                 float* __restrict__ xinv) {
+                 float* __restrict__ xinv, uint8_t* __restrict__ xbad) {
     const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (row >= m_pad) return;
@@ -69,17 +87,21 @@ __global__ void __launch_bounds__(256)
     const bool live = row < m;
     const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(live ? row : 0) * k);
     float mx = 0.0f;
+    bool bad = false;
     if (live) {
         for (int c = lane; c < chunks; c += 64) {
             const float4 a = xr[2 * c], b = xr[2 * c + 1];
             const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
-            for (int t = 0; t < 8; t++)
+            for (int t = 0; t < 8; t++) {
                 if (finite(v[t])) mx = fmaxf(mx, fabsf(v[t]));
+                else bad = true;
+            }
         }
     }
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    if (lane == 0) xbad[row] = __ballot(bad) != 0;
     // mx = f * 2^E with f in [0.5, 1): scale by 2^(15 - E).  A subnormal
     // maximum reads E = -126 and clamps like any tiny row.
     int e = 0;
@@ -111,27 +133,34 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// CTA tile BM x BN; 4 waves = WM x WN output sub-tiles x KW K-slices.
+// Workgroup tile BM x BN; NW = WM x WN x KW waves (output sub-tiles x
+// K-slices).  Tiles are numbered so that consecutive workgroups on one XCD
+// (the hardware deals workgroup ids round-robin over the 8 XCDs) take
+// consecutive tiles of one activation row-tile, which then stays in that XCD's L2.
 template <int BM, int BN, int WM, int WN, int KW>
-__global__ void __launch_bounds__(256)
-    k_gemm_mfma(const uint4* __restrict__ panel, const float* __restrict__ xinv, const int8_t* __restrict__ qs,
-                const uint16_t* __restrict__ dsc, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
-                int k, int tiles_n) {
-    static_assert(WM * WN * KW == 4, "four waves");
+__global__ void __launch_bounds__(64 * WM * WN * KW)
+    k_gemm_mfma(const uint4* __restrict__ panel, const float* __restrict__ xinv, const float* __restrict__ x,
+                const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const int8_t* __restrict__ rexp,
+                const float* __restrict__ bias, float* __restrict__ y, int m, int n, int k, int tiles_n) {
+    constexpr int NW = WM * WN * KW, NT = 64 * NW;
+    static_assert(NW == 4 || NW == 8, "four or eight waves");
     constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
     static_assert(TM >= 1 && TN >= 1 && TM * 32 * WM == BM && TN * 32 * WN == BN, "tile shape");
     constexpr int A_BYTES = KW * BM * kArow * 2, B_BYTES = KW * BN * kBrow * 2, S_BYTES = KW * BN * 4;
     constexpr int STAGE = A_BYTES + B_BYTES + S_BYTES;
     // 16-byte pieces per thread (the last weight round may leave threads idle)
-    constexpr int AP = KW * BM * 8 / 256, BPN = KW * BN * 2, BP = (BPN + 255) / 256;
-    static_assert(AP * 256 == KW * BM * 8 && KW * BN <= 256, "staging split");
+    constexpr int AP = KW * BM * 8 / NT, BPN = KW * BN * 2, BP = (BPN + NT - 1) / NT;
+    static_assert(AP * NT == KW * BM * 8 && KW * BN <= NT, "staging split");
     constexpr int RED = (KW - 1) * WM * WN * TM * TN * 16 * 64 * 4;
-    static_assert(RED <= 2 * STAGE, "reduction fits the stage buffers");
+    static_assert(RED + BM * 4 <= 2 * STAGE, "reduction and row scales fit the stage buffers");
     __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kw = wave / (WM * WN), wm = (wave % (WM * WN)) / WN, wn = wave % WN;
-    const int tile_m = static_cast<int>(blockIdx.x) / tiles_n, tile_n = static_cast<int>(blockIdx.x) % tiles_n;
+    const int tiles = static_cast<int>(gridDim.x), per_xcd = tiles / 8, rem = tiles % 8;
+    const int xcd = static_cast<int>(blockIdx.x) % 8, slot = static_cast<int>(blockIdx.x) / 8;
+    const int tile = xcd * per_xcd + min(xcd, rem) + slot;  // XCDs 0 .. rem-1 take one extra tile
+    const int tile_m = tile / tiles_n, tile_n = tile % tiles_n;
     const int j0 = tile_n * BN;
     const int kb = k >> 5, steps = (kb + KW - 1) / KW;
     const uint4* pan = panel + static_cast<size_t>(tile_m) * kb * BM * 8;
@@ -141,13 +170,13 @@ __global__ void __launch_bounds__(256)
     auto load = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
         for (int p = 0; p < AP; p++) {
-            const int piece = tid + 256 * p, blk = piece / (BM * 8), rem = piece % (BM * 8);
+            const int piece = tid + NT * p, blk = piece / (BM * 8), rem = piece % (BM * 8);
             const int b = st * KW + blk;
             ra[p] = b < kb ? pan[static_cast<size_t>(b) * BM * 8 + rem] : make_uint4(0, 0, 0, 0);
         }
 #pragma unroll
         for (int p = 0; p < BP; p++) {
-            const int piece = tid + 256 * p, blk = piece / (BN * 2), rem = piece % (BN * 2);
+            const int piece = tid + NT * p, blk = piece / (BN * 2), rem = piece % (BN * 2);
             const int b = st * KW + blk, j = j0 + rem / 2;
             rb[p] = (piece < BPN && b < kb && j < n)
                         ? *reinterpret_cast<const uint4*>(qs + static_cast<size_t>(j) * k + b * 32 + (rem & 1) * 16)
@@ -162,13 +191,13 @@ __global__ void __launch_bounds__(256)
         char* st = lds + buf * STAGE;
 #pragma unroll
         for (int p = 0; p < AP; p++) {
-            const int piece = tid + 256 * p, blk = piece / (BM * 8), rem = piece % (BM * 8);
+            const int piece = tid + NT * p, blk = piece / (BM * 8), rem = piece % (BM * 8);
             *reinterpret_cast<uint4*>(st + ((blk * BM + rem / 8) * kArow) * 2 + (rem % 8) * 16) = ra[p];
         }
 #pragma unroll
         for (int p = 0; p < BP; p++) {
-            const int piece = tid + 256 * p, blk = piece / (BN * 2), rem = piece % (BN * 2);
-            if (BPN % 256 != 0 && piece >= BPN) break;
+            const int piece = tid + NT * p, blk = piece / (BN * 2), rem = piece % (BN * 2);
+            if (BPN % NT != 0 && piece >= BPN) break;
             char* dst = st + A_BYTES + ((blk * BN + rem / 2) * kBrow) * 2 + (rem & 1) * 32;
             const uint2 a = quants_to_f16(rb[p].x), b = quants_to_f16(rb[p].y);
             const uint2 c = quants_to_f16(rb[p].z), d = quants_to_f16(rb[p].w);
@@ -196,16 +225,10 @@ __global__ void __launch_bounds__(256)
         const _Float16* As = reinterpret_cast<const _Float16*>(sb) + kw * BM * kArow;
         const _Float16* Bs = reinterpret_cast<const _Float16*>(sb + A_BYTES) + kw * BN * kBrow;
         const float* Ss = reinterpret_cast<const float*>(sb + A_BYTES + B_BYTES) + kw * BN;
-        h8 ah[TM][2], al[TM][2], bq[TN][2];
+        // Weight fragments and scales for all column tiles, then one row tile
+        // at a time (its four activation fragments, then its MFMAs).
+        h8 bq[TN][2];
         float dw[TN];
-#pragma unroll
-        for (int r = 0; r < TM; r++) {
-            const _Float16* a = As + ((wm * TM + r) * 32 + arow) * kArow + koff;
-            ah[r][0] = *reinterpret_cast<const h8*>(a);
-            ah[r][1] = *reinterpret_cast<const h8*>(a + 16);
-            al[r][0] = *reinterpret_cast<const h8*>(a + 32);
-            al[r][1] = *reinterpret_cast<const h8*>(a + 48);
-        }
 #pragma unroll
         for (int c = 0; c < TN; c++) {
             const int col = (wn * TN + c) * 32 + arow;
@@ -215,16 +238,20 @@ __global__ void __launch_bounds__(256)
             dw[c] = Ss[col];
         }
 #pragma unroll
-        for (int r = 0; r < TM; r++)
+        for (int r = 0; r < TM; r++) {
+            const _Float16* a = As + ((wm * TM + r) * 32 + arow) * kArow + koff;
+            const h8 ah0 = *reinterpret_cast<const h8*>(a), ah1 = *reinterpret_cast<const h8*>(a + 16);
+            const h8 al0 = *reinterpret_cast<const h8*>(a + 32), al1 = *reinterpret_cast<const h8*>(a + 48);
 #pragma unroll
             for (int c = 0; c < TN; c++) {
-                f16x p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[r][0], bq[c][0], zero, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[r][0], bq[c][0], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[r][1], bq[c][1], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[r][1], bq[c][1], p, 0, 0, 0);
+                f16x p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, bq[c][0], zero, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, bq[c][0], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, bq[c][1], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, bq[c][1], p, 0, 0, 0);
 #pragma unroll
                 for (int v = 0; v < 16; v++) acc[r][c][v] = fmaf(dw[c], p[v], acc[r][c][v]);
             }
+        }
         if (st + 1 < steps) store(buf ^ 1);
         __syncthreads();
     }
@@ -244,31 +271,202 @@ __global__ void __launch_bounds__(256)
                         red[((((kw - 1) * WM * WN + sub) * TM + r) * TN + c) * 1024 + v * 64 + lane] = acc[r][c][v];
         }
         __syncthreads();
-        if (kw > 0) return;
+        if (kw == 0) {
 #pragma unroll
-        for (int s = 1; s < KW; s++)
+            for (int s = 1; s < KW; s++)
 #pragma unroll
-            for (int r = 0; r < TM; r++)
+                for (int r = 0; r < TM; r++)
 #pragma unroll
-                for (int c = 0; c < TN; c++)
+                    for (int c = 0; c < TN; c++)
 #pragma unroll
-                    for (int v = 0; v < 16; v++)
-                        acc[r][c][v] += red[((((s - 1) * WM * WN + sub) * TM + r) * TN + c) * 1024 + v * 64 + lane];
+                        for (int v = 0; v < 16; v++)
+                            acc[r][c][v] += red[((((s - 1) * WM * WN + sub) * TM + r) * TN + c) * 1024 + v * 64 + lane];
+        }
     }
 
+    // Row scales of this tile through LDS (the stage buffers are free).
     const int i0 = tile_m * BM;
+    float* s_inv = reinterpret_cast<float*>(lds) + RED / 4;
+    __syncthreads();
+    for (int t = tid; t < BM; t += NT) s_inv[t] = xinv[i0 + t];  // rows < m_pad
+    __syncthreads();
+    if (KW > 1 && kw > 0) return;
 #pragma unroll
     for (int c = 0; c < TN; c++) {
         const int j = j0 + (wn * TN + c) * 32 + arow;
         if (j >= n) continue;
+        const bool jbad = rexp[j] == kFhBadRowExp;
         const float bj = bias ? bias[j] : 0.0f;
 #pragma unroll
         for (int r = 0; r < TM; r++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int i = i0 + (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4);
+                const int il = (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4), i = i0 + il;
                 if (i >= m) continue;
-                const float s = acc[r][c][v] * xinv[i];
+                float s = acc[r][c][v] * s_inv[il];
+                if (__builtin_expect(jbad, 0))
+                    s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(j) * k,
+                                  dsc + static_cast<size_t>(j) * kb);
+                y[static_cast<size_t>(i) * n + j] = bias ? s + bj : s;
+            }
+    }
+}
+
+// ---- large m: both operands split, block scales folded into the weights ----------
+// For the big tiles the per-block weight-scale FMA would need every output sum
+// in VGPRs; instead the weight operand carries its scale: per weight row j,
+//   2^e_j * f16(d_jb) * q   (e_j from the row's largest scale, at upload)
+// has at most 18 significant bits and is split exactly into f16 hi + lo.  The
+// products then accumulate across all Q8_0 blocks in the matrix core's
+// accumulators (AGPRs):  x_h W_h + x_h W_l + x_l W_h  (three MFMAs per K = 16;
+// the dropped x_l W_l is 2^-22 of a product), and the output is
+// acc * 2^-e_i * 2^-e_j (+ bias).  The dequantised weight is used exactly; the
+// only rounding beyond the f32 sums is the activations' 22-bit split.
+// Workgroup tile 256 x 256, eight waves of 128 x 64 (4 x 2 MFMA tiles), one
+// Q8_0 block per stage, two LDS stages of 72 KiB.
+template <int BM, int BN, int WM, int WN>
+__global__ void __launch_bounds__(64 * WM * WN)
+    k_gemm_wsplit(const uint4* __restrict__ panel, const float* __restrict__ xinv, const uint8_t* __restrict__ xbad,
+                  const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
+                  const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
+                  int k, int tiles_n) {
+    constexpr int NW = WM * WN, NTH = 64 * NW;
+    constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
+    static_assert(TM * 32 * WM == BM && TN * 32 * WN == BN, "tile shape");
+    constexpr int A_BYTES = BM * kArow * 2, B_BYTES = BN * kArow * 2, STAGE = A_BYTES + B_BYTES;
+    constexpr int AP = BM * 8 / NTH;  // 16-byte activation pieces per thread
+    static_assert(AP * NTH == BM * 8 && BN * 2 == NTH, "staging split: one weight half-row per thread");
+    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WN, wn = wave % WN;
+    const int tiles = static_cast<int>(gridDim.x), per_xcd = tiles / 8, rem = tiles % 8;
+    const int xcd = static_cast<int>(blockIdx.x) % 8, slot = static_cast<int>(blockIdx.x) / 8;
+    const int tile = xcd * per_xcd + min(xcd, rem) + slot;
+    const int tile_m = tile / tiles_n, tile_n = tile % tiles_n;
+    const int j0 = tile_n * BN;
+    const int kb = k >> 5;
+    const uint4* pan = panel + static_cast<size_t>(tile_m) * kb * BM * 8;
+
+    // This thread's weight half-row (rows past n repeat row n - 1: their
+    // output columns are never stored, and a column depends only on its row).
+    const int jr = tid >> 1, jhalf = tid & 1;
+    const int jw = min(j0 + jr, n - 1);
+    const int8_t* wsrc = qs + static_cast<size_t>(jw) * k + jhalf * 16;
+    const uint16_t* dsrc = dsc + static_cast<size_t>(jw) * kb;
+    const int ejw = rexp[jw] == kFhBadRowExp ? 0 : rexp[jw];  // flagged rows: recomputed at the end
+    const float wscale = __builtin_bit_cast(float, static_cast<uint32_t>(ejw + 127) << 23);
+
+    u4 ra[AP], rq;
+    uint16_t rd;
+    auto load = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int p = 0; p < AP; p++) ra[p] = reinterpret_cast<const u4*>(pan)[static_cast<size_t>(b) * BM * 8 + tid + NTH * p];
+        rq = *reinterpret_cast<const u4*>(wsrc + b * 32);
+        rd = dsrc[b];
+    };
+    auto store = [&](int buf) __attribute__((always_inline)) {
+        char* st = lds + buf * STAGE;
+#pragma unroll
+        for (int p = 0; p < AP; p++) {
+            const int piece = tid + NTH * p;
+            *reinterpret_cast<u4*>(st + (piece / 8) * kArow * 2 + (piece % 8) * 16) = ra[p];
+        }
+        const float ds = fh_h2f(rd) * wscale;  // exact (power of two)
+        uint32_t hi[8], lo[8];
+#pragma unroll
+        for (int t = 0; t < 8; t++) {
+            const uint32_t word = t < 2 ? rq.x : t < 4 ? rq.y : t < 6 ? rq.z : rq.w;
+            const int sh = (t & 1) * 16;
+            const f2 w = {static_cast<float>(static_cast<int8_t>((word >> sh) & 0xFF)) * ds,
+                          static_cast<float>(static_cast<int8_t>((word >> (sh + 8)) & 0xFF)) * ds};
+            const h2 h = __builtin_convertvector(w, h2);
+            f2 r = {w.x - static_cast<float>(h.x), w.y - static_cast<float>(h.y)};
+            r.x = finite(w.x) ? r.x : 0.0f;
+            r.y = finite(w.y) ? r.y : 0.0f;
+            hi[t] = __builtin_bit_cast(uint32_t, h);
+            lo[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, h2));
+        }
+        char* dst = st + A_BYTES + jr * kArow * 2 + jhalf * 32;
+        *reinterpret_cast<u4*>(dst) = u4{hi[0], hi[1], hi[2], hi[3]};
+        *reinterpret_cast<u4*>(dst + 16) = u4{hi[4], hi[5], hi[6], hi[7]};
+        *reinterpret_cast<u4*>(dst + 64) = u4{lo[0], lo[1], lo[2], lo[3]};
+        *reinterpret_cast<u4*>(dst + 80) = u4{lo[4], lo[5], lo[6], lo[7]};
+    };
+
+    f16x acc[TM][TN];
+#pragma unroll
+    for (int r = 0; r < TM; r++)
+#pragma unroll
+        for (int c = 0; c < TN; c++) acc[r][c] = f16x{};
+
+    load(0);
+    store(0);
+    __syncthreads();
+    const int arow = lane % 32, koff = (lane / 32) * 8;
+    for (int b = 0; b < kb; b++) {
+        const int buf = b & 1;
+        if (b + 1 < kb) load(b + 1);
+        const char* sb = lds + buf * STAGE;
+        const _Float16* As = reinterpret_cast<const _Float16*>(sb);
+        const _Float16* Bs = reinterpret_cast<const _Float16*>(sb + A_BYTES);
+        h8 wh[TN][2], wl[TN][2];
+#pragma unroll
+        for (int c = 0; c < TN; c++) {
+            const _Float16* q = Bs + ((wn * TN + c) * 32 + arow) * kArow + koff;
+            wh[c][0] = *reinterpret_cast<const h8*>(q);
+            wh[c][1] = *reinterpret_cast<const h8*>(q + 16);
+            wl[c][0] = *reinterpret_cast<const h8*>(q + 32);
+            wl[c][1] = *reinterpret_cast<const h8*>(q + 48);
+        }
+#pragma unroll
+        for (int r = 0; r < TM; r++) {
+            const _Float16* a = As + ((wm * TM + r) * 32 + arow) * kArow + koff;
+            const h8 ah0 = *reinterpret_cast<const h8*>(a), ah1 = *reinterpret_cast<const h8*>(a + 16);
+            const h8 al0 = *reinterpret_cast<const h8*>(a + 32), al1 = *reinterpret_cast<const h8*>(a + 48);
+#pragma unroll
+            for (int c = 0; c < TN; c++) {
+                f16x p = acc[r][c];
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wh[c][0], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wl[c][0], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, wh[c][0], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wh[c][1], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wl[c][1], p, 0, 0, 0);
+                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, wh[c][1], p, 0, 0, 0);
+                acc[r][c] = p;
+            }
+        }
+        if (b + 1 < kb) store(buf ^ 1);
+        __syncthreads();
+    }
+
+    // Row scales and flags of this tile through LDS (one load each, not one
+    // dependent global load per output).
+    const int i0 = tile_m * BM;
+    float* s_inv = reinterpret_cast<float*>(lds);
+    uint8_t* s_bad = reinterpret_cast<uint8_t*>(lds + BM * 4);
+    for (int t = tid; t < BM; t += NTH) {  // rows < m_pad: the panel arrays cover them
+        s_inv[t] = xinv[i0 + t];
+        s_bad[t] = xbad[i0 + t];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int c = 0; c < TN; c++) {
+        const int j = j0 + (wn * TN + c) * 32 + arow;
+        if (j >= n) continue;
+        const bool jbad = rexp[j] == kFhBadRowExp;
+        const float winv = __builtin_bit_cast(float, static_cast<uint32_t>(127 - (jbad ? 0 : rexp[j])) << 23);
+        const float bj = bias ? bias[j] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < TM; r++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int il = (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4), i = i0 + il;
+                if (i >= m) continue;
+                float s = acc[r][c][v] * s_inv[il] * winv;
+                if (__builtin_expect(jbad || s_bad[il], 0))
+                    s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(j) * k,
+                                  dsc + static_cast<size_t>(j) * kb);
                 y[static_cast<size_t>(i) * n + j] = bias ? s + bj : s;
             }
     }
@@ -290,7 +488,6 @@ __global__ void __launch_bounds__(256)
 // left at zero for the next launch) -- a fixed order either way.
 namespace {
 
-typedef float f2 __attribute__((ext_vector_type(2)));
 constexpr int kMaxSplits = 8;  // K splits of the skinny GEMM
 
 // 16 activations (one lane's half of a row's block) times 2^e as h + l; the
@@ -327,8 +524,8 @@ __device__ __forceinline__ int block_exponent(float mx) {
 template <int MT, int NT, int BPW>
 __global__ void __launch_bounds__(512)
     k_gemm_skinny(const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
-                  const float* __restrict__ bias, float* __restrict__ y, int m, int n, int k, int bps,
-                  float* __restrict__ part, unsigned* __restrict__ counters) {
+                  const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
+                  int k, int bps, float* __restrict__ part, unsigned* __restrict__ counters) {
     constexpr int OUT = MT * NT * 1024;  // outputs of one workgroup
     // [KW][OUT] wave sums, then [KW][MT][BPW][32] row scales
     extern __shared__ __attribute__((aligned(16))) float lds[];
@@ -456,13 +653,19 @@ __global__ void __launch_bounds__(512)
     auto row_of = [](int o) { const int t = o / (NT * 1024), v = (o / 64) % 16, l = o % 64;
                               return t * 32 + (v / 4) * 8 + (l / 32) * 4 + (v % 4); };
     auto col_of = [&](int o) { return (tile * NT + (o / 1024) % NT) * 32 + (o & 31); };
+    auto finish = [&](int i, int jj, float s) {
+        if (__builtin_expect(rexp[jj] == kFhBadRowExp, 0))
+            s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(jj) * k,
+                          dsc + static_cast<size_t>(jj) * kb);
+        y[static_cast<size_t>(i) * n + jj] = bias ? s + bias[jj] : s;
+    };
     const size_t tiles = gridDim.x;
     for (int o = threadIdx.x; o < OUT; o += blockDim.x) {
         float s = sums[o];
         for (int w = 1; w < kw; w++) s += sums[w * OUT + o];
         if (splits == 1) {
             const int i = row_of(o), jj = col_of(o);
-            if (i < m && jj < n) y[static_cast<size_t>(i) * n + jj] = bias ? s + bias[jj] : s;
+            if (i < m && jj < n) finish(i, jj, s);
         } else {
             __hip_atomic_store(part + (split * tiles + tile) * OUT + o, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -498,7 +701,7 @@ __global__ void __launch_bounds__(512)
             for (int sp = 1; sp < kMaxSplits; sp++) s = sp < splits ? s + pv[q][sp] : s;
             if (o >= OUT) continue;
             const int i = row_of(o), jj = col_of(o);
-            if (i < m && jj < n) y[static_cast<size_t>(i) * n + jj] = bias ? s + bias[jj] : s;
+            if (i < m && jj < n) finish(i, jj, s);
         }
     }
     if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -509,20 +712,27 @@ namespace {
 template <int BM, int BN, int WM, int WN, int KW>
 int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
     const size_t m_pad = (m + BM - 1) / BM * BM;
-    const size_t pbytes = fh_align256(m_pad * w->k * 4), ibytes = fh_align256(m_pad * 4);
+    const size_t pbytes = fh_align256(m_pad * w->k * 4), ibytes = fh_align256(m_pad * 4), fbytes = fh_align256(m_pad);
     void* ws = nullptr;
-    int rc = fh_workspace(ctx, pbytes + ibytes, &ws);
+    int rc = fh_workspace(ctx, pbytes + ibytes + fbytes, &ws);
     if (rc) return rc;
     uint4* panel = static_cast<uint4*>(ws);
     float* xinv = reinterpret_cast<float*>(static_cast<char*>(ws) + pbytes);
+    uint8_t* xbad = reinterpret_cast<uint8_t*>(static_cast<char*>(ws) + pbytes + ibytes);
     hipLaunchKernelGGL(k_split_rows, dim3(static_cast<unsigned>((m_pad + 3) / 4)), dim3(256), 0, ctx->stream, x,
-                       static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(w->k), BM, panel, xinv);
+                       static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(w->k), BM, panel, xinv, xbad);
     FH_HIP(ctx, hipGetLastError());
     const size_t tiles_n = (w->n + BN - 1) / BN, tiles = tiles_n * (m_pad / BM);
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
-    hipLaunchKernelGGL((k_gemm_mfma<BM, BN, WM, WN, KW>), dim3(static_cast<unsigned>(tiles)), dim3(256), 0,
-                       ctx->stream, panel, xinv, w->qs, w->d, bias, y, static_cast<int>(m), static_cast<int>(w->n),
-                       static_cast<int>(w->k), static_cast<int>(tiles_n));
+    if constexpr (KW == 0)  // the weight-split kernel
+        hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN), 0,
+                           ctx->stream, panel, xinv, xbad, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
+                           static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n));
+    else
+        hipLaunchKernelGGL((k_gemm_mfma<BM, BN, WM, WN, KW>), dim3(static_cast<unsigned>(tiles)),
+                           dim3(64 * WM * WN * KW), 0, ctx->stream, panel, xinv, x, w->qs, w->d, w->rexp, bias, y,
+                           static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k),
+                           static_cast<int>(tiles_n));
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -559,7 +769,7 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     }
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: too many output columns");
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), block(static_cast<unsigned>(64 * kw));
-    hipLaunchKernelGGL((k_gemm_skinny<MT, NT, BPW>), grid, block, lds, ctx->stream, x, w->qs, w->d, bias, y,
+    hipLaunchKernelGGL((k_gemm_skinny<MT, NT, BPW>), grid, block, lds, ctx->stream, x, w->qs, w->d, w->rexp, bias, y,
                        static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(bps), part,
                        counters);
     FH_HIP(ctx, hipGetLastError());
@@ -579,11 +789,13 @@ int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const
 
 }  // namespace
 
-// Tile choice: the 128 x 128 tile once it still yields two tiles per CU,
-// else 64 x 64, else 32 x 32 outputs with the four waves splitting K.
+// Tile choice: m <= 64 takes the skinny kernel; otherwise the 256 x 256
+// weight-split tile (eight waves) once it still yields a tile per CU, the 128 x 128 tile at two
+// tiles per CU, else 64 x 64, else 32 x 32 outputs with four waves splitting K.
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
     const size_t cus = static_cast<size_t>(ctx->num_cus);
     if (m <= 64) return launch_skinny(ctx, w, x, m, bias, y);
+    if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus) return launch_gemm<256, 256, 2, 4, 0>(ctx, w, x, m, bias, y);
     if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) return launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
     if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) return launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
     return launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);

@@ -39,12 +39,20 @@ struct fh_ctx {
     size_t counters_bytes = 0;
 };
 
+constexpr int8_t kFhBadRowExp = -128;
+
 struct fh_q8_0 {
     int device = 0;
     size_t n = 0, k = 0, kb = 0;
     int8_t* qs = nullptr;
     uint16_t* d = nullptr;
-    void* base = nullptr;  // the one allocation holding both planes
+    // Per row j, e_j with 127 * max_b |d_jb| * 2^e_j in [2^14, 2^15) (0 for a
+    // row without non-zero scales, kFhBadRowExp for a row with a non-finite
+    // scale): the large-m GEMM splits 2^e_j * d * q exactly into two f16
+    // terms, and every GEMM recomputes the flagged rows' outputs exactly.
+    // Derived from d at upload.
+    int8_t* rexp = nullptr;
+    void* base = nullptr;  // the one allocation holding all planes
 };
 
 // ---- error plumbing ---------------------------------------------------------
@@ -69,6 +77,7 @@ static inline size_t fh_align256(size_t b) { return (b + 255) & ~(size_t)255; }
 // ---- launchers implemented in the kernel translation units -------------------
 int fh_launch_repack(fh_ctx* ctx, const uint8_t* d_raw, size_t n, size_t k, int8_t* qs,
                      uint16_t* d);
+int fh_launch_row_exponents(fh_ctx* ctx, const uint16_t* d, size_t n, size_t kb, int8_t* rexp);
 int fh_launch_unpack(fh_ctx* ctx, const int8_t* qs, const uint16_t* d, size_t n, size_t k,
                      uint8_t* d_raw);
 int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,

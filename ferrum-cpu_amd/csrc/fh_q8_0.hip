@@ -72,6 +72,28 @@ __global__ void __launch_bounds__(kThreads) k_repack(const uint16_t* __restrict_
     for (int w = 0; w < 8; w++) dst[w] = static_cast<uint32_t>(src[1 + 2 * w]) | (static_cast<uint32_t>(src[2 + 2 * w]) << 16);
 }
 
+// One thread per weight row: e = 15 - E for 127 * max_b |d_b| = f * 2^E,
+// f in [0.5, 1); 0 for a row of zero scales, kFhBadRowExp if any scale is
+// inf or NaN.
+__global__ void __launch_bounds__(kThreads) k_row_exponents(const uint16_t* __restrict__ d, size_t n, size_t kb,
+                                                            int8_t* __restrict__ rexp) {
+    size_t j = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+    if (j >= n) return;
+    float mx = 0.0f;
+    bool bad = false;
+    for (size_t b = 0; b < kb; b++) {
+        const float v = fabsf(fh_h2f(d[j * kb + b]));
+        if (v <= 65504.0f) mx = fmaxf(mx, v);
+        else bad = true;  // inf or NaN
+    }
+    int e = 0;
+    if (mx > 0.0f) {
+        const float top = mx * 127.0f;  // exact: 11 x 7 significant bits
+        e = 15 - (static_cast<int>((__builtin_bit_cast(uint32_t, top) >> 23) & 0xFF) - 126);
+    }
+    rexp[j] = bad ? kFhBadRowExp : static_cast<int8_t>(e);
+}
+
 __global__ void __launch_bounds__(kThreads) k_unpack(const uint32_t* __restrict__ qs, const uint16_t* __restrict__ d,
                                                      size_t nblocks, uint16_t* __restrict__ raw) {
     size_t b = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
@@ -154,6 +176,12 @@ int fh_launch_repack(fh_ctx* ctx, const uint8_t* d_raw, size_t n, size_t k, int8
     size_t nb = n * (k / 32);
     hipLaunchKernelGGL(k_repack, dim3(grid_for(nb)), dim3(kThreads), 0, ctx->stream,
                        reinterpret_cast<const uint16_t*>(d_raw), nb, reinterpret_cast<uint32_t*>(qs), d);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_row_exponents(fh_ctx* ctx, const uint16_t* d, size_t n, size_t kb, int8_t* rexp) {
+    hipLaunchKernelGGL(k_row_exponents, dim3(grid_for(n)), dim3(kThreads), 0, ctx->stream, d, n, kb, rexp);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }

@@ -229,6 +229,74 @@ def test_gemm_propagates_inf_and_nan_like_the_reference(fh, orc):
     assert_close(got[fin], ref[fin], term_mass(orc, x, raw, n, k)[fin])
 
 
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4095, 96)])
+def test_gemm_weight_split_tiles_match(fh, orc, m, n, k):
+    """Shapes with >= 256 tiles of 256 x 256 take the kernel that folds the
+    block scales into an exact two-term f16 weight split; against the float64
+    product of the same weights (finite rows) and against the oracle on rows
+    with special values.  Weight rows of very different scale share tiles."""
+    import ferrum_hip
+
+    rng = np.random.default_rng(m + n + k)
+    w = rng.standard_normal((n, k)).astype(np.float32) * np.float32(0.02)
+    w[1::7] *= np.float32(1e-5)          # rows whose block scales are tiny
+    w[3::11, :32] *= np.float32(1e3)      # rows with one dominant block
+    w[5, :] = 0.0                         # an all-zero row (scales 0)
+    raw = orc.q8_0_encode(w.ravel())
+    x = acts(m, k, m + k)
+    special = [0, 1, 2, 3, 4, 5, 6, m - 1]
+    x[0, 3] = np.inf
+    x[1, 10] = np.nan
+    x[2] *= np.float32(1e-30)
+    x[3] *= np.float32(1e30)
+    x[4, :] = 0.0
+    x[6, 1], x[6, k - 1] = np.inf, -np.inf
+    b = bias_for(n, k)
+    wt = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    got = ferrum_hip.linear_forward(fh, x, wt, b)
+    wt.free()
+    plain = np.setdiff1d(np.arange(m), special)
+    mass = np.abs(x[plain].astype(np.float64)) @ np.abs(orc.q8_0_to_ferrum_weight(raw, n, k).astype(np.float64))
+    assert_close(got[plain], exact_linear(orc, x[plain], raw, n, k, b), mass)
+    ref = orc.q8_0_linear(x[special], raw, n, b)
+    g = got[special]
+    assert np.array_equal(np.isnan(g), np.isnan(ref))
+    assert np.array_equal(np.isposinf(g), np.isposinf(ref)) and np.array_equal(np.isneginf(g), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert_close(g[fin], ref[fin], term_mass(orc, x[special], raw, n, k)[fin])
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 96, 64), (5, 96, 64), (100, 300, 96), (4096, 4096, 64)])
+def test_non_finite_block_scales_match_the_reference(fh, orc, m, n, k):
+    """GGUF block scales of inf or NaN (f16 0x7C00 / 0x7E00), with zero and
+    non-zero quants in the block: inf * 0 = NaN and inf * q = +-inf per weight,
+    as the reference's f32 expansion has it.  Every path (GEMV, skinny, tiled,
+    weight-split) must reproduce the inf/NaN pattern and the finite values."""
+    import ferrum_hip
+
+    raw = orc.quantize_weight(n, k, 77 + m, 0.05).reshape(n, k // 32, 34).copy()
+    bad_rows = [2, 7, n - 1]
+    raw[2, 0, :2] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)       # +inf scale
+    raw[7, -1, :2] = np.frombuffer(np.uint16(0xFC00).tobytes(), np.uint8)      # -inf scale
+    raw[7, -1, 2:6] = 0                                                       # ... with zero quants
+    raw[n - 1, 1, :2] = np.frombuffer(np.uint16(0x7E00).tobytes(), np.uint8)   # NaN scale
+    raw = raw.ravel()
+    x = acts(m, k, 5 + m)
+    if m > 3:
+        x[3, 0] = 0.0                                                         # 0 * inf = NaN
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    got = ferrum_hip.linear_forward(fh, x, w, None)
+    w.free()
+    rows = np.unique(np.r_[0:min(m, 8), m - 1])
+    ref = orc.q8_0_linear(x[rows], raw, n, None)
+    g = got[rows]
+    assert np.array_equal(np.isnan(g), np.isnan(ref))
+    assert np.array_equal(np.isposinf(g), np.isposinf(ref)) and np.array_equal(np.isneginf(g), np.isneginf(ref))
+    assert not np.isfinite(ref[:, bad_rows]).any()
+    fin = np.isfinite(ref)
+    assert_close(g[fin], ref[fin], term_mass(orc, x[rows], raw, n, k)[fin])
+
+
 def test_expanded_weight_path_agrees(fh, orc):
     """The GPU result against ops::linear_forward on the f32 expansion the
     reference's loader builds (dequant + transpose), not only the row form."""
