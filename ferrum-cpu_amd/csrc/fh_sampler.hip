@@ -62,7 +62,7 @@ struct Shared {
     unsigned long long mass[kCopies][kBuckets];
     uint32_t rhist[256];
     unsigned long long rmass[256];
-    float slab[kW][kMaxItems];
+    alignas(16) float slab[kW][kMaxItems];
     float pa[256], pb[256];  // other workgroups' partials of the split kernel
     int qa[256], qb[256];
     float redf[kW];
@@ -593,20 +593,58 @@ __device__ __forceinline__ unsigned long long rl64(unsigned long long v, int lan
 // Sort one wave's keys (lanes < nc, distinct) descending: each lane counts the
 // keys above its own (readlane broadcasts, no LDS round trips), then the keys
 // are scattered to their ranks through `tmp` (64 entries of LDS).
-__device__ __forceinline__ unsigned long long wave_sort_desc(unsigned long long k, int nc, unsigned long long* tmp) {
+// Lane exchange with lane ^ S inside the wave, without LDS: DPP quad_perm for
+// 1 and 2, DPP row shifts left/right for 4 and 8, and the gfx950 half-row /
+// half-wave swaps (v_permlane16_swap, v_permlane32_swap) for 16 and 32.
+template <int S>
+__device__ __forceinline__ unsigned xor_lane(unsigned v) {
     const int lane = lane_id();
-    // lanes >= nc hold key 0, which is above no key: all 64 steps, no branches
-    k = lane < nc ? k : 0ull;
-    int rank = 0;
-#pragma unroll
-    for (int j = 0; j < 64; j++) rank += rl64(k, j) > k;
-    if (lane < nc) tmp[rank] = k;
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    const unsigned long long r = lane < nc ? tmp[lane] : 0ull;
-    __builtin_amdgcn_wave_barrier();
-    return r;
+    if constexpr (S == 1) return static_cast<unsigned>(dppi<0xB1>(static_cast<int>(v)));
+    else if constexpr (S == 2) return static_cast<unsigned>(dppi<0x4E>(static_cast<int>(v)));
+    else if constexpr (S == 4 || S == 8) {
+        const unsigned up = static_cast<unsigned>(dppi<0x100 + S>(static_cast<int>(v)));  // row_shl: lane + S
+        const unsigned dn = static_cast<unsigned>(dppi<0x110 + S>(static_cast<int>(v)));  // row_shr: lane - S
+        return (lane & S) ? dn : up;
+    } else if constexpr (S == 16) {
+        const auto r = __builtin_amdgcn_permlane16_swap(v, v, false, false);
+        return (lane & 16) ? r[0] : r[1];
+    } else {
+        static_assert(S == 32, "lane distance");
+        const auto r = __builtin_amdgcn_permlane32_swap(v, v, false, false);
+        return (lane & 32) ? r[0] : r[1];
+    }
+}
+
+// One compare-exchange of a bitonic network over the 64 lanes: blocks of SIZE
+// lanes alternate direction so the whole wave ends descending.
+template <int SIZE, int S>
+__device__ __forceinline__ unsigned long long bitonic_step(unsigned long long k) {
+    const int lane = lane_id();
+    const unsigned long long p = (static_cast<unsigned long long>(xor_lane<S>(static_cast<unsigned>(k >> 32))) << 32) |
+                                 xor_lane<S>(static_cast<unsigned>(k));
+    const bool keep_max = ((lane & S) == 0) == (SIZE == 64 || (lane & SIZE) == 0);
+    return keep_max == (p > k) ? p : k;
+}
+template <int SIZE>
+__device__ __forceinline__ unsigned long long bitonic_merge(unsigned long long k) {
+    if constexpr (SIZE >= 64) k = bitonic_step<SIZE, 32>(k);
+    if constexpr (SIZE >= 32) k = bitonic_step<SIZE, 16>(k);
+    if constexpr (SIZE >= 16) k = bitonic_step<SIZE, 8>(k);
+    if constexpr (SIZE >= 8) k = bitonic_step<SIZE, 4>(k);
+    if constexpr (SIZE >= 4) k = bitonic_step<SIZE, 2>(k);
+    return bitonic_step<SIZE, 1>(k);
+}
+
+// The wave's keys (lanes >= nc contribute 0, which is above no key) sorted
+// descending across the lanes, in registers: 21 compare-exchange steps.
+__device__ __forceinline__ unsigned long long wave_sort_desc(unsigned long long k, int nc) {
+    k = lane_id() < nc ? k : 0ull;
+    k = bitonic_merge<2>(k);
+    k = bitonic_merge<4>(k);
+    k = bitonic_merge<8>(k);
+    k = bitonic_merge<16>(k);
+    k = bitonic_merge<32>(k);
+    return bitonic_merge<64>(k);
 }
 
 // Running f32 sum over lanes 0..len-1 in lane order (the reference's
@@ -633,10 +671,10 @@ __device__ __forceinline__ float lane_running_sum(float v, int len) {
 // arguments; lane 0 writes *out.  Returns false, writing nothing, when the
 // top-p cut lies below the gathered ids.
 __device__ __forceinline__ bool wave_tail(unsigned long long key, int nc, int top_k, float top_p, bool use_k,
-                                          bool use_p, float r, uint32_t* __restrict__ out, unsigned long long* tmp) {
+                                          bool use_p, float r, uint32_t* __restrict__ out) {
     const int lane = lane_id();
     unsigned long long k = lane < nc ? key : 0ull;
-    k = wave_sort_desc(k, nc, tmp);
+    k = wave_sort_desc(k, nc);
     int len = nc;
     if (use_k) {
         const float thr = __builtin_bit_cast(float, rlu(static_cast<unsigned>(k >> 32), top_k - 1));
@@ -651,7 +689,7 @@ __device__ __forceinline__ bool wave_tail(unsigned long long key, int nc, int to
     }
     unsigned long long k2 =
         lane < len ? (static_cast<unsigned long long>(~static_cast<uint32_t>(key_i(k))) << 32) | (k >> 32) : 0ull;
-    k2 = wave_sort_desc(k2, len, tmp);  // descending ~index = ascending index
+    k2 = wave_sort_desc(k2, len);  // descending ~index = ascending index
     const float pl = lane < len ? __builtin_bit_cast(float, static_cast<unsigned>(k2)) : 0.0f;
     const int idx = static_cast<int>(~static_cast<unsigned>(k2 >> 32));
     // sum2 in index order, sequentially
@@ -940,8 +978,7 @@ __device__ __forceinline__ void sample_row(Shared& s, Row& row, const Params& P,
             const int nc = static_cast<int>(s.n_cand);
             if (nc <= 64) {
                 if (tid < 64) {
-                    const bool ok = wave_tail(s.u.cand[tid < nc ? tid : 0], nc, P.top_k, P.top_p, use_k, use_p, r, out,
-                                              reinterpret_cast<unsigned long long*>(&s.slab[0][0]));
+                    const bool ok = wave_tail(s.u.cand[tid < nc ? tid : 0], nc, P.top_k, P.top_p, use_k, use_p, r, out);
                     if (tid == 0) s.bi[2] = ok;
                 }
                 __syncthreads();
@@ -1377,8 +1414,7 @@ __global__ void __launch_bounds__(kT)
             const int nc = static_cast<int>(cload(&rs->n_cand));
             if (nc <= 64) {
                 if (tid < 64) {
-                    const bool ok = wave_tail(key, nc, P.top_k, P.top_p, use_k, use_p, r, o,
-                                              reinterpret_cast<unsigned long long*>(&s.slab[0][0]));
+                    const bool ok = wave_tail(key, nc, P.top_k, P.top_p, use_k, use_p, r, o);
                     if (tid == 0) s.bi[2] = ok;
                 }
                 __syncthreads();
