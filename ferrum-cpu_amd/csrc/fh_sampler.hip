@@ -1518,7 +1518,7 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
     // least 8192 ids.
     const size_t items = (vocab + kT - 1) / kT;
     if (vocab >= 8192 && rows <= 128) {
-        static const int kOpts[] = {4, 8, 16, 32};
+        static const int kOpts[] = {2, 4, 8, 16, 32};
         for (int it : kOpts) {
             const size_t S = (vocab + static_cast<size_t>(kT) * it - 1) / (static_cast<size_t>(kT) * it);
             if (S < 2 || rows * S > static_cast<size_t>(ctx->num_cus) || S > static_cast<size_t>(kSMax)) continue;
@@ -1531,6 +1531,7 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
             float* pbuf = static_cast<float*>(ws);
             const int s32 = static_cast<int>(S);
             switch (it) {
+                case 2: return launch_split<2>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
                 case 4: return launch_split<4>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
                 case 8: return launch_split<8>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
                 case 16: return launch_split<16>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
