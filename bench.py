@@ -263,6 +263,45 @@ def main():
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
                 "kernel": "k_gemv_w8a32<16,3,1,4,false> (lm_head 50257x768, Q8_0, m=1)",
                 "avg_launch_us": round(head_us, 3), "bytes_per_launch": head_bytes}
+    copy_GBps = None
+    if args.leg == "all":  # (kept out of the counter runs: their copy calibration must see one size)
+        # One GPU's share of a vocabulary-sharded head (50257 / 8 rows), the unit
+        # the multi-GPU design would run per rank; HBM-forced over 64 replicas.
+        shard_rows = (V + 7) // 8
+        shards = [make_weight(ctx, fh, torch, shard_rows, D, gen) for _ in range(64)]
+        shard_out = torch.empty((1, shard_rows), device=dev)
+        for i in range(64):
+            fh.linear_forward_async(ctx, shards[i], x_d, 1, D, None, 0, shard_out)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(400):
+            fh.linear_forward_async(ctx, shards[i % 64], x_d, 1, D, None, 0, shard_out)
+        e1.record()
+        torch.cuda.synchronize()
+        shard_us = e0.elapsed_time(e1) / 400 * 1e3
+        shard_bytes = q8_bytes(shard_rows, D) + 4 * D + 4 * shard_rows
+        result["shard_head"] = {"rows": shard_rows, "k": D, "us": round(shard_us, 3),
+                                "GBps": round(shard_bytes / (shard_us * 1e-6) / 1e9, 1)}
+        for w in shards:
+            w.free()
+        del shards
+
+        # Measured device copy bandwidth (1 GiB buffers, read + write counted), beside the 8 TB/s spec.
+        cbytes = 1 << 30
+        csrc = torch.empty(cbytes // 4, device=dev)
+        cdst = torch.empty_like(csrc)
+        for _ in range(3):
+            cdst.copy_(csrc)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(10):
+            cdst.copy_(csrc)
+        e1.record()
+        torch.cuda.synchronize()
+        copy_GBps = 2 * cbytes * 10 / (e0.elapsed_time(e1) * 1e-3) / 1e9
+        del csrc, cdst
+
     if args.leg == "head":
         # A plain device copy of known size, for scaling the PMC byte counters
         # (FETCH_SIZE / WRITE_SIZE) of the same run.
@@ -305,6 +344,8 @@ def main():
         "wall_ms_per_step": round(result["wall_ms_per_step"], 5),
         "b32": result["b32"],
         "prefill": result["prefill"],
+        "hbm_copy_GBps": round(copy_GBps, 1) if copy_GBps else None,
+        "shard_head_gemv": result["shard_head"],
     }
     print(json.dumps(line))
 
@@ -393,11 +434,44 @@ def cpu_baseline(budget_s):
         one_step()
         times.append(time.perf_counter() - t0)
     best, med = min(times), float(np.median(times))
-    return {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": 1, "kind": "port",
-            "sample": f"{len(times)} GPT-2-124M decode steps of the hot path (49 f32-expanded linears, serial "
-                      f"m=1 as ferrum_core runs them, + softmax/ln bridge + sampler) in {sum(times):.1f} s; "
-                      f"median {med * 1e3:.1f} ms/step, best {best * 1e3:.1f} ms; setup {setup:.1f} s",
-            "best_tok_s": round(1.0 / best, 3)}
+    out = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": 1, "kind": "port",
+           "sample": f"{len(times)} GPT-2-124M decode steps of the hot path (49 f32-expanded linears, serial "
+                     f"m=1 as ferrum_core runs them, + softmax/ln bridge + sampler) in {sum(times):.1f} s; "
+                     f"median {med * 1e3:.1f} ms/step, best {best * 1e3:.1f} ms; setup {setup:.1f} s",
+           "best_tok_s": round(1.0 / best, 3)}
+
+    # Second figure: the reference's only multi-core m = 1 decode, ops::qlinear
+    # on per-row int8 QWeights (column split over T threads, min chunk 64).
+    # Not the GPU path's numerics (those are GGUF Q8_0); a CPU bandwidth figure.
+    threads = max(1, min(os.cpu_count() or 1, 16))
+    qlayers = [[(oracle.QWeight(w_kn, w_kn.shape[0], w_kn.shape[1], oracle.INT8), b) for (w_kn, b) in ws]
+               for ws in layers]
+    qhead = oracle.QWeight(head, head.shape[0], head.shape[1], oracle.INT8)
+    zero_v = np.zeros(V, np.float32)
+
+    def one_qstep():
+        for ws in qlayers:
+            for (qw, b), (n, k) in zip(ws, LAYER_SHAPES):
+                oracle.qlinear(x_d if k == D else x_f, qw, b, threads=threads)
+        z = oracle.qlinear(x_d, qhead, zero_v, threads=threads)
+        l = oracle.ln_bridge(oracle.softmax_rows(z)[0])
+        oracle.sample_with_params(l, params, recent, orng)
+
+    one_qstep()
+    qt = []
+    t_end = time.perf_counter() + budget_s / 2
+    while time.perf_counter() < t_end or len(qt) < 3:
+        t0 = time.perf_counter()
+        one_qstep()
+        qt.append(time.perf_counter() - t0)
+    qmed = float(np.median(qt))
+    qbytes = sum(qw.q.size + qw.scales.size * 4 for ws in qlayers for (qw, _) in ws) + qhead.q.size + qhead.scales.size * 4
+    out["qlinear_int8"] = {"value": round(1.0 / qmed, 3), "unit": "tok/s", "cores": threads, "kind": "port",
+                           "weight_GBps": round(qbytes / qmed / 1e9, 2),
+                           "sample": f"{len(qt)} GPT-2-124M decode steps through ops::qlinear (per-row int8, "
+                                     f"{qbytes / 1e6:.0f} MB/token, m = 1 column split over {threads} threads); "
+                                     f"median {qmed * 1e3:.1f} ms/step"}
+    return out
 
 
 if __name__ == "__main__":

@@ -74,6 +74,25 @@ __device__ __attribute__((noinline)) float exact_dot(const float* __restrict__ x
     return s;
 }
 
+// The outputs of one tile whose activation row is flagged (xbad, may be null)
+// or whose weight row has a non-finite scale, recomputed by exact_dot.  Every
+// thread of the workgroup calls; a barrier first orders the tile's ordinary
+// stores before these.
+__device__ __attribute__((noinline)) void exact_tile(const float* __restrict__ x, const int8_t* __restrict__ qs,
+                                                     const uint16_t* __restrict__ dsc, const int8_t* __restrict__ rexp,
+                                                     const uint8_t* __restrict__ xbad, const float* __restrict__ bias,
+                                                     float* __restrict__ y, int m, int n, int k, int i0, int j0,
+                                                     int bm, int bn) {
+    __syncthreads();
+    for (int o = threadIdx.x; o < bm * bn; o += blockDim.x) {
+        const int i = i0 + o / bn, j = j0 + o % bn;
+        if (i >= m || j >= n || !((xbad && xbad[i]) || rexp[j] == kFhBadRowExp)) continue;
+        const float s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(j) * k,
+                                  dsc + static_cast<size_t>(j) * (k >> 5));
+        y[static_cast<size_t>(i) * n + j] = bias ? s + bias[j] : s;
+    }
+}
+
 }  // namespace
 
 // One wave per activation row (rows m .. m_pad - 1 are written as zeros).
@@ -290,26 +309,28 @@ __global__ void __launch_bounds__(64 * WM * WN * KW)
     __syncthreads();
     for (int t = tid; t < BM; t += NT) s_inv[t] = xinv[i0 + t];  // rows < m_pad
     __syncthreads();
-    if (KW > 1 && kw > 0) return;
+    if (KW == 1 || kw == 0) {  // K-slice 0 holds the totals
 #pragma unroll
-    for (int c = 0; c < TN; c++) {
-        const int j = j0 + (wn * TN + c) * 32 + arow;
-        if (j >= n) continue;
-        const bool jbad = rexp[j] == kFhBadRowExp;
-        const float bj = bias ? bias[j] : 0.0f;
+        for (int c = 0; c < TN; c++) {
+            const int j = j0 + (wn * TN + c) * 32 + arow;
+            if (j >= n) continue;
+            const float bj = bias ? bias[j] : 0.0f;
 #pragma unroll
-        for (int r = 0; r < TM; r++)
+            for (int r = 0; r < TM; r++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                const int il = (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4), i = i0 + il;
-                if (i >= m) continue;
-                float s = acc[r][c][v] * s_inv[il];
-                if (__builtin_expect(jbad, 0))
-                    s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(j) * k,
-                                  dsc + static_cast<size_t>(j) * kb);
-                y[static_cast<size_t>(i) * n + j] = bias ? s + bj : s;
-            }
+                for (int v = 0; v < 16; v++) {
+                    const int il = (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4), i = i0 + il;
+                    if (i >= m) continue;
+                    const float s = acc[r][c][v] * s_inv[il];
+                    y[static_cast<size_t>(i) * n + j] = bias ? s + bj : s;
+                }
+        }
     }
+    // Rare: weight rows with a non-finite scale are rewritten with the
+    // reference's own arithmetic (inf/NaN activations propagate exactly here).
+    bool flagged = false;
+    for (int t = tid; t < BN; t += NT) flagged |= j0 + t < n && rexp[j0 + t] == kFhBadRowExp;
+    if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, nullptr, bias, y, m, n, k, i0, j0, BM, BN);
 }
 
 // ---- large m: both operands split, block scales folded into the weights ----------
@@ -454,8 +475,8 @@ __global__ void __launch_bounds__(64 * WM * WN)
     for (int c = 0; c < TN; c++) {
         const int j = j0 + (wn * TN + c) * 32 + arow;
         if (j >= n) continue;
-        const bool jbad = rexp[j] == kFhBadRowExp;
-        const float winv = __builtin_bit_cast(float, static_cast<uint32_t>(127 - (jbad ? 0 : rexp[j])) << 23);
+        const float winv = __builtin_bit_cast(
+            float, static_cast<uint32_t>(127 - (rexp[j] == kFhBadRowExp ? 0 : rexp[j])) << 23);
         const float bj = bias ? bias[j] : 0.0f;
 #pragma unroll
         for (int r = 0; r < TM; r++)
@@ -463,13 +484,16 @@ __global__ void __launch_bounds__(64 * WM * WN)
             for (int v = 0; v < 16; v++) {
                 const int il = (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4), i = i0 + il;
                 if (i >= m) continue;
-                float s = acc[r][c][v] * s_inv[il] * winv;
-                if (__builtin_expect(jbad || s_bad[il], 0))
-                    s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(j) * k,
-                                  dsc + static_cast<size_t>(j) * kb);
+                const float s = acc[r][c][v] * s_inv[il] * winv;
                 y[static_cast<size_t>(i) * n + j] = bias ? s + bj : s;
             }
     }
+    // Rare: rows with inf/NaN activations or weight rows with a non-finite
+    // scale are rewritten with the reference's own arithmetic.
+    bool flagged = false;
+    for (int t = tid; t < BM || t < BN; t += NTH)
+        flagged |= (t < BM && s_bad[t]) || (t < BN && j0 + t < n && rexp[j0 + t] == kFhBadRowExp);
+    if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, xbad, bias, y, m, n, k, i0, j0, BM, BN);
 }
 
 // ---- skinny m (batched decode): m <= 32 * MT ------------------------------------

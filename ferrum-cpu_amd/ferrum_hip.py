@@ -349,3 +349,78 @@ def sample_with_params(ctx: Context, logits, params: SamplingParams, recent, rng
     draw = None if params.temperature <= 0.0 else [rng.next_u64()]
     return int(sample_rows(ctx, np.asarray(logits, np.float32)[None, :], params, [list(recent)], draw,
                            logits_kind)[0])
+
+
+# ---- decode loops at the token level (the callers of the hot path) -------------------
+# The model between two samples (embedding, attention, norms, GELU) belongs to
+# the caller: `forward` hands back the next position's raw head scores.
+
+class GPT2Window:
+    """The token window of GenerativeSLM::token_stream / stream_next
+    (slm/token_stream.rs:66-111, 150-168): capacity = the model's context
+    (at least 1), keep = capacity / 2 (at least 1).  The prompt (or [bos] when
+    empty) is cut to its last `capacity` ids; every sampled id that is not EOS
+    is appended, and a window that outgrows the capacity is cut to its last
+    `keep` ids and re-primed.  The window is also the penalty history."""
+
+    def __init__(self, capacity: int, prompt, bos: int = 0):
+        self.cap = max(int(capacity), 1)
+        self.keep = max(self.cap // 2, 1)
+        ids = [int(t) for t in prompt] or [int(bos)]
+        self.ids = ids[-self.cap:] if len(ids) > self.cap else ids
+
+    def push(self, tok: int) -> bool:
+        """Append a sampled id; True when the window was cut and must be re-primed."""
+        self.ids.append(int(tok))
+        if len(self.ids) > self.cap:
+            self.ids = self.ids[len(self.ids) - self.keep:]
+            return True
+        return False
+
+
+def gpt2_decode(ctx: Context, forward, prompt, max_tokens: int, params: SamplingParams, rng: Rng,
+                capacity: int, eos=None, bos: int = 0):
+    """Token-level stream_next loop (slm/token_stream.rs:121-190).
+    forward(window_ids, reprime) -> raw head scores z of the next position
+    (reprime: the whole window was (re)fed, else only its last id).  Each step
+    samples with the softmax -> ln(max(p, 1e-12)) bridge fused into the
+    sampler, the window as the penalty history, and one draw from rng unless
+    greedy.  Stops at max_tokens or EOS (not appended).  Returns the ids."""
+    win = GPT2Window(capacity, prompt, bos)
+    z = forward(list(win.ids), True)
+    out = []
+    while len(out) < max_tokens:
+        nxt = sample_with_params(ctx, z, params, win.ids, rng, LOGITS_GPT2_SOFTMAX)
+        if eos is not None and nxt == eos:
+            break
+        out.append(nxt)
+        reprime = win.push(nxt)
+        z = forward(list(win.ids), reprime)
+    return out
+
+
+def llama_decode(ctx: Context, forward_one, prompt, max_new: int, params: SamplingParams, rng: Rng,
+                 context_len: int, stops=()):
+    """LlamaModel::generate_inner at the token level (llm.rs:706-754): a
+    non-empty prompt shorter than the context, max_new clipped to
+    context - prompt, every prompt and generated id as the penalty history, a
+    stop id returned but not fed.  forward_one(token) -> raw logits."""
+    prompt = [int(t) for t in prompt]
+    if not prompt:
+        raise DimMismatch(FH_ERR_DIM, "prompt must be non-empty")
+    if len(prompt) >= context_len:
+        raise DimMismatch(FH_ERR_DIM, f"prompt of {len(prompt)} tokens does not fit the model's "
+                                      f"{context_len}-token context window")
+    max_new = min(int(max_new), context_len - len(prompt))
+    logits = None
+    for tok in prompt:
+        logits = forward_one(tok)
+    out, recent = [], list(prompt)
+    for _ in range(max_new):
+        nxt = sample_with_params(ctx, logits, params, recent, rng, LOGITS_RAW)
+        out.append(nxt)
+        if nxt in stops:
+            break
+        recent.append(nxt)
+        logits = forward_one(nxt)
+    return out

@@ -331,6 +331,138 @@ int fo_q8_0_linear_rows(const float* x, size_t m, size_t k, const uint8_t* raw, 
 }
 
 /* ------------------------------------------------------------------------ */
+/* Packed per-row int8 / int4 weights: QWeight and ops::qlinear               */
+/* ------------------------------------------------------------------------ */
+
+/* f32 -> integer level as Rust's `(v * inv).round().clamp(-lim, lim) as i8/i32`:
+ * round half away from zero, saturating, NaN -> 0. */
+static int q_level(float v, float lim) {
+    if (v != v) return 0;
+    float r = roundf(v);
+    if (r < -lim) r = -lim;
+    if (r > lim) r = lim;
+    return (int)r;
+}
+
+/* quant.rs:17-19 int8_scale / the int4 amax: fold max(abs) from 0 (NaN ignored). */
+static float row_amax(const float* row, size_t n) {
+    float m = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        float a = fabsf(row[i]);
+        if (a > m) m = a; /* a NaN compares false: skipped, as f32::max does */
+    }
+    return m;
+}
+
+size_t fo_qweight_row_bytes(size_t cols, int kind) { return kind == 0 ? cols : (cols + 1) / 2; }
+
+void fo_qweight_from_f32(const float* data, size_t rows, size_t cols, int kind, float* scales, uint8_t* q) {
+    size_t rb = fo_qweight_row_bytes(cols, kind), half = (cols + 1) / 2;
+    memset(q, 0, rows * rb);
+    for (size_t r = 0; r < rows; r++) {
+        const float* row = data + r * cols;
+        float scale = row_amax(row, cols) / (kind == 0 ? 127.0f : 7.0f);
+        scales[r] = scale;
+        float inv = scale > 0.0f ? 1.0f / scale : 0.0f;
+        uint8_t* dst = q + r * rb;
+        for (size_t c = 0; c < cols; c++) {
+            if (kind == 0) {
+                dst[c] = (uint8_t)(int8_t)q_level(row[c] * inv, 127.0f);
+            } else {
+                uint8_t nib = (uint8_t)(q_level(row[c] * inv, 7.0f) & 0x0F);
+                if (c < half)
+                    dst[c] = (uint8_t)((dst[c] & 0xF0) | nib);
+                else
+                    dst[c - half] = (uint8_t)((dst[c - half] & 0x0F) | (nib << 4));
+            }
+        }
+    }
+}
+
+static float qweight_level(const uint8_t* row, size_t c, size_t half, int kind) {
+    if (kind == 0) return (float)(int8_t)row[c];
+    uint8_t nib = c < half ? (uint8_t)(row[c] & 0x0F) : (uint8_t)(row[c - half] >> 4);
+    return (float)(int8_t)((int8_t)(nib << 4) >> 4); /* quant.rs:222-225 nibble_to_i8 */
+}
+
+void fo_qweight_to_f32(const float* scales, const uint8_t* q, size_t rows, size_t cols, int kind, float* out) {
+    size_t rb = fo_qweight_row_bytes(cols, kind), half = (cols + 1) / 2;
+    for (size_t r = 0; r < rows; r++)
+        for (size_t c = 0; c < cols; c++) out[r * cols + c] = qweight_level(q + r * rb, c, half, kind) * scales[r];
+}
+
+/* ops.rs:268-305 qaccum_cols: out[j - j0] += a[p] * level(p, j), p ascending. */
+static void qaccum_cols(const float* a, size_t k, const uint8_t* q, size_t cols, int kind, size_t j0, size_t j1,
+                        float* out) {
+    size_t rb = fo_qweight_row_bytes(cols, kind), half = (cols + 1) / 2;
+    for (size_t p = 0; p < k; p++) {
+        const uint8_t* row = q + p * rb;
+        float ap = a[p];
+        for (size_t j = j0; j < j1; j++) out[j - j0] += ap * qweight_level(row, j, half, kind);
+    }
+}
+
+typedef struct {
+    const float* a;
+    size_t k, n, r0, r1, j0, j1;
+    const uint8_t* q;
+    int kind;
+    const float* bias;
+    float* y;
+} q_job;
+
+static void* q_job_run(void* arg) {
+    q_job* j = (q_job*)arg;
+    for (size_t i = j->r0; i < j->r1; i++) {
+        float* o = j->y + i * j->n;
+        for (size_t c = j->j0; c < j->j1; c++) o[c] = j->bias[c];
+        qaccum_cols(j->a + i * j->k, j->k, j->q, j->n, j->kind, j->j0, j->j1, o + j->j0);
+    }
+    return NULL;
+}
+
+int fo_qlinear(const float* x, size_t m, size_t k, const float* scales, const uint8_t* q, size_t n, int kind,
+               const float* bias, float* y, int threads) {
+    /* a'[i, p] = x[i, p] * scale[p] (ops.rs:331-339) */
+    float* a = (float*)malloc((m * k > 0 ? m * k : 1) * sizeof(float));
+    if (!a) return -1;
+    for (size_t i = 0; i < m; i++)
+        for (size_t p = 0; p < k; p++) a[i * k + p] = x[i * k + p] * scales[p];
+    q_job jobs[256];
+    size_t nj = 0;
+    if (m == 1 && threads > 1 && n >= 2 && n * k >= (1u << 16)) {
+        /* parallel.rs:313-366, 370-372: column split, min chunk 64 */
+        size_t t = (size_t)threads, cap = (n + 63) / 64;
+        if (t > cap) t = cap;
+        if (t > 256) t = 256;
+        size_t per = (n + t - 1) / t;
+        for (size_t j0 = 0; j0 < n; j0 += per)
+            jobs[nj++] = (q_job){a, k, n, 0, 1, j0, j0 + per < n ? j0 + per : n, q, kind, bias, y};
+    } else if (m >= 2 && threads > 1 && m * k * n >= (1u << 16)) {
+        /* parallel.rs:90-92, 168-297: row split */
+        size_t t = (size_t)threads < m ? (size_t)threads : m;
+        if (t > 256) t = 256;
+        size_t per = (m + t - 1) / t;
+        for (size_t r0 = 0; r0 < m; r0 += per)
+            jobs[nj++] = (q_job){a, k, n, r0, r0 + per < m ? r0 + per : m, 0, n, q, kind, bias, y};
+    } else {
+        jobs[nj++] = (q_job){a, k, n, 0, m, 0, n, q, kind, bias, y};
+    }
+    pthread_t tids[256];
+    int started[256];
+    for (size_t i = 1; i < nj; i++) started[i] = pthread_create(&tids[i], NULL, q_job_run, &jobs[i]) == 0;
+    q_job_run(&jobs[0]);
+    for (size_t i = 1; i < nj; i++) {
+        if (started[i])
+            pthread_join(tids[i], NULL);
+        else
+            q_job_run(&jobs[i]);
+    }
+    free(a);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* W8A8                                                                       */
 /* ------------------------------------------------------------------------ */
 

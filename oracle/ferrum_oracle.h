@@ -73,6 +73,23 @@ int fo_linear_forward(const float* x, size_t m, size_t k, const float* w_kn, siz
 int fo_q8_0_linear_rows(const float* x, size_t m, size_t k, const uint8_t* raw, size_t n,
                         const float* bias, float* y);
 
+/* ---- packed per-row int8 / int4 weights (adjacent path, not GGUF Q8_0) ---- */
+/* quant.rs:130-217 QWeight::from_f32: row-major [rows, cols], one symmetric
+ * scale per row (amax/127 int8, amax/7 int4), levels round-half-away
+ * saturating (NaN -> 0); int4 in the split-half nibble layout (column c < half
+ * in the low nibble of byte c, else the high nibble of byte c - half).
+ * kind 0 = int8, 1 = int4. */
+size_t fo_qweight_row_bytes(size_t cols, int kind);
+void fo_qweight_from_f32(const float* data, size_t rows, size_t cols, int kind, float* scales, uint8_t* q);
+/* quant.rs:228-254 dequant_row over all rows. */
+void fo_qweight_to_f32(const float* scales, const uint8_t* q, size_t rows, size_t cols, int kind, float* out);
+/* ops.rs:268-377 qlinear: y[i, j] = bias[j] + sum_p (x[i, p] * scale[p]) * level(p, j),
+ * p ascending, no FMA, bias FIRST; k = rows, n = cols.  m == 1 splits columns
+ * over threads (min chunk 64, parallel.rs:313-372), m >= 2 splits rows; the
+ * result does not depend on the thread count. */
+int fo_qlinear(const float* x, size_t m, size_t k, const float* scales, const uint8_t* q, size_t n, int kind,
+               const float* bias, float* y, int threads);
+
 /* ---- W8A8 (activation re-quantization, llama.cpp semantics) ------------- */
 /* Activations are Q8_0-encoded with fo_q8_0_block per 32 (quant.rs:271-280).
  * d16: [m, k/32], q: [m, k]. */

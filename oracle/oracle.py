@@ -104,6 +104,13 @@ def lib():
         L.fo_q8_0_linear_w8a8.argtypes = [_f32p, C.c_size_t, C.c_size_t, _u8p, C.c_size_t,
                                           C.c_void_p, _f32p]
         L.fo_q8_0_linear_w8a8.restype = C.c_int
+        L.fo_qweight_row_bytes.argtypes = [C.c_size_t, C.c_int]
+        L.fo_qweight_row_bytes.restype = C.c_size_t
+        L.fo_qweight_from_f32.argtypes = [_f32p, C.c_size_t, C.c_size_t, C.c_int, _f32p, _u8p]
+        L.fo_qweight_to_f32.argtypes = [_f32p, _u8p, C.c_size_t, C.c_size_t, C.c_int, _f32p]
+        L.fo_qlinear.argtypes = [_f32p, C.c_size_t, C.c_size_t, _f32p, _u8p, C.c_size_t, C.c_int, _f32p, _f32p,
+                                 C.c_int]
+        L.fo_qlinear.restype = C.c_int
         L.fo_softmax_rows.argtypes = [_f32p, C.c_size_t, C.c_size_t, _f32p]
         L.fo_ln_bridge.argtypes = [_f32p, C.c_size_t, _f32p]
         L.fo_rng_new.argtypes = [C.c_uint64]
@@ -267,6 +274,44 @@ def q8_0_linear_w8a8(x, raw, n: int, bias=None) -> np.ndarray:
     b = None if bias is None else _f32(bias)
     y = np.zeros((m, n), np.float32)
     lib().fo_q8_0_linear_w8a8(x, m, k, np.ascontiguousarray(raw, np.uint8).ravel(), n, _ptr(b), y)
+    return y
+
+
+# ---- packed per-row int8 / int4 weights (QWeight, ops::qlinear) ------------
+
+INT8, INT4 = 0, 1
+
+
+class QWeight:
+    """quant.rs:130-217: [rows = in_features, cols = out_features], one scale per row."""
+
+    def __init__(self, data, rows: int, cols: int, kind: int):
+        data = _f32(np.asarray(data).reshape(rows, cols))
+        self.rows, self.cols, self.kind = rows, cols, kind
+        self.scales = np.zeros(rows, np.float32)
+        self.q = np.zeros(rows * int(lib().fo_qweight_row_bytes(cols, kind)), np.uint8)
+        lib().fo_qweight_from_f32(data, rows, cols, kind, self.scales, self.q)
+
+    def row_bytes(self) -> int:
+        return int(lib().fo_qweight_row_bytes(self.cols, self.kind))
+
+    def to_f32(self) -> np.ndarray:
+        out = np.zeros((self.rows, self.cols), np.float32)
+        lib().fo_qweight_to_f32(self.scales, self.q, self.rows, self.cols, self.kind, out)
+        return out
+
+
+def qlinear(x, w: QWeight, bias, threads: int = 1) -> np.ndarray:
+    """ops::qlinear (ops.rs:316-377): bias first, then (x * scale) . level, p ascending."""
+    x = _f32(np.atleast_2d(x))
+    m, k = x.shape
+    if k != w.rows:
+        raise ValueError(f"qlinear: input width {k} != weight rows {w.rows}")
+    b = _f32(bias)
+    if b.size != w.cols:
+        raise ValueError(f"qlinear: bias length {b.size} != out_features {w.cols}")
+    y = np.zeros((m, w.cols), np.float32)
+    lib().fo_qlinear(x, m, k, w.scales, w.q, w.cols, w.kind, b, y, int(threads))
     return y
 
 
