@@ -18,6 +18,7 @@
 #include <float.h>
 #include <math.h>
 #include <pthread.h>
+#include <stdint.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -391,15 +392,87 @@ void fo_qweight_to_f32(const float* scales, const uint8_t* q, size_t rows, size_
         for (size_t c = 0; c < cols; c++) out[r * cols + c] = qweight_level(q + r * rb, c, half, kind) * scales[r];
 }
 
-/* ops.rs:268-305 qaccum_cols: out[j - j0] += a[p] * level(p, j), p ascending. */
+/* ops.rs:268-305 qaccum_cols: out[j - j0] += a[p] * level(p, j), p ascending.
+ * Int8 walks each weight row as one contiguous i8 run; int4 as the two
+ * contiguous nibble lanes of the split-half layout (a low-nibble pass over
+ * [j0, min(j1, half)), a high-nibble pass over [max(j0, half), j1)), the same
+ * order and arithmetic, written so the compiler vectorises them. */
 static void qaccum_cols(const float* a, size_t k, const uint8_t* q, size_t cols, int kind, size_t j0, size_t j1,
                         float* out) {
     size_t rb = fo_qweight_row_bytes(cols, kind), half = (cols + 1) / 2;
     for (size_t p = 0; p < k; p++) {
         const uint8_t* row = q + p * rb;
-        float ap = a[p];
-        for (size_t j = j0; j < j1; j++) out[j - j0] += ap * qweight_level(row, j, half, kind);
+        const float ap = a[p];
+        if (kind == 0) {
+            const int8_t* r8 = (const int8_t*)row;
+            for (size_t j = j0; j < j1; j++) out[j - j0] += ap * (float)r8[j];
+        } else {
+            size_t lo_end = j1 < half ? j1 : half, hi_start = j0 > half ? j0 : half;
+            for (size_t j = j0; j < lo_end; j++) out[j - j0] += ap * (float)(int8_t)((int8_t)(row[j] << 4) >> 4);
+            for (size_t j = hi_start; j < j1; j++) out[j - j0] += ap * (float)((int8_t)row[j - half] >> 4);
+        }
     }
+}
+
+/* A persistent worker pool, as the reference keeps one (parallel.rs:94-166):
+ * workers are created once and wait on a condition variable; a parallel call
+ * hands job i to worker i - 1 and runs job 0 itself.  The partition (and so
+ * the result) is the caller's; the pool only saves creating threads per call. */
+typedef void* (*pool_fn)(void*);
+static struct {
+    pthread_mutex_t mu;
+    pthread_cond_t go, done;
+    pthread_t tids[256];
+    int n;                 /* workers started */
+    unsigned long gen;     /* bumps once per dispatch */
+    int pending;
+    pool_fn fn;
+    char* args;
+    size_t stride;
+    int njobs;
+} g_pool = {PTHREAD_MUTEX_INITIALIZER, PTHREAD_COND_INITIALIZER, PTHREAD_COND_INITIALIZER};
+
+static void* pool_worker(void* arg) {
+    const int id = (int)(intptr_t)arg; /* runs job id + 1 */
+    unsigned long seen = 0;
+    pthread_mutex_lock(&g_pool.mu);
+    for (;;) {
+        while (g_pool.gen == seen) pthread_cond_wait(&g_pool.go, &g_pool.mu);
+        seen = g_pool.gen;
+        if (id + 1 < g_pool.njobs) {
+            pool_fn fn = g_pool.fn;
+            void* a = g_pool.args + (size_t)(id + 1) * g_pool.stride;
+            pthread_mutex_unlock(&g_pool.mu);
+            fn(a);
+            pthread_mutex_lock(&g_pool.mu);
+            if (--g_pool.pending == 0) pthread_cond_signal(&g_pool.done);
+        }
+    }
+    return NULL;
+}
+
+/* Run fn over njobs job records (stride bytes apart); returns when all are done. */
+static void pool_run(pool_fn fn, void* args, size_t stride, int njobs) {
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.n < njobs - 1 && g_pool.n < 256) {
+        if (pthread_create(&g_pool.tids[g_pool.n], NULL, pool_worker, (void*)(intptr_t)g_pool.n) != 0) break;
+        pthread_detach(g_pool.tids[g_pool.n]);
+        g_pool.n++;
+    }
+    int remote = njobs - 1 < g_pool.n ? njobs - 1 : g_pool.n;
+    g_pool.fn = fn;
+    g_pool.args = (char*)args;
+    g_pool.stride = stride;
+    g_pool.njobs = remote + 1;
+    g_pool.pending = remote;
+    g_pool.gen++;
+    pthread_cond_broadcast(&g_pool.go);
+    pthread_mutex_unlock(&g_pool.mu);
+    fn(args);
+    for (int i = remote + 1; i < njobs; i++) fn((char*)args + (size_t)i * stride); /* no worker: run here */
+    pthread_mutex_lock(&g_pool.mu);
+    while (g_pool.pending > 0) pthread_cond_wait(&g_pool.done, &g_pool.mu);
+    pthread_mutex_unlock(&g_pool.mu);
 }
 
 typedef struct {
@@ -448,16 +521,7 @@ int fo_qlinear(const float* x, size_t m, size_t k, const float* scales, const ui
     } else {
         jobs[nj++] = (q_job){a, k, n, 0, m, 0, n, q, kind, bias, y};
     }
-    pthread_t tids[256];
-    int started[256];
-    for (size_t i = 1; i < nj; i++) started[i] = pthread_create(&tids[i], NULL, q_job_run, &jobs[i]) == 0;
-    q_job_run(&jobs[0]);
-    for (size_t i = 1; i < nj; i++) {
-        if (started[i])
-            pthread_join(tids[i], NULL);
-        else
-            q_job_run(&jobs[i]);
-    }
+    pool_run(q_job_run, jobs, sizeof(q_job), (int)nj);
     free(a);
     return 0;
 }
