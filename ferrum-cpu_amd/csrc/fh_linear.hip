@@ -99,9 +99,11 @@ __global__ void __launch_bounds__(64 * kWaves)
     for (int sb = set0; sb < set1; sb += U) {
         uint4 qv[U][CPL];
         uint32_t dh[U][CPL];
+        // Row-sets past this wave's range re-read its last one (cache hits,
+        // never computed), so no other wave's rows are fetched twice.
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int row = min((sb + u) * RW + grp, n - 1);
+            const int row = min(min(sb + u, set1 - 1) * RW + grp, n - 1);
 #pragma unroll
             for (int c = 0; c < CPL; c++) {
                 const int ci = min(gl + c * G, k16 - 1);
@@ -114,7 +116,7 @@ __global__ void __launch_bounds__(64 * kWaves)
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const bool live = sb + u < set1;  // dead row-sets run on clamped data, unstored
+            if (sb + u >= set1) break;  // wave-uniform: a short last batch skips its empty slots
             float acc[M];
 #pragma unroll
             for (int m = 0; m < M; m++) acc[m] = 0.0f;
@@ -137,7 +139,7 @@ __global__ void __launch_bounds__(64 * kWaves)
             if (G <= 16) {
 #pragma unroll
                 for (int m = 0; m < M; m++) acc[m] = group_sum<G>(acc[m]);
-                if (live && gl == 0 && row < n) {
+                if (gl == 0 && row < n) {
 #pragma unroll
                     for (int m = 0; m < M; m++)
                         y[static_cast<size_t>(m) * n + row] = kBias ? acc[m] + bias[row] : acc[m];
@@ -150,7 +152,7 @@ __global__ void __launch_bounds__(64 * kWaves)
                     const float lo = rdlane(r16, 0) + rdlane(r16, 16);
                     const float hi = rdlane(r16, 32) + rdlane(r16, 48);
                     const float tot = G == 64 ? lo + hi : (grp == 0 ? lo : hi);
-                    if (live && gl == 0 && row < n) y[static_cast<size_t>(m) * n + row] = kBias ? tot + bias[row] : tot;
+                    if (gl == 0 && row < n) y[static_cast<size_t>(m) * n + row] = kBias ? tot + bias[row] : tot;
                 }
             }
         }

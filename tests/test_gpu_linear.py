@@ -229,12 +229,14 @@ def test_gemm_propagates_inf_and_nan_like_the_reference(fh, orc):
     assert_close(got[fin], ref[fin], term_mass(orc, x, raw, n, k)[fin])
 
 
-@pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4095, 96)])
+@pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4095, 96), (4096, 4352, 128), (4000, 4100, 256),
+                                   (4352, 4096, 192)])
 def test_gemm_weight_split_tiles_match(fh, orc, m, n, k):
     """Shapes with >= 256 tiles of 256 x 256 take the kernel that folds the
-    block scales into an exact two-term f16 weight split; against the float64
-    product of the same weights (finite rows) and against the oracle on rows
-    with special values.  Weight rows of very different scale share tiles."""
+    block scales into an exact two-term f16 weight split (2 to 8 Q8_0 blocks
+    per row, ragged m and n); against the float64 product of the same weights
+    (finite rows) and against the oracle on rows with special values.  Weight
+    rows of very different scale share tiles."""
     import ferrum_hip
 
     rng = np.random.default_rng(m + n + k)
