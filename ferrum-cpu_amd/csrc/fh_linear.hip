@@ -21,6 +21,8 @@
 //                sum_b f32(dot_b) * (d_w * d_x) + b.
 #include "fh_internal.hpp"
 
+#include <type_traits>
+
 __global__ void fh_k_encode_split(const float* __restrict__ x, size_t nblocks, uint32_t* __restrict__ qx,
                                   uint16_t* __restrict__ dx);
 
@@ -96,27 +98,33 @@ __global__ void __launch_bounds__(64 * kWaves)
         }
     }
 
-    for (int sb = set0; sb < set1; sb += U) {
+    // One batch of row-sets [sb, sb + U).  Full batches have no branches, so
+    // every load is consumed before the next batch reuses its registers.  The
+    // short last batch (kTail) loads its own row-sets only (slots past the end
+    // re-read its last row-set: cache hits, never computed) and skips the
+    // empty slots; nothing follows it.
+    auto batch = [&](int sb, auto tail) __attribute__((always_inline)) {
+        constexpr bool kTail = decltype(tail)::value;
         uint4 qv[U][CPL];
         uint32_t dh[U][CPL];
-        // Row-sets past this wave's range re-read its last one (cache hits,
-        // never computed), so no other wave's rows are fetched twice.
+        float bv[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            const int row = min(min(sb + u, set1 - 1) * RW + grp, n - 1);
+            const int row = min((kTail ? min(sb + u, set1 - 1) : sb + u) * RW + grp, n - 1);
 #pragma unroll
             for (int c = 0; c < CPL; c++) {
                 const int ci = min(gl + c * G, k16 - 1);
                 qv[u][c] = *reinterpret_cast<const uint4*>(qs + static_cast<size_t>(row) * k + ci * 16);
                 dh[u][c] = dsc[static_cast<size_t>(row) * kb + (ci >> 1)];
             }
+            bv[u] = kBias ? bias[row] : 0.0f;
         }
         // Keep the scheduler from interleaving the batch's loads with its math:
         // all of them go out before the first wait.
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int u = 0; u < U; u++) {
-            if (sb + u >= set1) break;  // wave-uniform: a short last batch skips its empty slots
+            if (kTail && sb + u >= set1) break;  // wave-uniform
             float acc[M];
 #pragma unroll
             for (int m = 0; m < M; m++) acc[m] = 0.0f;
@@ -141,8 +149,7 @@ __global__ void __launch_bounds__(64 * kWaves)
                 for (int m = 0; m < M; m++) acc[m] = group_sum<G>(acc[m]);
                 if (gl == 0 && row < n) {
 #pragma unroll
-                    for (int m = 0; m < M; m++)
-                        y[static_cast<size_t>(m) * n + row] = kBias ? acc[m] + bias[row] : acc[m];
+                    for (int m = 0; m < M; m++) y[static_cast<size_t>(m) * n + row] = kBias ? acc[m] + bv[u] : acc[m];
                 }
             } else {
                 // G = 32 or 64: 16-lane row totals, then across rows with readlane
@@ -152,11 +159,14 @@ __global__ void __launch_bounds__(64 * kWaves)
                     const float lo = rdlane(r16, 0) + rdlane(r16, 16);
                     const float hi = rdlane(r16, 32) + rdlane(r16, 48);
                     const float tot = G == 64 ? lo + hi : (grp == 0 ? lo : hi);
-                    if (gl == 0 && row < n) y[static_cast<size_t>(m) * n + row] = kBias ? tot + bias[row] : tot;
+                    if (gl == 0 && row < n) y[static_cast<size_t>(m) * n + row] = kBias ? tot + bv[u] : tot;
                 }
             }
         }
-    }
+    };
+    int sb = set0;
+    for (; sb + U <= set1; sb += U) batch(sb, std::false_type{});
+    if (sb < set1) batch(sb, std::true_type{});
 }
 
 // ---- W8A8 ------------------------------------------------------------------------
