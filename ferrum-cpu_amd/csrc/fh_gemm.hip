@@ -37,6 +37,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 typedef float f2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u4 __attribute__((ext_vector_type(4)));  // staging registers (a struct copy would go through scratch)
+typedef float f4 __attribute__((ext_vector_type(4)));
 
 // Staged rows, in f16 elements.  Activations: 32 h, 32 l, 8 pad (144 B);
 // weights: 32 quants, 8 pad (80 B).  Both strides keep the 16 lanes of a
@@ -537,6 +538,10 @@ __device__ __forceinline__ void split16(const float* v, float sc, h8& ah0, h8& a
     }
 }
 
+// Staging row of the skinny kernel: 32 floats + 4 pad, so the 16 lanes of a
+// ds_read_b128 pass (16 rows) land on distinct banks.
+constexpr int kSkinnyRow = 36;
+
 __device__ __forceinline__ int block_exponent(float mx) {
     if (!(mx > 0.0f)) return 0;
     const int E = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 126;
@@ -551,7 +556,11 @@ __global__ void __launch_bounds__(512)
                   const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
                   int k, int bps, float* __restrict__ part, unsigned* __restrict__ counters) {
     constexpr int OUT = MT * NT * 1024;  // outputs of one workgroup
-    // [KW][OUT] wave sums, then [KW][MT][BPW][32] row scales
+    // Per wave, [SLOT] floats: during the K loop one Q8_0 block of its
+    // activation rows ([MT * 32][36]: the rows land there from row-contiguous
+    // loads and leave in MFMA lane order), afterwards its OUT sums; then
+    // [KW][MT][BPW][32] row scales.
+    constexpr int SLOT = OUT > MT * 32 * kSkinnyRow ? OUT : MT * 32 * kSkinnyRow;
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ int last;
     float* sums = lds;
@@ -567,7 +576,8 @@ __global__ void __launch_bounds__(512)
         wrow[c] = qs + static_cast<size_t>(j) * k + half * 16;
         drow[c] = dsc + static_cast<size_t>(j) * kb;
     }
-    float* inv_lds = lds + kw * OUT + wave * (MT * BPW * 32);  // this wave's row scales
+    float* inv_lds = lds + kw * SLOT + wave * (MT * BPW * 32);  // this wave's row scales
+    float* xst = lds + wave * SLOT;                              // this wave's staging rows
     f16x acc[MT][NT];
 #pragma unroll
     for (int t = 0; t < MT; t++)
@@ -582,7 +592,7 @@ __global__ void __launch_bounds__(512)
         // own activation row); blocks past the split are skipped whole.
         uint4 wq[NT][BPW];
         uint16_t wd[NT][BPW];
-        float4 xv[MT][BPW][4];
+        f4 xv[MT][BPW][4];
 #pragma unroll
         for (int u = 0; u < BPW; u++) {
             const int b = min(b0 + u, b_end - 1);
@@ -591,13 +601,16 @@ __global__ void __launch_bounds__(512)
                 wq[c][u] = *reinterpret_cast<const uint4*>(wrow[c] + b * 32);
                 wd[c][u] = drow[c][b];
             }
+            // Activations: eight lanes per row read one block's 128 bytes,
+            // eight rows per load (a load in MFMA lane order would touch 64
+            // cache lines; this one touches 16).
 #pragma unroll
-            for (int t = 0; t < MT; t++) {
-                const int i = min(t * 32 + r32, m - 1);
-                const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(i) * k + b * 32 + half * 16);
+            for (int t = 0; t < MT; t++)
 #pragma unroll
-                for (int q = 0; q < 4; q++) xv[t][u][q] = src[q];
-            }
+                for (int q = 0; q < 4; q++) {
+                    const int i = min(t * 32 + (lane >> 3) + 8 * q, m - 1);
+                    xv[t][u][q] = *reinterpret_cast<const f4*>(x + static_cast<size_t>(i) * k + b * 32 + (lane & 7) * 4);
+                }
         }
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -613,12 +626,24 @@ __global__ void __launch_bounds__(512)
                 bq1[c] = __builtin_bit_cast(h8, make_uint4(c2.x, c2.y, c3.x, c3.y));
                 dw[c] = fh_h2f(wd[c][u]);
             }
+            // Through this wave's staging rows into MFMA order: lane (r32, half)
+            // takes 16 values of row r32.  LDS operations of one wave run in
+            // order, so the next block's stores follow these reads.
+#pragma unroll
+            for (int t = 0; t < MT; t++)
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    *reinterpret_cast<f4*>(xst + (t * 32 + (lane >> 3) + 8 * q) * kSkinnyRow + (lane & 7) * 4) = xv[t][u][q];
+            __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int t = 0; t < MT; t++) {
-                const float v[16] = {xv[t][u][0].x, xv[t][u][0].y, xv[t][u][0].z, xv[t][u][0].w,
-                                     xv[t][u][1].x, xv[t][u][1].y, xv[t][u][1].z, xv[t][u][1].w,
-                                     xv[t][u][2].x, xv[t][u][2].y, xv[t][u][2].z, xv[t][u][2].w,
-                                     xv[t][u][3].x, xv[t][u][3].y, xv[t][u][3].z, xv[t][u][3].w};
+                float v[16];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const f4 f = *reinterpret_cast<const f4*>(xst + (t * 32 + r32) * kSkinnyRow + half * 16 + q * 4);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[4 * q + e] = f[e];
+                }
                 // fmaxf skips NaN; an infinite maximum takes the rare safe path.
                 float mx = 0.0f;
 #pragma unroll
@@ -664,14 +689,16 @@ __global__ void __launch_bounds__(512)
             }
         }
     }
-    // Wave sums: every wave stores its own, then each output is added over the
-    // waves in wave order.
+    // Wave sums (over the staging rows, once every wave is done with them):
+    // every wave stores its own, then each output is added over the waves in
+    // wave order.
+    __syncthreads();
 #pragma unroll
     for (int t = 0; t < MT; t++)
 #pragma unroll
         for (int c = 0; c < NT; c++)
 #pragma unroll
-            for (int v = 0; v < 16; v++) sums[wave * OUT + ((t * NT + c) * 16 + v) * 64 + lane] = acc[t][c][v];
+            for (int v = 0; v < 16; v++) sums[wave * SLOT + ((t * NT + c) * 16 + v) * 64 + lane] = acc[t][c][v];
     __syncthreads();
     // Output o = ((t * NT + c) * 16 + v) * 64 + l  ->  row, column.
     auto row_of = [](int o) { const int t = o / (NT * 1024), v = (o / 64) % 16, l = o % 64;
@@ -686,7 +713,7 @@ __global__ void __launch_bounds__(512)
     const size_t tiles = gridDim.x;
     for (int o = threadIdx.x; o < OUT; o += blockDim.x) {
         float s = sums[o];
-        for (int w = 1; w < kw; w++) s += sums[w * OUT + o];
+        for (int w = 1; w < kw; w++) s += sums[w * SLOT + o];
         if (splits == 1) {
             const int i = row_of(o), jj = col_of(o);
             if (i < m && jj < n) finish(i, jj, s);
@@ -764,7 +791,7 @@ int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const f
 // Splits of K only while the column tiles alone leave half the CUs idle, and
 // then as few as let one batch of BPW blocks per wave cover a split (each split
 // costs a round of partial stores and reloads).  Waves: at most 16 / (MT * NT)
-// (their sums fit 64 KiB of LDS) and 8 (256 VGPRs per lane).  Column tiles per
+// (their sums fit 64 KiB of LDS, two workgroups per CU) and 8 (256 VGPRs per lane).  Column tiles per
 // wave (NT): up to 4 while that still leaves >= 256 workgroups, so wide
 // outputs split each activation block once per 128 columns.
 template <int MT, int NT, int BPW>
@@ -778,7 +805,8 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     splits = (kb + bps - 1) / bps;  // no empty split
     size_t kw = (bps + BPW - 1) / BPW;
     if (kw > kMaxWaves) kw = kMaxWaves;
-    const size_t lds = kw * (static_cast<size_t>(MT * NT * 1024) + MT * BPW * 32) * sizeof(float);
+    constexpr size_t kSlot = MT * NT * 1024 > MT * 32 * kSkinnyRow ? MT * NT * 1024 : MT * 32 * kSkinnyRow;
+    const size_t lds = kw * (kSlot + MT * BPW * 32) * sizeof(float);
     float* part = nullptr;
     unsigned* counters = nullptr;
     if (splits > 1) {
