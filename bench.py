@@ -386,10 +386,29 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
     for lw in layers:
         for w in lw:
             w.free()
+    del x, y
+    # The same matrix-core work as a plain library f16 GEMM (torch -> hipBLASLt):
+    # three f16 products per Q8_0 weight-activation pair are one GEMM of depth 3k.
+    lib_ms = 0.0
+    for (n, k) in MED_SHAPES:
+        a = torch.randn((MED_M, 3 * k), generator=gen, device=dev).half()
+        b = torch.randn((3 * k, n), generator=gen, device=dev).half()
+        for _ in range(2):
+            torch.matmul(a, b)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(5):
+            torch.matmul(a, b)
+        e1.record()
+        torch.cuda.synchronize()
+        lib_ms += e0.elapsed_time(e1) / 5 * MED_L
+        del a, b
     return {"workload": "gpt2-medium prefill linears, 32 x 512 tokens (m = 16384), W8A32 f16-MFMA",
             "ms": round(ms, 3), "tflops": round(tflops, 1),
             "frac_f16_dense_peak": round(tflops / F16_DENSE_TFLOPS, 4),
-            "frac_i8_dense_peak": round(tflops / I8_DENSE_TOPS, 4)}
+            "frac_i8_dense_peak": round(tflops / I8_DENSE_TOPS, 4),
+            "mfma_f16_tflops": round(3 * tflops, 1), "mfma_frac_f16_dense_peak": round(3 * tflops / F16_DENSE_TFLOPS, 4),
+            "library_f16_same_mfma_work_ms": round(lib_ms, 3), "vs_library": round(lib_ms / ms, 3)}
 
 
 def cpu_baseline(budget_s):
