@@ -66,11 +66,12 @@ __device__ __forceinline__ bool finite(float v) { return (__builtin_bit_cast(uin
 // = NaN, inf - inf = NaN) and the value are the reference's bit for bit.
 __device__ __attribute__((noinline)) float exact_dot(const float* __restrict__ x, int k, const int8_t* __restrict__ q,
                                                    const uint16_t* __restrict__ d) {
+#pragma clang fp contract(off)  // plain operators: no FMA, each product and sum rounded
     float s = 0.0f;
     for (int b = 0; b < (k >> 5); b++) {
         const float ds = fh_h2f(d[b]);
         for (int t = 0; t < 32; t++)
-            s = __fadd_rn(s, __fmul_rn(x[b * 32 + t], ds * static_cast<float>(q[b * 32 + t])));
+            s = s + x[b * 32 + t] * (ds * static_cast<float>(q[b * 32 + t]));
     }
     return s;
 }
@@ -497,6 +498,108 @@ __global__ void __launch_bounds__(64 * WM * WN)
     if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, xbad, bias, y, m, n, k, i0, j0, BM, BN);
 }
 
+// ---- W8A8 on the int8 matrix cores ---------------------------------------------------
+// llama.cpp numerics (the activations re-quantised to Q8_0 per 32):
+//   y[i, j] = sum_b f32(dot_b(i, j)) * (d_w[j, b] * d_x[i, b])  (+ bias[j], last)
+// One v_mfma_i32_32x32x32_i8 is one Q8_0 block of a 32 x 32 output tile: the
+// int32 block dots are exact; each is scaled and added to the f32 sum in
+// ascending b with separately rounded products and sums, the reference's own
+// order, so the outputs are the reference's bit for bit.  That per-block VALU
+// epilogue (convert, two products, add: 64 instructions per MFMA) bounds the
+// kernel, not the matrix cores.  Each wave owns a (32 TM) x 64 output tile and
+// reads its fragments straight from global memory: the activation panel
+// (fh_k_encode_panel) in MFMA lane order, 1 KiB contiguous per fragment; the
+// weight rows 16 bytes per lane.  The next block's operands are loaded while
+// the current one is finished.
+template <int TM>
+__global__ void __launch_bounds__(256)
+    k_gemm_w8a8(const uint4* __restrict__ qp, const float* __restrict__ dp, const int8_t* __restrict__ qs,
+                const uint16_t* __restrict__ dsc, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
+                int k, int tiles_n, int tiles) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    typedef int i16 __attribute__((ext_vector_type(16)));
+    constexpr int TN = 2;
+    const int lane = threadIdx.x & 63, g = lane >> 5, l32 = lane & 31;
+    const int wid = static_cast<int>(blockIdx.x) * 4 + static_cast<int>(threadIdx.x >> 6);
+    if (wid >= tiles) return;  // no barriers below
+    const int tm = wid / tiles_n, tn = wid % tiles_n;
+    const int kb = k >> 5;
+    const int j0 = tn * 64;
+    const int8_t* wrow[TN];
+    const uint16_t* drow[TN];
+#pragma unroll
+    for (int c = 0; c < TN; c++) {
+        const int j = min(j0 + c * 32 + l32, n - 1);  // rows past n: computed, never stored
+        wrow[c] = qs + static_cast<size_t>(j) * k + g * 16;
+        drow[c] = dsc + static_cast<size_t>(j) * kb;
+    }
+    struct Ops {
+        i4 a[TM], w[TN];
+        f4 dx[TM][4];
+        uint16_t dw[TN];
+    };
+    auto load = [&](Ops& o, int b) __attribute__((always_inline)) {
+#pragma unroll
+        for (int r = 0; r < TM; r++) {
+            const size_t t = static_cast<size_t>(tm * TM + r) * kb + b;
+            o.a[r] = __builtin_bit_cast(i4, qp[t * 64 + lane]);
+#pragma unroll
+            for (int q = 0; q < 4; q++) o.dx[r][q] = *reinterpret_cast<const f4*>(dp + t * 32 + q * 8 + g * 4);
+        }
+#pragma unroll
+        for (int c = 0; c < TN; c++) {
+            o.w[c] = *reinterpret_cast<const i4*>(wrow[c] + b * 32);
+            o.dw[c] = drow[c][b];
+        }
+    };
+    float acc[TM][TN][16];
+#pragma unroll
+    for (int r = 0; r < TM; r++)
+#pragma unroll
+        for (int c = 0; c < TN; c++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[r][c][v] = 0.0f;
+    auto finish = [&](const Ops& o) __attribute__((always_inline)) {
+#pragma clang fp contract(off)  // plain operators: separately rounded products and sums
+#pragma unroll
+        for (int c = 0; c < TN; c++) {
+            const float dw = fh_h2f(o.dw[c]);
+#pragma unroll
+            for (int r = 0; r < TM; r++) {
+                const i16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(o.a[r], o.w[c], i16{}, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; v++) {
+                    // acc row (v / 4) * 8 + g * 4 + v % 4: its scale is dx[v / 4][v % 4]
+                    const float dd = dw * o.dx[r][v >> 2][v & 3];
+                    acc[r][c][v] = acc[r][c][v] + static_cast<float>(d[v]) * dd;
+                }
+            }
+        }
+    };
+    Ops o0, o1;
+    load(o0, 0);
+    for (int b = 0; b < kb; b += 2) {
+        if (b + 1 < kb) load(o1, b + 1);
+        finish(o0);
+        if (b + 1 >= kb) break;
+        if (b + 2 < kb) load(o0, b + 2);
+        finish(o1);
+    }
+#pragma unroll
+    for (int c = 0; c < TN; c++) {
+        const int j = j0 + c * 32 + l32;
+        if (j >= n) continue;
+        const float bj = bias ? bias[j] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < TM; r++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int i = (tm * TM + r) * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+                if (i < m) y[static_cast<size_t>(i) * n + j] = bias ? acc[r][c][v] + bj : acc[r][c][v];
+            }
+    }
+}
+
 // ---- skinny m (batched decode): m <= 32 * MT ------------------------------------
 // Grid: 32-wide weight-row tiles x S splits of the Q8_0 blocks.  A workgroup's
 // waves divide its split's blocks and issue every load of a batch of up to BPW
@@ -840,6 +943,39 @@ int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const
 }
 
 }  // namespace
+
+__global__ void fh_k_encode_panel(const float* __restrict__ x, int m, int m_pad, int kb, uint4* __restrict__ qp,
+                                  float* __restrict__ dp);
+
+// W8A8 through the int8 matrix cores: the activations are encoded into the
+// lane-order panel, then one wave per (32 TM) x 64 output tile.
+int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    const int tm_rows = m >= 64 ? 64 : 32;
+    const size_t kb = w->k / 32, m_pad = (m + tm_rows - 1) / tm_rows * tm_rows;
+    const size_t qbytes = fh_align256(m_pad * w->k), dbytes = fh_align256(m_pad * kb * 4);
+    void* ws = nullptr;
+    int rc = fh_workspace(ctx, qbytes + dbytes, &ws);
+    if (rc) return rc;
+    uint4* qp = static_cast<uint4*>(ws);
+    float* dp = reinterpret_cast<float*>(static_cast<char*>(ws) + qbytes);
+    const size_t nb = m_pad * kb;
+    hipLaunchKernelGGL(fh_k_encode_panel, dim3(static_cast<unsigned>((nb + 255) / 256)), dim3(256), 0, ctx->stream, x,
+                       static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(kb), qp, dp);
+    FH_HIP(ctx, hipGetLastError());
+    const size_t tiles_n = (w->n + 63) / 64, tiles = tiles_n * (m_pad / tm_rows);
+    if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
+    const dim3 grid(static_cast<unsigned>((tiles + 3) / 4)), block(256);
+    if (tm_rows == 64)
+        hipLaunchKernelGGL(k_gemm_w8a8<2>, grid, block, 0, ctx->stream, qp, dp, w->qs, w->d, bias, y,
+                           static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k),
+                           static_cast<int>(tiles_n), static_cast<int>(tiles));
+    else
+        hipLaunchKernelGGL(k_gemm_w8a8<1>, grid, block, 0, ctx->stream, qp, dp, w->qs, w->d, bias, y,
+                           static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k),
+                           static_cast<int>(tiles_n), static_cast<int>(tiles));
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
 
 // Tile choice: m <= 64 takes the skinny kernel; otherwise the 256 x 256
 // weight-split tile (eight waves) once it still yields a tile per CU, the 128 x 128 tile at two

@@ -84,6 +84,8 @@ int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t
                            const float* bias, float* y);
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                          const float* bias, float* y);
+int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
+                        const float* bias, float* y);
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                           const float* bias, float* y);
 int fh_launch_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out);

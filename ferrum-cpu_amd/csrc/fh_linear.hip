@@ -18,7 +18,9 @@
 //                fh_gemm.hip.
 //  k_linear_w8a8 llama.cpp numerics: x is Q8_0-encoded per 32 (bit-exact
 //                q8_0_block), exact int32 block dots with sdot4, then
-//                sum_b f32(dot_b) * (d_w * d_x) + b.
+//                sum_b f32(dot_b) * (d_w * d_x) + b (blocks summed in parallel).
+//                Larger problems go to the int8-MFMA kernel in fh_gemm.hip,
+//                which sums the blocks in order and is bit-exact.
 #include "fh_internal.hpp"
 
 #include <type_traits>
@@ -29,6 +31,10 @@ __global__ void fh_k_encode_split(const float* __restrict__ x, size_t nblocks, u
 namespace {
 
 constexpr int kWaves = 4;  // waves per block in the GEMV kernels
+// W8A8 runs on the int8 matrix cores (one wave per 32- or 64-row x 64-column
+// output tile, every Q8_0 block in order) once there are this many tiles;
+// fewer waves, each walking all of K, lose to the block-parallel kernel below.
+constexpr size_t kW8a8MfmaTiles = 96;
 
 __device__ __forceinline__ float sbyte(uint32_t w, int i) {
     return static_cast<float>(static_cast<int8_t>((w >> (8 * i)) & 0xFFu));
@@ -294,6 +300,9 @@ int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t 
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x must be 4-byte aligned");
     if (w->n > 0x7FFFFFFFu || w->k > 0x7FFFFFFFu || m * w->n > 0x7FFFFFFFu * size_t(64))
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: problem too large for the W8A8 kernel");
+    const size_t tile_rows = m >= 64 ? 64 : 32;
+    if (m >= 32 && (m + tile_rows - 1) / tile_rows * ((w->n + 63) / 64) >= kW8a8MfmaTiles)
+        return fh_launch_gemm_w8a8(ctx, w, x, m, bias, y);
     const size_t kb = w->k / 32;
     const size_t qbytes = fh_align256(m * w->k), dbytes = fh_align256(m * kb * 2);
     void* ws = nullptr;

@@ -170,6 +170,25 @@ __global__ void __launch_bounds__(256) fh_k_encode_split(const float* __restrict
     dst[1] = make_uint4(q[4], q[5], q[6], q[7]);
 }
 
+// f32 [m, k] -> Q8_0 activations in the W8A8 matrix-core panel: per 32-row
+// tile and block b, 1 KiB of quants in MFMA lane order (lane g * 32 + r holds
+// row r's quants 16 g .. 16 g + 15) and the 32 row scales as f32.  Rows m ..
+// m_pad - 1 are zero.  Same per-block arithmetic as the GGUF encoder.
+__global__ void __launch_bounds__(256) fh_k_encode_panel(const float* __restrict__ x, int m, int m_pad, int kb,
+                                                         uint4* __restrict__ qp, float* __restrict__ dp) {
+    const size_t t = blockIdx.x * static_cast<size_t>(256) + threadIdx.x;
+    if (t >= static_cast<size_t>(m_pad) * kb) return;
+    const int row = static_cast<int>(t / kb), b = static_cast<int>(t % kb);
+    uint32_t q[8] = {};
+    uint16_t d16 = 0;
+    if (row < m) d16 = encode_block(x + (static_cast<size_t>(row) * kb + b) * 32, q);
+    const size_t tile = (static_cast<size_t>(row >> 5) * kb + b);
+    uint4* dst = qp + tile * 64 + (row & 31);
+    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
+    dst[32] = make_uint4(q[4], q[5], q[6], q[7]);
+    dp[tile * 32 + (row & 31)] = fh_h2f(d16);
+}
+
 int fh_launch_repack(fh_ctx* ctx, const uint8_t* d_raw, size_t n, size_t k, int8_t* qs, uint16_t* d) {
     if (reinterpret_cast<uintptr_t>(d_raw) & 1)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_upload: device bytes must be 2-byte aligned");

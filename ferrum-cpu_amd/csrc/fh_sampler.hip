@@ -37,6 +37,10 @@
 
 #include "fh_internal.hpp"
 
+// The sequential parts replay the reference's arithmetic, which rounds every
+// product and sum (no FMA anywhere in it): no contraction in this file.
+#pragma clang fp contract(off)
+
 namespace {
 
 constexpr int kT = 1024;        // threads per row

@@ -366,6 +366,32 @@ def test_w8a8_matches_oracle(fh, orc, m, n, k):
     w.free()
 
 
+@pytest.mark.parametrize("m,n,k,has_bias", [(32, 6144, 32, True), (40, 6200, 96, False), (64, 6144, 64, True),
+                                            (100, 3100, 768, True), (257, 2304, 768, False), (1000, 1024, 1024, True)])
+def test_w8a8_matrix_cores_are_bit_exact(fh, orc, m, n, k, has_bias):
+    """With >= 96 output tiles of (32 or 64) x 64, W8A8 runs on the int8
+    matrix cores (one v_mfma_i32_32x32x32_i8 per Q8_0 block of a 32 x 32
+    tile) and adds the scaled block dots in the reference's order without FMA:
+    equal to the reference bit for bit, non-finite rows, ragged shapes and
+    odd block counts included."""
+    import ferrum_hip
+
+    raw = weight(orc, n, k, 7 * m + n + k)
+    x = acts(m, k, m + 3)
+    x[1, 5] = np.inf                 # amax inf: d = inf, quants 0 -> 0 * inf = NaN
+    x[2, :] = 0.0                    # d = 0
+    x[3] *= np.float32(1e-30)        # subnormal-range scales
+    x[4] *= np.float32(1e20)
+    x[m - 1, k - 1] = np.nan
+    b = bias_for(n, k) if has_bias else None
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    got = ferrum_hip.linear_forward(fh, x, w, b, numerics=ferrum_hip.W8A8)
+    w.free()
+    ref = orc.q8_0_linear_w8a8(x, raw, n, b)
+    assert np.array_equal(got, ref, equal_nan=True)
+    assert np.isnan(got[1]).all() and np.isfinite(got[5:m - 1]).all()
+
+
 def test_int32_block_dots_are_bit_exact(fh, orc):
     import torch
 
