@@ -352,37 +352,43 @@ def main():
 
 def prefill_leg(ctx, fh, torch, gen, dev, steps):
     """GPT-2-medium prefill linears: 24 x [QKV, attn-out, up, down] at m = 16,384
-    (32 prompts x 512 tokens), W8A32 on the f16 matrix cores.  One step = the 96
-    GEMMs (bias added), captured into one graph; FLOPs = 2 m n k per GEMM."""
+    (32 prompts x 512 tokens), W8A32 on the f16 matrix cores, then the same in
+    W8A8 on the int8 matrix cores.  One step = the 96 GEMMs (bias added),
+    captured into one graph; FLOPs = 2 m n k per GEMM."""
     layers = [[make_weight(ctx, fh, torch, n, k, gen) for (n, k) in MED_SHAPES] for _ in range(MED_L)]
     biases = {n: torch.randn(n, generator=gen, device=dev) * 0.1 for n in {s[0] for s in MED_SHAPES}}
     x = {k: torch.randn((MED_M, k), generator=gen, device=dev) for k in {s[1] for s in MED_SHAPES}}
     y = torch.empty((MED_M, max(s[0] for s in MED_SHAPES)), device=dev)
 
-    def step():
+    def step(numerics):
         for li in range(MED_L):
             for (n, k), w in zip(MED_SHAPES, layers[li]):
-                fh.linear_forward_async(ctx, w, x[k], MED_M, k, biases[n], n, y)
+                fh.linear_forward_async(ctx, w, x[k], MED_M, k, biases[n], n, y, numerics)
 
-    step()
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    def timed_graph(numerics):
+        step(numerics)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+            step(numerics)
         ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-        step()
-    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-    g.replay()
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record()
-    for _ in range(steps):
         g.replay()
-    e1.record()
-    torch.cuda.synchronize()
-    ms = e0.elapsed_time(e1) / steps
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / steps, e0, e1
+
     flops = sum(2.0 * MED_M * n * k for (n, k) in MED_SHAPES) * MED_L
+    ms, e0, e1 = timed_graph(fh.W8A32)
     tflops = flops / (ms * 1e-3) / 1e12
-    del g
+    ms8, _, _ = timed_graph(fh.W8A8)
+    tops8 = flops / (ms8 * 1e-3) / 1e12
     for lw in layers:
         for w in lw:
             w.free()
@@ -408,7 +414,10 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
             "frac_f16_dense_peak": round(tflops / F16_DENSE_TFLOPS, 4),
             "frac_i8_dense_peak": round(tflops / I8_DENSE_TOPS, 4),
             "mfma_f16_tflops": round(3 * tflops, 1), "mfma_frac_f16_dense_peak": round(3 * tflops / F16_DENSE_TFLOPS, 4),
-            "library_f16_same_mfma_work_ms": round(lib_ms, 3), "vs_library": round(lib_ms / ms, 3)}
+            "library_f16_same_mfma_work_ms": round(lib_ms, 3), "vs_library": round(lib_ms / ms, 3),
+            "w8a8_int8_mfma": {"ms": round(ms8, 3), "tops": round(tops8, 1),
+                               "frac_i8_dense_peak": round(tops8 / I8_DENSE_TOPS, 4),
+                               "numerics": "W8A8 (activations re-quantised to Q8_0), bit-exact with the reference"}}
 
 
 def cpu_baseline(budget_s):
