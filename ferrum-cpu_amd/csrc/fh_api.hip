@@ -491,3 +491,68 @@ int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, 
 }
 
 }  // extern "C"
+
+// ---- the rest of a GPT-2 decode step --------------------------------------------
+
+int fh_embed_one_async(fh_ctx* ctx, const float* d_token_w, const float* d_pos_w, size_t vocab, size_t max_seq,
+                       size_t d, const uint32_t* d_token, size_t pos, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (!d_token_w || !d_pos_w || !d_token || !d_out)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_embed_one: a pointer is NULL");
+    if (vocab == 0 || d == 0 || vocab > 0x7FFFFFFFu || d > 0x7FFFFFFFu)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_embed_one: vocab and d must be in 1 .. 2^31");
+    if (pos >= max_seq)
+        return fh_fail(ctx, FH_ERR_DIM, "Position " + std::to_string(pos) + " exceeds max_seq_len " +
+                                            std::to_string(max_seq));
+    FH_ON_DEVICE(ctx);
+    return fh_launch_embed_one(ctx, d_token_w, d_pos_w, vocab, d, d_token, pos, d_out);
+}
+
+int fh_layernorm_async(fh_ctx* ctx, const float* d_x, size_t rows, size_t d, const float* d_gamma,
+                       const float* d_beta, float* d_y) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rows == 0) return FH_OK;
+    if (!d_x || !d_gamma || !d_beta || !d_y) return fh_fail(ctx, FH_ERR_INVALID, "fh_layernorm: a pointer is NULL");
+    if (d == 0 || d > 0x7FFFFFFFu || rows > 0x7FFFFFFFu)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_layernorm: rows and d must be in 1 .. 2^31");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_layernorm(ctx, d_x, rows, d, d_gamma, d_beta, d_y);
+}
+
+int fh_gelu_async(fh_ctx* ctx, float* d_x, size_t n) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (n == 0) return FH_OK;
+    if (!d_x) return fh_fail(ctx, FH_ERR_INVALID, "fh_gelu: x is NULL");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_gelu(ctx, d_x, n);
+}
+
+int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (n == 0) return FH_OK;
+    if (!d_x || !d_y) return fh_fail(ctx, FH_ERR_INVALID, "fh_add: x or y is NULL");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_add(ctx, d_x, d_y, n);
+}
+
+int fh_attention_decode_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
+                              size_t capacity, size_t d, size_t heads, size_t pos, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (!d_qkv || !d_k_cache || !d_v_cache || !d_out)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_attention_decode: a pointer is NULL");
+    if (heads == 0 || d == 0 || d % heads != 0)
+        return fh_fail(ctx, FH_ERR_DIM, "fh_attention_decode: heads (" + std::to_string(heads) +
+                                            ") must divide the embedding dim (" + std::to_string(d) + ")");
+    if (pos >= capacity)
+        return fh_fail(ctx, FH_ERR_DIM, "KvCache full (" + std::to_string(capacity) +
+                                            " positions): clear and re-prime to continue");
+    if (d > 0x7FFFFFFFu || capacity > 0x7FFFFFFFu || capacity * d > (size_t(1) << 40))
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_attention_decode: cache too large");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_attention_decode(ctx, d_qkv, d_k_cache, d_v_cache, d, heads, pos, d_out);
+}

@@ -1,0 +1,233 @@
+// fh_block.hip — the rest of a GPT-2 decode step on gfx950: token + position
+// embedding, LayerNorm, GELU, the residual add and the KV-cache attention of
+// one new position.  With the Q8_0 linears (fh_linear.hip) and the fused
+// sampler (fh_sampler.hip) a whole decode step stays on the device.
+//
+//  k_embed_one   Embedding::embed_one (layer/embedding.rs:70-90).
+//  k_layernorm   LayerNorm::forward (layer/norm.rs:46-82), one workgroup per
+//                row; the row sums are tree reductions in a fixed order.
+//  k_gelu        activation::gelu (activation.rs:9-12), in place.
+//  k_add         the residual adds of forward_with_cache (layer/transformer.rs:
+//                281, 288), in place.
+//  k_attn_chunk  the attention of forward_with_cache (layer/transformer.rs:
+//                242-279) for one query: the new k and v rows are written at
+//                cache row pos, then each (head, 32-position chunk) workgroup
+//                forms its scores, their max, sum of exponentials and the
+//                exponential-weighted sum of v rows; the last chunk of a head to
+//                finish merges the chunks (max, rescaled sums) and writes the
+//                head's output.  The reference sums in position order with one
+//                global max; the merge is the same value up to rounding.
+// Arithmetic is written without contraction, as the reference has no FMA.
+#include "fh_internal.hpp"
+
+#pragma clang fp contract(off)
+
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kChunk = 32;    // cache positions per attention workgroup
+constexpr int kMaxHd = 128;   // head width the attention kernel supports
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum over the workgroup in a fixed order (wave sums, then waves in order).
+__device__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < static_cast<int>(blockDim.x >> 6); i++) s += red[i];
+    return s;
+}
+
+__global__ void __launch_bounds__(kThreads) k_embed_one(const float* __restrict__ tok_w, const float* __restrict__ pos_w,
+                                                       int vocab, int d, const uint32_t* __restrict__ token, int pos,
+                                                       float* __restrict__ out) {
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i >= d) return;
+    const uint32_t t = *token;
+    // An id past the vocabulary (never one the sampler returns) poisons the row.
+    out[i] = t < static_cast<uint32_t>(vocab) ? tok_w[static_cast<size_t>(t) * d + i] + pos_w[static_cast<size_t>(pos) * d + i]
+                                              : __builtin_nanf("");
+}
+
+__global__ void __launch_bounds__(kThreads) k_layernorm(const float* __restrict__ x, int d,
+                                                       const float* __restrict__ gamma, const float* __restrict__ beta,
+                                                       float* __restrict__ y) {
+    __shared__ float red[kThreads / 64];
+    const float* xr = x + static_cast<size_t>(blockIdx.x) * d;
+    float* yr = y + static_cast<size_t>(blockIdx.x) * d;
+    float s = 0.0f;
+    for (int c = threadIdx.x; c < d; c += kThreads) s += xr[c];
+    const float mean = block_sum(s, red) / static_cast<float>(d);
+    float ss = 0.0f;
+    for (int c = threadIdx.x; c < d; c += kThreads) {
+        const float dv = xr[c] - mean;
+        ss += dv * dv;
+    }
+    const float var = block_sum(ss, red) / static_cast<float>(d);
+    const float sd = sqrtf(var + 1e-5f);
+    for (int c = threadIdx.x; c < d; c += kThreads) yr[c] = ((xr[c] - mean) / sd) * gamma[c] + beta[c];
+}
+
+__global__ void __launch_bounds__(kThreads) k_gelu(float* __restrict__ x, size_t n) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    x[i] = 0.5f * v * (1.0f + tanhf(0.7978846f * (v + 0.044715f * v * v * v)));
+}
+
+__global__ void __launch_bounds__(kThreads) k_add(float* __restrict__ x, const float* __restrict__ y, size_t n) {
+    const size_t i = blockIdx.x * static_cast<size_t>(kThreads) + threadIdx.x;
+    if (i < n) x[i] = x[i] + y[i];
+}
+
+// Grid (chunks, heads).  part: [heads][chunks][2 + hd] (max, sum, weighted v
+// sum), written with device-coherent stores; counters: one per head, left at 0.
+__global__ void __launch_bounds__(kThreads)
+    k_attn_chunk(const float* __restrict__ qkv, float* __restrict__ kc, float* __restrict__ vc, int d, int hd, int pos,
+                 float scale, float* __restrict__ part, unsigned* __restrict__ counters, float* __restrict__ out) {
+    __shared__ float q[kMaxHd];
+    __shared__ float sc[kChunk];
+    __shared__ float acc[kThreads];
+    __shared__ int last;
+    const int chunk = blockIdx.x, head = blockIdx.y, chunks = gridDim.x;
+    const int hs = head * hd, tid = threadIdx.x;
+    const int len = pos + 1, j0 = chunk * kChunk, jn = min(kChunk, len - j0);
+    // The new row: chunk 0 of each head writes its slice of k and v at row
+    // pos.  Reads below take the new row from qkv itself, never from the
+    // cache, so no workgroup depends on another's store.
+    if (chunk == 0)
+        for (int t = tid; t < hd; t += kThreads) {
+            kc[static_cast<size_t>(pos) * d + hs + t] = qkv[d + hs + t];
+            vc[static_cast<size_t>(pos) * d + hs + t] = qkv[2 * d + hs + t];
+        }
+    for (int t = tid; t < hd; t += kThreads) q[t] = qkv[hs + t];
+    __syncthreads();
+    // scores: 8 lanes per position, each over hd / 8 consecutive dims, then a
+    // fixed 8-lane tree
+    {
+        const int jl = tid >> 3, part8 = tid & 7, per = hd / 8;
+        float dot = 0.0f;
+        if (jl < jn) {
+            const int j = j0 + jl;
+            const float* kr = j == pos ? qkv + d + hs : kc + static_cast<size_t>(j) * d + hs;
+            for (int t = part8 * per; t < part8 * per + per; t++) dot += q[t] * kr[t];
+        }
+        dot += __shfl_xor(dot, 1, 64);
+        dot += __shfl_xor(dot, 2, 64);
+        dot += __shfl_xor(dot, 4, 64);
+        if (part8 == 0 && jl < kChunk) sc[jl] = jl < jn ? dot * scale : -INFINITY;
+    }
+    __syncthreads();
+    float mx = -INFINITY;
+    for (int j = 0; j < jn; j++) mx = fmaxf(mx, sc[j]);
+    float se = 0.0f;
+    for (int j = 0; j < jn; j++) se += expf(sc[j] - mx);
+    // weighted v sum over this chunk: thread (g, t) takes positions g, g + G, ...
+    const int groups = kThreads / hd;
+    const int t = tid % hd, g = tid / hd;
+    float o = 0.0f;
+    if (g < groups)
+        for (int jl = g; jl < jn; jl += groups) {
+            const int j = j0 + jl;
+            const float* vr = j == pos ? qkv + 2 * d + hs : vc + static_cast<size_t>(j) * d + hs;
+            o += expf(sc[jl] - mx) * vr[t];
+        }
+    acc[tid] = o;
+    __syncthreads();
+    float* mine = part + (static_cast<size_t>(head) * chunks + chunk) * (2 + hd);
+    if (tid < hd) {
+        float s = 0.0f;
+        for (int gg = 0; gg < groups; gg++) s += acc[gg * hd + tid];
+        __hip_atomic_store(mine + 2 + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0) {
+        __hip_atomic_store(mine, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mine + 1, se, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Publish: every thread's coherent stores complete before the arrival
+    // count moves, so the last arrival reads whole partials.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) last = atomicAdd(counters + head, 1u) == static_cast<unsigned>(chunks - 1);
+    __syncthreads();
+    if (!last) return;
+    const float* hp = part + static_cast<size_t>(head) * chunks * (2 + hd);
+    float M = -INFINITY;
+    for (int c = 0; c < chunks; c++)
+        M = fmaxf(M, __hip_atomic_load(hp + c * (2 + hd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    float S = 0.0f;
+    for (int c = 0; c < chunks; c++) {
+        const float mc = __hip_atomic_load(hp + c * (2 + hd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        S += __hip_atomic_load(hp + c * (2 + hd) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * expf(mc - M);
+    }
+    if (tid < hd) {
+        float r = 0.0f;
+        for (int c = 0; c < chunks; c++) {
+            const float mc = __hip_atomic_load(hp + c * (2 + hd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            r += __hip_atomic_load(hp + c * (2 + hd) + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) *
+                 expf(mc - M);
+        }
+        out[hs + tid] = r / S;
+    }
+    if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+unsigned blocks_for(size_t n) { return static_cast<unsigned>((n + kThreads - 1) / kThreads); }
+
+}  // namespace
+
+int fh_launch_embed_one(fh_ctx* ctx, const float* tok_w, const float* pos_w, size_t vocab, size_t d,
+                        const uint32_t* token, size_t pos, float* out) {
+    hipLaunchKernelGGL(k_embed_one, dim3(blocks_for(d)), dim3(kThreads), 0, ctx->stream, tok_w, pos_w,
+                       static_cast<int>(vocab), static_cast<int>(d), token, static_cast<int>(pos), out);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_layernorm(fh_ctx* ctx, const float* x, size_t rows, size_t d, const float* gamma, const float* beta,
+                        float* y) {
+    hipLaunchKernelGGL(k_layernorm, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x,
+                       static_cast<int>(d), gamma, beta, y);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_gelu(fh_ctx* ctx, float* x, size_t n) {
+    hipLaunchKernelGGL(k_gelu, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream, x, n);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n) {
+    hipLaunchKernelGGL(k_add, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream, x, y, n);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads, size_t pos,
+                               float* out) {
+    const size_t hd = d / heads;
+    if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_attention_decode: head width must be 8, 16, 32, 64 or 128");
+    const size_t chunks = (pos + 1 + kChunk - 1) / kChunk;
+    void* ws = nullptr;
+    int rc = fh_workspace(ctx, heads * chunks * (2 + hd) * sizeof(float), &ws);
+    if (rc) return rc;
+    void* cnt = nullptr;
+    rc = fh_counter_area(ctx, heads * sizeof(unsigned), &cnt);
+    if (rc) return rc;
+    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
+    hipLaunchKernelGGL(k_attn_chunk, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(heads)), dim3(kThreads),
+                       0, ctx->stream, qkv, kc, vc, static_cast<int>(d), static_cast<int>(hd), static_cast<int>(pos),
+                       scale, static_cast<float*>(ws), static_cast<unsigned*>(cnt), out);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}

@@ -89,6 +89,14 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                           const float* bias, float* y);
 int fh_launch_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out);
+int fh_launch_embed_one(fh_ctx* ctx, const float* tok_w, const float* pos_w, size_t vocab, size_t d,
+                        const uint32_t* token, size_t pos, float* out);
+int fh_launch_layernorm(fh_ctx* ctx, const float* x, size_t rows, size_t d, const float* gamma,
+                        const float* beta, float* y);
+int fh_launch_gelu(fh_ctx* ctx, float* x, size_t n);
+int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n);
+int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
+                               size_t pos, float* out);
 int fh_launch_dequant(fh_ctx* ctx, const uint8_t* raw, size_t n, float* out);
 int fh_launch_block_dots(fh_ctx* ctx, const fh_q8_0* w, const int8_t* qx, size_t m,
                          int32_t* dots);

@@ -43,6 +43,7 @@ EXPORTS = (
     "fh_q8_0_dims", "fh_q8_0_free", "fh_q8_0_linear", "fh_q8_0_linear_async",
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async",
+    "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
 )
 
 
@@ -156,6 +157,11 @@ def lib():
         L.fh_q8_0_block_dots_async.argtypes = [vp, vp, vp, sz, vp]
         L.fh_sample_rows.argtypes = [vp, vp, sz, sz, i32, C.POINTER(SamplingParams), vp, vp, vp, vp]
         L.fh_sample_rows_async.argtypes = [vp, vp, sz, sz, i32, C.POINTER(SamplingParams), vp, vp, vp, vp]
+        L.fh_embed_one_async.argtypes = [vp, vp, vp, sz, sz, sz, vp, sz, vp]
+        L.fh_layernorm_async.argtypes = [vp, vp, sz, sz, vp, vp, vp]
+        L.fh_gelu_async.argtypes = [vp, vp, sz]
+        L.fh_add_async.argtypes = [vp, vp, vp, sz]
+        L.fh_attention_decode_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, vp]
         _lib = L
     return _lib
 
@@ -424,3 +430,126 @@ def llama_decode(ctx: Context, forward_one, prompt, max_new: int, params: Sampli
         recent.append(nxt)
         logits = forward_one(nxt)
     return out
+
+
+# ---- the rest of a GPT-2 decode step (device pointers) -----------------------------
+
+def embed_one_async(ctx: Context, token_w, pos_w, vocab: int, max_seq: int, d: int, d_token, pos: int, out):
+    """Embedding::embed_one (layer/embedding.rs:70-90); the token id is read on the device."""
+    ctx.check(lib().fh_embed_one_async(ctx.h, _ptr(token_w), _ptr(pos_w), vocab, max_seq, d, _ptr(d_token), pos,
+                                       _ptr(out)))
+
+
+def layernorm_async(ctx: Context, x, rows: int, d: int, gamma, beta, y):
+    """LayerNorm::forward (layer/norm.rs:46-82)."""
+    ctx.check(lib().fh_layernorm_async(ctx.h, _ptr(x), rows, d, _ptr(gamma), _ptr(beta), _ptr(y)))
+
+
+def gelu_async(ctx: Context, x, n: int):
+    """activation::gelu (activation.rs:9-12), in place."""
+    ctx.check(lib().fh_gelu_async(ctx.h, _ptr(x), n))
+
+
+def add_async(ctx: Context, x, y, n: int):
+    """x += y (the residual adds of layer/transformer.rs:281, 288)."""
+    ctx.check(lib().fh_add_async(ctx.h, _ptr(x), _ptr(y), n))
+
+
+def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d: int, heads: int, pos: int, out):
+    """The KV-cache attention of forward_with_cache (layer/transformer.rs:242-279)."""
+    ctx.check(lib().fh_attention_decode_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
+                                              pos, _ptr(out)))
+
+
+class GPT2Device:
+    """A GPT-2 decoder on the device, the way CachedTransformer::feed walks it
+    (slm/cached.rs:100-125): embed_one, then per block forward_with_cache
+    (layer/transformer.rs:221-290: LayerNorm, fused Q|K|V Q8_0 linear, KV-cache
+    attention, out projection, residual, LayerNorm, up, GELU, down, residual),
+    the final LayerNorm and the tied Q8_0 head.  The head's scores go to the
+    fused sampler (softmax -> ln bridge inside it).
+
+    weights: dict of numpy arrays -- token_embd_q8 (GGUF Q8_0 bytes of the
+    [vocab, d] token table; the embedding uses its f32 expansion and the head
+    the Q8_0 rows, as the reference ties them), position_embd [ctx, d] f32,
+    and per block i: ln1_g/ln1_b/ln2_g/ln2_b [d], qkv_q8 ([3d, d] Q8_0) /
+    qkv_b [3d], out_q8 / out_b, up_q8 ([ffn, d]) / up_b, down_q8 ([d, ffn]) /
+    down_b; lnf_g / lnf_b."""
+
+    def __init__(self, ctx: Context, weights: dict, vocab: int, d: int, heads: int, layers: int, ffn: int,
+                 context: int):
+        import torch
+
+        self.ctx, self.vocab, self.d, self.heads, self.layers, self.ffn, self.cap = ctx, vocab, d, heads, layers, ffn, context
+        dev = torch.device("cuda")
+        f = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)  # noqa: E731
+        tok = np.frombuffer(bytes(np.asarray(weights["token_embd_q8"], np.uint8)), np.uint8)
+        self.head = Q8_0Weight.upload(ctx, tok, vocab, d)
+        self.tok_w = torch.empty((vocab, d), device=dev)
+        q8_0_dequant_async(ctx, torch.from_numpy(tok.copy()).to(dev), vocab * d, self.tok_w)
+        self.pos_w = f(weights["position_embd"])
+        self.blocks = []
+        for i in range(layers):
+            g = lambda name: weights[f"blk{i}.{name}"]  # noqa: E731
+            up = lambda name, n, k: Q8_0Weight.upload(ctx, np.asarray(g(name), np.uint8), n, k)  # noqa: E731
+            self.blocks.append(dict(
+                ln1_g=f(g("ln1_g")), ln1_b=f(g("ln1_b")), ln2_g=f(g("ln2_g")), ln2_b=f(g("ln2_b")),
+                qkv=up("qkv_q8", 3 * d, d), qkv_b=f(g("qkv_b")), out=up("out_q8", d, d), out_b=f(g("out_b")),
+                up=up("up_q8", ffn, d), up_b=f(g("up_b")), down=up("down_q8", d, ffn), down_b=f(g("down_b")),
+                k=torch.zeros((context, d), device=dev), v=torch.zeros((context, d), device=dev)))
+        self.lnf_g, self.lnf_b = f(weights["lnf_g"]), f(weights["lnf_b"])
+        self.x = torch.empty(d, device=dev)
+        self.h = torch.empty(d, device=dev)
+        self.qkv = torch.empty(3 * d, device=dev)
+        self.att = torch.empty(d, device=dev)
+        self.proj = torch.empty(d, device=dev)
+        self.mid = torch.empty(ffn, device=dev)
+        self.z = torch.empty(vocab, device=dev)
+        self.token = torch.zeros(1, dtype=torch.int32, device=dev)
+        self.pos = 0
+        torch.cuda.synchronize()  # uploads above ran on torch's stream
+        ctx.sync()
+
+    def feed_async(self, d_token, pos: int):
+        """One position: the head's scores for the next token land in self.z."""
+        ctx, d = self.ctx, self.d
+        embed_one_async(ctx, self.tok_w, self.pos_w, self.vocab, self.pos_w.shape[0], d, d_token, pos, self.x)
+        for b in self.blocks:
+            layernorm_async(ctx, self.x, 1, d, b["ln1_g"], b["ln1_b"], self.h)
+            linear_forward_async(ctx, b["qkv"], self.h, 1, d, b["qkv_b"], 3 * d, self.qkv)
+            attention_decode_async(ctx, self.qkv, b["k"], b["v"], self.cap, d, self.heads, pos, self.att)
+            linear_forward_async(ctx, b["out"], self.att, 1, d, b["out_b"], d, self.proj)
+            add_async(ctx, self.x, self.proj, d)
+            layernorm_async(ctx, self.x, 1, d, b["ln2_g"], b["ln2_b"], self.h)
+            linear_forward_async(ctx, b["up"], self.h, 1, d, b["up_b"], self.ffn, self.mid)
+            gelu_async(ctx, self.mid, self.ffn)
+            linear_forward_async(ctx, b["down"], self.mid, 1, self.ffn, b["down_b"], d, self.proj)
+            add_async(ctx, self.x, self.proj, d)
+        layernorm_async(ctx, self.x, 1, d, self.lnf_g, self.lnf_b, self.h)
+        linear_forward_async(ctx, self.head, self.h, 1, d, None, 0, self.z)
+
+    def forward(self, ids, reprime: bool):
+        """gpt2_decode's forward: re-feed the whole window from position 0, or
+        feed its last id at the next position.  Returns the scores (host)."""
+        import torch
+
+        ids = list(ids)
+        if reprime:
+            self.pos = 0
+            todo = ids
+        else:
+            todo = ids[-1:]
+        for t in todo:
+            self.ctx.sync()
+            self.token.fill_(int(t))
+            torch.cuda.current_stream().synchronize()
+            self.feed_async(self.token, self.pos)
+            self.pos += 1
+        self.ctx.sync()
+        return self.z.cpu().numpy()
+
+    def free(self):
+        self.head.free()
+        for b in self.blocks:
+            for key in ("qkv", "out", "up", "down"):
+                b[key].free()

@@ -179,6 +179,35 @@ int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t
                          const uint32_t* d_recent, const uint32_t* d_recent_offsets,
                          const uint64_t* d_draws, uint32_t* d_out_ids);
 
+/* ---- the rest of a GPT-2 decode step ------------------------------------- */
+/* Device pointers, enqueued on the context's stream.  With fh_q8_0_linear_async
+ * and fh_sample_rows_async these keep a whole decode step on the device.
+ *
+ * Embedding::embed_one (ferrum_core/src/layer/embedding.rs:70-90):
+ * out[i] = token_w[token, i] + pos_w[pos, i].  The token id is read from device
+ * memory (so a sampled id feeds the next step without a copy); an id >= vocab
+ * makes the row NaN.  pos >= max_seq -> FH_ERR_DIM, the reference's message. */
+int fh_embed_one_async(fh_ctx* ctx, const float* d_token_w, const float* d_pos_w, size_t vocab, size_t max_seq,
+                       size_t d, const uint32_t* d_token, size_t pos, float* d_out);
+/* LayerNorm::forward (layer/norm.rs:46-82) over `rows` rows of width d:
+ * ((x - mean) / sqrt(var + 1e-5)) * gamma + beta, biased variance. */
+int fh_layernorm_async(fh_ctx* ctx, const float* d_x, size_t rows, size_t d, const float* d_gamma,
+                       const float* d_beta, float* d_y);
+/* activation::gelu (activation.rs:9-12, tanh approximation), in place. */
+int fh_gelu_async(fh_ctx* ctx, float* d_x, size_t n);
+/* x += y, the residual adds of TransformerBlock::forward_with_cache
+ * (layer/transformer.rs:281, 288). */
+int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n);
+/* The attention of TransformerBlock::forward_with_cache (layer/transformer.rs:
+ * 242-279) for one new position: qkv = [q | k | v] (3d floats, the fused
+ * attn_qkv output); k and v are written at row pos of the caches
+ * ([capacity, d] each), then every head attends over rows 0 .. pos with scale
+ * 1/sqrt(d / heads).  pos >= capacity -> FH_ERR_DIM (the reference's "KvCache
+ * full" error); heads not dividing d -> FH_ERR_DIM; head widths other than 8,
+ * 16, 32, 64, 128 -> FH_ERR_LIMIT. */
+int fh_attention_decode_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
+                              size_t capacity, size_t d, size_t heads, size_t pos, float* d_out);
+
 #ifdef __cplusplus
 }
 #endif

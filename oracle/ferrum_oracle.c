@@ -607,6 +607,90 @@ void fo_ln_bridge(const float* p, size_t n, float* out) {
 }
 
 /* ------------------------------------------------------------------------ */
+/* the rest of a GPT-2 decode step                                            */
+/* ------------------------------------------------------------------------ */
+
+/* LayerNorm::forward (layer/norm.rs:46-82): per row the mean and the biased
+ * variance as sequential sums over the row divided by cols, std =
+ * sqrt(var + 1e-5), out = ((x - mean) / std) * gamma + beta. */
+void fo_layernorm(const float* x, size_t rows, size_t cols, const float* gamma, const float* beta, float* out) {
+    for (size_t r = 0; r < rows; r++) {
+        const float* xr = x + r * cols;
+        float sum = 0.0f;
+        for (size_t c = 0; c < cols; c++) sum += xr[c];
+        const float mean = sum / (float)cols;
+        float ss = 0.0f;
+        for (size_t c = 0; c < cols; c++) {
+            const float dv = xr[c] - mean;
+            ss += dv * dv;
+        }
+        const float var = ss / (float)cols;
+        const float sd = sqrtf(var + 1e-5f);
+        for (size_t c = 0; c < cols; c++) out[r * cols + c] = ((xr[c] - mean) / sd) * gamma[c] + beta[c];
+    }
+}
+
+/* activation::gelu (activation.rs:9-12), tanh approximation, in place. */
+void fo_gelu(float* x, size_t n) {
+    const float k = 0.7978846f;
+    for (size_t i = 0; i < n; i++) {
+        const float v = x[i];
+        x[i] = 0.5f * v * (1.0f + tanhf(k * (v + 0.044715f * v * v * v)));
+    }
+}
+
+/* Embedding::embed_one (layer/embedding.rs:70-90): token row + position row.
+ * token >= vocab or pos >= max_seq -> -1 (the reference's DimMismatch). */
+int fo_embed_one(const float* tok_w, const float* pos_w, size_t vocab, size_t max_seq, size_t d, size_t token,
+                 size_t pos, float* out) {
+    if (token >= vocab || pos >= max_seq) return -1;
+    for (size_t i = 0; i < d; i++) out[i] = tok_w[token * d + i] + pos_w[pos * d + i];
+    return 0;
+}
+
+/* The attention of TransformerBlock::forward_with_cache (layer/transformer.rs:
+ * 242-279): the new k, v (qkv[d .. 2d), qkv[2d .. 3d)) are written at cache row
+ * pos, then per head h the query qkv[h hd ..] attends over rows 0..pos:
+ * s_j = (sum_d q k_j) * (1 / sqrt(hd)), e_j = exp(s_j - max), sum in j order,
+ * out_h += (e_j / sum) * v_j in j order.  pos >= capacity -> -1 (cache full);
+ * d % heads != 0 -> -2. */
+int fo_attention_decode(const float* qkv, float* k_cache, float* v_cache, size_t capacity, size_t d, size_t heads,
+                        size_t pos, float* out) {
+    if (pos >= capacity) return -1;
+    if (heads == 0 || d % heads != 0) return -2;
+    for (size_t i = 0; i < d; i++) {
+        k_cache[pos * d + i] = qkv[d + i];
+        v_cache[pos * d + i] = qkv[2 * d + i];
+    }
+    const size_t len = pos + 1, hd = d / heads;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* sc = (float*)malloc(len * sizeof(float));
+    if (!sc) return -3;
+    for (size_t i = 0; i < d; i++) out[i] = 0.0f;
+    for (size_t h = 0; h < heads; h++) {
+        const size_t hs = h * hd;
+        for (size_t j = 0; j < len; j++) {
+            float dot = 0.0f;
+            for (size_t t = 0; t < hd; t++) dot += qkv[hs + t] * k_cache[j * d + hs + t];
+            sc[j] = dot * scale;
+        }
+        float mx = -INFINITY;
+        for (size_t j = 0; j < len; j++) mx = fmaxf(mx, sc[j]);
+        float sum = 0.0f;
+        for (size_t j = 0; j < len; j++) {
+            sc[j] = expf(sc[j] - mx);
+            sum += sc[j];
+        }
+        for (size_t j = 0; j < len; j++) {
+            const float pj = sc[j] / sum;
+            for (size_t t = 0; t < hd; t++) out[hs + t] += pj * v_cache[j * d + hs + t];
+        }
+    }
+    free(sc);
+    return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* RNG                                                                        */
 /* ------------------------------------------------------------------------ */
 

@@ -160,6 +160,19 @@ uint32_t fo_sample_with_params(const float* logits, size_t n, const fo_sampling_
                                const uint32_t* recent, size_t n_recent, uint64_t* rng_state,
                                fo_sample_info* info);
 
+/* The rest of a GPT-2 decode step: LayerNorm::forward (layer/norm.rs:46-82),
+ * activation::gelu in place (activation.rs:9-12), Embedding::embed_one
+ * (layer/embedding.rs:70-90; -1 when token or pos is out of range) and the
+ * attention of TransformerBlock::forward_with_cache (layer/transformer.rs:
+ * 242-279; appends k, v from qkv = [q | k | v] at row pos, -1 when the cache is
+ * full, -2 when heads does not divide d). */
+void fo_layernorm(const float* x, size_t rows, size_t cols, const float* gamma, const float* beta, float* out);
+void fo_gelu(float* x, size_t n);
+int fo_embed_one(const float* tok_w, const float* pos_w, size_t vocab, size_t max_seq, size_t d, size_t token,
+                 size_t pos, float* out);
+int fo_attention_decode(const float* qkv, float* k_cache, float* v_cache, size_t capacity, size_t d, size_t heads,
+                        size_t pos, float* out);
+
 #ifdef __cplusplus
 }
 #endif

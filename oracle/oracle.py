@@ -112,6 +112,12 @@ def lib():
                                  C.c_int]
         L.fo_qlinear.restype = C.c_int
         L.fo_softmax_rows.argtypes = [_f32p, C.c_size_t, C.c_size_t, _f32p]
+        L.fo_layernorm.argtypes = [_f32p, C.c_size_t, C.c_size_t, _f32p, _f32p, _f32p]
+        L.fo_gelu.argtypes = [_f32p, C.c_size_t]
+        L.fo_embed_one.argtypes = [_f32p, _f32p] + [C.c_size_t] * 5 + [_f32p]
+        L.fo_embed_one.restype = C.c_int
+        L.fo_attention_decode.argtypes = [_f32p, _f32p, _f32p] + [C.c_size_t] * 4 + [_f32p]
+        L.fo_attention_decode.restype = C.c_int
         L.fo_ln_bridge.argtypes = [_f32p, C.c_size_t, _f32p]
         L.fo_rng_new.argtypes = [C.c_uint64]
         L.fo_rng_new.restype = C.c_uint64
@@ -321,6 +327,43 @@ def softmax_rows(z) -> np.ndarray:
     z = _f32(np.atleast_2d(z))
     out = np.zeros_like(z)
     lib().fo_softmax_rows(z, z.shape[0], z.shape[1], out)
+    return out
+
+
+def layernorm(x, gamma, beta) -> np.ndarray:
+    """LayerNorm::forward (layer/norm.rs:46-82) over the rows of x."""
+    x = _f32(np.atleast_2d(x))
+    out = np.zeros_like(x)
+    lib().fo_layernorm(x, x.shape[0], x.shape[1], _f32(gamma), _f32(beta), out)
+    return out
+
+
+def gelu(x) -> np.ndarray:
+    """activation::gelu (activation.rs:9-12), elementwise."""
+    out = _f32(x).copy()
+    lib().fo_gelu(out.ravel(), out.size)
+    return out
+
+
+def embed_one(tok_w, pos_w, token: int, pos: int) -> np.ndarray:
+    """Embedding::embed_one (layer/embedding.rs:70-90)."""
+    tok_w, pos_w = _f32(tok_w), _f32(pos_w)
+    d = tok_w.shape[1]
+    out = np.zeros(d, np.float32)
+    if lib().fo_embed_one(tok_w, pos_w, tok_w.shape[0], pos_w.shape[0], d, token, pos, out) != 0:
+        raise ValueError(f"token {token} or position {pos} out of range")
+    return out
+
+
+def attention_decode(qkv, k_cache, v_cache, heads: int, pos: int) -> np.ndarray:
+    """The attention of TransformerBlock::forward_with_cache
+    (layer/transformer.rs:242-279): appends k, v at row pos of the caches
+    (updated in place) and returns the attention output for the new position."""
+    d = k_cache.shape[1]
+    out = np.zeros(d, np.float32)
+    rc = lib().fo_attention_decode(_f32(qkv), k_cache, v_cache, k_cache.shape[0], d, heads, pos, out)
+    if rc != 0:
+        raise ValueError(f"attention_decode: status {rc}")
     return out
 
 

@@ -1,0 +1,211 @@
+"""The rest of a GPT-2 decode step on the GPU (fh_block.hip through the C ABI)
+against the oracle: LayerNorm, GELU, the residual add, embed_one and the
+KV-cache attention one op at a time, then a small GPT-2 decoded on the device
+against the same model on the oracle (scores per position, and greedy and
+sampled token ids with the reference's tie rule)."""
+import numpy as np
+import pytest
+
+import gpt2_tiny
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, dtype=None):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def host(fh, t):
+    import torch
+
+    fh.sync()
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def ready():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def close(got, want, rtol):
+    want = np.asarray(want, np.float64)
+    err = np.abs(np.asarray(got, np.float64) - want)
+    assert np.all(err <= rtol * np.maximum(1.0, np.abs(want))), float(err.max())
+
+
+@pytest.mark.parametrize("rows,d", [(1, 768), (5, 1024), (3, 128), (2, 3)])
+def test_layernorm_matches_oracle(fh, orc, rows, d):
+    import ferrum_hip
+
+    rng = np.random.default_rng(rows * d)
+    x = (rng.standard_normal((rows, d)) * rng.choice([1e-3, 1.0, 50.0], (rows, 1))).astype(np.float32)
+    x[0, :] += np.float32(7.0)
+    g, b = rng.standard_normal(d).astype(np.float32), rng.standard_normal(d).astype(np.float32)
+    y = dev(np.zeros((rows, d), np.float32))
+    xs, gs, bs = dev(x), dev(g), dev(b)
+    ready()
+    ferrum_hip.layernorm_async(fh, xs, rows, d, gs, bs, y)
+    close(host(fh, y), orc.layernorm(x, g, b), 2e-5)
+
+
+def test_layernorm_constant_row_gives_beta(fh, orc):
+    import ferrum_hip
+
+    x, g, b = dev(np.full((1, 4), 5.0, np.float32)), dev(np.full(4, 2.0, np.float32)), dev(np.ones(4, np.float32))
+    y = dev(np.zeros((1, 4), np.float32))
+    ready()
+    ferrum_hip.layernorm_async(fh, x, 1, 4, g, b, y)
+    assert np.array_equal(host(fh, y), np.ones((1, 4), np.float32))
+
+
+def test_gelu_matches_oracle_including_saturation(fh, orc):
+    import ferrum_hip
+
+    x = np.concatenate([np.linspace(-12, 12, 4801), [0.0, -0.0, 1e4, -1e4, 1e20, 3e38, -3e38]]).astype(np.float32)
+    t = dev(x)
+    ready()
+    ferrum_hip.gelu_async(fh, t, x.size)
+    got, want = host(fh, t), orc.gelu(x)
+    close(got, want, 2e-6)
+    assert got[4801] == 0.0 and np.array_equal(got[-5:-2], want[-5:-2])
+
+
+def test_add_is_exact(fh):
+    import ferrum_hip
+
+    rng = np.random.default_rng(1)
+    a, b = rng.standard_normal(3001).astype(np.float32), rng.standard_normal(3001).astype(np.float32)
+    ta, tb = dev(a), dev(b)
+    ready()
+    ferrum_hip.add_async(fh, ta, tb, a.size)
+    assert np.array_equal(host(fh, ta), (a + b).astype(np.float32))
+
+
+def test_embed_one_reads_the_token_on_the_device(fh, orc):
+    import torch
+
+    import ferrum_hip
+
+    rng = np.random.default_rng(2)
+    tok, pos = rng.standard_normal((50, 96)).astype(np.float32), rng.standard_normal((20, 96)).astype(np.float32)
+    tt, tp, out = dev(tok), dev(pos), dev(np.zeros(96, np.float32))
+    token = torch.tensor([37], dtype=torch.int32, device="cuda")
+    ready()
+    ferrum_hip.embed_one_async(fh, tt, tp, 50, 20, 96, token, 19, out)
+    assert np.array_equal(host(fh, out), orc.embed_one(tok, pos, 37, 19))
+    with pytest.raises(ferrum_hip.DimMismatch, match="Position 20 exceeds max_seq_len 20"):
+        ferrum_hip.embed_one_async(fh, tt, tp, 50, 20, 96, token, 20, out)
+    token.fill_(50)                                   # past the vocabulary: a NaN row
+    ready()
+    ferrum_hip.embed_one_async(fh, tt, tp, 50, 20, 96, token, 0, out)
+    assert np.isnan(host(fh, out)).all()
+
+
+@pytest.mark.parametrize("d,heads,T", [(768, 12, 70), (128, 4, 33), (96, 3, 5), (256, 2, 40)])
+def test_attention_decode_matches_oracle(fh, orc, d, heads, T):
+    import ferrum_hip
+
+    rng = np.random.default_rng(d + T)
+    cap = T + 3
+    qkv = (rng.standard_normal((T, 3 * d)) * 1.5).astype(np.float32)
+    kc, vc = dev(np.zeros((cap, d), np.float32)), dev(np.zeros((cap, d), np.float32))
+    ko, vo = np.zeros((cap, d), np.float32), np.zeros((cap, d), np.float32)
+    out = dev(np.zeros(d, np.float32))
+    for t in range(T):
+        q = dev(qkv[t])
+        ready()
+        ferrum_hip.attention_decode_async(fh, q, kc, vc, cap, d, heads, t, out)
+        close(host(fh, out), orc.attention_decode(qkv[t], ko, vo, heads, t), 1e-5)
+    assert np.array_equal(host(fh, kc), ko) and np.array_equal(host(fh, vc), vo)
+
+
+def test_attention_decode_errors(fh):
+    import ferrum_hip
+
+    q, kc, vc, out = (dev(np.zeros(n, np.float32)) for n in (24, 32, 32, 8))
+    ready()
+    with pytest.raises(ferrum_hip.DimMismatch, match="KvCache full"):
+        ferrum_hip.attention_decode_async(fh, q, kc, vc, 4, 8, 2, 4, out)
+    with pytest.raises(ferrum_hip.DimMismatch, match="must divide"):
+        ferrum_hip.attention_decode_async(fh, q, kc, vc, 4, 8, 3, 0, out)
+    with pytest.raises(ferrum_hip.FerrumHipError):
+        ferrum_hip.attention_decode_async(fh, dev(np.zeros(3 * 12, np.float32)), dev(np.zeros(48, np.float32)),
+                                          dev(np.zeros(48, np.float32)), 4, 12, 1, 0, dev(np.zeros(12, np.float32)))
+
+
+@pytest.fixture(scope="module")
+def tiny(fh, orc):
+    import ferrum_hip
+
+    w = gpt2_tiny.make_weights(orc, seed=11)
+    model = ferrum_hip.GPT2Device(fh, w, gpt2_tiny.VOCAB, gpt2_tiny.D, gpt2_tiny.HEADS, gpt2_tiny.LAYERS,
+                                  gpt2_tiny.FFN, gpt2_tiny.CTX)
+    yield w, model
+    model.free()
+
+
+def test_tiny_gpt2_scores_match_the_oracle_per_position(orc, tiny):
+    w, model = tiny
+    ref = gpt2_tiny.OracleGPT2(orc, w)
+    ids = list(np.random.default_rng(4).integers(0, gpt2_tiny.VOCAB, 24))
+    for i, t in enumerate(ids):
+        got = model.forward(ids[: i + 1], reprime=(i == 0))
+        want = ref.forward(ids[: i + 1], reprime=(i == 0))
+        close(got, want, 2e-5 * max(1.0, float(np.abs(want).max())))
+
+
+def test_tiny_gpt2_greedy_decode_matches_the_oracle(fh, orc, tiny):
+    """The tiny configuration's run: 16-token prompt, 64 greedy tokens.  Each
+    step's id must be the oracle's greedy id on the same window unless the
+    oracle's top-2 gap there is below 1e-5 (then the runs may part)."""
+    import ferrum_hip
+
+    w, model = tiny
+    prompt = list(np.random.default_rng(6).integers(0, gpt2_tiny.VOCAB, 16))
+    scores = []
+
+    def fwd(ids, reprime):
+        z = model.forward(ids, reprime)
+        scores.append(z)
+        return z
+
+    got = ferrum_hip.gpt2_decode(fh, fwd, prompt, 64, ferrum_hip.SamplingParams(temperature=0.0),
+                                 ferrum_hip.Rng(1), gpt2_tiny.CTX)
+    assert len(got) == 64
+    ref = gpt2_tiny.OracleGPT2(orc, w)
+    win = ferrum_hip.GPT2Window(gpt2_tiny.CTX, prompt)
+    z = ref.forward(win.ids, True)
+    for step, tok in enumerate(got):
+        p = orc.ln_bridge(orc.softmax_rows(z)[0])
+        want = int(np.argmax(p))
+        if want != tok:
+            top2 = np.sort(p)[-2:]
+            assert top2[1] - top2[0] < 1e-5, (step, tok, want)
+            break
+        reprime = win.push(tok)
+        z = ref.forward(win.ids, reprime)
+
+
+def test_tiny_gpt2_sampled_decode_replays_on_the_oracle(fh, orc, tiny):
+    import ferrum_hip
+
+    w, model = tiny
+    kw = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
+    prompt = list(np.random.default_rng(7).integers(0, gpt2_tiny.VOCAB, 16))
+    got = ferrum_hip.gpt2_decode(fh, model.forward, prompt, 48, ferrum_hip.SamplingParams(**kw),
+                                 ferrum_hip.Rng(5), gpt2_tiny.CTX)
+    ref = gpt2_tiny.OracleGPT2(orc, w)
+    win, rng, op = ferrum_hip.GPT2Window(gpt2_tiny.CTX, prompt), orc.Rng(5), orc.SamplingParams(**kw)
+    z = ref.forward(win.ids, True)
+    for step, tok in enumerate(got):
+        want, info = orc.sample(orc.ln_bridge(orc.softmax_rows(z)[0]), op, win.ids, rng.next_u64())
+        if want != tok:
+            assert info.margin < 1e-4, (step, tok, want, info.margin)
+            break
+        reprime = win.push(tok)
+        z = ref.forward(win.ids, reprime)
