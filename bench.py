@@ -51,6 +51,7 @@ B32 = 32
 MED_D, MED_L, MED_FFN, MED_M = 1024, 24, 4096, 32 * 512
 MED_SHAPES = [(3 * MED_D, MED_D), (MED_D, MED_D), (MED_FFN, MED_D), (MED_D, MED_FFN)]
 F16_DENSE_TFLOPS, I8_DENSE_TOPS = 2500.0, 5000.0
+HEADS, CTX, FULL_POS = 12, 1024, 255  # GPT-2-124M attention; the whole-step leg's position
 
 COPY_BYTES = 256 << 20
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q8_0_lm_head_pmc.json")
@@ -199,6 +200,44 @@ def main():
         del graphs
         torch.cuda.synchronize()
 
+        # The whole decode step on the device (GPT-2-124M, b1): embed_one, 12
+        # blocks (LayerNorm, fused QKV, KV-cache attention, out projection,
+        # residual, LayerNorm, up, GELU, down, residual), the final LayerNorm,
+        # the head and the sampler, whose id feeds the next replay's embedding
+        # on the device.  At position FULL_POS (mid-run of the 128-token prompt
+        # + 256 steps); one model per replica (HBM-forced).
+        models = [fh.GPT2Device.random(ctx, V, D, HEADS, L, FFN, CTX, gen) for _ in range(args.replicas)]
+
+        def full_step(mdl):
+            mdl.feed_async(mdl.token, FULL_POS)
+            fh.sample_rows_async(ctx, mdl.z, 1, V, params, rec, rec_off, draws, mdl.token, fh.LOGITS_GPT2_SOFTMAX)
+
+        for mdl in models:
+            full_step(mdl)
+        torch.cuda.synchronize()
+        graphs_f = []
+        for mdl in models:
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+                full_step(mdl)
+            ctx.set_stream(stream.cuda_stream)
+            graphs_f.append(g)
+        torch.cuda.synchronize()
+        ms_full, _ = timed(graphs_f, max(args.steps // 4, 10), args.warmup)
+        kv_bytes = 2 * L * (FULL_POS + 1) * D * 4
+        result["full_step"] = {
+            "tok_s": round(1000.0 / ms_full, 1), "ms_per_step": round(ms_full, 5), "position": FULL_POS,
+            "launches_per_step": 2 + 6 * L + 2, "kv_cache_bytes_read": kv_bytes,
+            "residency": f"hbm-forced ({args.replicas} model replicas)",
+            "what": "embed_one + LayerNorm + 12 x (QKV, attention, out, add+LayerNorm, up+GELU, down, "
+                    "add+LayerNorm) + head + sampler, all on the device"}
+        del graphs_f
+        for mdl in models:
+            mdl.free()
+        del models
+        torch.cuda.synchronize()
+
         # ---- batch 32: the same step for 32 sequences (BASELINE's b32 decode) ----
         B = B32
         xb_d = torch.randn((B, D), generator=gen, device=dev)
@@ -342,6 +381,7 @@ def main():
         "step_weight_GBps": round(result["step_weight_bytes"] / (ms * 1e-3) / 1e9, 1),
         "sampler_us_per_row": result["sampler_us_per_row"],
         "wall_ms_per_step": round(result["wall_ms_per_step"], 5),
+        "full_decode_step": result["full_step"],
         "b32": result["b32"],
         "prefill": result["prefill"],
         "hbm_copy_GBps": round(copy_GBps, 1) if copy_GBps else None,

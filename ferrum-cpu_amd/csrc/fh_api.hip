@@ -556,3 +556,33 @@ int fh_attention_decode_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache,
     FH_ON_DEVICE(ctx);
     return fh_launch_attention_decode(ctx, d_qkv, d_k_cache, d_v_cache, d, heads, pos, d_out);
 }
+
+int fh_q8_0_linear_act_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                             const float* d_bias, size_t bias_len, float* d_y, int numerics, int activation) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (activation != FH_ACT_NONE && activation != FH_ACT_GELU)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: unknown activation " + std::to_string(activation));
+    int rc = check_linear(ctx, w, k, d_bias, bias_len, numerics);
+    if (rc) return rc;
+    if (m == 0) return FH_OK;
+    if (!d_x || !d_y) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x or y is NULL");
+    FH_ON_DEVICE(ctx);
+    if (numerics == FH_W8A32) return fh_launch_linear_w8a32(ctx, w, d_x, m, d_bias, d_y, activation);
+    rc = fh_launch_linear_w8a8(ctx, w, d_x, m, d_bias, d_y);
+    if (rc == FH_OK && activation == FH_ACT_GELU) rc = fh_launch_gelu(ctx, d_y, m * w->n);
+    return rc;
+}
+
+int fh_add_layernorm_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t rows, size_t d, const float* d_gamma,
+                           const float* d_beta, float* d_ln) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rows == 0) return FH_OK;
+    if (!d_x || !d_y || !d_gamma || !d_beta || !d_ln)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_add_layernorm: a pointer is NULL");
+    if (d == 0 || rows > 0x7FFFFFFFu)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_add_layernorm: d must be positive");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_add_layernorm(ctx, d_x, d_y, rows, d, d_gamma, d_beta, d_ln);
+}

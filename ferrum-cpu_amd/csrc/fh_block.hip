@@ -9,6 +9,9 @@
 //  k_gelu        activation::gelu (activation.rs:9-12), in place.
 //  k_add         the residual adds of forward_with_cache (layer/transformer.rs:
 //                281, 288), in place.
+//  k_add_layernorm  a residual add and the LayerNorm that follows it (ln2 of
+//                the block, or the next block's ln1 / the final LayerNorm) in
+//                one pass: the same arithmetic as k_add then k_layernorm.
 //  k_attn_chunk  the attention of forward_with_cache (layer/transformer.rs:
 //                242-279) for one query: the new k and v rows are written at
 //                cache row pos, then each (head, 32-position chunk) workgroup
@@ -96,6 +99,7 @@ __global__ void __launch_bounds__(kThreads)
     __shared__ float q[kMaxHd];
     __shared__ float sc[kChunk];
     __shared__ float acc[kThreads];
+    __shared__ float stat[2];
     __shared__ int last;
     const int chunk = blockIdx.x, head = blockIdx.y, chunks = gridDim.x;
     const int hs = head * hd, tid = threadIdx.x;
@@ -123,23 +127,34 @@ __global__ void __launch_bounds__(kThreads)
         dot += __shfl_xor(dot, 1, 64);
         dot += __shfl_xor(dot, 2, 64);
         dot += __shfl_xor(dot, 4, 64);
-        if (part8 == 0 && jl < kChunk) sc[jl] = jl < jn ? dot * scale : -INFINITY;
+        if (part8 == 0) sc[jl] = jl < jn ? dot * scale : -INFINITY;
     }
     __syncthreads();
-    float mx = -INFINITY;
-    for (int j = 0; j < jn; j++) mx = fmaxf(mx, sc[j]);
-    float se = 0.0f;
-    for (int j = 0; j < jn; j++) se += expf(sc[j] - mx);
+    // the chunk's max and exponentials, once each (wave 0; lanes past the
+    // chunk hold -inf and 0)
+    if (tid < 64) {
+        const float s = tid < kChunk ? sc[tid] : -INFINITY;
+        float mx = s;
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+        const float e = tid < jn ? expf(s - mx) : 0.0f;
+        const float se = wave_sum(e);
+        if (tid < kChunk) sc[tid] = e;
+        if (tid == 0) {
+            stat[0] = mx;
+            stat[1] = se;
+        }
+    }
+    __syncthreads();
     // weighted v sum over this chunk: thread (g, t) takes positions g, g + G, ...
     const int groups = kThreads / hd;
     const int t = tid % hd, g = tid / hd;
     float o = 0.0f;
-    if (g < groups)
-        for (int jl = g; jl < jn; jl += groups) {
-            const int j = j0 + jl;
-            const float* vr = j == pos ? qkv + 2 * d + hs : vc + static_cast<size_t>(j) * d + hs;
-            o += expf(sc[jl] - mx) * vr[t];
-        }
+    for (int jl = g; jl < jn; jl += groups) {
+        const int j = j0 + jl;
+        const float* vr = j == pos ? qkv + 2 * d + hs : vc + static_cast<size_t>(j) * d + hs;
+        o += sc[jl] * vr[t];
+    }
     acc[tid] = o;
     __syncthreads();
     float* mine = part + (static_cast<size_t>(head) * chunks + chunk) * (2 + hd);
@@ -149,8 +164,8 @@ __global__ void __launch_bounds__(kThreads)
         __hip_atomic_store(mine + 2 + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     if (tid == 0) {
-        __hip_atomic_store(mine, mx, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(mine + 1, se, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mine, stat[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(mine + 1, stat[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // Publish: every thread's coherent stores complete before the arrival
     // count moves, so the last arrival reads whole partials.
@@ -159,25 +174,80 @@ __global__ void __launch_bounds__(kThreads)
     if (tid == 0) last = atomicAdd(counters + head, 1u) == static_cast<unsigned>(chunks - 1);
     __syncthreads();
     if (!last) return;
+    // Merge, eight chunks per round with all their loads in flight at once.
     const float* hp = part + static_cast<size_t>(head) * chunks * (2 + hd);
+    constexpr int R = 8;
     float M = -INFINITY;
-    for (int c = 0; c < chunks; c++)
-        M = fmaxf(M, __hip_atomic_load(hp + c * (2 + hd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    float S = 0.0f;
-    for (int c = 0; c < chunks; c++) {
-        const float mc = __hip_atomic_load(hp + c * (2 + hd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        S += __hip_atomic_load(hp + c * (2 + hd) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) * expf(mc - M);
+    for (int c0 = 0; c0 < chunks; c0 += R) {
+        float mc[R];
+#pragma unroll
+        for (int i = 0; i < R; i++)
+            mc[i] = __hip_atomic_load(hp + min(c0 + i, chunks - 1) * (2 + hd), __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+        for (int i = 0; i < R; i++) M = fmaxf(M, mc[i]);  // repeats of the last chunk change nothing
     }
-    if (tid < hd) {
-        float r = 0.0f;
-        for (int c = 0; c < chunks; c++) {
-            const float mc = __hip_atomic_load(hp + c * (2 + hd), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            r += __hip_atomic_load(hp + c * (2 + hd) + 2 + tid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) *
-                 expf(mc - M);
+    float S = 0.0f, r = 0.0f;
+    const int tt = min(tid, hd - 1);
+    for (int c0 = 0; c0 < chunks; c0 += R) {
+        float mc[R], sc8[R], oc[R];
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            const float* cp = hp + min(c0 + i, chunks - 1) * (2 + hd);
+            mc[i] = __hip_atomic_load(cp, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            sc8[i] = __hip_atomic_load(cp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            oc[i] = __hip_atomic_load(cp + 2 + tt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
-        out[hs + tid] = r / S;
+#pragma unroll
+        for (int i = 0; i < R; i++) {
+            if (c0 + i >= chunks) break;
+            const float f = expf(mc[i] - M);
+            S += sc8[i] * f;
+            r += oc[i] * f;
+        }
     }
+    if (tid < hd) out[hs + tid] = r / S;
     if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// x += y, then LayerNorm of the sum into ln (the residual add of
+// forward_with_cache followed by the next LayerNorm), one workgroup per row.
+__global__ void __launch_bounds__(kThreads) k_add_layernorm(float* __restrict__ x, const float* __restrict__ y, int d,
+                                                           const float* __restrict__ gamma,
+                                                           const float* __restrict__ beta, float* __restrict__ ln) {
+    __shared__ float red[kThreads / 64];
+    float* xr = x + static_cast<size_t>(blockIdx.x) * d;
+    const float* yr = y + static_cast<size_t>(blockIdx.x) * d;
+    float* lr = ln + static_cast<size_t>(blockIdx.x) * d;
+    constexpr int kPer = 8;  // row elements a thread keeps in registers (d <= 2048 here)
+    float v[kPer];
+    float s = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int c = threadIdx.x + i * kThreads;
+        v[i] = c < d ? xr[c] + yr[c] : 0.0f;
+        if (c < d) {
+            xr[c] = v[i];
+            s += v[i];
+        }
+    }
+    const float mean = block_sum(s, red) / static_cast<float>(d);
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int c = threadIdx.x + i * kThreads;
+        if (c < d) {
+            const float dv = v[i] - mean;
+            ss += dv * dv;
+        }
+    }
+    const float var = block_sum(ss, red) / static_cast<float>(d);
+    const float sd = sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int c = threadIdx.x + i * kThreads;
+        if (c < d) lr[c] = ((v[i] - mean) / sd) * gamma[c] + beta[c];
+    }
 }
 
 unsigned blocks_for(size_t n) { return static_cast<unsigned>((n + kThreads - 1) / kThreads); }
@@ -208,6 +278,16 @@ int fh_launch_gelu(fh_ctx* ctx, float* x, size_t n) {
 
 int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n) {
     hipLaunchKernelGGL(k_add, dim3(blocks_for(n)), dim3(kThreads), 0, ctx->stream, x, y, n);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_add_layernorm(fh_ctx* ctx, float* x, const float* y, size_t rows, size_t d, const float* gamma,
+                            const float* beta, float* ln) {
+    if (d > 8 * static_cast<size_t>(kThreads))
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_add_layernorm: rows wider than 2048");
+    hipLaunchKernelGGL(k_add_layernorm, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x, y,
+                       static_cast<int>(d), gamma, beta, ln);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }

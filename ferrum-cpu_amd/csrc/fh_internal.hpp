@@ -81,7 +81,7 @@ int fh_launch_row_exponents(fh_ctx* ctx, const uint16_t* d, size_t n, size_t kb,
 int fh_launch_unpack(fh_ctx* ctx, const int8_t* qs, const uint16_t* d, size_t n, size_t k,
                      uint8_t* d_raw);
 int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
-                           const float* bias, float* y);
+                           const float* bias, float* y, int act = FH_ACT_NONE);
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                          const float* bias, float* y);
 int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
@@ -95,6 +95,8 @@ int fh_launch_layernorm(fh_ctx* ctx, const float* x, size_t rows, size_t d, cons
                         const float* beta, float* y);
 int fh_launch_gelu(fh_ctx* ctx, float* x, size_t n);
 int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n);
+int fh_launch_add_layernorm(fh_ctx* ctx, float* x, const float* y, size_t rows, size_t d, const float* gamma,
+                            const float* beta, float* ln);
 int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
                                size_t pos, float* out);
 int fh_launch_dequant(fh_ctx* ctx, const uint8_t* raw, size_t n, float* out);

@@ -25,6 +25,10 @@
 
 #include <type_traits>
 
+// The epilogues round every product and sum as the reference does (its GELU
+// and bias adds have no FMA); the dot products use explicit fmaf.
+#pragma clang fp contract(off)
+
 __global__ void fh_k_encode_split(const float* __restrict__ x, size_t nblocks, uint32_t* __restrict__ qx,
                                   uint16_t* __restrict__ dx);
 
@@ -69,7 +73,7 @@ __device__ __forceinline__ float group_sum(float v) {
 template <int G, int CPL, int M, int U, bool kBias>
 __global__ void __launch_bounds__(64 * kWaves)
     k_gemv_w8a32(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const float* __restrict__ x,
-                 const float* __restrict__ bias, float* __restrict__ y, int n, int k, int per_wave) {
+                 const float* __restrict__ bias, float* __restrict__ y, int n, int k, int per_wave, int act) {
     constexpr int RW = 64 / G;  // rows per row-set
     const int lane = threadIdx.x & 63;
     const int grp = lane / G, gl = lane % G;
@@ -109,6 +113,13 @@ __global__ void __launch_bounds__(64 * kWaves)
     // short last batch (kTail) loads its own row-sets only (slots past the end
     // re-read its last row-set: cache hits, never computed) and skips the
     // empty slots; nothing follows it.
+    // Bias, then the optional GELU the caller's next op would apply
+    // (activation::gelu, activation.rs:9-12), rounded as the reference does.
+    auto finish = [](float v, float b, int a) __attribute__((always_inline)) {
+        if (kBias) v = v + b;
+        if (a == FH_ACT_GELU) v = 0.5f * v * (1.0f + tanhf(0.7978846f * (v + 0.044715f * v * v * v)));
+        return v;
+    };
     auto batch = [&](int sb, auto tail) __attribute__((always_inline)) {
         constexpr bool kTail = decltype(tail)::value;
         uint4 qv[U][CPL];
@@ -155,7 +166,7 @@ __global__ void __launch_bounds__(64 * kWaves)
                 for (int m = 0; m < M; m++) acc[m] = group_sum<G>(acc[m]);
                 if (gl == 0 && row < n) {
 #pragma unroll
-                    for (int m = 0; m < M; m++) y[static_cast<size_t>(m) * n + row] = kBias ? acc[m] + bv[u] : acc[m];
+                    for (int m = 0; m < M; m++) y[static_cast<size_t>(m) * n + row] = finish(acc[m], bv[u], act);
                 }
             } else {
                 // G = 32 or 64: 16-lane row totals, then across rows with readlane
@@ -165,7 +176,7 @@ __global__ void __launch_bounds__(64 * kWaves)
                     const float lo = rdlane(r16, 0) + rdlane(r16, 16);
                     const float hi = rdlane(r16, 32) + rdlane(r16, 48);
                     const float tot = G == 64 ? lo + hi : (grp == 0 ? lo : hi);
-                    if (gl == 0 && row < n) y[static_cast<size_t>(m) * n + row] = kBias ? tot + bv[u] : tot;
+                    if (gl == 0 && row < n) y[static_cast<size_t>(m) * n + row] = finish(tot, bv[u], act);
                 }
             }
         }
@@ -218,7 +229,7 @@ __global__ void __launch_bounds__(256)
 // Row-sets per wave: enough waves to cover the chip (12 per CU on 256 CUs)
 // before a wave takes more than one row-set; beyond U, whole batches of U.
 template <int G, int CPL, int M, int U>
-int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y) {
+int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y, int act) {
     constexpr int RW = 64 / G;
     const size_t nsets = (w->n + RW - 1) / RW;
     size_t per_wave = (nsets + 3071) / 3072;
@@ -229,7 +240,7 @@ int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias
     // The bias-free form (ops::matmul, the tied lm_head) is its own instance.
     auto kernel = bias ? k_gemv_w8a32<G, CPL, M, U, true> : k_gemv_w8a32<G, CPL, M, U, false>;
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves), 0, ctx->stream, w->qs, w->d,
-                       x, bias, y, static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(per_wave));
+                       x, bias, y, static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(per_wave), act);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -239,9 +250,9 @@ int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias
 // smallest power-of-two G with at most 4 chunks per lane.  U keeps about 12
 // quant loads in flight per lane.
 template <int M>
-int dispatch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y) {
+int dispatch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y, int act) {
     const size_t k16 = w->k / 16;
-#define FH_GEMV(G, C) return launch_gemv<G, C, M, (12 / C > 0 ? 12 / C : 1)>(ctx, w, x, bias, y)
+#define FH_GEMV(G, C) return launch_gemv<G, C, M, (12 / C > 0 ? 12 / C : 1)>(ctx, w, x, bias, y, act)
     if (k16 >= 64) {
         switch ((k16 + 63) / 64) {
             case 1: FH_GEMV(64, 1);
@@ -283,16 +294,19 @@ int launch_w8a8(fh_ctx* ctx, const fh_q8_0* w, const int8_t* qx, const uint16_t*
 
 }  // namespace
 
-int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                           int act) {
     if (reinterpret_cast<uintptr_t>(x) & 15)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x must be 16-byte aligned");
     if (w->n > 0x7FFFFFFFu || w->k > 0x7FFFFFFFu || m > 0x7FFFFFFFu)
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: a dimension is above 2^31 - 1");
     if (m <= 2) {
-        int rc = m == 1 ? dispatch_gemv<1>(ctx, w, x, bias, y) : dispatch_gemv<2>(ctx, w, x, bias, y);
+        int rc = m == 1 ? dispatch_gemv<1>(ctx, w, x, bias, y, act) : dispatch_gemv<2>(ctx, w, x, bias, y, act);
         if (rc >= 0) return rc;
     }
-    return fh_launch_gemm_w8a32(ctx, w, x, m, bias, y);
+    int rc = fh_launch_gemm_w8a32(ctx, w, x, m, bias, y);
+    if (rc == FH_OK && act == FH_ACT_GELU) rc = fh_launch_gelu(ctx, y, m * w->n);
+    return rc;
 }
 
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {

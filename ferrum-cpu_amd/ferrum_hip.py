@@ -44,6 +44,7 @@ EXPORTS = (
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
+    "fh_q8_0_linear_act_async", "fh_add_layernorm_async",
 )
 
 
@@ -162,6 +163,8 @@ def lib():
         L.fh_gelu_async.argtypes = [vp, vp, sz]
         L.fh_add_async.argtypes = [vp, vp, vp, sz]
         L.fh_attention_decode_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, vp]
+        L.fh_q8_0_linear_act_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32, i32]
+        L.fh_add_layernorm_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         _lib = L
     return _lib
 
@@ -455,6 +458,21 @@ def add_async(ctx: Context, x, y, n: int):
     ctx.check(lib().fh_add_async(ctx.h, _ptr(x), _ptr(y), n))
 
 
+ACT_NONE, ACT_GELU = 0, 1
+
+
+def linear_act_async(ctx: Context, weight: "Q8_0Weight", x, m: int, k: int, bias, bias_len: int, y, act: int,
+                     numerics: int = W8A32):
+    """Linear::forward followed by an activation (ACT_GELU: the block's ffn1 + gelu)."""
+    ctx.check(lib().fh_q8_0_linear_act_async(ctx.h, weight.h, _ptr(x), m, k, _ptr(bias), bias_len, _ptr(y),
+                                             numerics, act))
+
+
+def add_layernorm_async(ctx: Context, x, y, rows: int, d: int, gamma, beta, ln):
+    """x += y, then LayerNorm(x) into ln (a residual add and the LayerNorm after it)."""
+    ctx.check(lib().fh_add_layernorm_async(ctx.h, _ptr(x), _ptr(y), rows, d, _ptr(gamma), _ptr(beta), _ptr(ln)))
+
+
 def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d: int, heads: int, pos: int, out):
     """The KV-cache attention of forward_with_cache (layer/transformer.rs:242-279)."""
     ctx.check(lib().fh_attention_decode_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
@@ -469,35 +487,19 @@ class GPT2Device:
     the final LayerNorm and the tied Q8_0 head.  The head's scores go to the
     fused sampler (softmax -> ln bridge inside it).
 
-    weights: dict of numpy arrays -- token_embd_q8 (GGUF Q8_0 bytes of the
-    [vocab, d] token table; the embedding uses its f32 expansion and the head
-    the Q8_0 rows, as the reference ties them), position_embd [ctx, d] f32,
-    and per block i: ln1_g/ln1_b/ln2_g/ln2_b [d], qkv_q8 ([3d, d] Q8_0) /
-    qkv_b [3d], out_q8 / out_b, up_q8 ([ffn, d]) / up_b, down_q8 ([d, ffn]) /
-    down_b; lnf_g / lnf_b."""
+    from_weights takes a dict of numpy arrays -- token_embd_q8 (GGUF Q8_0
+    bytes of the [vocab, d] token table; the embedding uses its f32 expansion
+    and the head the Q8_0 rows, as the reference ties them), position_embd
+    [ctx, d] f32, and per block i: ln1_g/ln1_b/ln2_g/ln2_b [d], qkv_q8
+    ([3d, d] Q8_0) / qkv_b [3d], out_q8 / out_b, up_q8 ([ffn, d]) / up_b,
+    down_q8 ([d, ffn]) / down_b; lnf_g / lnf_b.  random builds the same on the
+    device from a torch generator (N(0, 0.02) weights, for timing)."""
 
-    def __init__(self, ctx: Context, weights: dict, vocab: int, d: int, heads: int, layers: int, ffn: int,
-                 context: int):
+    def __init__(self, ctx: Context, vocab: int, d: int, heads: int, layers: int, ffn: int, context: int):
         import torch
 
         self.ctx, self.vocab, self.d, self.heads, self.layers, self.ffn, self.cap = ctx, vocab, d, heads, layers, ffn, context
         dev = torch.device("cuda")
-        f = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(dev)  # noqa: E731
-        tok = np.frombuffer(bytes(np.asarray(weights["token_embd_q8"], np.uint8)), np.uint8)
-        self.head = Q8_0Weight.upload(ctx, tok, vocab, d)
-        self.tok_w = torch.empty((vocab, d), device=dev)
-        q8_0_dequant_async(ctx, torch.from_numpy(tok.copy()).to(dev), vocab * d, self.tok_w)
-        self.pos_w = f(weights["position_embd"])
-        self.blocks = []
-        for i in range(layers):
-            g = lambda name: weights[f"blk{i}.{name}"]  # noqa: E731
-            up = lambda name, n, k: Q8_0Weight.upload(ctx, np.asarray(g(name), np.uint8), n, k)  # noqa: E731
-            self.blocks.append(dict(
-                ln1_g=f(g("ln1_g")), ln1_b=f(g("ln1_b")), ln2_g=f(g("ln2_g")), ln2_b=f(g("ln2_b")),
-                qkv=up("qkv_q8", 3 * d, d), qkv_b=f(g("qkv_b")), out=up("out_q8", d, d), out_b=f(g("out_b")),
-                up=up("up_q8", ffn, d), up_b=f(g("up_b")), down=up("down_q8", d, ffn), down_b=f(g("down_b")),
-                k=torch.zeros((context, d), device=dev), v=torch.zeros((context, d), device=dev)))
-        self.lnf_g, self.lnf_b = f(weights["lnf_g"]), f(weights["lnf_b"])
         self.x = torch.empty(d, device=dev)
         self.h = torch.empty(d, device=dev)
         self.qkv = torch.empty(3 * d, device=dev)
@@ -507,25 +509,86 @@ class GPT2Device:
         self.z = torch.empty(vocab, device=dev)
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.pos = 0
-        torch.cuda.synchronize()  # uploads above ran on torch's stream
+        self.blocks = []
+
+    def _block(self, ln, qkv, qkv_b, out, out_b, up, up_b, down, down_b):
+        import torch
+
+        return dict(ln1_g=ln[0], ln1_b=ln[1], ln2_g=ln[2], ln2_b=ln[3], qkv=qkv, qkv_b=qkv_b, out=out, out_b=out_b,
+                    up=up, up_b=up_b, down=down, down_b=down_b,
+                    k=torch.zeros((self.cap, self.d), device="cuda"), v=torch.zeros((self.cap, self.d), device="cuda"))
+
+    @classmethod
+    def from_weights(cls, ctx: Context, weights: dict, vocab: int, d: int, heads: int, layers: int, ffn: int,
+                     context: int) -> "GPT2Device":
+        import torch
+
+        m = cls(ctx, vocab, d, heads, layers, ffn, context)
+        f = lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda()  # noqa: E731
+        tok = np.frombuffer(bytes(np.asarray(weights["token_embd_q8"], np.uint8)), np.uint8)
+        m.head = Q8_0Weight.upload(ctx, tok, vocab, d)
+        m.tok_w = torch.empty((vocab, d), device="cuda")
+        raw = torch.from_numpy(tok.copy()).cuda()
+        torch.cuda.synchronize()
+        q8_0_dequant_async(ctx, raw, vocab * d, m.tok_w)
+        m.pos_w = f(weights["position_embd"])
+        for i in range(layers):
+            g = lambda name: weights[f"blk{i}.{name}"]  # noqa: E731
+            up = lambda name, n, k: Q8_0Weight.upload(ctx, np.asarray(g(name), np.uint8), n, k)  # noqa: E731
+            m.blocks.append(m._block([f(g(n)) for n in ("ln1_g", "ln1_b", "ln2_g", "ln2_b")],
+                                     up("qkv_q8", 3 * d, d), f(g("qkv_b")), up("out_q8", d, d), f(g("out_b")),
+                                     up("up_q8", ffn, d), f(g("up_b")), up("down_q8", d, ffn), f(g("down_b"))))
+        m.lnf_g, m.lnf_b = f(weights["lnf_g"]), f(weights["lnf_b"])
+        torch.cuda.synchronize()  # uploads ran on torch's stream
         ctx.sync()
+        return m
+
+    @classmethod
+    def random(cls, ctx: Context, vocab: int, d: int, heads: int, layers: int, ffn: int, context: int,
+               gen) -> "GPT2Device":
+        import torch
+
+        m = cls(ctx, vocab, d, heads, layers, ffn, context)
+
+        def q8(n, k):
+            w = torch.randn((n, k), generator=gen, device="cuda") * 0.02
+            raw = torch.empty(n * k // 32 * 34, dtype=torch.uint8, device="cuda")
+            torch.cuda.synchronize()
+            q8_0_encode_async(ctx, w, n * k, raw)
+            q = Q8_0Weight.upload_device(ctx, raw, n, k)
+            ctx.sync()
+            return q, raw
+
+        vec = lambda n, base=0.0: torch.randn(n, generator=gen, device="cuda") * 0.02 + base  # noqa: E731
+        m.head, raw = q8(vocab, d)
+        m.tok_w = torch.empty((vocab, d), device="cuda")
+        q8_0_dequant_async(ctx, raw, vocab * d, m.tok_w)
+        ctx.sync()
+        m.pos_w = vec(context * d).reshape(context, d)
+        for _ in range(layers):
+            m.blocks.append(m._block([vec(d, 1.0), vec(d), vec(d, 1.0), vec(d)], q8(3 * d, d)[0], vec(3 * d),
+                                     q8(d, d)[0], vec(d), q8(ffn, d)[0], vec(ffn), q8(d, ffn)[0], vec(d)))
+        m.lnf_g, m.lnf_b = vec(d, 1.0), vec(d)
+        torch.cuda.synchronize()
+        ctx.sync()
+        return m
 
     def feed_async(self, d_token, pos: int):
         """One position: the head's scores for the next token land in self.z."""
         ctx, d = self.ctx, self.d
         embed_one_async(ctx, self.tok_w, self.pos_w, self.vocab, self.pos_w.shape[0], d, d_token, pos, self.x)
-        for b in self.blocks:
-            layernorm_async(ctx, self.x, 1, d, b["ln1_g"], b["ln1_b"], self.h)
+        layernorm_async(ctx, self.x, 1, d, self.blocks[0]["ln1_g"], self.blocks[0]["ln1_b"], self.h)
+        for i, b in enumerate(self.blocks):
+            # self.h holds ln1(x) here
             linear_forward_async(ctx, b["qkv"], self.h, 1, d, b["qkv_b"], 3 * d, self.qkv)
             attention_decode_async(ctx, self.qkv, b["k"], b["v"], self.cap, d, self.heads, pos, self.att)
             linear_forward_async(ctx, b["out"], self.att, 1, d, b["out_b"], d, self.proj)
-            add_async(ctx, self.x, self.proj, d)
-            layernorm_async(ctx, self.x, 1, d, b["ln2_g"], b["ln2_b"], self.h)
-            linear_forward_async(ctx, b["up"], self.h, 1, d, b["up_b"], self.ffn, self.mid)
-            gelu_async(ctx, self.mid, self.ffn)
+            add_layernorm_async(ctx, self.x, self.proj, 1, d, b["ln2_g"], b["ln2_b"], self.h)
+            linear_act_async(ctx, b["up"], self.h, 1, d, b["up_b"], self.ffn, self.mid, ACT_GELU)
             linear_forward_async(ctx, b["down"], self.mid, 1, self.ffn, b["down_b"], d, self.proj)
-            add_async(ctx, self.x, self.proj, d)
-        layernorm_async(ctx, self.x, 1, d, self.lnf_g, self.lnf_b, self.h)
+            nxt = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
+            g, bb = (nxt["ln1_g"], nxt["ln1_b"]) if nxt else (self.lnf_g, self.lnf_b)
+            add_layernorm_async(ctx, self.x, self.proj, 1, d, g, bb, self.h)
         linear_forward_async(ctx, self.head, self.h, 1, d, None, 0, self.z)
 
     def forward(self, ids, reprime: bool):

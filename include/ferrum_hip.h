@@ -180,6 +180,8 @@ int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t
                          const uint64_t* d_draws, uint32_t* d_out_ids);
 
 /* ---- the rest of a GPT-2 decode step ------------------------------------- */
+/* Activation applied to a linear's output before it is stored. */
+enum { FH_ACT_NONE = 0, FH_ACT_GELU = 1 };
 /* Device pointers, enqueued on the context's stream.  With fh_q8_0_linear_async
  * and fh_sample_rows_async these keep a whole decode step on the device.
  *
@@ -195,6 +197,18 @@ int fh_layernorm_async(fh_ctx* ctx, const float* d_x, size_t rows, size_t d, con
                        const float* d_beta, float* d_y);
 /* activation::gelu (activation.rs:9-12, tanh approximation), in place. */
 int fh_gelu_async(fh_ctx* ctx, float* d_x, size_t n);
+/* fh_q8_0_linear_async followed by an activation (FH_ACT_*) on its output:
+ * Linear::forward then `.map(gelu)` as the block's ffn1 does
+ * (layer/transformer.rs:286).  The decode GEMV (m <= 2, W8A32) applies it in
+ * its epilogue, other paths in a second kernel; the result is the same. */
+int fh_q8_0_linear_act_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                             const float* d_bias, size_t bias_len, float* d_y, int numerics, int activation);
+/* x += y, then LayerNorm of the sum into ln (forward_with_cache's residual add
+ * and the LayerNorm that follows it: layer/transformer.rs:281-285, or the next
+ * block's ln1 after line 288), rows of width d <= 2048.  Same arithmetic as
+ * fh_add_async then fh_layernorm_async. */
+int fh_add_layernorm_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t rows, size_t d,
+                           const float* d_gamma, const float* d_beta, float* d_ln);
 /* x += y, the residual adds of TransformerBlock::forward_with_cache
  * (layer/transformer.rs:281, 288). */
 int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n);

@@ -138,12 +138,54 @@ def test_attention_decode_errors(fh):
                                           dev(np.zeros(48, np.float32)), 4, 12, 1, 0, dev(np.zeros(12, np.float32)))
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 3072, 768), (2, 512, 256), (5, 640, 768)])
+def test_linear_with_gelu_equals_linear_then_gelu(fh, orc, m, n, k):
+    """The fused epilogue (decode GEMV) and the two-kernel path give the
+    separate ops' values bit for bit; both track the oracle."""
+    import torch
+
+    import ferrum_hip
+
+    raw = orc.quantize_weight(n, k, m + n, 0.05)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x = np.random.default_rng(m).standard_normal((m, k)).astype(np.float32)
+    b = (np.random.default_rng(n).standard_normal(n) * 0.1).astype(np.float32)
+    tx, tb = dev(x), dev(b)
+    fused, plain = (torch.empty((m, n), device="cuda") for _ in range(2))
+    ready()
+    ferrum_hip.linear_act_async(fh, w, tx, m, k, tb, n, fused, ferrum_hip.ACT_GELU)
+    ferrum_hip.linear_forward_async(fh, w, tx, m, k, tb, n, plain)
+    ferrum_hip.gelu_async(fh, plain, m * n)
+    got, sep = host(fh, fused), host(fh, plain)
+    w.free()
+    assert np.array_equal(got, sep)
+    close(got, orc.gelu(orc.q8_0_linear(x, raw, n, b)), 1e-5)
+    with pytest.raises(ferrum_hip.FerrumHipError, match="unknown activation"):
+        ferrum_hip.linear_act_async(fh, w, tx, m, k, tb, n, fused, 7)
+
+
+def test_add_layernorm_equals_add_then_layernorm(fh, orc):
+    import ferrum_hip
+
+    rng = np.random.default_rng(8)
+    x, y = rng.standard_normal((3, 768)).astype(np.float32), rng.standard_normal((3, 768)).astype(np.float32)
+    g, b = rng.standard_normal(768).astype(np.float32), rng.standard_normal(768).astype(np.float32)
+    x1, x2, ty, tg, tb = dev(x), dev(x), dev(y), dev(g), dev(b)
+    l1, l2 = dev(np.zeros((3, 768), np.float32)), dev(np.zeros((3, 768), np.float32))
+    ready()
+    ferrum_hip.add_layernorm_async(fh, x1, ty, 3, 768, tg, tb, l1)
+    ferrum_hip.add_async(fh, x2, ty, 3 * 768)
+    ferrum_hip.layernorm_async(fh, x2, 3, 768, tg, tb, l2)
+    assert np.array_equal(host(fh, x1), host(fh, x2)) and np.array_equal(host(fh, l1), host(fh, l2))
+    close(host(fh, l1), orc.layernorm((x + y).astype(np.float32), g, b), 2e-5)
+
+
 @pytest.fixture(scope="module")
 def tiny(fh, orc):
     import ferrum_hip
 
     w = gpt2_tiny.make_weights(orc, seed=11)
-    model = ferrum_hip.GPT2Device(fh, w, gpt2_tiny.VOCAB, gpt2_tiny.D, gpt2_tiny.HEADS, gpt2_tiny.LAYERS,
+    model = ferrum_hip.GPT2Device.from_weights(fh, w, gpt2_tiny.VOCAB, gpt2_tiny.D, gpt2_tiny.HEADS, gpt2_tiny.LAYERS,
                                   gpt2_tiny.FFN, gpt2_tiny.CTX)
     yield w, model
     model.free()
