@@ -228,10 +228,10 @@ def main():
         kv_bytes = 2 * L * (FULL_POS + 1) * D * 4
         result["full_step"] = {
             "tok_s": round(1000.0 / ms_full, 1), "ms_per_step": round(ms_full, 5), "position": FULL_POS,
-            "launches_per_step": 2 + 6 * L + 2, "kv_cache_bytes_read": kv_bytes,
+            "launches_per_step": models[0].launches_per_step() + 1, "kv_cache_bytes_read": kv_bytes,
             "residency": f"hbm-forced ({args.replicas} model replicas)",
-            "what": "embed_one + LayerNorm + 12 x (QKV, attention, out, add+LayerNorm, up+GELU, down, "
-                    "add+LayerNorm) + head + sampler, all on the device"}
+            "what": "embed_one + LayerNorm + QKV, then 12 x (attention, out, add+LayerNorm+up+GELU, down, "
+                    "add+LayerNorm+next QKV or head) + sampler, all on the device"}
         del graphs_f
         for mdl in models:
             mdl.free()

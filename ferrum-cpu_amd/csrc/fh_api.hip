@@ -25,28 +25,33 @@ int fh_hip_fail(fh_ctx* ctx, hipError_t e, const char* what) {
     return fh_fail(ctx, code, m);
 }
 
-int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) {
+// Grow a plain device area; the old one is freed after the stream drains.
+static int grow_area(fh_ctx* ctx, void** area, size_t* area_bytes, size_t bytes, void** out) {
     bytes = fh_align256(bytes ? bytes : 256);
-    if (ctx->ws_bytes < bytes) {
+    if (*area_bytes < bytes) {
         hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
         FH_HIP(ctx, hipStreamIsCapturing(ctx->stream, &cs));
         if (cs != hipStreamCaptureStatusNone)
             return fh_fail(ctx, FH_ERR_INVALID,
                            "the context workspace must grow, which cannot happen during graph capture: "
                            "run the same call once outside capture first");
-        if (ctx->ws) {
-            // The previous workspace may still be read by queued kernels.
+        if (*area) {
+            // The previous area may still be read by queued kernels.
             FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
-            FH_HIP(ctx, hipFree(ctx->ws));
-            ctx->ws = nullptr;
-            ctx->ws_bytes = 0;
+            FH_HIP(ctx, hipFree(*area));
+            *area = nullptr;
+            *area_bytes = 0;
         }
-        FH_HIP(ctx, hipMalloc(&ctx->ws, bytes));
-        ctx->ws_bytes = bytes;
+        FH_HIP(ctx, hipMalloc(area, bytes));
+        *area_bytes = bytes;
     }
-    *out = ctx->ws;
+    *out = *area;
     return FH_OK;
 }
+
+int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) { return grow_area(ctx, &ctx->ws, &ctx->ws_bytes, bytes, out); }
+
+int fh_act_area(fh_ctx* ctx, size_t bytes, void** out) { return grow_area(ctx, &ctx->act, &ctx->act_bytes, bytes, out); }
 
 // Grow a zero-initialised area (kernels leave it zeroed again).  Growing
 // synchronises the stream and is refused under graph capture.
@@ -134,6 +139,7 @@ void fh_ctx_destroy(fh_ctx* ctx) {
     if (ctx->ws) (void)hipFree(ctx->ws);
     if (ctx->sync) (void)hipFree(ctx->sync);
     if (ctx->counters) (void)hipFree(ctx->counters);
+    if (ctx->act) (void)hipFree(ctx->act);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
 }
@@ -584,5 +590,38 @@ int fh_add_layernorm_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t row
     if (d == 0 || rows > 0x7FFFFFFFu)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_add_layernorm: d must be positive");
     FH_ON_DEVICE(ctx);
-    return fh_launch_add_layernorm(ctx, d_x, d_y, rows, d, d_gamma, d_beta, d_ln);
+    return fh_launch_add_layernorm(ctx, d_x, d_y, d_x, rows, d, d_gamma, d_beta, d_ln);
+}
+
+int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, const float* d_r, float* d_s, size_t m,
+                            size_t k, const float* d_gamma, const float* d_beta, const float* d_bias, size_t bias_len,
+                            float* d_y, int numerics, int activation) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (activation != FH_ACT_NONE && activation != FH_ACT_GELU)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_ln: unknown activation " + std::to_string(activation));
+    int rc = check_linear(ctx, w, k, d_bias, bias_len, numerics);
+    if (rc) return rc;
+    if (m == 0) return FH_OK;
+    if (!d_x || !d_y || !d_gamma || !d_beta)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_ln: x, y, gamma or beta is NULL");
+    if (d_s && (d_s == d_x || d_s == d_r))
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_ln: s must not alias x or r");
+    if (k > 2048) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_ln: rows wider than 2048");
+    if (m > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_ln: m is above 2^31 - 1");
+    FH_ON_DEVICE(ctx);
+    if (numerics == FH_W8A32 && d_r) {
+        const fh_ln_args ln{d_r, d_gamma, d_beta, d_s};
+        return fh_launch_linear_ln_w8a32(ctx, w, d_x, m, ln, d_bias, d_y, activation);
+    }
+    void* h = nullptr;
+    rc = fh_act_area(ctx, m * k * sizeof(float), &h);
+    if (rc) return rc;
+    float* hf = static_cast<float*>(h);
+    rc = fh_launch_add_layernorm(ctx, d_x, d_r, d_s, m, k, d_gamma, d_beta, hf);
+    if (rc) return rc;
+    if (numerics == FH_W8A32) return fh_launch_linear_w8a32(ctx, w, hf, m, d_bias, d_y, activation);
+    rc = fh_launch_linear_w8a8(ctx, w, hf, m, d_bias, d_y);
+    if (rc == FH_OK && activation == FH_ACT_GELU) rc = fh_launch_gelu(ctx, d_y, m * w->n);
+    return rc;
 }

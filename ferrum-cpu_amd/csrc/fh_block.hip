@@ -14,14 +14,16 @@
 //                one pass: the same arithmetic as k_add then k_layernorm.
 //  k_attn_chunk  the attention of forward_with_cache (layer/transformer.rs:
 //                242-279) for one query: the new k and v rows are written at
-//                cache row pos, then each (head, 32-position chunk) workgroup
-//                forms its scores, their max, sum of exponentials and the
-//                exponential-weighted sum of v rows; the last chunk of a head to
-//                finish merges the chunks (max, rescaled sums) and writes the
-//                head's output.  The reference sums in position order with one
+//                cache row pos, then each (head, chunk of 32 to 128 positions)
+//                workgroup forms its scores, their max, sum of exponentials and
+//                the exponential-weighted sum of v rows; with one chunk per head
+//                it writes the output, otherwise the last chunk of a head to
+//                finish merges the chunks (max, rescaled sums).  The reference sums in position order with one
 //                global max; the merge is the same value up to rounding.
 // Arithmetic is written without contraction, as the reference has no FMA.
 #include "fh_internal.hpp"
+
+#include <type_traits>
 
 #pragma clang fp contract(off)
 
@@ -91,78 +93,118 @@ __global__ void __launch_bounds__(kThreads) k_add(float* __restrict__ x, const f
     if (i < n) x[i] = x[i] + y[i];
 }
 
-// Grid (chunks, heads).  part: [heads][chunks][2 + hd] (max, sum, weighted v
-// sum), written with device-coherent stores; counters: one per head, left at 0.
+// Grid (chunks, heads); a workgroup covers S sub-chunks of 32 positions.
+// Every K, V and q element a thread needs is loaded at entry, so one memory
+// latency covers the whole chunk.  With one chunk per head the workgroup
+// writes the head's output itself; otherwise part: [heads][chunks][2 + hd]
+// (max, sum, weighted v sum) is written with device-coherent stores and the
+// last chunk of a head to arrive merges them.  counters: one per head, left 0.
+template <int S, int HD>
 __global__ void __launch_bounds__(kThreads)
-    k_attn_chunk(const float* __restrict__ qkv, float* __restrict__ kc, float* __restrict__ vc, int d, int hd, int pos,
+    k_attn_chunk(const float* __restrict__ qkv, float* __restrict__ kc, float* __restrict__ vc, int d, int pos,
                  float scale, float* __restrict__ part, unsigned* __restrict__ counters, float* __restrict__ out) {
-    __shared__ float q[kMaxHd];
-    __shared__ float sc[kChunk];
+    constexpr int kPos = S * kChunk;             // positions per workgroup
+    constexpr int hd = HD, per = HD / 8;         // dims per lane of a score
+    constexpr int groups = kThreads / HD;        // threads per v column
+    constexpr int vper = kChunk / groups;        // v rows per thread and sub-chunk
+    __shared__ float sc[kPos];
     __shared__ float acc[kThreads];
     __shared__ float stat[2];
     __shared__ int last;
     const int chunk = blockIdx.x, head = blockIdx.y, chunks = gridDim.x;
     const int hs = head * hd, tid = threadIdx.x;
-    const int len = pos + 1, j0 = chunk * kChunk, jn = min(kChunk, len - j0);
-    // The new row: chunk 0 of each head writes its slice of k and v at row
-    // pos.  Reads below take the new row from qkv itself, never from the
-    // cache, so no workgroup depends on another's store.
-    if (chunk == 0)
-        for (int t = tid; t < hd; t += kThreads) {
-            kc[static_cast<size_t>(pos) * d + hs + t] = qkv[d + hs + t];
-            vc[static_cast<size_t>(pos) * d + hs + t] = qkv[2 * d + hs + t];
+    const int len = pos + 1, j0 = chunk * kPos, jn = min(kPos, len - j0);
+    const int jl = tid >> 3, part8 = tid & 7, t = tid % hd, g = tid / hd;
+    const float* knew = qkv + d + hs;
+    const float* vnew = qkv + 2 * d + hs;
+    // loads: this lane's q slice, its K slices (one position per sub-chunk)
+    // and its V elements (vper positions per sub-chunk).  Position pos (and
+    // any position past it, which is masked) comes from qkv itself, never
+    // from the cache, so no workgroup depends on another's store.
+    float qr[per], kr[S][per], vr[S][vper];
+#pragma unroll
+    for (int i = 0; i < per; i++) qr[i] = qkv[hs + part8 * per + i];
+#pragma unroll
+    for (int u = 0; u < S; u++) {
+        const int j = j0 + u * kChunk + jl;
+        const float* row = j >= pos ? knew : kc + static_cast<size_t>(j) * d + hs;
+#pragma unroll
+        for (int i = 0; i < per; i++) kr[u][i] = row[part8 * per + i];
+#pragma unroll
+        for (int i = 0; i < vper; i++) {
+            const int jv = j0 + u * kChunk + g + i * groups;
+            const float* vrow = jv >= pos ? vnew : vc + static_cast<size_t>(jv) * d + hs;
+            vr[u][i] = vrow[t];
         }
-    for (int t = tid; t < hd; t += kThreads) q[t] = qkv[hs + t];
-    __syncthreads();
-    // scores: 8 lanes per position, each over hd / 8 consecutive dims, then a
-    // fixed 8-lane tree
-    {
-        const int jl = tid >> 3, part8 = tid & 7, per = hd / 8;
+    }
+    // the new row: chunk 0 of each head writes its slice of k and v at row pos
+    if (chunk == 0 && tid < hd) {
+        kc[static_cast<size_t>(pos) * d + hs + tid] = knew[tid];
+        vc[static_cast<size_t>(pos) * d + hs + tid] = vnew[tid];
+    }
+    // scores: 8 lanes per position, each over hd / 8 consecutive dims in
+    // ascending order, then a fixed 8-lane tree
+#pragma unroll
+    for (int u = 0; u < S; u++) {
         float dot = 0.0f;
-        if (jl < jn) {
-            const int j = j0 + jl;
-            const float* kr = j == pos ? qkv + d + hs : kc + static_cast<size_t>(j) * d + hs;
-            for (int t = part8 * per; t < part8 * per + per; t++) dot += q[t] * kr[t];
-        }
+#pragma unroll
+        for (int i = 0; i < per; i++) dot += qr[i] * kr[u][i];
         dot += __shfl_xor(dot, 1, 64);
         dot += __shfl_xor(dot, 2, 64);
         dot += __shfl_xor(dot, 4, 64);
-        if (part8 == 0) sc[jl] = jl < jn ? dot * scale : -INFINITY;
+        const int jc = u * kChunk + jl;
+        if (part8 == 0) sc[jc] = jc < jn ? dot * scale : -INFINITY;
     }
     __syncthreads();
-    // the chunk's max and exponentials, once each (wave 0; lanes past the
-    // chunk hold -inf and 0)
+    // the chunk's max and exponentials, once each (wave 0; position l + 64 i)
     if (tid < 64) {
-        const float s = tid < kChunk ? sc[tid] : -INFINITY;
-        float mx = s;
+        constexpr int kL = (kPos + 63) / 64;
+        float s[kL];
+        float mx = -INFINITY;
+#pragma unroll
+        for (int i = 0; i < kL; i++) {
+            const int jc = tid + 64 * i;
+            s[i] = jc < kPos ? sc[jc] : -INFINITY;
+            mx = fmaxf(mx, s[i]);
+        }
 #pragma unroll
         for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-        const float e = tid < jn ? expf(s - mx) : 0.0f;
-        const float se = wave_sum(e);
-        if (tid < kChunk) sc[tid] = e;
+        float se = 0.0f;
+#pragma unroll
+        for (int i = 0; i < kL; i++) {
+            const int jc = tid + 64 * i;
+            const float e = jc < jn ? expf(s[i] - mx) : 0.0f;
+            if (jc < kPos) sc[jc] = e;
+            se += e;
+        }
+        se = wave_sum(se);
         if (tid == 0) {
             stat[0] = mx;
             stat[1] = se;
         }
     }
     __syncthreads();
-    // weighted v sum over this chunk: thread (g, t) takes positions g, g + G, ...
-    const int groups = kThreads / hd;
-    const int t = tid % hd, g = tid / hd;
+    // weighted v sum: thread (g, t) takes positions g, g + groups, ... of
+    // each sub-chunk, in order; positions past the chunk are skipped
     float o = 0.0f;
-    for (int jl = g; jl < jn; jl += groups) {
-        const int j = j0 + jl;
-        const float* vr = j == pos ? qkv + 2 * d + hs : vc + static_cast<size_t>(j) * d + hs;
-        o += sc[jl] * vr[t];
-    }
+#pragma unroll
+    for (int u = 0; u < S; u++)
+#pragma unroll
+        for (int i = 0; i < vper; i++) {
+            const int jc = u * kChunk + g + i * groups;
+            if (jc < jn) o += sc[jc] * vr[u][i];
+        }
     acc[tid] = o;
     __syncthreads();
-    float* mine = part + (static_cast<size_t>(head) * chunks + chunk) * (2 + hd);
-    if (tid < hd) {
-        float s = 0.0f;
-        for (int gg = 0; gg < groups; gg++) s += acc[gg * hd + tid];
-        __hip_atomic_store(mine + 2 + tid, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    float r = 0.0f;
+    if (tid < hd)
+        for (int gg = 0; gg < groups; gg++) r += acc[gg * hd + tid];
+    if (chunks == 1) {
+        if (tid < hd) out[hs + tid] = r / stat[1];
+        return;
     }
+    float* mine = part + (static_cast<size_t>(head) * chunks + chunk) * (2 + hd);
+    if (tid < hd) __hip_atomic_store(mine + 2 + tid, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
         __hip_atomic_store(mine, stat[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(mine + 1, stat[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -174,21 +216,12 @@ __global__ void __launch_bounds__(kThreads)
     if (tid == 0) last = atomicAdd(counters + head, 1u) == static_cast<unsigned>(chunks - 1);
     __syncthreads();
     if (!last) return;
-    // Merge, eight chunks per round with all their loads in flight at once.
+    // Merge, eight chunks per round with all their loads in flight at once;
+    // a running max rescales the sums when a later round raises it.
     const float* hp = part + static_cast<size_t>(head) * chunks * (2 + hd);
     constexpr int R = 8;
-    float M = -INFINITY;
-    for (int c0 = 0; c0 < chunks; c0 += R) {
-        float mc[R];
-#pragma unroll
-        for (int i = 0; i < R; i++)
-            mc[i] = __hip_atomic_load(hp + min(c0 + i, chunks - 1) * (2 + hd), __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-        for (int i = 0; i < R; i++) M = fmaxf(M, mc[i]);  // repeats of the last chunk change nothing
-    }
-    float S = 0.0f, r = 0.0f;
     const int tt = min(tid, hd - 1);
+    float M = -INFINITY, Sm = 0.0f, rm = 0.0f;
     for (int c0 = 0; c0 < chunks; c0 += R) {
         float mc[R], sc8[R], oc[R];
 #pragma unroll
@@ -198,36 +231,55 @@ __global__ void __launch_bounds__(kThreads)
             sc8[i] = __hip_atomic_load(cp + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             oc[i] = __hip_atomic_load(cp + 2 + tt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
+        float Mn = M;
+#pragma unroll
+        for (int i = 0; i < R; i++) Mn = fmaxf(Mn, mc[i]);  // repeats of the last chunk change nothing
+        if (Mn != M) {
+            const float f = expf(M - Mn);  // 0 on the first round (M = -inf)
+            Sm = Sm * f;
+            rm = rm * f;
+            M = Mn;
+        }
 #pragma unroll
         for (int i = 0; i < R; i++) {
             if (c0 + i >= chunks) break;
             const float f = expf(mc[i] - M);
-            S += sc8[i] * f;
-            r += oc[i] * f;
+            Sm += sc8[i] * f;
+            rm += oc[i] * f;
         }
     }
-    if (tid < hd) out[hs + tid] = r / S;
+    if (tid < hd) out[hs + tid] = rm / Sm;
     if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // x += y, then LayerNorm of the sum into ln (the residual add of
 // forward_with_cache followed by the next LayerNorm), one workgroup per row.
-__global__ void __launch_bounds__(kThreads) k_add_layernorm(float* __restrict__ x, const float* __restrict__ y, int d,
-                                                           const float* __restrict__ gamma,
+// v = x (+ y); s (nullable, may alias x) receives v; ln = LayerNorm(v).
+template <bool kAdd>
+__global__ void __launch_bounds__(kThreads) k_add_layernorm(const float* x, const float* __restrict__ y, float* s_out,
+                                                           int d, const float* __restrict__ gamma,
                                                            const float* __restrict__ beta, float* __restrict__ ln) {
     __shared__ float red[kThreads / 64];
-    float* xr = x + static_cast<size_t>(blockIdx.x) * d;
-    const float* yr = y + static_cast<size_t>(blockIdx.x) * d;
+    const float* xr = x + static_cast<size_t>(blockIdx.x) * d;
+    const float* yr = kAdd ? y + static_cast<size_t>(blockIdx.x) * d : nullptr;
+    float* sr = s_out ? s_out + static_cast<size_t>(blockIdx.x) * d : nullptr;
     float* lr = ln + static_cast<size_t>(blockIdx.x) * d;
     constexpr int kPer = 8;  // row elements a thread keeps in registers (d <= 2048 here)
-    float v[kPer];
+    float v[kPer], gm[kPer], bt[kPer];
+    // every load is issued before the first reduction
+#pragma unroll
+    for (int i = 0; i < kPer; i++) {
+        const int c = threadIdx.x + i * kThreads;
+        v[i] = c < d ? (kAdd ? xr[c] + yr[c] : xr[c]) : 0.0f;
+        gm[i] = c < d ? gamma[c] : 0.0f;
+        bt[i] = c < d ? beta[c] : 0.0f;
+    }
     float s = 0.0f;
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
         const int c = threadIdx.x + i * kThreads;
-        v[i] = c < d ? xr[c] + yr[c] : 0.0f;
         if (c < d) {
-            xr[c] = v[i];
+            if (sr) sr[c] = v[i];
             s += v[i];
         }
     }
@@ -246,7 +298,7 @@ __global__ void __launch_bounds__(kThreads) k_add_layernorm(float* __restrict__ 
 #pragma unroll
     for (int i = 0; i < kPer; i++) {
         const int c = threadIdx.x + i * kThreads;
-        if (c < d) lr[c] = ((v[i] - mean) / sd) * gamma[c] + beta[c];
+        if (c < d) lr[c] = ((v[i] - mean) / sd) * gm[i] + bt[i];
     }
 }
 
@@ -264,8 +316,13 @@ int fh_launch_embed_one(fh_ctx* ctx, const float* tok_w, const float* pos_w, siz
 
 int fh_launch_layernorm(fh_ctx* ctx, const float* x, size_t rows, size_t d, const float* gamma, const float* beta,
                         float* y) {
-    hipLaunchKernelGGL(k_layernorm, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x,
-                       static_cast<int>(d), gamma, beta, y);
+    // Rows up to 2048 wide stay in registers (same arithmetic, same order).
+    if (d <= 8 * static_cast<size_t>(kThreads))
+        hipLaunchKernelGGL(k_add_layernorm<false>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x,
+                           nullptr, nullptr, static_cast<int>(d), gamma, beta, y);
+    else
+        hipLaunchKernelGGL(k_layernorm, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x,
+                           static_cast<int>(d), gamma, beta, y);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -282,12 +339,16 @@ int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n) {
     return FH_OK;
 }
 
-int fh_launch_add_layernorm(fh_ctx* ctx, float* x, const float* y, size_t rows, size_t d, const float* gamma,
-                            const float* beta, float* ln) {
+int fh_launch_add_layernorm(fh_ctx* ctx, const float* x, const float* y, float* s, size_t rows, size_t d,
+                            const float* gamma, const float* beta, float* ln) {
     if (d > 8 * static_cast<size_t>(kThreads))
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_add_layernorm: rows wider than 2048");
-    hipLaunchKernelGGL(k_add_layernorm, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x, y,
-                       static_cast<int>(d), gamma, beta, ln);
+    if (y)
+        hipLaunchKernelGGL(k_add_layernorm<true>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x,
+                           y, s, static_cast<int>(d), gamma, beta, ln);
+    else
+        hipLaunchKernelGGL(k_add_layernorm<false>, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x,
+                           nullptr, s, static_cast<int>(d), gamma, beta, ln);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -297,7 +358,15 @@ int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* 
     const size_t hd = d / heads;
     if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_attention_decode: head width must be 8, 16, 32, 64 or 128");
-    const size_t chunks = (pos + 1 + kChunk - 1) / kChunk;
+    // Sub-chunks per workgroup, from timings of 12 heads of 64 at positions
+    // 63 to 1023: one workgroup per head while the head fits in 64
+    // positions, then 64 positions per workgroup (enough workgroups in
+    // flight to cover the load latency; one workgroup per head over 256
+    // positions runs about 1.5x slower), 128 past position 767.
+    const size_t len = pos + 1;
+    const size_t need = (len + kChunk - 1) / kChunk;
+    const size_t sub = need <= 2 ? need : len > 768 ? 4 : 2;
+    const size_t chunks = (len + sub * kChunk - 1) / (sub * kChunk);
     void* ws = nullptr;
     int rc = fh_workspace(ctx, heads * chunks * (2 + hd) * sizeof(float), &ws);
     if (rc) return rc;
@@ -305,9 +374,26 @@ int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* 
     rc = fh_counter_area(ctx, heads * sizeof(unsigned), &cnt);
     if (rc) return rc;
     const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-    hipLaunchKernelGGL(k_attn_chunk, dim3(static_cast<unsigned>(chunks), static_cast<unsigned>(heads)), dim3(kThreads),
-                       0, ctx->stream, qkv, kc, vc, static_cast<int>(d), static_cast<int>(hd), static_cast<int>(pos),
-                       scale, static_cast<float*>(ws), static_cast<unsigned*>(cnt), out);
+    const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(heads));
+    auto go = [&](auto hdc) {
+        constexpr int HD = decltype(hdc)::value;
+        auto launch = [&](auto kern) {
+            hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, ctx->stream, qkv, kc, vc, static_cast<int>(d),
+                               static_cast<int>(pos), scale, static_cast<float*>(ws), static_cast<unsigned*>(cnt), out);
+        };
+        switch (sub) {
+            case 1: launch(k_attn_chunk<1, HD>); break;
+            case 2: launch(k_attn_chunk<2, HD>); break;
+            default: launch(k_attn_chunk<4, HD>); break;
+        }
+    };
+    switch (hd) {
+        case 8: go(std::integral_constant<int, 8>{}); break;
+        case 16: go(std::integral_constant<int, 16>{}); break;
+        case 32: go(std::integral_constant<int, 32>{}); break;
+        case 64: go(std::integral_constant<int, 64>{}); break;
+        default: go(std::integral_constant<int, 128>{}); break;
+    }
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }

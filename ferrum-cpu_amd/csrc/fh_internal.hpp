@@ -37,6 +37,10 @@ struct fh_ctx {
     // generation tags there must never be reset behind its back.
     void* counters = nullptr;
     size_t counters_bytes = 0;
+    // Grow-on-demand activation staging (a LayerNorm output feeding a
+    // linear), separate from ws, which the linear itself may use.
+    void* act = nullptr;
+    size_t act_bytes = 0;
 };
 
 constexpr int8_t kFhBadRowExp = -128;
@@ -66,6 +70,8 @@ int fh_hip_fail(fh_ctx* ctx, hipError_t e, const char* what);
 
 // Make sure ctx->ws holds at least `bytes` (device, 256-B aligned).
 int fh_workspace(fh_ctx* ctx, size_t bytes, void** out);
+// The same for ctx->act.
+int fh_act_area(fh_ctx* ctx, size_t bytes, void** out);
 // Make sure ctx->sync holds at least `bytes`, zeroed when (re)allocated.
 // Growing is refused while the stream is being captured into a graph.
 int fh_sync_area(fh_ctx* ctx, size_t bytes, void** out);
@@ -82,6 +88,15 @@ int fh_launch_unpack(fh_ctx* ctx, const int8_t* qs, const uint16_t* d, size_t n,
                      uint8_t* d_raw);
 int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                            const float* bias, float* y, int act = FH_ACT_NONE);
+// LayerNorm of (x + r) feeding the linear; s (nullable) receives x + r.
+struct fh_ln_args {
+    const float* r;
+    const float* gamma;
+    const float* beta;
+    float* s;
+};
+int fh_launch_linear_ln_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_ln_args& ln,
+                              const float* bias, float* y, int act);
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                          const float* bias, float* y);
 int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
@@ -95,8 +110,10 @@ int fh_launch_layernorm(fh_ctx* ctx, const float* x, size_t rows, size_t d, cons
                         const float* beta, float* y);
 int fh_launch_gelu(fh_ctx* ctx, float* x, size_t n);
 int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n);
-int fh_launch_add_layernorm(fh_ctx* ctx, float* x, const float* y, size_t rows, size_t d, const float* gamma,
-                            const float* beta, float* ln);
+// ln = LayerNorm(x + y) (y nullable: LayerNorm(x)); s (nullable, may be x)
+// receives x + y.  d <= 2048.
+int fh_launch_add_layernorm(fh_ctx* ctx, const float* x, const float* y, float* s, size_t rows, size_t d,
+                            const float* gamma, const float* beta, float* ln);
 int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
                                size_t pos, float* out);
 int fh_launch_dequant(fh_ctx* ctx, const uint8_t* raw, size_t n, float* out);

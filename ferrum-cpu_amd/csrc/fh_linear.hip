@@ -14,6 +14,8 @@
 //                the activation chunks a lane needs stay in its registers for
 //                every row it visits.  G lanes share a row and finish it with a
 //                butterfly shuffle reduction; 64/G rows per wave per step.
+//                With a LayerNorm prologue (fh_q8_0_linear_ln) every wave
+//                first forms LayerNorm(x + r) of the rows it holds.
 //  m >= 3 (and rows too long for the GEMV) go to the matrix-core GEMM in
 //                fh_gemm.hip.
 //  k_linear_w8a8 llama.cpp numerics: x is Q8_0-encoded per 32 (bit-exact
@@ -64,16 +66,35 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Sum over each group of G lanes for any G <= 64 (every lane of the group
+// gets the total).
+template <int G>
+__device__ __forceinline__ float group_total(float v) {
+    if constexpr (G <= 16) {
+        return group_sum<G>(v);
+    } else {
+        const float r16 = group_sum<16>(v);
+        const float lo = rdlane(r16, 0) + rdlane(r16, 16);
+        const float hi = rdlane(r16, 32) + rdlane(r16, 48);
+        return G == 64 ? lo + hi : ((threadIdx.x & 63) < 32 ? lo : hi);
+    }
+}
+
 // Q8_0 GEMV, m = M <= 2.  A wave owns `per_wave` consecutive row-sets (a
 // row-set = 64 / G rows, G lanes per row); it issues the loads of up to U
 // row-sets at once — CPL 16-byte quant chunks and their f16 scales per lane —
 // next to its activation chunks, so a whole batch costs one memory latency.
 // Lane gl of a row holds chunks gl, gl + G, ... (coalesced: the G lanes of a
 // row read G consecutive 16-byte chunks).
-template <int G, int CPL, int M, int U, bool kBias>
+// kLn: the activations are LayerNorm(x + ln.r) (the residual add and the
+// LayerNorm in front of this linear).  The G lanes of a row group hold the
+// whole row, so every wave forms the row's mean and variance with group
+// shuffles; wave 0 of block 0 writes x + r to ln.s (when given).
+template <int G, int CPL, int M, int U, bool kBias, bool kLn>
 __global__ void __launch_bounds__(64 * kWaves)
     k_gemv_w8a32(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const float* __restrict__ x,
-                 const float* __restrict__ bias, float* __restrict__ y, int n, int k, int per_wave, int act) {
+                 const float* __restrict__ bias, float* __restrict__ y, int n, int k, int per_wave, int act,
+                 fh_ln_args ln) {
     constexpr int RW = 64 / G;  // rows per row-set
     const int lane = threadIdx.x & 63;
     const int grp = lane / G, gl = lane % G;
@@ -90,20 +111,79 @@ __global__ void __launch_bounds__(64 * kWaves)
     // A chunk past the row end (k16 not a multiple of G) re-reads the last one
     // and gets its activations masked to +0.0 bit-wise, so it adds nothing.
     float xr[M][CPL][16];
+    [[maybe_unused]] float lg[kLn ? CPL : 1][16], lb[kLn ? CPL : 1][16];
 #pragma unroll
     for (int c = 0; c < CPL; c++) {
         const int ci = min(gl + c * G, k16 - 1);
         const uint32_t keep = gl + c * G < k16 ? 0xFFFFFFFFu : 0u;
+        if constexpr (kLn) {
+            const float4* gs = reinterpret_cast<const float4*>(ln.gamma + ci * 16);
+            const float4* bs = reinterpret_cast<const float4*>(ln.beta + ci * 16);
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float4 gf = gs[v], bf = bs[v];
+                lg[c][4 * v] = gf.x, lg[c][4 * v + 1] = gf.y, lg[c][4 * v + 2] = gf.z, lg[c][4 * v + 3] = gf.w;
+                lb[c][4 * v] = bf.x, lb[c][4 * v + 1] = bf.y, lb[c][4 * v + 2] = bf.z, lb[c][4 * v + 3] = bf.w;
+            }
+        }
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * k + ci * 16);
+            [[maybe_unused]] const float4* rsrc =
+                kLn ? reinterpret_cast<const float4*>(ln.r + static_cast<size_t>(m) * k + ci * 16) : nullptr;
 #pragma unroll
             for (int v = 0; v < 4; v++) {
-                const float4 f = src[v];
+                float4 f = src[v];
+                if constexpr (kLn) {
+                    const float4 rf = rsrc[v];
+                    f.x = f.x + rf.x, f.y = f.y + rf.y, f.z = f.z + rf.z, f.w = f.w + rf.w;
+                }
                 const float fv[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
                 for (int e = 0; e < 4; e++)
                     xr[m][c][4 * v + e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, fv[e]) & keep);
+            }
+        }
+    }
+    if constexpr (kLn) {
+        // LayerNorm::forward (layer/norm.rs:46-82) of each row: mean, biased
+        // variance, ((v - mean) / sqrt(var + 1e-5)) * gamma + beta.  Chunks
+        // past the row end hold +0 and stay +0.
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            float s = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; c++)
+#pragma unroll
+                for (int t = 0; t < 16; t++) s += xr[m][c][t];
+            const float mean = group_total<G>(s) / static_cast<float>(k);
+            float ss = 0.0f;
+#pragma unroll
+            for (int c = 0; c < CPL; c++)
+                if (gl + c * G < k16)
+#pragma unroll
+                    for (int t = 0; t < 16; t++) {
+                        const float dv = xr[m][c][t] - mean;
+                        ss += dv * dv;
+                    }
+            const float sd = sqrtf(group_total<G>(ss) / static_cast<float>(k) + 1e-5f);
+            if (ln.s && blockIdx.x == 0 && threadIdx.x < G) {
+#pragma unroll
+                for (int c = 0; c < CPL; c++) {
+                    if (gl + c * G >= k16) continue;
+                    float4* dst = reinterpret_cast<float4*>(ln.s + static_cast<size_t>(m) * k + (gl + c * G) * 16);
+#pragma unroll
+                    for (int v = 0; v < 4; v++)
+                        dst[v] = make_float4(xr[m][c][4 * v], xr[m][c][4 * v + 1], xr[m][c][4 * v + 2],
+                                             xr[m][c][4 * v + 3]);
+                }
+            }
+#pragma unroll
+            for (int c = 0; c < CPL; c++) {
+                const bool valid = gl + c * G < k16;
+#pragma unroll
+                for (int t = 0; t < 16; t++)
+                    xr[m][c][t] = valid ? ((xr[m][c][t] - mean) / sd) * lg[c][t] + lb[c][t] : 0.0f;
             }
         }
     }
@@ -229,7 +309,8 @@ __global__ void __launch_bounds__(256)
 // Row-sets per wave: enough waves to cover the chip (12 per CU on 256 CUs)
 // before a wave takes more than one row-set; beyond U, whole batches of U.
 template <int G, int CPL, int M, int U>
-int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y, int act) {
+int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y, int act,
+                const fh_ln_args* ln) {
     constexpr int RW = 64 / G;
     const size_t nsets = (w->n + RW - 1) / RW;
     size_t per_wave = (nsets + 3071) / 3072;
@@ -238,9 +319,20 @@ int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias
     const size_t waves = (nsets + per_wave - 1) / per_wave;
     const size_t blocks = (waves + kWaves - 1) / kWaves;
     // The bias-free form (ops::matmul, the tied lm_head) is its own instance.
-    auto kernel = bias ? k_gemv_w8a32<G, CPL, M, U, true> : k_gemv_w8a32<G, CPL, M, U, false>;
+    auto kernel = bias ? k_gemv_w8a32<G, CPL, M, U, true, false> : k_gemv_w8a32<G, CPL, M, U, false, false>;
+    // The LayerNorm prologue serves rows of at most 2048 (at most 2 chunks
+    // per lane at G = 64); longer rows take the two-kernel path.
+    if (ln) {
+        if constexpr (G == 64 && CPL > 2) {
+            return -1;
+        } else {
+            kernel = bias ? k_gemv_w8a32<G, CPL, M, U, true, true> : k_gemv_w8a32<G, CPL, M, U, false, true>;
+        }
+    }
+    const fh_ln_args none{nullptr, nullptr, nullptr, nullptr};
     hipLaunchKernelGGL(kernel, dim3(static_cast<unsigned>(blocks)), dim3(64 * kWaves), 0, ctx->stream, w->qs, w->d,
-                       x, bias, y, static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(per_wave), act);
+                       x, bias, y, static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(per_wave), act,
+                       ln ? *ln : none);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -250,9 +342,10 @@ int launch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias
 // smallest power-of-two G with at most 4 chunks per lane.  U keeps about 12
 // quant loads in flight per lane.
 template <int M>
-int dispatch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y, int act) {
+int dispatch_gemv(fh_ctx* ctx, const fh_q8_0* w, const float* x, const float* bias, float* y, int act,
+                  const fh_ln_args* ln = nullptr) {
     const size_t k16 = w->k / 16;
-#define FH_GEMV(G, C) return launch_gemv<G, C, M, (12 / C > 0 ? 12 / C : 1)>(ctx, w, x, bias, y, act)
+#define FH_GEMV(G, C) return launch_gemv<G, C, M, (12 / C > 0 ? 12 / C : 1)>(ctx, w, x, bias, y, act, ln)
     if (k16 >= 64) {
         switch ((k16 + 63) / 64) {
             case 1: FH_GEMV(64, 1);
@@ -307,6 +400,25 @@ int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t
     int rc = fh_launch_gemm_w8a32(ctx, w, x, m, bias, y);
     if (rc == FH_OK && act == FH_ACT_GELU) rc = fh_launch_gelu(ctx, y, m * w->n);
     return rc;
+}
+
+int fh_launch_linear_ln_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_ln_args& ln,
+                              const float* bias, float* y, int act) {
+    const bool aligned = !((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(ln.r) |
+                            reinterpret_cast<uintptr_t>(ln.gamma) | reinterpret_cast<uintptr_t>(ln.beta) |
+                            reinterpret_cast<uintptr_t>(ln.s)) & 15);
+    if (m <= 2 && aligned && w->n <= 0x7FFFFFFFu) {
+        int rc = m == 1 ? dispatch_gemv<1>(ctx, w, x, bias, y, act, &ln) : dispatch_gemv<2>(ctx, w, x, bias, y, act, &ln);
+        if (rc >= 0) return rc;
+    }
+    // Other shapes: the add + LayerNorm kernel into the context's activation
+    // area, then the plain linear.
+    void* h = nullptr;
+    int rc = fh_act_area(ctx, m * w->k * sizeof(float), &h);
+    if (rc) return rc;
+    rc = fh_launch_add_layernorm(ctx, x, ln.r, ln.s, m, w->k, ln.gamma, ln.beta, static_cast<float*>(h));
+    if (rc) return rc;
+    return fh_launch_linear_w8a32(ctx, w, static_cast<float*>(h), m, bias, y, act);
 }
 
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {

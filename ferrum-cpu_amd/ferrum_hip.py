@@ -44,7 +44,7 @@ EXPORTS = (
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
-    "fh_q8_0_linear_act_async", "fh_add_layernorm_async",
+    "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
 )
 
 
@@ -165,6 +165,7 @@ def lib():
         L.fh_attention_decode_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, vp]
         L.fh_q8_0_linear_act_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32, i32]
         L.fh_add_layernorm_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
+        L.fh_q8_0_linear_ln_async.argtypes = [vp, vp, vp, vp, vp, sz, sz, vp, vp, vp, sz, vp, i32, i32]
         _lib = L
     return _lib
 
@@ -473,6 +474,15 @@ def add_layernorm_async(ctx: Context, x, y, rows: int, d: int, gamma, beta, ln):
     ctx.check(lib().fh_add_layernorm_async(ctx.h, _ptr(x), _ptr(y), rows, d, _ptr(gamma), _ptr(beta), _ptr(ln)))
 
 
+def linear_ln_async(ctx: Context, weight: "Q8_0Weight", x, r, s, m: int, k: int, gamma, beta, bias, bias_len: int,
+                    y, act: int = ACT_NONE, numerics: int = W8A32):
+    """y = act(LayerNorm(x + r) . W^T + b), with x + r written to s when s is
+    given (r may be None: LayerNorm(x)): a residual add, the LayerNorm after it
+    and the Linear that reads it, as one call."""
+    ctx.check(lib().fh_q8_0_linear_ln_async(ctx.h, weight.h, _ptr(x), _ptr(r), _ptr(s), m, k, _ptr(gamma), _ptr(beta),
+                                            _ptr(bias), bias_len, _ptr(y), numerics, act))
+
+
 def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d: int, heads: int, pos: int, out):
     """The KV-cache attention of forward_with_cache (layer/transformer.rs:242-279)."""
     ctx.check(lib().fh_attention_decode_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
@@ -501,6 +511,7 @@ class GPT2Device:
         self.ctx, self.vocab, self.d, self.heads, self.layers, self.ffn, self.cap = ctx, vocab, d, heads, layers, ffn, context
         dev = torch.device("cuda")
         self.x = torch.empty(d, device=dev)
+        self.x2 = torch.empty(d, device=dev)  # the residual stream ping-pongs between x and x2
         self.h = torch.empty(d, device=dev)
         self.qkv = torch.empty(3 * d, device=dev)
         self.att = torch.empty(d, device=dev)
@@ -577,19 +588,28 @@ class GPT2Device:
         """One position: the head's scores for the next token land in self.z."""
         ctx, d = self.ctx, self.d
         embed_one_async(ctx, self.tok_w, self.pos_w, self.vocab, self.pos_w.shape[0], d, d_token, pos, self.x)
-        layernorm_async(ctx, self.x, 1, d, self.blocks[0]["ln1_g"], self.blocks[0]["ln1_b"], self.h)
+        cur, other = self.x, self.x2
         for i, b in enumerate(self.blocks):
-            # self.h holds ln1(x) here
-            linear_forward_async(ctx, b["qkv"], self.h, 1, d, b["qkv_b"], 3 * d, self.qkv)
+            # Each residual add runs inside the linear after it, together with
+            # the LayerNorm: the sum lands in `other`, which becomes `cur`.
+            if i == 0:
+                layernorm_async(ctx, cur, 1, d, b["ln1_g"], b["ln1_b"], self.h)
+                linear_forward_async(ctx, b["qkv"], self.h, 1, d, b["qkv_b"], 3 * d, self.qkv)
+            else:
+                linear_ln_async(ctx, b["qkv"], cur, self.proj, other, 1, d, b["ln1_g"], b["ln1_b"], b["qkv_b"], 3 * d,
+                                self.qkv)
+                cur, other = other, cur
             attention_decode_async(ctx, self.qkv, b["k"], b["v"], self.cap, d, self.heads, pos, self.att)
             linear_forward_async(ctx, b["out"], self.att, 1, d, b["out_b"], d, self.proj)
-            add_layernorm_async(ctx, self.x, self.proj, 1, d, b["ln2_g"], b["ln2_b"], self.h)
-            linear_act_async(ctx, b["up"], self.h, 1, d, b["up_b"], self.ffn, self.mid, ACT_GELU)
+            linear_ln_async(ctx, b["up"], cur, self.proj, other, 1, d, b["ln2_g"], b["ln2_b"], b["up_b"], self.ffn,
+                            self.mid, ACT_GELU)
+            cur, other = other, cur
             linear_forward_async(ctx, b["down"], self.mid, 1, self.ffn, b["down_b"], d, self.proj)
-            nxt = self.blocks[i + 1] if i + 1 < len(self.blocks) else None
-            g, bb = (nxt["ln1_g"], nxt["ln1_b"]) if nxt else (self.lnf_g, self.lnf_b)
-            add_layernorm_async(ctx, self.x, self.proj, 1, d, g, bb, self.h)
-        linear_forward_async(ctx, self.head, self.h, 1, d, None, 0, self.z)
+        linear_ln_async(ctx, self.head, cur, self.proj, None, 1, d, self.lnf_g, self.lnf_b, None, 0, self.z)
+
+    def launches_per_step(self) -> int:
+        """Kernel launches of feed_async (the sampler not included)."""
+        return 2 + 5 * self.layers + 1
 
     def forward(self, ids, reprime: bool):
         """gpt2_decode's forward: re-feed the whole window from position 0, or

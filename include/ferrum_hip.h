@@ -209,6 +209,19 @@ int fh_q8_0_linear_act_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, si
  * fh_add_async then fh_layernorm_async. */
 int fh_add_layernorm_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t rows, size_t d,
                            const float* d_gamma, const float* d_beta, float* d_ln);
+/* A residual add, the LayerNorm after it and the Q8_0 linear that reads the
+ * LayerNorm's output, as one call (forward_with_cache's `x + attn` -> ln2 ->
+ * ffn1 -> gelu, layer/transformer.rs:281-286; `x + ffn` -> the next block's
+ * ln1 -> qkv, or the final LayerNorm -> the head, slm/cached.rs:118-124):
+ *   s = x + r (written to s when s is not NULL; r NULL means s = x),
+ *   y = act(LayerNorm(s; gamma, beta) . W^T + bias).
+ * s must not alias x or r.  Rows of width k <= 2048.  The decode GEMV
+ * (m <= 2, W8A32) forms each row's mean and variance inside every wave, so
+ * the whole step is one launch; other shapes run fh_add_layernorm's kernel
+ * into a context buffer, then the linear. */
+int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, const float* d_r, float* d_s,
+                            size_t m, size_t k, const float* d_gamma, const float* d_beta, const float* d_bias,
+                            size_t bias_len, float* d_y, int numerics, int activation);
 /* x += y, the residual adds of TransformerBlock::forward_with_cache
  * (layer/transformer.rs:281, 288). */
 int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n);

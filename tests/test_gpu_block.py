@@ -106,22 +106,34 @@ def test_embed_one_reads_the_token_on_the_device(fh, orc):
     assert np.isnan(host(fh, out)).all()
 
 
-@pytest.mark.parametrize("d,heads,T", [(768, 12, 70), (128, 4, 33), (96, 3, 5), (256, 2, 40)])
+@pytest.mark.parametrize(
+    "d,heads,T",
+    [(768, 12, 70), (128, 4, 33), (96, 3, 5), (256, 2, 40),
+     # several workgroups per head (merge through the partials): 256
+     # positions per workgroup at head width <= 64, 128 at 128; the last two
+     # need more than one merge round of eight chunks
+     (768, 12, 600), (64, 8, 300), (256, 2, 1100), (64, 8, 2100)])
 def test_attention_decode_matches_oracle(fh, orc, d, heads, T):
     import ferrum_hip
 
     rng = np.random.default_rng(d + T)
     cap = T + 3
     qkv = (rng.standard_normal((T, 3 * d)) * 1.5).astype(np.float32)
-    kc, vc = dev(np.zeros((cap, d), np.float32)), dev(np.zeros((cap, d), np.float32))
-    ko, vo = np.zeros((cap, d), np.float32), np.zeros((cap, d), np.float32)
+    # rows at and past the position have never been written: NaN there must
+    # not reach the output
+    kc, vc = dev(np.full((cap, d), np.nan, np.float32)), dev(np.full((cap, d), np.nan, np.float32))
+    ko, vo = np.full((cap, d), np.nan, np.float32), np.full((cap, d), np.nan, np.float32)
     out = dev(np.zeros(d, np.float32))
+    edges = {31, 32, 33, 63, 64, 65, 95, 96, 97, 127, 128, 129, 255, 256, 257, 511, 512, 1023, 1024, 1025, 2047, 2048}
     for t in range(T):
         q = dev(qkv[t])
         ready()
         ferrum_hip.attention_decode_async(fh, q, kc, vc, cap, d, heads, t, out)
-        close(host(fh, out), orc.attention_decode(qkv[t], ko, vo, heads, t), 1e-5)
-    assert np.array_equal(host(fh, kc), ko) and np.array_equal(host(fh, vc), vo)
+        if t < 40 or t % 97 == 0 or t in edges or t >= T - 2:
+            close(host(fh, out), orc.attention_decode(qkv[t], ko, vo, heads, t), 1e-5)
+        else:
+            orc.attention_decode(qkv[t], ko, vo, heads, t)  # keeps the oracle's cache in step
+    assert np.array_equal(host(fh, kc), ko, equal_nan=True) and np.array_equal(host(fh, vc), vo, equal_nan=True)
 
 
 def test_attention_decode_errors(fh):
@@ -162,6 +174,70 @@ def test_linear_with_gelu_equals_linear_then_gelu(fh, orc, m, n, k):
     close(got, orc.gelu(orc.q8_0_linear(x, raw, n, b)), 1e-5)
     with pytest.raises(ferrum_hip.FerrumHipError, match="unknown activation"):
         ferrum_hip.linear_act_async(fh, w, tx, m, k, tb, n, fused, 7)
+
+
+@pytest.mark.parametrize(
+    "m,n,k,res,act,numerics",
+    [(1, 2304, 768, True, 0, 0), (1, 3072, 768, True, 1, 0), (1, 50257, 768, True, 0, 0),  # GPT-2 shapes (G = 16)
+     (2, 640, 1024, True, 1, 0), (1, 512, 2048, True, 0, 0),   # 64 lanes per row, 1 and 2 chunks per lane
+     (1, 96, 128, True, 0, 0), (2, 100, 896, True, 1, 0),      # narrow rows, ragged group tails
+     (5, 640, 768, True, 1, 0), (1, 384, 768, False, 0, 0),    # two-kernel path: m > 2, no residual
+     (3, 256, 512, True, 1, 1)])                              # W8A8
+def test_linear_ln_matches_oracle(fh, orc, m, n, k, res, act, numerics):
+    """y = act(LayerNorm(x + r) W^T + b) and s = x + r, against the oracle's
+    add, layernorm, Q8_0 linear and gelu."""
+    import torch
+
+    import ferrum_hip
+
+    rng = np.random.default_rng(m * n + k)
+    raw = orc.quantize_weight(n, k, n + k, 0.05)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x = (rng.standard_normal((m, k)) * 2 + 0.5).astype(np.float32)
+    r = rng.standard_normal((m, k)).astype(np.float32)
+    g, be = rng.standard_normal(k).astype(np.float32), (rng.standard_normal(k) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    tx, tr, tg, tbe, tb = dev(x), dev(r), dev(g), dev(be), dev(b)
+    ts = dev(np.full((m, k), np.nan, np.float32))
+    y = torch.empty((m, n), device="cuda")
+    ready()
+    ferrum_hip.linear_ln_async(fh, w, tx, tr if res else None, ts, m, k, tg, tbe, tb, n, y, act, numerics)
+    got, s_got = host(fh, y), host(fh, ts)
+    sm = (x + r).astype(np.float32) if res else x
+    assert np.array_equal(s_got, sm)
+    if numerics == 0:
+        want = orc.q8_0_linear(orc.layernorm(sm, g, be), raw, n, b)
+        close(got, orc.gelu(want) if act else want, 1e-5)
+    else:
+        # W8A8 re-quantises the LayerNorm output, so a last-bit difference
+        # in it can move a quant: compare with the same steps as separate calls.
+        tx2, th = dev(x), dev(np.zeros((m, k), np.float32))
+        y2 = torch.empty((m, n), device="cuda")
+        ready()
+        ferrum_hip.add_layernorm_async(fh, tx2, tr, m, k, tg, tbe, th)
+        ferrum_hip.linear_act_async(fh, w, th, m, k, tb, n, y2, act, numerics)
+        assert np.array_equal(got, host(fh, y2))
+    w.free()
+
+
+def test_linear_ln_errors(fh, orc):
+    import torch
+
+    import ferrum_hip
+
+    raw = orc.quantize_weight(64, 256, 1, 0.05)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, 64, 256)
+    x, r, g = (dev(np.ones((1, 256), np.float32)) for _ in range(3))
+    y = torch.empty(64, device="cuda")
+    with pytest.raises(ferrum_hip.FerrumHipError, match="must not alias"):
+        ferrum_hip.linear_ln_async(fh, w, x, r, x, 1, 256, g, g, None, 0, y)
+    with pytest.raises(ferrum_hip.FerrumHipError, match="must not alias"):
+        ferrum_hip.linear_ln_async(fh, w, x, r, r, 1, 256, g, g, None, 0, y)
+    with pytest.raises(ferrum_hip.FerrumHipError, match="gamma"):
+        ferrum_hip.linear_ln_async(fh, w, x, r, None, 1, 256, None, g, None, 0, y)
+    with pytest.raises(ferrum_hip.FerrumHipError, match="unknown activation"):
+        ferrum_hip.linear_ln_async(fh, w, x, r, None, 1, 256, g, g, None, 0, y, 9)
+    w.free()
 
 
 def test_add_layernorm_equals_add_then_layernorm(fh, orc):
