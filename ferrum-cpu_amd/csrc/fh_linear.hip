@@ -37,6 +37,7 @@ __global__ void fh_k_encode_split(const float* __restrict__ x, size_t nblocks, u
 namespace {
 
 constexpr int kWaves = 4;  // waves per block in the GEMV kernels
+constexpr int kLnMaxK = 2048;  // widest row the GEMV's LayerNorm prologue takes
 // W8A8 runs on the int8 matrix cores (one wave per 32- or 64-row x 64-column
 // output tile, every Q8_0 block in order) once there are this many tiles;
 // fewer waves, each walking all of K, lose to the block-parallel kernel below.
@@ -102,8 +103,10 @@ __global__ void __launch_bounds__(64 * kWaves)
     const int nsets = (n + RW - 1) / RW;
     const int wave = blockIdx.x * kWaves + (threadIdx.x >> 6);
     const int set0 = wave * per_wave;
-    if (set0 >= nsets) return;
+    if (!kLn && set0 >= nsets) return;  // (with kLn every wave joins the LayerNorm's barriers first)
     const int set1 = min(nsets, set0 + per_wave);
+    [[maybe_unused]] __shared__ __align__(16) float ln_x[kLn ? M : 1][kLn ? kLnMaxK : 4];
+    [[maybe_unused]] __shared__ float ln_red[kLn ? 2 * M : 1][kWaves];
 
     // Every load below is unconditional, from a clamped (always valid)
     // address, so the compiler issues them back to back without waits; the
@@ -111,82 +114,116 @@ __global__ void __launch_bounds__(64 * kWaves)
     // A chunk past the row end (k16 not a multiple of G) re-reads the last one
     // and gets its activations masked to +0.0 bit-wise, so it adds nothing.
     float xr[M][CPL][16];
-    [[maybe_unused]] float lg[kLn ? CPL : 1][16], lb[kLn ? CPL : 1][16];
+    if constexpr (!kLn) {
 #pragma unroll
-    for (int c = 0; c < CPL; c++) {
-        const int ci = min(gl + c * G, k16 - 1);
-        const uint32_t keep = gl + c * G < k16 ? 0xFFFFFFFFu : 0u;
-        if constexpr (kLn) {
-            const float4* gs = reinterpret_cast<const float4*>(ln.gamma + ci * 16);
-            const float4* bs = reinterpret_cast<const float4*>(ln.beta + ci * 16);
+        for (int c = 0; c < CPL; c++) {
+            const int ci = min(gl + c * G, k16 - 1);
+            const uint32_t keep = gl + c * G < k16 ? 0xFFFFFFFFu : 0u;
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                const float4 gf = gs[v], bf = bs[v];
-                lg[c][4 * v] = gf.x, lg[c][4 * v + 1] = gf.y, lg[c][4 * v + 2] = gf.z, lg[c][4 * v + 3] = gf.w;
-                lb[c][4 * v] = bf.x, lb[c][4 * v + 1] = bf.y, lb[c][4 * v + 2] = bf.z, lb[c][4 * v + 3] = bf.w;
-            }
-        }
+            for (int m = 0; m < M; m++) {
+                const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * k + ci * 16);
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            const float4* src = reinterpret_cast<const float4*>(x + static_cast<size_t>(m) * k + ci * 16);
-            [[maybe_unused]] const float4* rsrc =
-                kLn ? reinterpret_cast<const float4*>(ln.r + static_cast<size_t>(m) * k + ci * 16) : nullptr;
+                for (int v = 0; v < 4; v++) {
+                    const float4 f = src[v];
+                    const float fv[4] = {f.x, f.y, f.z, f.w};
 #pragma unroll
-            for (int v = 0; v < 4; v++) {
-                float4 f = src[v];
-                if constexpr (kLn) {
-                    const float4 rf = rsrc[v];
-                    f.x = f.x + rf.x, f.y = f.y + rf.y, f.z = f.z + rf.z, f.w = f.w + rf.w;
+                    for (int e = 0; e < 4; e++)
+                        xr[m][c][4 * v + e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, fv[e]) & keep);
                 }
-                const float fv[4] = {f.x, f.y, f.z, f.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    xr[m][c][4 * v + e] = __builtin_bit_cast(float, __builtin_bit_cast(uint32_t, fv[e]) & keep);
             }
         }
     }
+    // kLn: LayerNorm::forward (layer/norm.rs:46-82) of each row of x + r,
+    // once per workgroup: thread t holds elements t, t + 256, ... (loaded
+    // here, before any weight load), the workgroup sums them in a fixed
+    // order, writes (v - mean) * (1 / sqrt(var + 1e-5)) * gamma + beta to LDS,
+    // and every wave reads its chunks back from there.  Workgroup 0 writes
+    // x + r to ln.s.  It runs after the first batch's weight loads are in
+    // flight, so their latency covers it.
+    constexpr int kLnPer = kLnMaxK / (64 * kWaves);
+    [[maybe_unused]] float lv[kLn ? M : 1][kLn ? kLnPer : 1], lg[kLn ? kLnPer : 1], lb[kLn ? kLnPer : 1];
     if constexpr (kLn) {
-        // LayerNorm::forward (layer/norm.rs:46-82) of each row: mean, biased
-        // variance, ((v - mean) / sqrt(var + 1e-5)) * gamma + beta.  Chunks
-        // past the row end hold +0 and stay +0.
 #pragma unroll
-        for (int m = 0; m < M; m++) {
-            float s = 0.0f;
+        for (int i = 0; i < kLnPer; i++) {
+            const int c = threadIdx.x + i * 64 * kWaves;
+            const int cc = min(c, k - 1);
+            lg[i] = ln.gamma[cc];
+            lb[i] = ln.beta[cc];
 #pragma unroll
-            for (int c = 0; c < CPL; c++)
+            for (int m = 0; m < M; m++) lv[m][i] = x[static_cast<size_t>(m) * k + cc] + ln.r[static_cast<size_t>(m) * k + cc];
+        }
+    }
+    auto layer_norm = [&]() __attribute__((always_inline)) {
+        if constexpr (kLn) {
+            const int w = threadIdx.x >> 6;
+            float mean[M], rsd[M];
 #pragma unroll
-                for (int t = 0; t < 16; t++) s += xr[m][c][t];
-            const float mean = group_total<G>(s) / static_cast<float>(k);
-            float ss = 0.0f;
+            for (int m = 0; m < M; m++) {
+                float s = 0.0f;
 #pragma unroll
-            for (int c = 0; c < CPL; c++)
-                if (gl + c * G < k16)
+                for (int i = 0; i < kLnPer; i++)
+                    if (threadIdx.x + i * 64 * kWaves < k) s += lv[m][i];
+                s = group_total<64>(s);
+                if ((threadIdx.x & 63) == 0) ln_red[m][w] = s;
+            }
+            __syncthreads();
 #pragma unroll
-                    for (int t = 0; t < 16; t++) {
-                        const float dv = xr[m][c][t] - mean;
+            for (int m = 0; m < M; m++) {
+                float s = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kWaves; i++) s += ln_red[m][i];
+                mean[m] = s / static_cast<float>(k);
+                float ss = 0.0f;
+#pragma unroll
+                for (int i = 0; i < kLnPer; i++)
+                    if (threadIdx.x + i * 64 * kWaves < k) {
+                        const float dv = lv[m][i] - mean[m];
                         ss += dv * dv;
                     }
-            const float sd = sqrtf(group_total<G>(ss) / static_cast<float>(k) + 1e-5f);
-            if (ln.s && blockIdx.x == 0 && threadIdx.x < G) {
+                ss = group_total<64>(ss);
+                if ((threadIdx.x & 63) == 0) ln_red[M + m][w] = ss;
+            }
+            __syncthreads();
 #pragma unroll
-                for (int c = 0; c < CPL; c++) {
-                    if (gl + c * G >= k16) continue;
-                    float4* dst = reinterpret_cast<float4*>(ln.s + static_cast<size_t>(m) * k + (gl + c * G) * 16);
+            for (int m = 0; m < M; m++) {
+                float ss = 0.0f;
 #pragma unroll
-                    for (int v = 0; v < 4; v++)
-                        dst[v] = make_float4(xr[m][c][4 * v], xr[m][c][4 * v + 1], xr[m][c][4 * v + 2],
-                                             xr[m][c][4 * v + 3]);
+                for (int i = 0; i < kWaves; i++) ss += ln_red[M + m][i];
+                rsd[m] = 1.0f / sqrtf(ss / static_cast<float>(k) + 1e-5f);
+#pragma unroll
+                for (int i = 0; i < kLnPer; i++) {
+                    const int c = threadIdx.x + i * 64 * kWaves;
+                    if (c < k) {
+                        ln_x[m][c] = ((lv[m][i] - mean[m]) * rsd[m]) * lg[i] + lb[i];
+                        if (ln.s && blockIdx.x == 0) ln.s[static_cast<size_t>(m) * k + c] = lv[m][i];
+                    }
                 }
             }
+            __syncthreads();
 #pragma unroll
             for (int c = 0; c < CPL; c++) {
                 const bool valid = gl + c * G < k16;
+                const int ci = min(gl + c * G, k16 - 1);
 #pragma unroll
-                for (int t = 0; t < 16; t++)
-                    xr[m][c][t] = valid ? ((xr[m][c][t] - mean) / sd) * lg[c][t] + lb[c][t] : 0.0f;
+                for (int m = 0; m < M; m++) {
+                    const float4* src = reinterpret_cast<const float4*>(&ln_x[m][ci * 16]);
+#pragma unroll
+                    for (int v = 0; v < 4; v++) {
+                        const float4 f = src[v];
+                        xr[m][c][4 * v] = valid ? f.x : 0.0f;
+                        xr[m][c][4 * v + 1] = valid ? f.y : 0.0f;
+                        xr[m][c][4 * v + 2] = valid ? f.z : 0.0f;
+                        xr[m][c][4 * v + 3] = valid ? f.w : 0.0f;
+                    }
+                }
             }
         }
+    };
+    if (set0 >= nsets) {
+        if constexpr (kLn) layer_norm();  // the workgroup's barriers need every wave
+        return;
     }
+    [[maybe_unused]] bool normed = false;
 
     // One batch of row-sets [sb, sb + U).  Full batches have no branches, so
     // every load is consumed before the next batch reuses its registers.  The
@@ -219,6 +256,12 @@ __global__ void __launch_bounds__(64 * kWaves)
         // Keep the scheduler from interleaving the batch's loads with its math:
         // all of them go out before the first wait.
         __builtin_amdgcn_sched_barrier(0);
+        if constexpr (kLn) {
+            if (!normed) {  // wave-uniform
+                layer_norm();
+                normed = true;
+            }
+        }
 #pragma unroll
         for (int u = 0; u < U; u++) {
             if (kTail && sb + u >= set1) break;  // wave-uniform
