@@ -10,6 +10,8 @@
 
 #include "fh_internal.hpp"
 
+#include <cmath>
+
 static thread_local std::string g_create_err;
 
 int fh_fail(fh_ctx* ctx, int code, const std::string& msg) {
@@ -624,4 +626,83 @@ int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, con
     rc = fh_launch_linear_w8a8(ctx, w, hf, m, d_bias, d_y);
     if (rc == FH_OK && activation == FH_ACT_GELU) rc = fh_launch_gelu(ctx, d_y, m * w->n);
     return rc;
+}
+
+// ---- Llama / Qwen block pieces ---------------------------------------------------
+
+int fh_rmsnorm_async(fh_ctx* ctx, const float* d_x, const float* d_r, float* d_s, size_t rows, size_t d,
+                     const float* d_w, float eps, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rows == 0) return FH_OK;
+    if (!d_x || !d_w || !d_out) return fh_fail(ctx, FH_ERR_INVALID, "fh_rmsnorm: x, w or out is NULL");
+    if (d == 0 || rows > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_INVALID, "fh_rmsnorm: d must be positive");
+    if (d_s && d_r && d_s == d_r) return fh_fail(ctx, FH_ERR_INVALID, "fh_rmsnorm: s must not alias r");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_rmsnorm(ctx, d_x, d_r, d_s, rows, d, d_w, eps, d_out);
+}
+
+int fh_rope_async(fh_ctx* ctx, float* d_x, size_t rows, size_t ld, size_t n_heads, size_t head_dim, size_t rope_dim,
+                  const uint32_t* d_pos, float base, int rope_type, const float* d_freq_factors, float linear_factor) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rope_dim > head_dim || rope_dim % 2 != 0)
+        return fh_fail(ctx, FH_ERR_DIM, "rope_dim " + std::to_string(rope_dim) + " must be even and \u2264 head_dim " +
+                                            std::to_string(head_dim));
+    if (!(linear_factor > 0.0f) || !std::isfinite(linear_factor))
+        return fh_fail(ctx, FH_ERR_DIM, "RoPE scaling factors must be finite and > 0");
+    if (rope_type != FH_ROPE_NORM && rope_type != FH_ROPE_NEOX)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_rope: unknown rope_type " + std::to_string(rope_type));
+    if (rows == 0 || n_heads == 0 || rope_dim == 0) return FH_OK;
+    if (!d_x || !d_pos) return fh_fail(ctx, FH_ERR_INVALID, "fh_rope: x or pos is NULL");
+    if (ld < n_heads * head_dim) return fh_fail(ctx, FH_ERR_DIM, "fh_rope: ld is below n_heads * head_dim");
+    if (rows * ld > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_rope: more than 2^31 - 1 values");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_rope(ctx, d_x, rows, ld, n_heads, head_dim, rope_dim, d_pos, base, rope_type, d_freq_factors,
+                          linear_factor);
+}
+
+int fh_gqa_attention_decode_async(fh_ctx* ctx, const float* d_qkv, size_t ld, size_t rows, size_t n_heads,
+                                  size_t n_kv, size_t head_dim, float* d_k_cache, float* d_v_cache, size_t capacity,
+                                  const uint32_t* d_pos, size_t max_pos, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (n_kv == 0 || n_heads % n_kv != 0)
+        return fh_fail(ctx, FH_ERR_DIM, "n_heads " + std::to_string(n_heads) + " must be a multiple of n_kv_heads " +
+                                            std::to_string(n_kv));
+    if (rows == 0 || n_heads == 0) return FH_OK;
+    if (!d_qkv || !d_k_cache || !d_v_cache || !d_pos || !d_out)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_gqa_attention_decode: a pointer is NULL");
+    if (capacity == 0) return fh_fail(ctx, FH_ERR_INVALID, "fh_gqa_attention_decode: capacity is 0");
+    if (ld < (n_heads + 2 * n_kv) * head_dim)
+        return fh_fail(ctx, FH_ERR_DIM, "fh_gqa_attention_decode: ld is below (n_heads + 2 n_kv) * head_dim");
+    if (rows > 65535 || n_heads > 65535 || ld * rows > 0x7FFFFFFFu || capacity > 0x7FFFFFFFu ||
+        rows * capacity * n_kv * head_dim > (size_t(1) << 40))
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_gqa_attention_decode: a dimension is too large");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_gqa_attention_decode(ctx, d_qkv, ld, rows, n_heads, n_kv, head_dim, d_k_cache, d_v_cache,
+                                          capacity, d_pos, max_pos, d_out);
+}
+
+int fh_swiglu_async(fh_ctx* ctx, const float* d_g, const float* d_u, size_t rows, size_t n, size_t ld, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rows == 0 || n == 0) return FH_OK;
+    if (!d_g || !d_u || !d_out) return fh_fail(ctx, FH_ERR_INVALID, "fh_swiglu: a pointer is NULL");
+    if (ld < n) return fh_fail(ctx, FH_ERR_DIM, "fh_swiglu: ld is below n");
+    if (rows * ld > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_swiglu: more than 2^31 - 1 values");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_swiglu(ctx, d_g, d_u, rows, n, ld, d_out);
+}
+
+int fh_embed_rows_async(fh_ctx* ctx, const float* d_tok_w, size_t vocab, size_t d, const uint32_t* d_tokens,
+                        size_t rows, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rows == 0 || d == 0) return FH_OK;
+    if (!d_tok_w || !d_tokens || !d_out) return fh_fail(ctx, FH_ERR_INVALID, "fh_embed_rows: a pointer is NULL");
+    if (rows * d > 0x7FFFFFFFu || vocab > 0x7FFFFFFFu)
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_embed_rows: more than 2^31 - 1 values");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_embed_rows(ctx, d_tok_w, vocab, d, d_tokens, rows, d_out);
 }

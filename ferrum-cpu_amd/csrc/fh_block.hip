@@ -33,23 +33,8 @@ constexpr int kThreads = 256;
 constexpr int kChunk = 32;    // cache positions per attention workgroup
 constexpr int kMaxHd = 128;   // head width the attention kernel supports
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-// Sum over the workgroup in a fixed order (wave sums, then waves in order).
-__device__ float block_sum(float v, float* red) {
-    v = wave_sum(v);
-    const int w = threadIdx.x >> 6;
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) red[w] = v;
-    __syncthreads();
-    float s = 0.0f;
-    for (int i = 0; i < static_cast<int>(blockDim.x >> 6); i++) s += red[i];
-    return s;
-}
+using fh::block_sum;
+using fh::wave_sum;
 
 __global__ void __launch_bounds__(kThreads) k_embed_one(const float* __restrict__ tok_w, const float* __restrict__ pos_w,
                                                        int vocab, int d, const uint32_t* __restrict__ token, int pos,
@@ -93,16 +78,36 @@ __global__ void __launch_bounds__(kThreads) k_add(float* __restrict__ x, const f
     if (i < n) x[i] = x[i] + y[i];
 }
 
-// Grid (chunks, heads); a workgroup covers S sub-chunks of 32 positions.
+// Grid (chunks, heads, rows); a workgroup covers S sub-chunks of 32
+// positions of one query head of one row (sequence).  Row r's q|k|v sits at
+// qkv + r * ld (q heads, then kv heads at k_off and v_off); its caches at
+// kc / vc + r * seq_stride, one kv_dim-wide row per position; query head h
+// reads kv head h / group (group 1: multi-head, GPT-2).  Row r's position is
+// dpos[r] (device) or pos; chunks past it exit at once, and a position at or
+// past cap gives a NaN output and writes nothing.
 // Every K, V and q element a thread needs is loaded at entry, so one memory
-// latency covers the whole chunk.  With one chunk per head the workgroup
-// writes the head's output itself; otherwise part: [heads][chunks][2 + hd]
-// (max, sum, weighted v sum) is written with device-coherent stores and the
-// last chunk of a head to arrive merges them.  counters: one per head, left 0.
+// latency covers the whole chunk.  With one chunk the workgroup writes the
+// head's output itself; otherwise part: [rows][heads][chunks][2 + hd] (max,
+// sum, weighted v sum) is written with device-coherent stores and the last
+// chunk of a (row, head) to arrive merges them.  counters: [rows][heads], left 0.
+struct AttnArgs {
+    const float* qkv;
+    int ld, k_off, v_off;
+    float* kc;
+    float* vc;
+    size_t seq_stride;
+    int kv_dim, group;
+    const uint32_t* dpos;
+    int pos, cap;
+    float scale;
+    float* part;
+    unsigned* counters;
+    float* out;
+    int out_ld;
+};
+
 template <int S, int HD>
-__global__ void __launch_bounds__(kThreads)
-    k_attn_chunk(const float* __restrict__ qkv, float* __restrict__ kc, float* __restrict__ vc, int d, int pos,
-                 float scale, float* __restrict__ part, unsigned* __restrict__ counters, float* __restrict__ out) {
+__global__ void __launch_bounds__(kThreads) k_attn_chunk(AttnArgs a) {
     constexpr int kPos = S * kChunk;             // positions per workgroup
     constexpr int hd = HD, per = HD / 8;         // dims per lane of a score
     constexpr int groups = kThreads / HD;        // threads per v column
@@ -111,12 +116,30 @@ __global__ void __launch_bounds__(kThreads)
     __shared__ float acc[kThreads];
     __shared__ float stat[2];
     __shared__ int last;
-    const int chunk = blockIdx.x, head = blockIdx.y, chunks = gridDim.x;
+    const int chunk = blockIdx.x, head = blockIdx.y, row = blockIdx.z;
     const int hs = head * hd, tid = threadIdx.x;
-    const int len = pos + 1, j0 = chunk * kPos, jn = min(kPos, len - j0);
+    const int kvs = (head / a.group) * hd;  // this head's kv slice
+    const int pos = a.dpos ? static_cast<int>(min(a.dpos[row], 0x7FFFFFFFu)) : a.pos;
+    float* out = a.out + static_cast<size_t>(row) * a.out_ld + hs;
+    if (pos >= a.cap) {  // a position the cache cannot hold
+        if (chunk == 0 && tid < hd) out[tid] = __builtin_nanf("");
+        return;
+    }
+    const int len = pos + 1, chunks = (len + kPos - 1) / kPos;
+    if (chunks > static_cast<int>(gridDim.x)) {  // a position past the launch's max_pos
+        if (chunk == 0 && tid < hd) out[tid] = __builtin_nanf("");
+        return;
+    }
+    if (chunk >= chunks) return;
+    const int j0 = chunk * kPos, jn = min(kPos, len - j0);
     const int jl = tid >> 3, part8 = tid & 7, t = tid % hd, g = tid / hd;
-    const float* knew = qkv + d + hs;
-    const float* vnew = qkv + 2 * d + hs;
+    const float* qkv = a.qkv + static_cast<size_t>(row) * a.ld;
+    const int d = a.kv_dim;
+    float* kc = a.kc + row * a.seq_stride + kvs;
+    float* vc = a.vc + row * a.seq_stride + kvs;
+    const float* knew = qkv + a.k_off + kvs;
+    const float* vnew = qkv + a.v_off + kvs;
+    const float scale = a.scale;
     // loads: this lane's q slice, its K slices (one position per sub-chunk)
     // and its V elements (vper positions per sub-chunk).  Position pos (and
     // any position past it, which is masked) comes from qkv itself, never
@@ -127,20 +150,21 @@ __global__ void __launch_bounds__(kThreads)
 #pragma unroll
     for (int u = 0; u < S; u++) {
         const int j = j0 + u * kChunk + jl;
-        const float* row = j >= pos ? knew : kc + static_cast<size_t>(j) * d + hs;
+        const float* krow = j >= pos ? knew : kc + static_cast<size_t>(j) * d;
 #pragma unroll
-        for (int i = 0; i < per; i++) kr[u][i] = row[part8 * per + i];
+        for (int i = 0; i < per; i++) kr[u][i] = krow[part8 * per + i];
 #pragma unroll
         for (int i = 0; i < vper; i++) {
             const int jv = j0 + u * kChunk + g + i * groups;
-            const float* vrow = jv >= pos ? vnew : vc + static_cast<size_t>(jv) * d + hs;
+            const float* vrow = jv >= pos ? vnew : vc + static_cast<size_t>(jv) * d;
             vr[u][i] = vrow[t];
         }
     }
-    // the new row: chunk 0 of each head writes its slice of k and v at row pos
-    if (chunk == 0 && tid < hd) {
-        kc[static_cast<size_t>(pos) * d + hs + tid] = knew[tid];
-        vc[static_cast<size_t>(pos) * d + hs + tid] = vnew[tid];
+    // the new row: chunk 0 of the first query head of each kv head writes
+    // that kv head's slice of k and v at row pos
+    if (chunk == 0 && head % a.group == 0 && tid < hd) {
+        kc[static_cast<size_t>(pos) * d + tid] = knew[tid];
+        vc[static_cast<size_t>(pos) * d + tid] = vnew[tid];
     }
     // scores: 8 lanes per position, each over hd / 8 consecutive dims in
     // ascending order, then a fixed 8-lane tree
@@ -200,10 +224,12 @@ __global__ void __launch_bounds__(kThreads)
     if (tid < hd)
         for (int gg = 0; gg < groups; gg++) r += acc[gg * hd + tid];
     if (chunks == 1) {
-        if (tid < hd) out[hs + tid] = r / stat[1];
+        if (tid < hd) out[tid] = r / stat[1];
         return;
     }
-    float* mine = part + (static_cast<size_t>(head) * chunks + chunk) * (2 + hd);
+    const int cmax = gridDim.x;  // partial slots per (row, head)
+    const size_t rh = static_cast<size_t>(row) * gridDim.y + head;
+    float* mine = a.part + (rh * cmax + chunk) * (2 + hd);
     if (tid < hd) __hip_atomic_store(mine + 2 + tid, r, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (tid == 0) {
         __hip_atomic_store(mine, stat[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -213,12 +239,12 @@ __global__ void __launch_bounds__(kThreads)
     // count moves, so the last arrival reads whole partials.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (tid == 0) last = atomicAdd(counters + head, 1u) == static_cast<unsigned>(chunks - 1);
+    if (tid == 0) last = atomicAdd(a.counters + rh, 1u) == static_cast<unsigned>(chunks - 1);
     __syncthreads();
     if (!last) return;
     // Merge, eight chunks per round with all their loads in flight at once;
     // a running max rescales the sums when a later round raises it.
-    const float* hp = part + static_cast<size_t>(head) * chunks * (2 + hd);
+    const float* hp = a.part + rh * cmax * (2 + hd);
     constexpr int R = 8;
     const int tt = min(tid, hd - 1);
     float M = -INFINITY, Sm = 0.0f, rm = 0.0f;
@@ -248,8 +274,8 @@ __global__ void __launch_bounds__(kThreads)
             rm += oc[i] * f;
         }
     }
-    if (tid < hd) out[hs + tid] = rm / Sm;
-    if (tid == 0) __hip_atomic_store(counters + head, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid < hd) out[tid] = rm / Sm;
+    if (tid == 0) __hip_atomic_store(a.counters + rh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // x += y, then LayerNorm of the sum into ln (the residual add of
@@ -353,34 +379,37 @@ int fh_launch_add_layernorm(fh_ctx* ctx, const float* x, const float* y, float* 
     return FH_OK;
 }
 
-int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads, size_t pos,
-                               float* out) {
-    const size_t hd = d / heads;
-    if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
-        return fh_fail(ctx, FH_ERR_LIMIT, "fh_attention_decode: head width must be 8, 16, 32, 64 or 128");
-    // Sub-chunks per workgroup, from timings of 12 heads of 64 at positions
-    // 63 to 1023: one workgroup per head while the head fits in 64
-    // positions, then 64 positions per workgroup (enough workgroups in
-    // flight to cover the load latency; one workgroup per head over 256
-    // positions runs about 1.5x slower), 128 past position 767.
-    const size_t len = pos + 1;
+namespace {
+
+// Sub-chunks per workgroup, from timings of 12 heads of 64 at positions 63
+// to 1023: one workgroup per head while the head fits in 64 positions, then
+// 64 positions per workgroup (enough workgroups in flight to cover the load
+// latency; one workgroup per head over 256 positions runs about 1.5x
+// slower), 128 past position 767.
+size_t attn_sub(size_t len) {
     const size_t need = (len + kChunk - 1) / kChunk;
-    const size_t sub = need <= 2 ? need : len > 768 ? 4 : 2;
-    const size_t chunks = (len + sub * kChunk - 1) / (sub * kChunk);
+    return need <= 2 ? need : len > 768 ? 4 : 2;
+}
+
+// max_len: the longest row (positions + 1) the launch may see.
+int launch_attention(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t hd, size_t max_len) {
+    if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
+        return fh_fail(ctx, FH_ERR_LIMIT, "attention: head width must be 8, 16, 32, 64 or 128");
+    const size_t sub = attn_sub(max_len);
+    const size_t chunks = (max_len + sub * kChunk - 1) / (sub * kChunk);
     void* ws = nullptr;
-    int rc = fh_workspace(ctx, heads * chunks * (2 + hd) * sizeof(float), &ws);
+    int rc = fh_workspace(ctx, rows * heads * chunks * (2 + hd) * sizeof(float), &ws);
     if (rc) return rc;
     void* cnt = nullptr;
-    rc = fh_counter_area(ctx, heads * sizeof(unsigned), &cnt);
+    rc = fh_counter_area(ctx, rows * heads * sizeof(unsigned), &cnt);
     if (rc) return rc;
-    const float scale = 1.0f / sqrtf(static_cast<float>(hd));
-    const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(heads));
+    a.scale = 1.0f / sqrtf(static_cast<float>(hd));
+    a.part = static_cast<float*>(ws);
+    a.counters = static_cast<unsigned*>(cnt);
+    const dim3 grid(static_cast<unsigned>(chunks), static_cast<unsigned>(heads), static_cast<unsigned>(rows));
     auto go = [&](auto hdc) {
         constexpr int HD = decltype(hdc)::value;
-        auto launch = [&](auto kern) {
-            hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, ctx->stream, qkv, kc, vc, static_cast<int>(d),
-                               static_cast<int>(pos), scale, static_cast<float*>(ws), static_cast<unsigned*>(cnt), out);
-        };
+        auto launch = [&](auto kern) { hipLaunchKernelGGL(kern, grid, dim3(kThreads), 0, ctx->stream, a); };
         switch (sub) {
             case 1: launch(k_attn_chunk<1, HD>); break;
             case 2: launch(k_attn_chunk<2, HD>); break;
@@ -396,4 +425,47 @@ int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* 
     }
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
+}
+
+}  // namespace
+
+int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads, size_t pos,
+                               float* out) {
+    AttnArgs a{};
+    a.qkv = qkv;
+    a.ld = static_cast<int>(3 * d);
+    a.k_off = static_cast<int>(d);
+    a.v_off = static_cast<int>(2 * d);
+    a.kc = kc;
+    a.vc = vc;
+    a.seq_stride = 0;
+    a.kv_dim = static_cast<int>(d);
+    a.group = 1;
+    a.dpos = nullptr;
+    a.pos = static_cast<int>(pos);
+    a.cap = 0x7FFFFFFF;  // checked by the caller
+    a.out = out;
+    a.out_ld = static_cast<int>(d);
+    return launch_attention(ctx, a, 1, heads, d / heads, pos + 1);
+}
+
+int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,
+                                   size_t hd, float* kc, float* vc, size_t cap, const uint32_t* dpos, size_t max_pos,
+                                   float* out) {
+    AttnArgs a{};
+    a.qkv = qkv;
+    a.ld = static_cast<int>(ld);
+    a.k_off = static_cast<int>(n_heads * hd);
+    a.v_off = static_cast<int>((n_heads + n_kv) * hd);
+    a.kc = kc;
+    a.vc = vc;
+    a.seq_stride = cap * n_kv * hd;
+    a.kv_dim = static_cast<int>(n_kv * hd);
+    a.group = static_cast<int>(n_heads / n_kv);
+    a.dpos = dpos;
+    a.pos = 0;
+    a.cap = static_cast<int>(cap);
+    a.out = out;
+    a.out_ld = static_cast<int>(n_heads * hd);
+    return launch_attention(ctx, a, rows, n_heads, hd, (max_pos < cap ? max_pos : cap - 1) + 1);
 }

@@ -116,6 +116,16 @@ int fh_launch_add_layernorm(fh_ctx* ctx, const float* x, const float* y, float* 
                             const float* gamma, const float* beta, float* ln);
 int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
                                size_t pos, float* out);
+int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,
+                                   size_t hd, float* kc, float* vc, size_t cap, const uint32_t* dpos, size_t max_pos,
+                                   float* out);
+int fh_launch_rmsnorm(fh_ctx* ctx, const float* x, const float* r, float* s, size_t rows, size_t d, const float* w,
+                      float eps, float* out);
+int fh_launch_rope(fh_ctx* ctx, float* x, size_t rows, size_t ld, size_t n_heads, size_t hd, size_t rope_dim,
+                   const uint32_t* dpos, float base, int rope_type, const float* freq_factors, float linear_factor);
+int fh_launch_swiglu(fh_ctx* ctx, const float* g, const float* u, size_t rows, size_t n, size_t ld, float* out);
+int fh_launch_embed_rows(fh_ctx* ctx, const float* tok_w, size_t vocab, size_t d, const uint32_t* tokens, size_t rows,
+                         float* out);
 int fh_launch_dequant(fh_ctx* ctx, const uint8_t* raw, size_t n, float* out);
 int fh_launch_block_dots(fh_ctx* ctx, const fh_q8_0* w, const int8_t* qx, size_t m,
                          int32_t* dots);
@@ -130,4 +140,25 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
 __device__ __forceinline__ float fh_h2f(uint16_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));
 }
+
+namespace fh {
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// Sum over the workgroup in a fixed order (wave sums, then waves in order);
+// red holds one float per wave.
+__device__ __forceinline__ float block_sum(float v, float* red) {
+    v = wave_sum(v);
+    const int w = threadIdx.x >> 6;
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) red[w] = v;
+    __syncthreads();
+    float s = 0.0f;
+    for (int i = 0; i < static_cast<int>(blockDim.x >> 6); i++) s += red[i];
+    return s;
+}
+}  // namespace fh
 #endif

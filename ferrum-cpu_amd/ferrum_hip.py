@@ -45,6 +45,7 @@ EXPORTS = (
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
+    "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
 )
 
 
@@ -166,6 +167,12 @@ def lib():
         L.fh_q8_0_linear_act_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32, i32]
         L.fh_add_layernorm_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         L.fh_q8_0_linear_ln_async.argtypes = [vp, vp, vp, vp, vp, sz, sz, vp, vp, vp, sz, vp, i32, i32]
+        f32 = C.c_float
+        L.fh_rmsnorm_async.argtypes = [vp, vp, vp, vp, sz, sz, vp, f32, vp]
+        L.fh_rope_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, f32, i32, vp, f32]
+        L.fh_gqa_attention_decode_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, sz, vp, sz, vp]
+        L.fh_swiglu_async.argtypes = [vp, vp, vp, sz, sz, sz, vp]
+        L.fh_embed_rows_async.argtypes = [vp, vp, sz, sz, vp, sz, vp]
         _lib = L
     return _lib
 
@@ -487,6 +494,192 @@ def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d
     """The KV-cache attention of forward_with_cache (layer/transformer.rs:242-279)."""
     ctx.check(lib().fh_attention_decode_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
                                               pos, _ptr(out)))
+
+
+# ---- Llama / Qwen block pieces (llm.rs), batched over rows --------------------
+
+ROPE_NORM, ROPE_NEOX = 0, 1
+
+
+def rmsnorm_async(ctx: Context, x, r, s, rows: int, d: int, w, eps: float, out):
+    """RmsNorm::forward_row over rows; with r, the residual add in front of it
+    (x + r is normalised and written to s when s is given)."""
+    ctx.check(lib().fh_rmsnorm_async(ctx.h, _ptr(x), _ptr(r), _ptr(s), rows, d, _ptr(w), eps, _ptr(out)))
+
+
+def rope_async(ctx: Context, x, rows: int, ld: int, n_heads: int, head_dim: int, rope_dim: int, pos, base: float,
+               rope_type: int, freq_factors=None, linear_factor: float = 1.0):
+    """apply_rope in place on n_heads heads of each row (row r at x + r * ld,
+    position pos[r] on the device)."""
+    ctx.check(lib().fh_rope_async(ctx.h, _ptr(x), rows, ld, n_heads, head_dim, rope_dim, _ptr(pos), base, rope_type,
+                                  _ptr(freq_factors), linear_factor))
+
+
+def gqa_attention_decode_async(ctx: Context, qkv, ld: int, rows: int, n_heads: int, n_kv: int, head_dim: int, k_cache,
+                               v_cache, capacity: int, pos, max_pos: int, out):
+    """Attention::forward_one's cache append + attend for `rows` sequences."""
+    ctx.check(lib().fh_gqa_attention_decode_async(ctx.h, _ptr(qkv), ld, rows, n_heads, n_kv, head_dim, _ptr(k_cache),
+                                                  _ptr(v_cache), capacity, _ptr(pos), max_pos, _ptr(out)))
+
+
+def swiglu_async(ctx: Context, g, u, rows: int, n: int, ld: int, out):
+    """(g / (1 + exp(-g))) * u per row (row r of g and u at r * ld)."""
+    ctx.check(lib().fh_swiglu_async(ctx.h, _ptr(g), _ptr(u), rows, n, ld, _ptr(out)))
+
+
+def embed_rows_async(ctx: Context, tok_w, vocab: int, d: int, tokens, rows: int, out):
+    """LlamaModel::embed for token ids on the device."""
+    ctx.check(lib().fh_embed_rows_async(ctx.h, _ptr(tok_w), vocab, d, _ptr(tokens), rows, _ptr(out)))
+
+
+class LlamaDevice:
+    """A Llama / Qwen2 decoder on the device for `rows` independent sequences
+    (a batched decode step), the way LlamaModel::forward_one walks it
+    (llm.rs:606-616): embed, then per LlamaBlock::forward_one (llm.rs:445-456)
+    RmsNorm, the q|k|v Q8_0 linear (one weight: the three GGUF tensors' rows
+    stacked, with the q/k/v biases a Qwen2 file carries), RoPE on q and k,
+    grouped-query attention over the row's KV cache, the output projection,
+    residual, RmsNorm, the gate|up Q8_0 linear (stacked the same way), SwiGLU,
+    down, residual; the final RmsNorm and the head (the tied token table or
+    output.weight).  Each row's token and position live on the device
+    (self.tokens, self.pos), so a step can be captured in one graph.
+
+    from_weights takes numpy arrays keyed as a GGUF file names them
+    (gguf/llama.rs:171-340): token_embd (Q8_0 bytes [vocab, d]), output
+    (optional, Q8_0 [vocab, d]), output_norm [d], and per block i
+    blk.i.attn_norm, attn_q / attn_k / attn_v (Q8_0) with optional .bias,
+    attn_output, ffn_norm, ffn_gate, ffn_up, ffn_down (Q8_0)."""
+
+    def __init__(self, ctx: Context, cfg: dict, rows: int):
+        import torch
+
+        self.ctx, self.cfg, self.rows = ctx, dict(cfg), rows
+        c = self.cfg
+        self.vocab, self.d, self.nh, self.nkv, self.hd = c["vocab"], c["d"], c["n_heads"], c["n_kv"], c["head_dim"]
+        self.layers, self.ffn, self.cap = c["layers"], c["ffn"], c["context"]
+        self.rope_dim, self.rope_base = c.get("rope_dim", self.hd), c.get("rope_base", 10000.0)
+        self.rope_type, self.eps = c.get("rope_type", ROPE_NEOX), c.get("eps", 1e-5)
+        self.q_dim, self.kv_dim = self.nh * self.hd, self.nkv * self.hd
+        self.qkv_dim = self.q_dim + 2 * self.kv_dim
+        dev, B = torch.device("cuda"), rows
+        self.x = torch.zeros((B, self.d), device=dev)
+        self.x2 = torch.zeros((B, self.d), device=dev)  # the residual stream alternates between x and x2
+        self.h = torch.empty((B, self.d), device=dev)
+        self.qkv = torch.empty((B, self.qkv_dim), device=dev)
+        self.att = torch.empty((B, self.q_dim), device=dev)
+        self.proj = torch.empty((B, self.d), device=dev)
+        self.gu = torch.empty((B, 2 * self.ffn), device=dev)
+        self.mid = torch.empty((B, self.ffn), device=dev)
+        self.z = torch.empty((B, self.vocab), device=dev)
+        self.tokens = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.blocks = []
+
+    def _alloc_cache(self):
+        import torch
+
+        n = self.rows * self.cap * self.kv_dim
+        return torch.zeros(n, device="cuda"), torch.zeros(n, device="cuda")
+
+    @classmethod
+    def from_weights(cls, ctx: Context, weights: dict, cfg: dict, rows: int) -> "LlamaDevice":
+        import torch
+
+        m = cls(ctx, cfg, rows)
+        d, f = m.d, (lambda a: torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).cuda())
+        raw = lambda name: np.asarray(weights[name], np.uint8).ravel()  # noqa: E731
+        tok = raw("token_embd")
+        m.tok_w = torch.empty((m.vocab, d), device="cuda")
+        traw = torch.from_numpy(tok.copy()).cuda()
+        torch.cuda.synchronize()
+        q8_0_dequant_async(ctx, traw, m.vocab * d, m.tok_w)
+        m.head = Q8_0Weight.upload(ctx, raw("output") if "output" in weights else tok, m.vocab, d)
+        for i in range(m.layers):
+            p = f"blk.{i}."
+            qkv = np.concatenate([raw(p + "attn_q"), raw(p + "attn_k"), raw(p + "attn_v")])
+            bias = np.concatenate([np.asarray(weights.get(p + f"attn_{s}.bias", np.zeros(n, np.float32)), np.float32)
+                                   for s, n in (("q", m.q_dim), ("k", m.kv_dim), ("v", m.kv_dim))])
+            gate_up = np.concatenate([raw(p + "ffn_gate"), raw(p + "ffn_up")])
+            k, v = m._alloc_cache()
+            m.blocks.append({
+                "attn_norm": f(weights[p + "attn_norm"]), "ffn_norm": f(weights[p + "ffn_norm"]),
+                "qkv": Q8_0Weight.upload(ctx, qkv, m.qkv_dim, d), "qkv_b": f(bias),
+                "o": Q8_0Weight.upload(ctx, raw(p + "attn_output"), d, m.q_dim),
+                "gate_up": Q8_0Weight.upload(ctx, gate_up, 2 * m.ffn, d),
+                "down": Q8_0Weight.upload(ctx, raw(p + "ffn_down"), d, m.ffn), "k": k, "v": v})
+        m.out_norm = f(weights["output_norm"])
+        torch.cuda.synchronize()
+        ctx.sync()
+        return m
+
+    @classmethod
+    def random(cls, ctx: Context, cfg: dict, rows: int, gen) -> "LlamaDevice":
+        """N(0, 0.02) Q8_0 weights generated and encoded on the device (for timing)."""
+        import torch
+
+        m = cls(ctx, cfg, rows)
+        d = m.d
+
+        def q8(n, k):
+            w = torch.randn((n, k), generator=gen, device="cuda") * 0.02
+            raw = torch.empty(n * k // 32 * 34, dtype=torch.uint8, device="cuda")
+            torch.cuda.synchronize()
+            q8_0_encode_async(ctx, w, n * k, raw)
+            q = Q8_0Weight.upload_device(ctx, raw, n, k)
+            ctx.sync()
+            return q, raw
+
+        vec = lambda n, base=0.0: torch.randn(n, generator=gen, device="cuda") * 0.02 + base  # noqa: E731
+        m.head, raw = q8(m.vocab, d)
+        m.tok_w = torch.empty((m.vocab, d), device="cuda")
+        q8_0_dequant_async(ctx, raw, m.vocab * d, m.tok_w)
+        ctx.sync()
+        for _ in range(m.layers):
+            k, v = m._alloc_cache()
+            m.blocks.append({"attn_norm": vec(d, 1.0), "ffn_norm": vec(d, 1.0), "qkv": q8(m.qkv_dim, d)[0],
+                             "qkv_b": vec(m.qkv_dim), "o": q8(d, m.q_dim)[0], "gate_up": q8(2 * m.ffn, d)[0],
+                             "down": q8(d, m.ffn)[0], "k": k, "v": v})
+        m.out_norm = vec(d, 1.0)
+        torch.cuda.synchronize()
+        ctx.sync()
+        return m
+
+    def launches_per_step(self) -> int:
+        """Kernel launches of feed_async (the sampler not included)."""
+        return 1 + 9 * self.layers + 2
+
+    def feed_async(self, max_pos: int):
+        """One decode step of every row: token self.tokens[r] at position
+        self.pos[r] (both on the device; max_pos bounds the positions).  The
+        head's scores land in self.z; positions are not advanced."""
+        ctx, d, B = self.ctx, self.d, self.rows
+        embed_rows_async(ctx, self.tok_w, self.vocab, d, self.tokens, B, self.x)
+        cur, other = self.x, self.x2
+        for i, b in enumerate(self.blocks):
+            if i == 0:
+                rmsnorm_async(ctx, cur, None, None, B, d, b["attn_norm"], self.eps, self.h)
+            else:  # the previous block's second residual add, then attn_norm
+                rmsnorm_async(ctx, cur, self.proj, other, B, d, b["attn_norm"], self.eps, self.h)
+                cur, other = other, cur
+            linear_forward_async(ctx, b["qkv"], self.h, B, d, b["qkv_b"], self.qkv_dim, self.qkv)
+            rope_async(ctx, self.qkv, B, self.qkv_dim, self.nh + self.nkv, self.hd, self.rope_dim, self.pos,
+                       self.rope_base, self.rope_type)
+            gqa_attention_decode_async(ctx, self.qkv, self.qkv_dim, B, self.nh, self.nkv, self.hd, b["k"], b["v"],
+                                       self.cap, self.pos, max_pos, self.att)
+            linear_forward_async(ctx, b["o"], self.att, B, self.q_dim, None, 0, self.proj)
+            rmsnorm_async(ctx, cur, self.proj, other, B, d, b["ffn_norm"], self.eps, self.h)
+            cur, other = other, cur
+            linear_forward_async(ctx, b["gate_up"], self.h, B, d, None, 0, self.gu)
+            swiglu_async(ctx, self.gu, self.gu[:, self.ffn:], B, self.ffn, 2 * self.ffn, self.mid)
+            linear_forward_async(ctx, b["down"], self.mid, B, self.ffn, None, 0, self.proj)
+        rmsnorm_async(ctx, cur, self.proj, None, B, d, self.out_norm, self.eps, self.h)
+        linear_forward_async(ctx, self.head, self.h, B, d, None, 0, self.z)
+
+    def free(self):
+        self.head.free()
+        for b in self.blocks:
+            for key in ("qkv", "o", "gate_up", "down"):
+                b[key].free()
 
 
 class GPT2Device:

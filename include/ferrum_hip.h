@@ -222,6 +222,45 @@ int fh_add_layernorm_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t row
 int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, const float* d_r, float* d_s,
                             size_t m, size_t k, const float* d_gamma, const float* d_beta, const float* d_bias,
                             size_t bias_len, float* d_y, int numerics, int activation);
+
+/* ---- Llama / Qwen block pieces (ferrum_core llm.rs), batched over rows ------
+ * Each row is one sequence of a batched decode.  Positions live on the device
+ * (d_pos[r] for row r), so a decode loop can run without the host. */
+enum { FH_ROPE_NORM = 0, FH_ROPE_NEOX = 1 };
+/* RmsNorm::forward_row (llm.rs:58-65), x * (1 / sqrt(mean(x^2) + eps)) * w,
+ * over rows of width d <= 8192.  With d_r (nullable) the residual add in front
+ * of it: h = x + r is normalised and, when d_s is not NULL (it may be d_x),
+ * written there (LlamaBlock::forward_one, llm.rs:445-456). */
+int fh_rmsnorm_async(fh_ctx* ctx, const float* d_x, const float* d_r, float* d_s, size_t rows, size_t d,
+                     const float* d_w, float eps, float* d_out);
+/* apply_rope (llm.rs:146-175, angle llm.rs:118-121) in place on n_heads
+ * consecutive heads of head_dim starting at d_x + r * ld, row r at position
+ * d_pos[r]: FH_ROPE_NORM rotates pairs (2i, 2i+1), FH_ROPE_NEOX (i, i +
+ * rope_dim/2); channels past rope_dim pass through.  d_freq_factors: NULL or
+ * rope_dim / 2 divisors on the device.  Errors as Attention::new and
+ * RopeScaling::check (llm.rs:123-139, 239-246): rope_dim odd or above
+ * head_dim, linear_factor not finite and > 0. */
+int fh_rope_async(fh_ctx* ctx, float* d_x, size_t rows, size_t ld, size_t n_heads, size_t head_dim, size_t rope_dim,
+                  const uint32_t* d_pos, float base, int rope_type, const float* d_freq_factors, float linear_factor);
+/* Attention::forward_one's cache append and attend (llm.rs:285-358) for
+ * `rows` sequences: row r's RoPE'd [q (n_heads heads) | k (n_kv) | v (n_kv)]
+ * at d_qkv + r * ld; its caches at d_k_cache / d_v_cache + r * capacity *
+ * n_kv * head_dim ([capacity, n_kv * head_dim] each); k and v go to cache row
+ * d_pos[r], then each query head h attends over rows 0..d_pos[r] with kv head
+ * h / (n_heads / n_kv).  Output [rows, n_heads * head_dim].  max_pos bounds the
+ * positions (it sizes the launch); a row whose position is above max_pos or
+ * at or past capacity gets NaN and its cache is not touched.  head_dim 8, 16,
+ * 32, 64 or 128.  n_heads not a multiple of n_kv is FH_ERR_DIM (llm.rs:233-238). */
+int fh_gqa_attention_decode_async(fh_ctx* ctx, const float* d_qkv, size_t ld, size_t rows, size_t n_heads,
+                                  size_t n_kv, size_t head_dim, float* d_k_cache, float* d_v_cache, size_t capacity,
+                                  const uint32_t* d_pos, size_t max_pos, float* d_out);
+/* FeedForward::forward's gate (llm.rs:415-421): out[r, j] = (g / (1 +
+ * exp(-g))) * u, g = d_g[r * ld + j], u = d_u[r * ld + j], j < n. */
+int fh_swiglu_async(fh_ctx* ctx, const float* d_g, const float* d_u, size_t rows, size_t n, size_t ld, float* d_out);
+/* LlamaModel::embed (llm.rs:588-596) for `rows` token ids on the device; an id
+ * at or past vocab gives a NaN row (the sampler never returns one). */
+int fh_embed_rows_async(fh_ctx* ctx, const float* d_tok_w, size_t vocab, size_t d, const uint32_t* d_tokens,
+                        size_t rows, float* d_out);
 /* x += y, the residual adds of TransformerBlock::forward_with_cache
  * (layer/transformer.rs:281, 288). */
 int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n);

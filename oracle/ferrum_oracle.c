@@ -691,6 +691,86 @@ int fo_attention_decode(const float* qkv, float* k_cache, float* v_cache, size_t
 }
 
 /* ------------------------------------------------------------------------ */
+/* Llama / Qwen block pieces                                                  */
+/* ------------------------------------------------------------------------ */
+
+void fo_rmsnorm(const float* x, size_t rows, size_t dim, const float* w, float eps, float* out) {
+    for (size_t r = 0; r < rows; r++) {
+        const float* xr = x + r * dim;
+        float* o = out + r * dim;
+        float ss = 0.0f;
+        for (size_t i = 0; i < dim; i++) ss += xr[i] * xr[i];
+        const float ms = ss / (float)dim;
+        const float inv = 1.0f / sqrtf(ms + eps);
+        for (size_t i = 0; i < dim; i++) o[i] = xr[i] * inv * w[i];
+    }
+}
+
+void fo_rope(float* x, size_t n_heads, size_t head_dim, size_t rope_dim, size_t pos, float base, int rope_type,
+             const float* freq_factors, float linear_factor) {
+    const size_t half = rope_dim / 2;
+    for (size_t h = 0; h < n_heads; h++) {
+        const size_t off = h * head_dim;
+        for (size_t i = 0; i < half; i++) {
+            const float freq = (float)pow((double)base, -2.0 * (double)i / (double)rope_dim);
+            const float ff = freq_factors ? freq_factors[i] : 1.0f;
+            const float theta = (float)pos * freq / ff * (1.0f / linear_factor);
+            const float sn = sinf(theta), cs = cosf(theta);
+            const size_t ia = rope_type == 0 ? off + 2 * i : off + i;
+            const size_t ib = rope_type == 0 ? off + 2 * i + 1 : off + i + half;
+            const float a = x[ia], b = x[ib];
+            x[ia] = a * cs - b * sn;
+            x[ib] = a * sn + b * cs;
+        }
+    }
+}
+
+int fo_gqa_attention_decode(const float* qkv, float* k_cache, float* v_cache, size_t capacity, size_t n_heads,
+                            size_t n_kv, size_t head_dim, size_t pos, float* out) {
+    if (pos >= capacity) return -1;
+    if (n_kv == 0 || n_heads % n_kv != 0 || head_dim == 0) return -2;
+    const size_t hd = head_dim, q_dim = n_heads * hd, kv_dim = n_kv * hd, group = n_heads / n_kv;
+    for (size_t i = 0; i < kv_dim; i++) {
+        k_cache[pos * kv_dim + i] = qkv[q_dim + i];
+        v_cache[pos * kv_dim + i] = qkv[q_dim + kv_dim + i];
+    }
+    const size_t len = pos + 1;
+    const float scale = 1.0f / sqrtf((float)hd);
+    float* sc = (float*)malloc(len * sizeof(float));
+    if (!sc) return -3;
+    for (size_t h = 0; h < n_heads; h++) {
+        const size_t kvh = h / group;
+        const float* qh = qkv + h * hd;
+        for (size_t j = 0; j < len; j++) {
+            const float* kj = k_cache + j * kv_dim + kvh * hd;
+            float dot = 0.0f;
+            for (size_t t = 0; t < hd; t++) dot += qh[t] * kj[t];
+            sc[j] = dot * scale;
+        }
+        float mx = -INFINITY;
+        for (size_t j = 0; j < len; j++) mx = fmaxf(mx, sc[j]);
+        float sum = 0.0f;
+        for (size_t j = 0; j < len; j++) {
+            sc[j] = expf(sc[j] - mx);
+            sum += sc[j];
+        }
+        float* oh = out + h * hd;
+        for (size_t t = 0; t < hd; t++) oh[t] = 0.0f;
+        for (size_t j = 0; j < len; j++) {
+            const float p = sc[j] / sum;
+            const float* vj = v_cache + j * kv_dim + kvh * hd;
+            for (size_t t = 0; t < hd; t++) oh[t] += p * vj[t];
+        }
+    }
+    free(sc);
+    return 0;
+}
+
+void fo_swiglu(const float* g, const float* u, size_t n, float* out) {
+    for (size_t i = 0; i < n; i++) out[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+}
+
+/* ------------------------------------------------------------------------ */
 /* RNG                                                                        */
 /* ------------------------------------------------------------------------ */
 

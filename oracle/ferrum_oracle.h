@@ -173,6 +173,28 @@ int fo_embed_one(const float* tok_w, const float* pos_w, size_t vocab, size_t ma
 int fo_attention_decode(const float* qkv, float* k_cache, float* v_cache, size_t capacity, size_t d, size_t heads,
                         size_t pos, float* out);
 
+/* ---- Llama / Qwen block pieces (llm.rs) ---------------------------------- */
+/* RmsNorm::forward_row (llm.rs:58-65), every row: ms = sequential sum of v*v
+ * divided by dim, inv = 1 / sqrt(ms + eps), out = x * inv * w. */
+void fo_rmsnorm(const float* x, size_t rows, size_t dim, const float* w, float eps, float* out);
+/* apply_rope (llm.rs:146-175) with RopeScaling::angle (llm.rs:118-121):
+ * freq_i = (f32) pow((f64) base, -2 i / rope_dim), theta = pos * freq / ff_i
+ * * (1 / linear_factor), pairs (2i, 2i+1) for NORM (rope_type 0) or
+ * (i, i + rope_dim/2) for NEOX (1); channels past rope_dim pass through.
+ * freq_factors may be NULL (none) or hold rope_dim / 2 values. */
+void fo_rope(float* x, size_t n_heads, size_t head_dim, size_t rope_dim, size_t pos, float base, int rope_type,
+             const float* freq_factors, float linear_factor);
+/* Attention::forward_one's cache append + attend (llm.rs:285-358) for one
+ * query row: qkv = [q (n_heads*hd) | k (n_kv*hd) | v (n_kv*hd)], already
+ * RoPE'd; k and v are written at row pos of the [capacity, n_kv*hd] caches,
+ * then every head h attends over rows 0..pos with kv head h / (n_heads/n_kv),
+ * p = exp(s - max) / sum applied before the v sum.  Returns -1 when the cache
+ * is full, -2 on a bad head split. */
+int fo_gqa_attention_decode(const float* qkv, float* k_cache, float* v_cache, size_t capacity, size_t n_heads,
+                            size_t n_kv, size_t head_dim, size_t pos, float* out);
+/* FeedForward::forward's gate (llm.rs:415-421): out = (g / (1 + exp(-g))) * u. */
+void fo_swiglu(const float* g, const float* u, size_t n, float* out);
+
 #ifdef __cplusplus
 }
 #endif

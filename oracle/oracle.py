@@ -20,6 +20,14 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libferrum_oracle.so")
 
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+
+
+class _f32p_or_null:
+    """A float32 array argument that may be None (NULL)."""
+
+    @classmethod
+    def from_param(cls, obj):
+        return None if obj is None else _f32p.from_param(obj)
 _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
@@ -119,6 +127,11 @@ def lib():
         L.fo_attention_decode.argtypes = [_f32p, _f32p, _f32p] + [C.c_size_t] * 4 + [_f32p]
         L.fo_attention_decode.restype = C.c_int
         L.fo_ln_bridge.argtypes = [_f32p, C.c_size_t, _f32p]
+        L.fo_rmsnorm.argtypes = [_f32p, C.c_size_t, C.c_size_t, _f32p, C.c_float, _f32p]
+        L.fo_rope.argtypes = [_f32p] + [C.c_size_t] * 4 + [C.c_float, C.c_int, _f32p_or_null, C.c_float]
+        L.fo_gqa_attention_decode.argtypes = [_f32p, _f32p, _f32p] + [C.c_size_t] * 5 + [_f32p]
+        L.fo_gqa_attention_decode.restype = C.c_int
+        L.fo_swiglu.argtypes = [_f32p, _f32p, C.c_size_t, _f32p]
         L.fo_rng_new.argtypes = [C.c_uint64]
         L.fo_rng_new.restype = C.c_uint64
         L.fo_rng_next_u64.argtypes = [C.POINTER(C.c_uint64)]
@@ -364,6 +377,49 @@ def attention_decode(qkv, k_cache, v_cache, heads: int, pos: int) -> np.ndarray:
     rc = lib().fo_attention_decode(_f32(qkv), k_cache, v_cache, k_cache.shape[0], d, heads, pos, out)
     if rc != 0:
         raise ValueError(f"attention_decode: status {rc}")
+    return out
+
+
+# ---- Llama / Qwen block pieces ---------------------------------------------
+
+ROPE_NORM, ROPE_NEOX = 0, 1
+
+
+def rmsnorm(x, w, eps: float) -> np.ndarray:
+    """RmsNorm::forward_row (llm.rs:58-65) over every row."""
+    x = _f32(x)
+    w = _f32(w)
+    out = np.zeros_like(x)
+    dim = x.shape[-1]
+    lib().fo_rmsnorm(x, x.size // dim, dim, w, C.c_float(eps), out)
+    return out
+
+
+def rope(x, n_heads: int, head_dim: int, rope_dim: int, pos: int, base: float, rope_type: int,
+         freq_factors=None, linear_factor: float = 1.0) -> np.ndarray:
+    """apply_rope (llm.rs:146-175) on a copy of x ([n_heads * head_dim])."""
+    out = _f32(x).copy()
+    ff = None if freq_factors is None else _f32(freq_factors)
+    lib().fo_rope(out, n_heads, head_dim, rope_dim, pos, C.c_float(base), rope_type, ff, C.c_float(linear_factor))
+    return out
+
+
+def gqa_attention_decode(qkv, k_cache, v_cache, n_heads: int, n_kv: int, head_dim: int, pos: int) -> np.ndarray:
+    """Attention::forward_one's cache append and attend (llm.rs:285-358) for one
+    RoPE'd q|k|v row; the caches ([capacity, n_kv*head_dim]) are updated in place."""
+    out = np.zeros(n_heads * head_dim, np.float32)
+    rc = lib().fo_gqa_attention_decode(_f32(qkv), k_cache, v_cache, k_cache.shape[0], n_heads, n_kv, head_dim, pos,
+                                       out)
+    if rc != 0:
+        raise ValueError(f"gqa_attention_decode: status {rc}")
+    return out
+
+
+def swiglu(g, u) -> np.ndarray:
+    """(g / (1 + exp(-g))) * u (llm.rs:415-421)."""
+    g, u = _f32(g), _f32(u)
+    out = np.zeros_like(g)
+    lib().fo_swiglu(g.ravel(), u.ravel(), g.size, out.ravel())
     return out
 
 

@@ -1,0 +1,72 @@
+"""Small random Llama / Qwen2 models for the batched decode tests, and their
+decode on the CPU oracle, composed the way LlamaModel::forward_one walks the
+model (llm.rs:606-616) with LlamaBlock::forward_one (llm.rs:445-456) and
+Attention::forward_one (llm.rs:345-358): separate q, k, v, gate and up linears,
+as the reference holds them."""
+import numpy as np
+
+# Qwen2-shaped: NEOX rope, q/k/v biases, tied head (gguf/llama.rs:181-185, 250-262, 301-306)
+QWEN = dict(vocab=512, d=128, n_heads=4, n_kv=2, head_dim=32, layers=2, ffn=256, context=48, rope_type=1,
+            rope_base=1e6, eps=1e-6)
+# Llama-shaped: NORM rope on 8 of 16 channels, no biases, its own output.weight
+LLAMA = dict(vocab=384, d=96, n_heads=6, n_kv=2, head_dim=16, layers=2, ffn=160, context=40, rope_type=0,
+             rope_base=10000.0, eps=1e-5, rope_dim=8)
+
+
+def make_weights(orc, cfg, seed, biases, tied):
+    rng = np.random.default_rng(seed)
+    d, qd, kvd, ffn = cfg["d"], cfg["n_heads"] * cfg["head_dim"], cfg["n_kv"] * cfg["head_dim"], cfg["ffn"]
+
+    def q8(n, k, scale):
+        return orc.q8_0_encode((rng.standard_normal(n * k) * scale).astype(np.float32))
+
+    def vec(n, scale, base=0.0):
+        return (base + rng.standard_normal(n) * scale).astype(np.float32)
+
+    w = {"token_embd": q8(cfg["vocab"], d, 0.5), "output_norm": vec(d, 0.1, 1.0)}
+    if not tied:
+        w["output"] = q8(cfg["vocab"], d, 0.1)
+    for i in range(cfg["layers"]):
+        p = f"blk.{i}."
+        w.update({p + "attn_norm": vec(d, 0.1, 1.0), p + "ffn_norm": vec(d, 0.1, 1.0),
+                  p + "attn_q": q8(qd, d, 0.12), p + "attn_k": q8(kvd, d, 0.12), p + "attn_v": q8(kvd, d, 0.12),
+                  p + "attn_output": q8(d, qd, 0.08), p + "ffn_gate": q8(ffn, d, 0.1), p + "ffn_up": q8(ffn, d, 0.1),
+                  p + "ffn_down": q8(d, ffn, 0.06)})
+        if biases:
+            w.update({p + "attn_q.bias": vec(qd, 0.05), p + "attn_k.bias": vec(kvd, 0.05),
+                      p + "attn_v.bias": vec(kvd, 0.05)})
+    return w
+
+
+class OracleLlamaRow:
+    """One sequence decoded on the oracle; its caches start zeroed, like the
+    device's, so a row may start at any position."""
+
+    def __init__(self, orc, w, cfg, pos0=0):
+        self.orc, self.w, self.c = orc, w, cfg
+        kvd = cfg["n_kv"] * cfg["head_dim"]
+        self.tok_w = orc.q8_0_dequant(w["token_embd"], cfg["vocab"] * cfg["d"]).reshape(cfg["vocab"], cfg["d"])
+        self.k = [np.zeros((cfg["context"], kvd), np.float32) for _ in range(cfg["layers"])]
+        self.v = [np.zeros((cfg["context"], kvd), np.float32) for _ in range(cfg["layers"])]
+        self.pos = pos0
+
+    def feed(self, token):
+        orc, w, c = self.orc, self.w, self.c
+        d, nh, nkv, hd = c["d"], c["n_heads"], c["n_kv"], c["head_dim"]
+        rd, base, rt, eps = c.get("rope_dim", hd), c["rope_base"], c["rope_type"], c["eps"]
+        lin = lambda x, name, n: orc.q8_0_linear(x[None, :], w[name], n, w.get(name + ".bias"))[0]  # noqa: E731
+        x = self.tok_w[int(token)].copy()
+        for i in range(c["layers"]):
+            p = f"blk.{i}."
+            h = orc.rmsnorm(x, w[p + "attn_norm"], eps)
+            q = orc.rope(lin(h, p + "attn_q", nh * hd), nh, hd, rd, self.pos, base, rt)
+            k = orc.rope(lin(h, p + "attn_k", nkv * hd), nkv, hd, rd, self.pos, base, rt)
+            v = lin(h, p + "attn_v", nkv * hd)
+            att = orc.gqa_attention_decode(np.concatenate([q, k, v]), self.k[i], self.v[i], nh, nkv, hd, self.pos)
+            x = (x + lin(att, p + "attn_output", d)).astype(np.float32)
+            h = orc.rmsnorm(x, w[p + "ffn_norm"], eps)
+            m = orc.swiglu(lin(h, p + "ffn_gate", c["ffn"]), lin(h, p + "ffn_up", c["ffn"]))
+            x = (x + lin(m, p + "ffn_down", d)).astype(np.float32)
+        self.pos += 1
+        h = orc.rmsnorm(x, w["output_norm"], eps)
+        return orc.q8_0_linear(h[None, :], w.get("output", w["token_embd"]), c["vocab"], None)[0]

@@ -1,0 +1,249 @@
+"""The Llama / Qwen block pieces on the GPU against the oracle: RmsNorm (with
+the residual add), RoPE (NORM / NEOX, partial rotary, frequency factors,
+linear scaling, a position per row), grouped-query attention over per-row KV
+caches, SwiGLU, the row embedding, and a whole batched decode of tiny
+Qwen2- and Llama-shaped models (ferrum_core llm.rs)."""
+import numpy as np
+import pytest
+
+import llama_tiny
+
+pytestmark = pytest.mark.gpu
+
+
+def dev(a, dtype=None):
+    import torch
+
+    t = torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    return t if dtype is None else t.to(dtype)
+
+
+def host(fh, t):
+    import torch
+
+    fh.sync()
+    torch.cuda.synchronize()
+    return t.cpu().numpy()
+
+
+def ready():
+    import torch
+
+    torch.cuda.synchronize()
+
+
+def close(got, want, rtol):
+    want = np.asarray(want, np.float64)
+    err = np.abs(np.asarray(got, np.float64) - want)
+    assert np.all(err <= rtol * np.maximum(1.0, np.abs(want))), float(err.max())
+
+
+@pytest.mark.parametrize("rows,d,res", [(1, 896, False), (64, 896, True), (3, 4096, True), (2, 100, False)])
+def test_rmsnorm_matches_oracle(fh, orc, rows, d, res):
+    import torch
+
+    import ferrum_hip
+
+    rng = np.random.default_rng(rows + d)
+    x = (rng.standard_normal((rows, d)) * rng.choice([1e-3, 1.0, 40.0], (rows, 1))).astype(np.float32)
+    r = rng.standard_normal((rows, d)).astype(np.float32)
+    w = rng.standard_normal(d).astype(np.float32)
+    tx, tr, tw = dev(x), dev(r), dev(w)
+    ts, out = dev(np.full((rows, d), np.nan, np.float32)), torch.empty((rows, d), device="cuda")
+    ready()
+    ferrum_hip.rmsnorm_async(fh, tx, tr if res else None, ts if res else None, rows, d, tw, 1e-6, out)
+    h = (x + r).astype(np.float32) if res else x
+    if res:
+        assert np.array_equal(host(fh, ts), h)
+    close(host(fh, out), orc.rmsnorm(h, w, 1e-6), 1e-5)
+
+
+@pytest.mark.parametrize("rt", [0, 1])
+@pytest.mark.parametrize("hd,rope_dim,ff,lf", [(64, 64, False, 1.0), (32, 16, False, 1.0), (16, 16, True, 1.0),
+                                               (64, 64, False, 4.0)])
+def test_rope_matches_oracle(fh, orc, rt, hd, rope_dim, ff, lf):
+    import ferrum_hip
+
+    rows, nh, ld = 3, 6, 6 * hd + 40  # rows of a wider q|k|v buffer
+    rng = np.random.default_rng(hd * 7 + rope_dim + rt)
+    x = (rng.standard_normal((rows, ld)) * 2).astype(np.float32)
+    pos = np.array([0, 17, 1000], np.uint32)
+    fac = (rng.uniform(0.5, 8.0, rope_dim // 2)).astype(np.float32) if ff else None
+    tx = dev(x)
+    ready()
+    ferrum_hip.rope_async(fh, tx, rows, ld, nh, hd, rope_dim, dev(pos.view(np.int32)), 1e4, rt,
+                          None if fac is None else dev(fac), lf)
+    got = host(fh, tx)
+    for r in range(rows):
+        want = orc.rope(x[r, :nh * hd], nh, hd, rope_dim, int(pos[r]), 1e4, rt, fac, lf)
+        np.testing.assert_allclose(got[r, :nh * hd], want, rtol=0, atol=2e-6 * 4)
+        assert np.array_equal(got[r, nh * hd:], x[r, nh * hd:])  # past the heads: untouched
+
+
+def test_rope_errors(fh):
+    import ferrum_hip
+
+    x, p = dev(np.zeros(64, np.float32)), dev(np.zeros(1, np.int32))
+    ready()
+    with pytest.raises(ferrum_hip.DimMismatch, match="must be even"):
+        ferrum_hip.rope_async(fh, x, 1, 64, 2, 32, 7, p, 1e4, 0)
+    with pytest.raises(ferrum_hip.DimMismatch, match="must be even"):
+        ferrum_hip.rope_async(fh, x, 1, 64, 2, 32, 34, p, 1e4, 0)
+    with pytest.raises(ferrum_hip.DimMismatch, match="finite and > 0"):
+        ferrum_hip.rope_async(fh, x, 1, 64, 2, 32, 32, p, 1e4, 0, None, 0.0)
+    with pytest.raises(ferrum_hip.FerrumHipError, match="rope_type"):
+        ferrum_hip.rope_async(fh, x, 1, 64, 2, 32, 32, p, 1e4, 2)
+
+
+@pytest.mark.parametrize("nh,nkv,hd,T", [(14, 2, 64, 140), (4, 4, 32, 40), (8, 1, 128, 300), (6, 2, 16, 70)])
+def test_gqa_attention_matches_oracle(fh, orc, nh, nkv, hd, T):
+    """Three sequences at different positions (starting at 0, 60 and 129 with
+    zeroed caches), every step checked against the oracle."""
+    import torch
+
+    import ferrum_hip
+
+    rows, cap = 3, T + 140
+    qd, kvd = nh * hd, nkv * hd
+    ld = qd + 2 * kvd
+    start = [0, 60, 129]
+    rng = np.random.default_rng(nh * T + hd)
+    kc, vc = torch.zeros(rows * cap * kvd, device="cuda"), torch.zeros(rows * cap * kvd, device="cuda")
+    ko = [np.zeros((cap, kvd), np.float32) for _ in range(rows)]
+    vo = [np.zeros((cap, kvd), np.float32) for _ in range(rows)]
+    out = torch.empty((rows, qd), device="cuda")
+    for t in range(T):
+        qkv = (rng.standard_normal((rows, ld)) * 1.5).astype(np.float32)
+        pos = np.array([s + t for s in start], np.uint32)
+        ready()
+        ferrum_hip.gqa_attention_decode_async(fh, dev(qkv), ld, rows, nh, nkv, hd, kc, vc, cap,
+                                              dev(pos.view(np.int32)), int(pos.max()), out)
+        got = host(fh, out)
+        for r in range(rows):
+            close(got[r], orc.gqa_attention_decode(qkv[r], ko[r], vo[r], nh, nkv, hd, int(pos[r])), 1e-5)
+    kh, vh = host(fh, kc).reshape(rows, cap, kvd), host(fh, vc).reshape(rows, cap, kvd)
+    for r in range(rows):
+        assert np.array_equal(kh[r], ko[r]) and np.array_equal(vh[r], vo[r])
+
+
+def test_gqa_attention_bad_positions_give_nan_and_leave_the_cache(fh, orc):
+    import torch
+
+    import ferrum_hip
+
+    rows, nh, nkv, hd, cap = 3, 4, 2, 32, 100
+    qd, kvd = nh * hd, nkv * hd
+    ld = qd + 2 * kvd
+    qkv = np.random.default_rng(1).standard_normal((rows, ld)).astype(np.float32)
+    kc, vc = torch.zeros(rows * cap * kvd, device="cuda"), torch.zeros(rows * cap * kvd, device="cuda")
+    out = torch.empty((rows, qd), device="cuda")
+    pos = np.array([5, 100, 70], np.uint32)  # fine, at capacity, above max_pos
+    ready()
+    ferrum_hip.gqa_attention_decode_async(fh, dev(qkv), ld, rows, nh, nkv, hd, kc, vc, cap, dev(pos.view(np.int32)),
+                                          40, out)
+    got = host(fh, out)
+    ko, vo = np.zeros((cap, kvd), np.float32), np.zeros((cap, kvd), np.float32)
+    close(got[0], orc.gqa_attention_decode(qkv[0], ko, vo, nh, nkv, hd, 5), 1e-5)
+    assert np.isnan(got[1]).all() and np.isnan(got[2]).all()
+    kh = host(fh, kc).reshape(rows, cap, kvd)
+    assert not kh[1].any() and not kh[2].any()
+    with pytest.raises(ferrum_hip.DimMismatch, match="multiple of n_kv_heads"):
+        ferrum_hip.gqa_attention_decode_async(fh, dev(qkv), ld, rows, 3, 2, hd, kc, vc, cap, dev(pos.view(np.int32)),
+                                              40, out)
+
+
+@pytest.mark.parametrize("rows,n,ld", [(1, 4864, 4864), (64, 4864, 9728), (3, 100, 256)])
+def test_swiglu_matches_oracle(fh, orc, rows, n, ld):
+    import torch
+
+    import ferrum_hip
+
+    rng = np.random.default_rng(n + rows)
+    g = (rng.standard_normal((rows, ld)) * 4).astype(np.float32)
+    u = rng.standard_normal((rows, ld)).astype(np.float32)
+    out = torch.empty((rows, n), device="cuda")
+    ready()
+    ferrum_hip.swiglu_async(fh, dev(g), dev(u), rows, n, ld, out)
+    close(host(fh, out), orc.swiglu(g[:, :n], u[:, :n]), 1e-5)
+
+
+def test_embed_rows_copies_rows_and_poisons_bad_ids(fh):
+    import torch
+
+    import ferrum_hip
+
+    tw = np.random.default_rng(2).standard_normal((50, 24)).astype(np.float32)
+    toks = np.array([3, 49, 50, 0], np.uint32)
+    out = torch.empty((4, 24), device="cuda")
+    ready()
+    ferrum_hip.embed_rows_async(fh, dev(tw), 50, 24, dev(toks.view(np.int32)), 4, out)
+    got = host(fh, out)
+    assert np.array_equal(got[[0, 1, 3]], tw[[3, 49, 0]]) and np.isnan(got[2]).all()
+
+
+@pytest.mark.parametrize("name,biases,tied", [("QWEN", True, True), ("LLAMA", False, False)])
+def test_tiny_model_batched_decode_matches_the_oracle(fh, orc, name, biases, tied):
+    """Three sequences starting at positions 0, 5 and 11 (zeroed caches), 14
+    teacher-forced steps: every row's scores at every step against the oracle."""
+    import ferrum_hip
+
+    cfg = getattr(llama_tiny, name)
+    w = llama_tiny.make_weights(orc, cfg, 21, biases, tied)
+    rows, start = 3, [0, 5, 11]
+    m = ferrum_hip.LlamaDevice.from_weights(fh, w, cfg, rows)
+    refs = [llama_tiny.OracleLlamaRow(orc, w, cfg, s) for s in start]
+    toks = np.random.default_rng(5).integers(0, cfg["vocab"], (14, rows))
+    try:
+        for t in range(14):
+            m.tokens.copy_(dev(toks[t].astype(np.int32)))
+            m.pos.copy_(dev(np.array([s + t for s in start], np.int32)))
+            ready()
+            m.feed_async(start[-1] + t)
+            got = host(fh, m.z)
+            for r in range(rows):
+                want = refs[r].feed(toks[t, r])
+                close(got[r], want, 2e-5 * max(1.0, float(np.abs(want).max())))
+    finally:
+        m.free()
+
+
+def test_tiny_qwen_greedy_batch_runs_on_the_device(fh, orc):
+    """A batch of 4 greedy decodes with the token and position fed back on the
+    device (sampler -> tokens, pos + 1) replays on the oracle: each id is the
+    oracle's argmax unless its top-2 gap is below 1e-5."""
+    import torch
+
+    import ferrum_hip
+
+    cfg = llama_tiny.QWEN
+    w = llama_tiny.make_weights(orc, cfg, 23, True, True)
+    rows = 4
+    m = ferrum_hip.LlamaDevice.from_weights(fh, w, cfg, rows)
+    refs = [llama_tiny.OracleLlamaRow(orc, w, cfg, 0) for _ in range(rows)]
+    first = np.random.default_rng(9).integers(0, cfg["vocab"], rows)
+    m.tokens.copy_(dev(first.astype(np.int32)))
+    off = dev(np.zeros(rows + 1, np.int32))
+    greedy = ferrum_hip.SamplingParams(temperature=0.0)
+    out = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    want_tok = [int(t) for t in first]
+    live = [True] * rows
+    try:
+        for t in range(20):
+            ready()
+            m.feed_async(t)
+            ferrum_hip.sample_rows_async(fh, m.z, rows, cfg["vocab"], greedy, None, off, None, out)
+            got = host(fh, out).astype(np.int64)
+            for r in range(rows):
+                if not live[r]:
+                    continue
+                z = refs[r].feed(want_tok[r])
+                want = int(np.argmax(z))
+                if want != got[r]:
+                    top2 = np.sort(z)[-2:]
+                    assert top2[1] - top2[0] < 1e-5, (t, r, int(got[r]), want)
+                    live[r] = False
+                want_tok[r] = want
+            m.tokens.copy_(out)
+            m.pos.add_(1)
+    finally:
+        m.free()
