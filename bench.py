@@ -97,7 +97,7 @@ def main():
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--leg", choices=["all", "head", "prefill"], default="all",
+    ap.add_argument("--leg", choices=["all", "head", "prefill", "qwen"], default="all",
                     help="'head': only the lm_head GEMV roofline leg (for counter runs); "
                          "'prefill': only the GPT-2-medium prefill GEMMs")
     ap.add_argument("--prefill-steps", type=int, default=3)
@@ -281,6 +281,12 @@ def main():
         print(json.dumps({"leg": "prefill", "prefill": result["prefill"]}))
         return
 
+    if args.leg in ("all", "qwen"):
+        result["qwen2_b64"] = qwen_leg(ctx, fh, torch, gen, dev, max(args.steps // 20, 10), args.warmup)
+    if args.leg == "qwen":
+        print(json.dumps({"leg": "qwen", "qwen2_b64": result["qwen2_b64"]}))
+        return
+
     # ---- roofline leg: lm_head GEMV, back-to-back, HBM-forced ----------------------
     n_head_rep = 32  # 32 x 41 MB = 1.3 GB, five times the MALL
     heads = [make_weight(ctx, fh, torch, V, D, gen) for _ in range(n_head_rep)]
@@ -384,6 +390,7 @@ def main():
         "full_decode_step": result["full_step"],
         "b32": result["b32"],
         "prefill": result["prefill"],
+        "qwen2_b64": result.get("qwen2_b64"),
         "hbm_copy_GBps": round(copy_GBps, 1) if copy_GBps else None,
         "shard_head_gemv": result["shard_head"],
     }
@@ -458,6 +465,88 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
             "w8a8_int8_mfma": {"ms": round(ms8, 3), "tops": round(tops8, 1),
                                "frac_i8_dense_peak": round(tops8 / I8_DENSE_TOPS, 4),
                                "numerics": "W8A8 (activations re-quantised to Q8_0), bit-exact with the reference"}}
+
+
+QWEN05 = dict(vocab=151936, d=896, n_heads=14, n_kv=2, head_dim=64, layers=24, ffn=4864, context=512,
+              rope_type=1, rope_base=1e6, eps=1e-6)
+QWEN_B, QWEN_POS, QWEN_HIST = 64, 255, 1024
+
+
+def qwen_leg(ctx, fh, torch, gen, dev, steps, warmup):
+    """Config 5: a Qwen2-0.5B-shaped decode step for 64 sequences on the
+    device (embed, 24 x [RmsNorm, q|k|v Q8_0 linear, RoPE NEOX, GQA attention
+    at position 255, output projection, residual + RmsNorm, gate|up Q8_0
+    linear, SwiGLU, down], final RmsNorm, tied 151936 x 896 head) and the fused
+    sampler on its [64 x 151936] scores (top-k 50, top-p 0.9, repetition
+    penalty 1.05 over a 1024-token history per row); and the sampler alone on
+    the configuration's logits, N(0, 3) plus 5 planted peaks (+12)."""
+    import numpy as np
+
+    B, V = QWEN_B, QWEN05["vocab"]
+    rng = np.random.default_rng(55)
+    peaks = rng.choice(V, 5, replace=False)
+    # histories: 1024 ids per row, repeats included (multiplicity matters)
+    hist = np.concatenate([rng.integers(0, V, QWEN_HIST - 24), np.repeat(peaks[:3], 8)])
+    rec = torch.from_numpy(np.concatenate([rng.permutation(hist) for _ in range(B)]).astype(np.uint32)).to(dev)
+    off = torch.arange(0, (B + 1) * QWEN_HIST, QWEN_HIST, dtype=torch.int32, device=dev)
+    draws = torch.from_numpy(rng.integers(0, 2**63, size=B, dtype=np.int64)).to(dev)
+    out = torch.zeros(B, dtype=torch.int32, device=dev)
+    params = fh.SamplingParams(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.05)
+
+    def timed(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+            fn()
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        for _ in range(max(warmup // 10, 2)):
+            g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        del g
+        return e0.elapsed_time(e1) / n
+
+    logits = torch.randn((B, V), generator=gen, device=dev) * 3.0
+    logits[:, torch.from_numpy(peaks).to(dev)] += 12.0
+    sampler_ms = timed(lambda: fh.sample_rows_async(ctx, logits, B, V, params, rec, off, draws, out), steps * 4)
+    del logits
+
+    m = fh.LlamaDevice.random(ctx, QWEN05, B, gen)
+    m.tokens.copy_(torch.from_numpy(rng.integers(0, V, B).astype(np.int32)).to(dev))
+    m.pos.fill_(QWEN_POS)
+
+    def step():
+        m.feed_async(QWEN_POS)
+        fh.sample_rows_async(ctx, m.z, B, V, params, rec, off, draws, m.tokens)
+
+    ms = timed(step, steps)
+    c = QWEN05
+    qkv = c["n_heads"] * c["head_dim"] + 2 * c["n_kv"] * c["head_dim"]
+    per_layer = [(qkv, c["d"]), (c["d"], c["n_heads"] * c["head_dim"]), (2 * c["ffn"], c["d"]), (c["d"], c["ffn"])]
+    wbytes = sum(q8_bytes(n, k) for n, k in per_layer) * c["layers"] + q8_bytes(V, c["d"])
+    flops = 2.0 * B * (sum(n * k for n, k in per_layer) * c["layers"] + V * c["d"])
+    kv_bytes = 2 * c["layers"] * B * (QWEN_POS + 1) * c["n_kv"] * c["head_dim"] * 4
+    launches = m.launches_per_step() + 1
+    m.free()
+    del m
+    torch.cuda.synchronize()
+    gbps = (wbytes + kv_bytes) / (ms * 1e-3) / 1e9
+    return {"workload": "qwen2-0.5b-shaped Q8_0 decode step, batch 64, position 255, tied head, fused sampler",
+            "tok_s": round(B * 1000.0 / ms, 1), "ms_per_step": round(ms, 4), "launches_per_step": launches,
+            "weight_bytes": wbytes, "kv_cache_bytes_read": kv_bytes, "gemm_gflop": round(flops / 1e9, 1),
+            "hbm_GBps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4),
+            "sampler_only": {"rows": B, "vocab": V, "us_per_step": round(sampler_ms * 1e3, 2),
+                             "us_per_row": round(sampler_ms * 1e3 / B, 3),
+                             "logits": "N(0,3) + 5 planted peaks (+12)", "history": QWEN_HIST,
+                             "params": {"temperature": 0.8, "top_k": 50, "top_p": 0.9, "repetition_penalty": 1.05}},
+            "data": "synthetic (random-init N(0,0.02) Q8_0 weights generated on the GPU)"}
 
 
 def cpu_baseline(budget_s):

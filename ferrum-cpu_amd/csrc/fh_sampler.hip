@@ -20,8 +20,9 @@
 // vocabularies keep the row in a per-row global buffer (L2-resident) and each
 // pass streams it with eight loads in flight per thread.
 //
-// Steps 4-6.  A 64-bucket histogram of the top 12 bits of p (8 buckets per
-// octave, the 8 octaves under the largest p) finds the bucket where the top-k
+// Steps 4-6.  A 64-bucket histogram of p under the largest p (from the top 12
+// bits: 8 buckets per octave for 5 octaves, then 2, then 1 per octave; 21
+// octaves in all) finds the bucket where the top-k
 // count or the top-p mass is reached; every element at or above it (at most
 // kCap) is gathered into LDS, sorted by (p descending, index ascending) with a
 // bitonic sort, and one wave replays steps 4-6 in the reference's own order —
@@ -46,7 +47,7 @@ namespace {
 constexpr int kT = 1024;        // threads per row
 constexpr int kW = kT / 64;     // waves per row
 constexpr int kCap = 4096;      // LDS survivor capacity
-constexpr int kBuckets = 64;    // 8 octaves x 8 sub-buckets under the max p
+constexpr int kBuckets = 64;    // histogram buckets under the max p (bucket_of)
 constexpr int kCopies = 16;     // histogram copies (lane & 15) against same-bin conflicts
 constexpr int kSlots = 8192;    // repetition-penalty hash table
 constexpr int kChunk = 4096;    // recent ids deduplicated per table fill
@@ -320,6 +321,15 @@ __device__ __forceinline__ int key_i(unsigned long long k) {
 // 12-bit bucket key of a non-negative float: 8 exponent bits and the top 3
 // mantissa bits (8 buckets per octave).
 __device__ __forceinline__ int key12(float p) { return static_cast<int>(__builtin_bit_cast(uint32_t, p) >> 20); }
+
+// Histogram bucket of p under the largest p (ktop = key12(pmax)), coarser with
+// depth: 8 buckets per octave for the first 5 octaves, 2 per octave for the
+// next 8, one per octave for the next 8 (21 octaves; kBuckets past them).
+// Monotone in p, so "bucket <= depth" gathers every id at or above a bucket.
+__device__ __forceinline__ int bucket_of(int ktop, float p) {
+    const int d = ktop - key12(p);
+    return d < 40 ? d : d < 104 ? 40 + ((d - 40) >> 2) : d < 168 ? 56 + ((d - 104) >> 3) : kBuckets;
+}
 
 // Fixed-point image of a probability, for order-independent mass sums.
 __device__ __forceinline__ unsigned long long fix40(float p) {
@@ -951,7 +961,7 @@ __device__ __forceinline__ void sample_row(Shared& s, Row& row, const Params& P,
         }
         __syncthreads();
         row.visit([&](float p, int) {
-            const int b = ktop - key12(p);
+            const int b = bucket_of(ktop, p);
             if (p > 0.0f && b < kBuckets) {
                 atomicAdd(&s.hist[copy][b], 1u);
                 if (!use_k) atomicAdd(&s.mass[copy][b], fix40(p));
@@ -977,7 +987,7 @@ __device__ __forceinline__ void sample_row(Shared& s, Row& row, const Params& P,
         const int depth = s.bi[0];
         int n_list = -1;
         if (depth >= 0) {
-            row.visit([&](float p, int i) { append(s, p > 0.0f && ktop - key12(p) <= depth, cand_key(p, i)); });
+            row.visit([&](float p, int i) { append(s, p > 0.0f && bucket_of(ktop, p) <= depth, cand_key(p, i)); });
             __syncthreads();
             const int nc = static_cast<int>(s.n_cand);
             if (nc <= 64) {
@@ -1347,7 +1357,7 @@ __global__ void __launch_bounds__(kT)
         }
         __syncthreads();
         st.visit([&](float p, int) {
-            const int b = ktop - key12(p);
+            const int b = bucket_of(ktop, p);
             if (p > 0.0f && b < kBuckets) {
                 atomicAdd(&s.hist[copy][b], 1u);
                 if (!use_k) atomicAdd(&s.mass[copy][b], fix40(p));
@@ -1393,7 +1403,7 @@ __global__ void __launch_bounds__(kT)
         if (depth >= 0) {
             // append this segment's survivors to the row's list, one atomic per wave
             st.visit([&](float p, int i) {
-                const bool take = p > 0.0f && ktop - key12(p) <= depth;
+                const bool take = p > 0.0f && bucket_of(ktop, p) <= depth;
                 const unsigned long long mask = __ballot(take);
                 if (mask == 0) return;
                 const int lane = lane_id();
@@ -1516,31 +1526,54 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
     P.pen = p->repetition_penalty;
     P.kind = kind;
     P.n = static_cast<int>(vocab);
-    // Split rows over S workgroups while rows * S fits one workgroup per CU
-    // (the kernel's LDS allows one per CU, so all of a row's workgroups are
-    // resident together): the fewest ids per thread that fits, for rows of at
-    // least 8192 ids.
+    // Split rows over S workgroups while a launch's rows * S fit one
+    // workgroup per CU (the kernel's LDS allows one per CU, so all workgroups
+    // of a launch are resident together and their exchanges cannot wait on an
+    // undispatched one): for rows of at least 8192 ids, the fewest ids per
+    // thread that fits all rows in one launch; when none does, consecutive
+    // launches of as many rows as fit (fewest launches, at most 8), each row
+    // keeping its own exchange slots.
     const size_t items = (vocab + kT - 1) / kT;
-    if (vocab >= 8192 && rows <= 128) {
+    if (vocab >= 8192 && rows <= 1024) {
         static const int kOpts[] = {2, 4, 8, 16, 32};
+        const size_t cus = static_cast<size_t>(ctx->num_cus);
+        int pick = 0;
+        size_t pick_rows = 0, pick_launches = 9;
         for (int it : kOpts) {
             const size_t S = (vocab + static_cast<size_t>(kT) * it - 1) / (static_cast<size_t>(kT) * it);
-            if (S < 2 || rows * S > static_cast<size_t>(ctx->num_cus) || S > static_cast<size_t>(kSMax)) continue;
+            if (S < 2 || S > static_cast<size_t>(kSMax) || S > cus) continue;
+            const size_t per = cus / S, launches = (rows + per - 1) / per;
+            if (launches < pick_launches) {
+                pick = it, pick_rows = per, pick_launches = launches;
+                if (launches == 1) break;
+            }
+        }
+        if (pick) {
+            const size_t S = (vocab + static_cast<size_t>(kT) * pick - 1) / (static_cast<size_t>(kT) * pick);
             void* sync = nullptr;
             int rc = fh_sync_area(ctx, rows * sizeof(RowSync), &sync);
             if (rc) return rc;
             void* ws = nullptr;
             rc = fh_workspace(ctx, rows * vocab * sizeof(float), &ws);
             if (rc) return rc;
-            float* pbuf = static_cast<float*>(ws);
             const int s32 = static_cast<int>(S);
-            switch (it) {
-                case 2: return launch_split<2>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
-                case 4: return launch_split<4>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
-                case 8: return launch_split<8>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
-                case 16: return launch_split<16>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
-                default: return launch_split<32>(ctx, rows, s32, logits, P, recent, offsets, draws, out, sync, pbuf);
+            for (size_t r0 = 0; r0 < rows; r0 += pick_rows) {
+                const size_t nr = rows - r0 < pick_rows ? rows - r0 : pick_rows;
+                const float* lg = logits + r0 * vocab;
+                const uint32_t* of = offsets ? offsets + r0 : nullptr;
+                const uint64_t* dr = draws ? draws + r0 : nullptr;
+                void* sy = static_cast<RowSync*>(sync) + r0;
+                float* pb = static_cast<float*>(ws) + r0 * vocab;
+                switch (pick) {
+                    case 2: rc = launch_split<2>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
+                    case 4: rc = launch_split<4>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
+                    case 8: rc = launch_split<8>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
+                    case 16: rc = launch_split<16>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
+                    default: rc = launch_split<32>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
+                }
+                if (rc) return rc;
             }
+            return FH_OK;
         }
     }
     if (items <= 1) return launch_regs<1>(ctx, rows, logits, P, recent, offsets, draws, out);

@@ -163,16 +163,27 @@ def test_flat_top_p_takes_the_general_path(fh, orc):
     run_and_compare(fh, orc, lg, dict(temperature=1.0, top_k=10000, top_p=0.9), max_exempt=0.1)
 
 
-def test_qwen_config5_rows(fh, orc):
+@pytest.mark.parametrize("rows", [16, 64])
+def test_qwen_config5_rows(fh, orc, rows):
     """Config 5: 151936-wide logits ~N(0,3) plus 5 planted peaks (+12), top-k 50,
-    top-p 0.9, repetition penalty 1.05 over a 1024-token random history."""
-    rows, vocab = 16, 151936
+    top-p 0.9, repetition penalty 1.05 over a 1024-token random history.  At 64
+    rows the split sampler runs as consecutive launches of the rows that fit
+    the CUs together."""
+    vocab = 151936
     rng = np.random.default_rng(55)
     lg = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
     peaks = rng.integers(0, vocab, size=5)
     lg[:, peaks] += 12.0
     rec = [list(rng.integers(0, vocab, size=1024)) + list(peaks[:2]) for _ in range(rows)]
     run_and_compare(fh, orc, lg, dict(temperature=0.8, top_k=50, top_p=0.9, repetition_penalty=1.05), rec)
+
+
+def test_many_rows_run_as_consecutive_split_launches(fh, orc):
+    """600 rows of 8192 ids: more rows than one split launch holds."""
+    lg = normal_logits(600, 8192, 31)
+    rng = np.random.default_rng(32)
+    rec = [list(rng.integers(0, 8192, size=64)) for _ in range(600)]
+    run_and_compare(fh, orc, lg, dict(temperature=0.9, top_k=40, top_p=0.95, repetition_penalty=1.1), rec)
 
 
 def test_sampler_errors(fh):
