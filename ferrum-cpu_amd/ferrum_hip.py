@@ -33,7 +33,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libferrum_hip.so")
 
-FH_OK, FH_ERR_DIM, FH_ERR_INVALID, FH_ERR_OOM, FH_ERR_HIP, FH_ERR_LIMIT = range(6)
+FH_OK, FH_ERR_DIM, FH_ERR_INVALID, FH_ERR_OOM, FH_ERR_HIP, FH_ERR_LIMIT, FH_ERR_FORMAT = range(7)
 W8A32, W8A8 = 0, 1
 LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
 
@@ -46,6 +46,9 @@ EXPORTS = (
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
     "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
+    "fh_gguf_open", "fh_gguf_close", "fh_gguf_error", "fh_gguf_version", "fh_gguf_tensor_count", "fh_gguf_find_tensor",
+    "fh_gguf_tensor_info", "fh_gguf_tensor_data", "fh_gguf_meta_type", "fh_gguf_meta_u64", "fh_gguf_meta_f64",
+    "fh_gguf_meta_str", "fh_gguf_meta_array_data", "fh_gguf_read_f32", "fh_gguf_upload_q8_0",
 )
 
 
@@ -173,6 +176,29 @@ def lib():
         L.fh_gqa_attention_decode_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, sz, vp, sz, vp]
         L.fh_swiglu_async.argtypes = [vp, vp, vp, sz, sz, sz, vp]
         L.fh_embed_rows_async.argtypes = [vp, vp, sz, sz, vp, sz, vp]
+        u32, u64 = C.c_uint32, C.c_uint64
+        L.fh_gguf_open.argtypes = [C.c_char_p, C.POINTER(vp)]
+        L.fh_gguf_close.argtypes = [vp]
+        L.fh_gguf_close.restype = None
+        L.fh_gguf_error.argtypes = [vp]
+        L.fh_gguf_error.restype = C.c_char_p
+        L.fh_gguf_version.argtypes = [vp]
+        L.fh_gguf_version.restype = u32
+        L.fh_gguf_tensor_count.argtypes = [vp]
+        L.fh_gguf_tensor_count.restype = sz
+        L.fh_gguf_find_tensor.argtypes = [vp, C.c_char_p]
+        L.fh_gguf_find_tensor.restype = C.c_long
+        L.fh_gguf_tensor_info.argtypes = [vp, sz, C.POINTER(C.c_char_p), C.POINTER(u32), C.POINTER(u64),
+                                          C.POINTER(u32), C.POINTER(u64)]
+        L.fh_gguf_tensor_data.argtypes = [vp, sz]
+        L.fh_gguf_tensor_data.restype = vp
+        L.fh_gguf_meta_type.argtypes = [vp, C.c_char_p, C.POINTER(u32), C.POINTER(u32), C.POINTER(u64)]
+        L.fh_gguf_meta_u64.argtypes = [vp, C.c_char_p, C.POINTER(u64)]
+        L.fh_gguf_meta_f64.argtypes = [vp, C.c_char_p, C.POINTER(C.c_double)]
+        L.fh_gguf_meta_str.argtypes = [vp, C.c_char_p, sz, C.POINTER(C.c_char_p), C.POINTER(sz)]
+        L.fh_gguf_meta_array_data.argtypes = [vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)]
+        L.fh_gguf_read_f32.argtypes = [vp, vp, C.c_char_p, vp, sz]
+        L.fh_gguf_upload_q8_0.argtypes = [vp, vp, C.c_char_p, C.POINTER(vp)]
         _lib = L
     return _lib
 
@@ -496,6 +522,111 @@ def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d
                                               pos, _ptr(out)))
 
 
+# ---- GGUF files (the library's native reader) ----------------------------------
+
+class GGUFFormatError(FerrumHipError):
+    """A malformed GGUF file (ferrum_core's InferError::Format)."""
+
+
+class GGUFFile:
+    """A GGUF file opened by the library's reader (memory-mapped; Gguf::open,
+    gguf/mod.rs:208-310).  Tensors: name -> (dims in GGML order, GGML type,
+    byte count); metadata through meta(); Q8_0 tensors go straight to the
+    device with upload_q8_0."""
+
+    def __init__(self, path):
+        h = C.c_void_p()
+        rc = lib().fh_gguf_open(os.fsencode(path), C.byref(h))
+        if rc != FH_OK:
+            msg = lib().fh_gguf_error(h).decode(errors="replace")
+            lib().fh_gguf_close(h)
+            raise (GGUFFormatError if rc == FH_ERR_FORMAT else FerrumHipError)(rc, msg)
+        self.h = h
+        self.version = lib().fh_gguf_version(h)
+        self.tensors = {}
+        for i in range(lib().fh_gguf_tensor_count(h)):
+            name, nd, ty, nb = C.c_char_p(), C.c_uint32(), C.c_uint32(), C.c_uint64()
+            dims = (C.c_uint64 * 8)()
+            lib().fh_gguf_tensor_info(h, i, C.byref(name), C.byref(nd), dims, C.byref(ty), C.byref(nb))
+            key = name.value.decode(errors="replace")
+            self.tensors.setdefault(key, (tuple(dims[:nd.value]), ty.value, nb.value, i))
+
+    def close(self):
+        if self.h:
+            lib().fh_gguf_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def meta(self, key: str):
+        """The value of a metadata key (int, float, str, or list), None if absent."""
+        k = key.encode()
+        ty, el, cnt = C.c_uint32(), C.c_uint32(), C.c_uint64()
+        if lib().fh_gguf_meta_type(self.h, k, C.byref(ty), C.byref(el), C.byref(cnt)) != FH_OK:
+            return None
+        ty, el, cnt = ty.value, el.value, cnt.value
+        if ty == 8:  # string
+            out, n = C.c_char_p(), C.c_size_t()
+            lib().fh_gguf_meta_str(self.h, k, 0, C.byref(out), C.byref(n))
+            return C.string_at(out, n.value).decode(errors="replace")
+        if ty == 9:  # array
+            if el == 8:
+                vals = []
+                for i in range(cnt):
+                    out, n = C.c_char_p(), C.c_size_t()
+                    lib().fh_gguf_meta_str(self.h, k, i, C.byref(out), C.byref(n))
+                    vals.append(C.string_at(out, n.value).decode(errors="replace"))
+                return vals
+            data, es = C.c_void_p(), C.c_size_t()
+            lib().fh_gguf_meta_array_data(self.h, k, C.byref(data), C.byref(es))
+            dt = {0: "<u1", 1: "<i1", 2: "<u2", 3: "<i2", 4: "<u4", 5: "<i4", 6: "<f4", 7: "<u1", 10: "<u8",
+                  11: "<i8", 12: "<f8"}[el]
+            if cnt == 0:
+                return []
+            return list(np.frombuffer(C.string_at(data, cnt * es.value), dtype=dt))
+        if ty in (6, 12):
+            v = C.c_double()
+            lib().fh_gguf_meta_f64(self.h, k, C.byref(v))
+            return v.value
+        if ty in (1, 3, 5, 11):  # signed
+            v = C.c_double()
+            lib().fh_gguf_meta_f64(self.h, k, C.byref(v))
+            return int(v.value)
+        v = C.c_uint64()
+        lib().fh_gguf_meta_u64(self.h, k, C.byref(v))
+        return v.value
+
+    def raw(self, name: str) -> bytes:
+        """The tensor's bytes (a copy)."""
+        dims, ty, nb, i = self.tensors[name]
+        return C.string_at(lib().fh_gguf_tensor_data(self.h, i), nb)
+
+    def read_f32(self, ctx, name: str) -> np.ndarray:
+        """An F32 / F16 tensor as float32 (numpy, GGML order reversed: [ne1, ne0]).
+        ctx may be None (host-only; errors then carry no message)."""
+        dims = self.tensors[name][0]
+        n = int(np.prod(dims)) if dims else 1
+        out = np.empty(n, np.float32)
+        rc = lib().fh_gguf_read_f32(ctx.h if ctx else None, self.h, name.encode(), out.ctypes.data, n)
+        if ctx:
+            ctx.check(rc)
+        elif rc != FH_OK:
+            raise FerrumHipError(rc, f"fh_gguf_read_f32 '{name}' failed")
+        return out.reshape(tuple(reversed(dims))) if len(dims) > 1 else out
+
+    def upload_q8_0(self, ctx: "Context", name: str) -> "Q8_0Weight":
+        """A Q8_0 tensor [ne0 = k, ne1 = n] straight from the mapping to the device."""
+        dims = self.tensors[name][0]
+        h = C.c_void_p()
+        ctx.check(lib().fh_gguf_upload_q8_0(ctx.h, self.h, name.encode(), C.byref(h)))
+        k, n = int(dims[0]), int(dims[1]) if len(dims) > 1 else 1
+        return Q8_0Weight(ctx, h, n, k)
+
+
 # ---- Llama / Qwen block pieces (llm.rs), batched over rows --------------------
 
 ROPE_NORM, ROPE_NEOX = 0, 1
@@ -745,6 +876,43 @@ class GPT2Device:
         m.lnf_g, m.lnf_b = f(weights["lnf_g"]), f(weights["lnf_b"])
         torch.cuda.synchronize()  # uploads ran on torch's stream
         ctx.sync()
+        return m
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, path) -> "GPT2Device":
+        """A GPT-2 GGUF in GgufOut::gpt2's layout (loader/gpt2.rs:61-146, read
+        back by gpt2_from, loader/gpt2.rs:201-295): hyperparameters from the
+        gpt2.* keys, Q8_0 matrices uploaded straight from the file's mapping,
+        f32 vectors copied; the head is output.weight when present, else the
+        token table (tied)."""
+        import torch
+
+        with GGUFFile(path) as g:
+            if g.meta("general.architecture") != "gpt2":
+                raise FerrumHipError(FH_ERR_INVALID, f"{path}: general.architecture is not gpt2")
+            d, layers = g.meta("gpt2.embedding_length"), g.meta("gpt2.block_count")
+            heads, ffn, context = g.meta("gpt2.attention.head_count"), g.meta("gpt2.feed_forward_length"), \
+                g.meta("gpt2.context_length")
+            vocab = g.tensors["token_embd.weight"][0][1]
+            m = cls(ctx, vocab, d, heads, layers, ffn, context)
+            f = lambda name: torch.from_numpy(g.read_f32(ctx, name).copy()).cuda()  # noqa: E731
+            tok = torch.from_numpy(np.frombuffer(g.raw("token_embd.weight"), np.uint8).copy()).cuda()
+            m.tok_w = torch.empty((vocab, d), device="cuda")
+            torch.cuda.synchronize()
+            q8_0_dequant_async(ctx, tok, vocab * d, m.tok_w)
+            m.head = g.upload_q8_0(ctx, "output.weight" if "output.weight" in g.tensors else "token_embd.weight")
+            m.pos_w = f("position_embd.weight")
+            for i in range(layers):
+                n = lambda s: f"blk.{i}.{s}"  # noqa: E731
+                m.blocks.append(m._block([f(n("attn_norm.weight")), f(n("attn_norm.bias")), f(n("ffn_norm.weight")),
+                                          f(n("ffn_norm.bias"))],
+                                         g.upload_q8_0(ctx, n("attn_qkv.weight")), f(n("attn_qkv.bias")),
+                                         g.upload_q8_0(ctx, n("attn_output.weight")), f(n("attn_output.bias")),
+                                         g.upload_q8_0(ctx, n("ffn_up.weight")), f(n("ffn_up.bias")),
+                                         g.upload_q8_0(ctx, n("ffn_down.weight")), f(n("ffn_down.bias"))))
+            m.lnf_g, m.lnf_b = f("output_norm.weight"), f("output_norm.bias")
+            torch.cuda.synchronize()
+            ctx.sync()
         return m
 
     @classmethod

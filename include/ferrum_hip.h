@@ -52,7 +52,8 @@ enum {
     FH_ERR_INVALID = 2, /* null pointer, unknown enum value, k % 32 != 0 */
     FH_ERR_OOM = 3,     /* device or host allocation failed */
     FH_ERR_HIP = 4,     /* a HIP runtime call failed (message carries hipGetErrorString) */
-    FH_ERR_LIMIT = 5    /* a size beyond a documented kernel limit */
+    FH_ERR_LIMIT = 5,   /* a size beyond a documented kernel limit */
+    FH_ERR_FORMAT = 6   /* a malformed GGUF file: ferrum_core's InferError::Format (gguf/cursor.rs) */
 };
 
 /* Numerics of a Q8_0 linear.
@@ -273,6 +274,48 @@ int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n);
  * 16, 32, 64, 128 -> FH_ERR_LIMIT. */
 int fh_attention_decode_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
                               size_t capacity, size_t d, size_t heads, size_t pos, float* d_out);
+
+/* ---- GGUF reader (gguf/mod.rs:208-310, gguf/header.rs, gguf/tensors.rs:26-87) ----
+ * The file is memory-mapped read-only and parsed as ferrum_core's parse_header
+ * does: magic "GGUF", version 2 or 3, metadata table, tensor directory, data
+ * at the next multiple of general.alignment (default 32); every sized tensor
+ * must lie inside the file and no two may overlap.  Host-only calls, no GPU
+ * needed, except fh_gguf_upload_q8_0. */
+typedef struct fh_gguf fh_gguf;
+/* Always sets *out (even on failure, so fh_gguf_error can say why); close it
+ * with fh_gguf_close.  A malformed file is FH_ERR_FORMAT with the reference's
+ * messages ("not a GGUF file (bad magic)", "unsupported GGUF version N (need 2
+ * or 3)", "GGUF truncated at +P: need N bytes, file has T", "tensor 'X' data
+ * runs past EOF", "tensors 'X' and 'Y' overlap", ...). */
+int fh_gguf_open(const char* path, fh_gguf** out);
+void fh_gguf_close(fh_gguf* g);
+const char* fh_gguf_error(const fh_gguf* g);
+uint32_t fh_gguf_version(const fh_gguf* g);
+size_t fh_gguf_tensor_count(const fh_gguf* g);
+/* Index of the first tensor called name, or -1 (Gguf::tensor). */
+long fh_gguf_find_tensor(const fh_gguf* g, const char* name);
+/* dims: room for 8 (GGML order: dims[0] = ne0, the contiguous one); nbytes 0
+ * for a type the reader cannot size (gguf/format.rs:87-129). */
+int fh_gguf_tensor_info(const fh_gguf* g, size_t i, const char** name, uint32_t* n_dims, uint64_t* dims,
+                        uint32_t* ggml_type, uint64_t* nbytes);
+/* Host pointer to the tensor's bytes inside the mapping (valid until close). */
+const void* fh_gguf_tensor_data(const fh_gguf* g, size_t i);
+/* Metadata: the value type (GGUF value type codes), the element type and
+ * length of an array; integer / bool values as u64; numbers as f64; a string
+ * or element `index` of a string array. */
+int fh_gguf_meta_type(const fh_gguf* g, const char* key, uint32_t* type, uint32_t* elem_type, uint64_t* count);
+int fh_gguf_meta_u64(const fh_gguf* g, const char* key, uint64_t* out);
+int fh_gguf_meta_f64(const fh_gguf* g, const char* key, double* out);
+int fh_gguf_meta_str(const fh_gguf* g, const char* key, size_t index, const char** out, size_t* len);
+/* Raw little-endian elements of a numeric array. */
+int fh_gguf_meta_array_data(const fh_gguf* g, const char* key, const void** data, size_t* elem_size);
+/* An F32 or F16 tensor of n elements into host floats (F16 decoded exactly,
+ * gguf/dequant.rs:7-35).  ctx may be NULL (the message is then not kept). */
+int fh_gguf_read_f32(fh_ctx* ctx, const fh_gguf* g, const char* name, float* out, size_t n);
+/* A Q8_0 tensor [ne0 = k, ne1 = n] straight from the mapping to the device, as
+ * fh_q8_0_upload (GgufIn::rows/matrix/linear, loader/decode.rs:57-81, without
+ * the f32 expansion). */
+int fh_gguf_upload_q8_0(fh_ctx* ctx, const fh_gguf* g, const char* name, fh_q8_0** out);
 
 #ifdef __cplusplus
 }

@@ -277,6 +277,30 @@ def test_tiny_gpt2_scores_match_the_oracle_per_position(orc, tiny):
         close(got, want, 2e-5 * max(1.0, float(np.abs(want).max())))
 
 
+def test_gpt2_from_gguf_equals_the_model_built_from_arrays(fh, orc, tiny, tmp_path):
+    """The tiny model written as a GPT-2 GGUF (the reference's export layout)
+    and loaded through the library's reader, Q8_0 tensors uploaded from the
+    file mapping: scores bit-identical to the model built from the arrays."""
+    import ferrum_gguf
+    import ferrum_hip
+
+    w, model = tiny
+    path = str(tmp_path / "tiny.gguf")
+    ferrum_gguf.gpt2_gguf(w, gpt2_tiny.VOCAB, gpt2_tiny.D, gpt2_tiny.HEADS, gpt2_tiny.LAYERS, gpt2_tiny.FFN,
+                          gpt2_tiny.CTX).write(path)
+    m2 = ferrum_hip.GPT2Device.from_gguf(fh, path)
+    try:
+        assert (m2.vocab, m2.d, m2.heads, m2.layers, m2.ffn, m2.cap) == (
+            gpt2_tiny.VOCAB, gpt2_tiny.D, gpt2_tiny.HEADS, gpt2_tiny.LAYERS, gpt2_tiny.FFN, gpt2_tiny.CTX)
+        ids = list(np.random.default_rng(8).integers(0, gpt2_tiny.VOCAB, 12))
+        for i in range(len(ids)):
+            z1 = model.forward(ids[: i + 1], reprime=(i == 0))
+            z2 = m2.forward(ids[: i + 1], reprime=(i == 0))
+            assert np.array_equal(z1, z2)
+    finally:
+        m2.free()
+
+
 def test_tiny_gpt2_greedy_decode_matches_the_oracle(fh, orc, tiny):
     """The tiny configuration's run: 16-token prompt, 64 greedy tokens.  Each
     step's id must be the oracle's greedy id on the same window unless the
