@@ -49,6 +49,7 @@ EXPORTS = (
     "fh_gguf_open", "fh_gguf_close", "fh_gguf_error", "fh_gguf_version", "fh_gguf_tensor_count", "fh_gguf_find_tensor",
     "fh_gguf_tensor_info", "fh_gguf_tensor_data", "fh_gguf_meta_type", "fh_gguf_meta_u64", "fh_gguf_meta_f64",
     "fh_gguf_meta_str", "fh_gguf_meta_array_data", "fh_gguf_read_f32", "fh_gguf_upload_q8_0",
+    "fh_qweight_upload", "fh_qweight_free", "fh_qlinear_async",
 )
 
 
@@ -199,6 +200,10 @@ def lib():
         L.fh_gguf_meta_array_data.argtypes = [vp, C.c_char_p, C.POINTER(vp), C.POINTER(sz)]
         L.fh_gguf_read_f32.argtypes = [vp, vp, C.c_char_p, vp, sz]
         L.fh_gguf_upload_q8_0.argtypes = [vp, vp, C.c_char_p, C.POINTER(vp)]
+        L.fh_qweight_upload.argtypes = [vp, vp, vp, sz, sz, i32, C.POINTER(vp)]
+        L.fh_qweight_free.argtypes = [vp]
+        L.fh_qweight_free.restype = None
+        L.fh_qlinear_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp]
         _lib = L
     return _lib
 
@@ -520,6 +525,37 @@ def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d
     """The KV-cache attention of forward_with_cache (layer/transformer.rs:242-279)."""
     ctx.check(lib().fh_attention_decode_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
                                               pos, _ptr(out)))
+
+
+# ---- packed per-row int8 / int4 weights: ops::qlinear ---------------------------
+
+QINT8, QINT4 = 0, 1
+
+
+class QWeight:
+    """A device-resident QWeight (quant.rs:130-217): k input rows x n outputs,
+    one scale per row, int8 or split-half int4 levels as the reference stores
+    them (fh_qweight)."""
+
+    def __init__(self, ctx: Context, scales, q, k: int, n: int, kind: int):
+        s = np.ascontiguousarray(scales, np.float32)
+        b = np.ascontiguousarray(q, np.uint8)
+        row = n if kind == QINT8 else (n + 1) // 2
+        if kind in (QINT8, QINT4) and (s.size != k or b.size != k * row):
+            raise FerrumHipError(FH_ERR_INVALID, f"QWeight: expected {k} scales and {k * row} level bytes")
+        h = C.c_void_p()
+        ctx.check(lib().fh_qweight_upload(ctx.h, s.ctypes.data, b.ctypes.data, k, n, kind, C.byref(h)))
+        self.ctx, self.h, self.k, self.n, self.kind = ctx, h, k, n, kind
+
+    def free(self):
+        if self.h:
+            lib().fh_qweight_free(self.h)
+            self.h = None
+
+
+def qlinear_async(ctx: Context, w: QWeight, x, m: int, k: int, bias, bias_len: int, y):
+    """ops::qlinear on device pointers: y = x . W + b, the reference's bits."""
+    ctx.check(lib().fh_qlinear_async(ctx.h, w.h, _ptr(x), m, k, _ptr(bias), bias_len, _ptr(y)))
 
 
 # ---- GGUF files (the library's native reader) ----------------------------------

@@ -275,6 +275,26 @@ int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n);
 int fh_attention_decode_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
                               size_t capacity, size_t d, size_t heads, size_t pos, float* d_out);
 
+/* ---- packed per-row int8 / int4 weights: ops::qlinear (ops.rs:268-377) ------
+ * QWeight (quant.rs:130-217): k rows (input features) x n columns (outputs),
+ * one f32 scale per row, int8 levels ([k][n] bytes) or int4 levels in the
+ * split-half nibble layout ([k][ceil(n/2)] bytes: column c < half in the low
+ * nibble of byte c, else the high nibble of byte c - half). */
+enum { FH_QINT8 = 0, FH_QINT4 = 1 };
+typedef struct fh_qweight fh_qweight;
+/* Host scales [k] and levels as the reference stores them; the device copy pads
+ * each row to 64 bytes.  Blocks until the copy is done. */
+int fh_qweight_upload(fh_ctx* ctx, const float* scales, const uint8_t* q, size_t k, size_t n, int kind,
+                      fh_qweight** out);
+void fh_qweight_free(fh_qweight* w);
+/* y[i, j] = b[j] + sum over p ascending of (x[i, p] * scale[p]) * level(p, j),
+ * bias first and no FMA, as qaccum_cols: the reference's outputs bit for bit.
+ * d_x [m, k], d_y [m, n] device pointers; bias NULL (bias_len 0) means zeros.
+ * Errors as qlinear: "qlinear: input width K ≠ weight rows R", "qlinear: bias
+ * length B ≠ out_features N" (FH_ERR_DIM). */
+int fh_qlinear_async(fh_ctx* ctx, const fh_qweight* w, const float* d_x, size_t m, size_t k, const float* d_bias,
+                     size_t bias_len, float* d_y);
+
 /* ---- GGUF reader (gguf/mod.rs:208-310, gguf/header.rs, gguf/tensors.rs:26-87) ----
  * The file is memory-mapped read-only and parsed as ferrum_core's parse_header
  * does: magic "GGUF", version 2 or 3, metadata table, tensor directory, data
