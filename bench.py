@@ -97,7 +97,7 @@ def main():
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--leg", choices=["all", "head", "prefill", "qwen"], default="all",
+    ap.add_argument("--leg", choices=["all", "head", "prefill", "qwen", "qlinear"], default="all",
                     help="'head': only the lm_head GEMV roofline leg (for counter runs); "
                          "'prefill': only the GPT-2-medium prefill GEMMs")
     ap.add_argument("--prefill-steps", type=int, default=3)
@@ -281,6 +281,12 @@ def main():
         print(json.dumps({"leg": "prefill", "prefill": result["prefill"]}))
         return
 
+    if args.leg in ("all", "qlinear"):
+        result["qlinear_gpu"] = qlinear_gpu_leg(ctx, fh, torch, dev, max(args.steps // 10, 10), args.replicas)
+    if args.leg == "qlinear":
+        print(json.dumps({"leg": "qlinear", "qlinear_int8_gpu": result["qlinear_gpu"]}))
+        return
+
     if args.leg in ("all", "qwen"):
         result["qwen2_b64"] = qwen_leg(ctx, fh, torch, gen, dev, max(args.steps // 20, 10), args.warmup)
     if args.leg == "qwen":
@@ -391,6 +397,7 @@ def main():
         "b32": result["b32"],
         "prefill": result["prefill"],
         "qwen2_b64": result.get("qwen2_b64"),
+        "qlinear_int8_gpu": result.get("qlinear_gpu"),
         "hbm_copy_GBps": round(copy_GBps, 1) if copy_GBps else None,
         "shard_head_gemv": result["shard_head"],
     }
@@ -465,6 +472,64 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
             "w8a8_int8_mfma": {"ms": round(ms8, 3), "tops": round(tops8, 1),
                                "frac_i8_dense_peak": round(tops8 / I8_DENSE_TOPS, 4),
                                "numerics": "W8A8 (activations re-quantised to Q8_0), bit-exact with the reference"}}
+
+
+def qlinear_gpu_leg(ctx, fh, torch, dev, steps, replicas):
+    """The reference's per-row int8 path on the GPU: the 49 ops::qlinear calls
+    of a GPT-2-124M decode step (m = 1, bias-first ascending-p sums, the
+    reference's bits), random levels and scales, `replicas` weight sets (HBM-
+    forced), one graph per set."""
+    import numpy as np
+
+    rng = np.random.default_rng(77)
+
+    def qw(k, n):
+        return fh.QWeight(ctx, np.abs(rng.standard_normal(k)).astype(np.float32) * 1e-3,
+                          rng.integers(-127, 128, size=k * n, dtype=np.int8).view(np.uint8), k, n, fh.QINT8)
+
+    shapes = [(k, n) for (n, k) in LAYER_SHAPES]  # QWeight: k input rows x n outputs
+    sets = [([[qw(k, n) for (k, n) in shapes] for _ in range(L)], qw(D, V)) for _ in range(replicas)]
+    bias = {n: torch.randn(n, device=dev) * 0.1 for n in {n for (_, n) in shapes} | {V}}
+    xs = {k: torch.randn(k, device=dev) for k in (D, FFN)}
+    y = torch.empty(V, device=dev)
+
+    def step(ws, head):
+        for layer in ws:
+            for w in layer:
+                fh.qlinear_async(ctx, w, xs[w.k], 1, w.k, bias[w.n], w.n, y)
+        fh.qlinear_async(ctx, head, xs[D], 1, D, bias[V], V, y)
+
+    graphs = []
+    for ws, head in sets:
+        step(ws, head)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+            step(ws, head)
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        graphs.append(g)
+    for g in graphs:
+        g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(steps):
+        graphs[i % len(graphs)].replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    qbytes = L * sum(k * n + 4 * k for (k, n) in shapes) + D * V + 4 * D
+    for ws, head in sets:
+        head.free()
+        for layer in ws:
+            for w in layer:
+                w.free()
+    del graphs
+    torch.cuda.synchronize()
+    return {"ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 1), "weight_bytes": qbytes,
+            "weight_GBps": round(qbytes / (ms * 1e-3) / 1e9, 1), "residency": f"hbm-forced ({replicas} weight sets)",
+            "what": "49 ops::qlinear (per-row int8) of a GPT-2-124M step at m = 1, bit-exact numerics"}
 
 
 QWEN05 = dict(vocab=151936, d=896, n_heads=14, n_kv=2, head_dim=64, layers=24, ffn=4864, context=512,

@@ -13,11 +13,13 @@
 // (and rows of x).
 //
 // Device layout: the reference's row-major bytes, each row padded to a
-// multiple of 64 bytes (16-byte-aligned dword loads, whole cache lines).
-// Lane l of the grid owns dword l of every row: 4 int8 columns, or the 4 low
-// and 4 high nibble columns of 4 bytes.  A wave reads 256 contiguous bytes per
-// row; each lane keeps two batches of 16 rows' dwords in flight (double
-// buffered) while it accumulates the previous batch in order.
+// multiple of 64 bytes.  A workgroup owns one 64-byte column tile of every row
+// (64 int8 columns, or 64 low- and 64 high-nibble int4 columns) and walks K in
+// chunks of 512 rows: all 256 threads stream a chunk (32 KB, row segments of
+// 16 bytes) and its scaled activations into one LDS buffer while wave i sums
+// the previous chunk for x row i, one lane per column, in ascending p.  The
+// sums are dependency chains of K adds, so the columns (and rows of x) are the
+// parallelism and the chunk pipeline keeps the loads in flight meanwhile.
 #include "fh_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -33,98 +35,104 @@ struct fh_qweight {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kChunk = 512;  // rows p of scaled activations staged in LDS at a time
-constexpr int kBatch = 16;   // weight dwords per lane per batch
+typedef uint32_t u4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ float level8(uint32_t w, int t) {
-    return static_cast<float>(static_cast<int8_t>((w >> (8 * t)) & 0xFFu));
-}
+constexpr int kThreads = 256;
+constexpr int kTile = 64;    // column bytes per workgroup
+constexpr int kChunk = 512;  // rows p per LDS chunk
+constexpr int kSegs = kChunk * kTile / 16 / kThreads;  // 16-byte row segments per thread and chunk
+
 // quant.rs:222-225 nibble_to_i8: sign-extend a 4-bit level
-__device__ __forceinline__ float level4(uint32_t w, int t, bool hi) {
-    const uint32_t nib = (w >> (8 * t + (hi ? 4 : 0))) & 0xFu;
+__device__ __forceinline__ float level4(uint32_t b, bool hi) {
+    const uint32_t nib = (hi ? b >> 4 : b) & 0xFu;
     return static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(nib << 4)) >> 4);
 }
 
-// KIND 0: int8, 1: int4.  M rows of x per workgroup (grid.y over row groups).
+// KIND 0: int8, 1: int4.  M rows of x per workgroup (grid.y over row groups),
+// one summing wave per row.
 template <int KIND, int M>
 __global__ void __launch_bounds__(kThreads)
     k_qlinear(const uint8_t* __restrict__ q, const float* __restrict__ scales, const float* __restrict__ x,
               const float* __restrict__ bias, float* __restrict__ y, int m, int k, int n, int pitch) {
-    constexpr int C = KIND == 0 ? 4 : 8;  // outputs per lane
-    __shared__ float a[M][kChunk];
-    const int lane_dw = blockIdx.x * kThreads + threadIdx.x;  // dword of the row this lane owns
-    const int row0 = blockIdx.y * M;
+    static_assert(M <= kThreads / 64, "one summing wave per row");
+    __shared__ __align__(16) uint8_t wt[2][kChunk][kTile];
+    __shared__ float a[2][M][kChunk];
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c0 = blockIdx.x * kTile, row0 = blockIdx.y * M;
     const int half = (n + 1) / 2;
-    int col[C];
+    // the column(s) lane `lane` of a summing wave owns
+    const int col_lo = c0 + lane, col_hi = half + c0 + lane;
+    const bool live_lo = KIND == 0 ? col_lo < n : col_lo < half;
+    const bool live_hi = KIND == 1 && col_hi < n;
+    const bool summing = wave < M && row0 + wave < m;
+    // every output starts at its bias (the reference fuses the bias first)
+    float acc_lo = bias && live_lo ? bias[col_lo] : 0.0f;
+    float acc_hi = bias && live_hi ? bias[col_hi] : 0.0f;
+    const int chunks = (k + kChunk - 1) / kChunk;
+    constexpr int kAPer = kChunk / kThreads;  // activation rows per thread and chunk
+    u4 seg[kSegs];
+    float xv[M][kAPer], sv[kAPer];
+    // Chunk c: thread t loads segment t % 4 of rows t / 4 + 64 j, and x and the
+    // scale of rows t + 256 j (all clamped to valid rows: rows past K are
+    // loaded, never summed).
+    auto fetch = [&](int c) __attribute__((always_inline)) {
+        const int p0 = c * kChunk;
 #pragma unroll
-    for (int t = 0; t < 4; t++) {
-        col[t] = 4 * lane_dw + t;
-        if (KIND == 1) col[4 + t] = half + 4 * lane_dw + t;
-    }
-    bool live[C];
-#pragma unroll
-    for (int c = 0; c < C; c++) live[c] = KIND == 0 ? col[c] < n : (c < 4 ? col[c] < half : col[c] < n);
-    // every output starts at its bias (ops.rs: the bias is fused first)
-    float acc[M][C];
-#pragma unroll
-    for (int i = 0; i < M; i++)
-#pragma unroll
-        for (int c = 0; c < C; c++) acc[i][c] = bias && live[c] ? bias[col[c]] : 0.0f;
-    const bool active = 4 * lane_dw < pitch;
-    const uint8_t* qp = q + 4 * static_cast<size_t>(active ? lane_dw : 0);
-    for (int p0 = 0; p0 < k; p0 += kChunk) {
-        const int pn = min(kChunk, k - p0);
-        __syncthreads();  // the previous chunk's activations are consumed
-        // a'[i, p] = x[i, p] * scale[p] (ops.rs:331-339)
-        for (int e = threadIdx.x; e < M * kChunk; e += kThreads) {
-            const int i = e / kChunk, pp = e % kChunk;
-            a[i][pp] = (pp < pn && row0 + i < m) ? x[static_cast<size_t>(row0 + i) * k + p0 + pp] * scales[p0 + pp]
-                                                 : 0.0f;
+        for (int j = 0; j < kSegs; j++) {
+            const int p = min(p0 + (tid >> 2) + j * (kThreads / 4), k - 1);
+            seg[j] = *reinterpret_cast<const u4*>(q + static_cast<size_t>(p) * pitch + c0 + (tid & 3) * 16);
         }
-        __syncthreads();
-        if (!active) continue;
-        uint32_t buf[2][kBatch];
-        auto load = [&](int b, int pb) __attribute__((always_inline)) {
 #pragma unroll
-            for (int u = 0; u < kBatch; u++) {
-                const int pp = min(pb + u, pn - 1);  // clamped: rows past the chunk are loaded, never used
-                buf[b][u] = *reinterpret_cast<const uint32_t*>(qp + static_cast<size_t>(p0 + pp) * pitch);
-            }
-        };
-        load(0, 0);
-        for (int pb = 0, b = 0; pb < pn; pb += kBatch, b ^= 1) {
-            if (pb + kBatch < pn) load(b ^ 1, pb + kBatch);
+        for (int j = 0; j < kAPer; j++) {
+            const int p = min(p0 + tid + j * kThreads, k - 1);
+            sv[j] = scales[p];
 #pragma unroll
-            for (int u = 0; u < kBatch; u++) {
-                if (pb + u >= pn) break;
-                const uint32_t w = buf[b][u];
+            for (int i = 0; i < M; i++) xv[i][j] = x[static_cast<size_t>(min(row0 + i, m - 1)) * k + p];
+        }
+    };
+    // a'[i, p] = x[i, p] * scale[p] (ops.rs:331-339) and the levels, into buffer b
+    auto store = [&](int b) __attribute__((always_inline)) {
 #pragma unroll
-                for (int i = 0; i < M; i++) {
-                    const float ap = a[i][pb + u];
+        for (int j = 0; j < kSegs; j++)
+            *reinterpret_cast<u4*>(&wt[b][(tid >> 2) + j * (kThreads / 4)][(tid & 3) * 16]) = seg[j];
 #pragma unroll
-                    for (int c = 0; c < C; c++) {
-                        const float lv = KIND == 0 ? level8(w, c) : level4(w, c & 3, c >= 4);
-                        acc[i][c] = acc[i][c] + ap * lv;
-                    }
+        for (int j = 0; j < kAPer; j++)
+#pragma unroll
+            for (int i = 0; i < M; i++) a[b][i][tid + j * kThreads] = xv[i][j] * sv[j];
+    };
+    fetch(0);
+    store(0);
+    __syncthreads();
+    for (int c = 0; c < chunks; c++) {
+        const int b = c & 1;
+        if (c + 1 < chunks) fetch(c + 1);  // next chunk in flight during the sums
+        if (summing) {
+            const int pn = min(kChunk, k - c * kChunk);
+            const float* ar = a[b][wave];
+            for (int u = 0; u < pn; u++) {
+                const uint32_t wb = wt[b][u][lane];
+                const float ap = ar[u];
+                if (KIND == 0) {
+                    acc_lo = acc_lo + ap * static_cast<float>(static_cast<int8_t>(wb));
+                } else {
+                    acc_lo = acc_lo + ap * level4(wb, false);
+                    acc_hi = acc_hi + ap * level4(wb, true);
                 }
             }
         }
+        if (c + 1 < chunks) store(b ^ 1);  // the other buffer: last read two chunks ago
+        __syncthreads();
     }
-    if (!active) return;
-#pragma unroll
-    for (int i = 0; i < M; i++) {
-        if (row0 + i >= m) break;
-#pragma unroll
-        for (int c = 0; c < C; c++)
-            if (live[c]) y[static_cast<size_t>(row0 + i) * n + col[c]] = acc[i][c];
+    if (summing) {
+        float* yr = y + static_cast<size_t>(row0 + wave) * n;
+        if (live_lo) yr[col_lo] = acc_lo;
+        if (live_hi) yr[col_hi] = acc_hi;
     }
 }
 
 template <int KIND>
 int launch(fh_ctx* ctx, const fh_qweight* w, const float* x, size_t m, const float* bias, float* y) {
-    const size_t dwords = w->pitch / 4;
-    const unsigned gx = static_cast<unsigned>((dwords + kThreads - 1) / kThreads);
+    const unsigned gx = static_cast<unsigned>(w->pitch / kTile);
     const int mi = static_cast<int>(m), ki = static_cast<int>(w->k), ni = static_cast<int>(w->n);
     const int pi = static_cast<int>(w->pitch);
     if (m == 1) {
