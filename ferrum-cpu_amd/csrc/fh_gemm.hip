@@ -935,13 +935,17 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
 // shapes: two column tiles per wave pay off from about 256 tiles of 32
 // columns (a 9728-wide output: 14.2 -> 11.8 us at m = 32), four only at m <=
 // 32 (four at m = 64 ran the 151936-wide head 2.8x slower); at m = 64 two
-// blocks per wave batch beat three (small layers 11.4 -> 10.4 us).
+// blocks per wave batch beat three (small layers 11.4 -> 10.4 us); at m <=
+// 32 outputs narrower than 2048 take one block per wave batch (more K splits,
+// so more workgroups: 896 x 896 7.9 -> 6.9 us, 768 x 3072 8.5 -> 7.7 us; a
+// 3072-wide one slows down).
 int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
     const size_t t32 = (w->n + 31) / 32;
     if (m <= 32) {
         if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y);
         if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y);
-        return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y);
+        if (t32 >= 64) return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y);
+        return launch_skinny_t<1, 1, 1>(ctx, w, x, m, bias, y);
     }
     if (t32 >= 4 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y);
     if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y);
