@@ -936,9 +936,9 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
 // columns (a 9728-wide output: 14.2 -> 11.8 us at m = 32), four only at m <=
 // 32 (four at m = 64 ran the 151936-wide head 2.8x slower); at m = 64 two
 // blocks per wave batch beat three (small layers 11.4 -> 10.4 us); at m <=
-// 32 outputs narrower than 2048 take one block per wave batch (more K splits,
-// so more workgroups: 896 x 896 7.9 -> 6.9 us, 768 x 3072 8.5 -> 7.7 us; a
-// 3072-wide one slows down).
+// 32 and 64 outputs narrower than 2048 take one block per wave batch (more K
+// splits, so more workgroups: 896 x 896 7.9 -> 6.9 us at m = 32, 10.4 -> 9.2
+// us at m = 64; a 3072-wide one slows down).
 int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
     const size_t t32 = (w->n + 31) / 32;
     if (m <= 32) {
@@ -949,7 +949,8 @@ int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const
     }
     if (t32 >= 4 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y);
     if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y);
-    return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y);
+    if (t32 >= 64) return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y);
+    return launch_skinny_t<2, 1, 1>(ctx, w, x, m, bias, y);  // 896 x 896: 10.4 -> 9.2 us
 }
 
 }  // namespace
