@@ -815,6 +815,26 @@ class LlamaDevice:
         """Kernel launches of feed_async (the sampler not included)."""
         return 1 + 9 * self.layers + 2
 
+    def forward_one(self, token: int):
+        """LlamaModel::forward_one (llm.rs:606-616) for a single sequence (rows
+        == 1): feed `token` at the next position and return the logits (host)
+        — the callback llama_decode drives.  A full cache is FH_ERR_DIM."""
+        import torch
+
+        if self.rows != 1:
+            raise FerrumHipError(FH_ERR_INVALID, "forward_one drives a single-row LlamaDevice")
+        nxt = getattr(self, "next_pos", 0)
+        if nxt >= self.cap:
+            raise DimMismatch(FH_ERR_DIM, f"KvCache full ({self.cap} positions): clear and re-prime to continue")
+        self.ctx.sync()
+        self.tokens.fill_(int(token))
+        self.pos.fill_(nxt)
+        torch.cuda.current_stream().synchronize()
+        self.feed_async(nxt)
+        self.next_pos = nxt + 1
+        self.ctx.sync()
+        return self.z[0].cpu().numpy()
+
     def feed_async(self, max_pos: int):
         """One decode step of every row: token self.tokens[r] at position
         self.pos[r] (both on the device; max_pos bounds the positions).  The

@@ -247,3 +247,47 @@ def test_tiny_qwen_greedy_batch_runs_on_the_device(fh, orc):
             m.pos.add_(1)
     finally:
         m.free()
+
+
+def test_tiny_qwen_generate_replays_on_the_oracle(fh, orc):
+    """LlamaModel::generate_inner's loop (llm.rs:706-754, ferrum_hip.llama_decode)
+    driving the device decoder: a 6-token prompt, sampled ids (temperature,
+    top-k, top-p, repetition penalty over every prompt and generated id) with
+    draws from the reference's Rng.  Replayed on the oracle model and sampler
+    with the same draws: the same scores at every position (2e-5 of the row's
+    largest) and the same ids unless the oracle reports a near-tie margin."""
+    import ferrum_hip
+
+    cfg = llama_tiny.QWEN
+    w = llama_tiny.make_weights(orc, cfg, 29, True, True)
+    m = ferrum_hip.LlamaDevice.from_weights(fh, w, cfg, 1)
+    scores = []
+
+    def fwd(tok):
+        z = m.forward_one(tok)
+        scores.append(z)
+        return z
+
+    kw = dict(temperature=0.9, top_k=50, top_p=0.9, repetition_penalty=1.05)
+    prompt = list(np.random.default_rng(12).integers(0, cfg["vocab"], 6))
+    try:
+        got = ferrum_hip.llama_decode(fh, fwd, prompt, 30, ferrum_hip.SamplingParams(**kw), ferrum_hip.Rng(4),
+                                      context_len=cfg["context"])
+    finally:
+        m.free()
+    assert len(got) == 30
+    ref = llama_tiny.OracleLlamaRow(orc, w, cfg, 0)
+    for i, t in enumerate(prompt[:-1]):
+        close(scores[i], ref.feed(t), 2e-5 * max(1.0, float(np.abs(scores[i]).max())))
+    recent, op, rng = list(prompt), orc.SamplingParams(**kw), orc.Rng(4)
+    z = ref.feed(prompt[-1])
+    for step, tok in enumerate(got):
+        zg = scores[len(prompt) - 1 + step]
+        close(zg, z, 2e-5 * max(1.0, float(np.abs(z).max())))
+        want, info = orc.sample(z, op, recent, rng.next_u64())
+        if want != tok:
+            assert info.margin < 1e-5, (step, tok, want, info.margin)
+            break
+        recent.append(tok)
+        if step + 1 < len(got):
+            z = ref.feed(tok)
