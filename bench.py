@@ -444,10 +444,45 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
     tflops = flops / (ms * 1e-3) / 1e12
     ms8, _, _ = timed_graph(fh.W8A8)
     tops8 = flops / (ms8 * 1e-3) / 1e12
+    # Config 4's decode: the same model's linears at batch 32 (96 Q8_0 GEMMs at
+    # m = 32 + the 50257 x 1024 head) and the greedy sampler on the 32 rows;
+    # 357 MB of Q8_0 per step, more than the MALL holds, so it streams from HBM.
+    head = make_weight(ctx, fh, torch, V, MED_D, gen)
+    xb = {k: torch.randn((B32, k), generator=gen, device=dev) for k in {s_[1] for s_ in MED_SHAPES}}
+    yb = torch.empty((B32, max(s_[0] for s_ in MED_SHAPES)), device=dev)
+    lb = torch.empty((B32, V), device=dev)
+    ob = torch.zeros(B32, dtype=torch.int32, device=dev)
+    greedy = fh.SamplingParams(temperature=0.0)
+
+    def dstep():
+        for li in range(MED_L):
+            for (n, k), w in zip(MED_SHAPES, layers[li]):
+                fh.linear_forward_async(ctx, w, xb[k], B32, k, biases[n], n, yb)
+        fh.linear_forward_async(ctx, head, xb[MED_D], B32, MED_D, None, 0, lb)
+        fh.sample_rows_async(ctx, lb, B32, V, greedy, None, None, None, ob)
+
+    dstep()
+    torch.cuda.synchronize()
+    gd = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(gd):
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        dstep()
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    gd.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(20):
+        gd.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    dms = e0.elapsed_time(e1) / 20
+    dbytes = MED_L * sum(q8_bytes(n, k) for (n, k) in MED_SHAPES) + q8_bytes(V, MED_D)
+    del gd
+    head.free()
     for lw in layers:
         for w in lw:
             w.free()
-    del x, y
+    del x, y, xb, yb, lb
     # The same matrix-core work as a plain library f16 GEMM (torch -> hipBLASLt):
     # three f16 products per Q8_0 weight-activation pair are one GEMM of depth 3k.
     lib_ms = 0.0
@@ -470,6 +505,9 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
             "frac_i8_dense_peak": round(tflops / I8_DENSE_TOPS, 4),
             "mfma_f16_tflops": round(3 * tflops, 1), "mfma_frac_f16_dense_peak": round(3 * tflops / F16_DENSE_TFLOPS, 4),
             "library_f16_same_mfma_work_ms": round(lib_ms, 3), "vs_library": round(lib_ms / ms, 3),
+            "decode_b32": {"ms_per_step": round(dms, 4), "tok_s": round(B32 * 1000.0 / dms, 1),
+                           "weight_bytes": dbytes, "weight_GBps": round(dbytes / (dms * 1e-3) / 1e9, 1),
+                           "what": "gpt2-medium decode step at batch 32: 96 Q8_0 GEMMs + head + greedy sampler"},
             "w8a8_int8_mfma": {"ms": round(ms8, 3), "tops": round(tops8, 1),
                                "frac_i8_dense_peak": round(tops8 / I8_DENSE_TOPS, 4),
                                "numerics": "W8A8 (activations re-quantised to Q8_0), bit-exact with the reference"}}
