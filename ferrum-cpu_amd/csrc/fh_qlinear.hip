@@ -14,12 +14,16 @@
 //
 // Device layout: the reference's row-major bytes, each row padded to a
 // multiple of 64 bytes.  A workgroup owns one 64-byte column tile of every row
-// (64 int8 columns, or 64 low- and 64 high-nibble int4 columns) and walks K in
-// chunks of 512 rows: all 256 threads stream a chunk (32 KB, row segments of
-// 16 bytes) and its scaled activations into one LDS buffer while wave i sums
-// the previous chunk for x row i, one lane per column, in ascending p.  The
-// sums are dependency chains of K adds, so the columns (and rows of x) are the
-// parallelism and the chunk pipeline keeps the loads in flight meanwhile.
+// (64 int8 columns, or 64 low- and 64 high-nibble int4 columns).  With several
+// rows of x (k_qlinear) it walks K in chunks of 512 rows: all 256 threads
+// stream a chunk (32 KB, row segments of 16 bytes) and its scaled activations
+// into one LDS buffer while wave i sums the previous chunk for x row i, one
+// lane per column, in ascending p.  With one row (k_qlinear_row, the decode
+// case) one wave sums and three form the products.  The sums are dependency
+// chains of K adds, so the columns (and rows of x) are the parallelism and the
+// chunk pipeline keeps the loads in flight meanwhile.
+#include <type_traits>
+
 #include "fh_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -130,14 +134,145 @@ __global__ void __launch_bounds__(kThreads)
     }
 }
 
+// One row of x (the decode case).  A sum is a chain of K dependent adds, so
+// the time of the kernel is K times the cost of one step of that chain.  Here
+// the summing wave (wave 0) does nothing but the adds: waves 1-3 form the
+// products a'[p] * level(p, j) of the next chunk into LDS meanwhile (the same
+// f32 multiplications the reference makes), so each step of the chain is one
+// add and a quarter of a 16-byte LDS read.
+//
+// LDS holds a chunk's products as float4 [group g of 4 rows][column], so the
+// summing lane reads 4 consecutive rows of its column at once.  Columns are
+// permuted within a group row (low 3 bits XOR ((col >> 3) + g)) so that the
+// producers' 16-byte writes spread over the banks; the summing wave reads one
+// contiguous 1 KB (or 2 KB) group row, conflict-free under any permutation.
+template <int KIND>
+__global__ void __launch_bounds__(kThreads)
+    k_qlinear_row(const uint8_t* __restrict__ q, const float* __restrict__ scales, const float* __restrict__ x,
+                  const float* __restrict__ bias, float* __restrict__ y, int k, int n, int pitch) {
+    constexpr int kRows = KIND == 0 ? 192 : 96;  // rows p per chunk
+    constexpr int kGroups = kRows / 4;
+    constexpr int kCols = KIND == 0 ? kTile : 2 * kTile;  // output columns per workgroup
+    __shared__ float4 prod[2][kGroups * kCols];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int c0 = blockIdx.x * kTile;
+    const int half = (n + 1) / 2;
+    const int chunks = (k + kRows - 1) / kRows;
+    auto slot = [](int col, int g) __attribute__((always_inline)) { return col ^ (((col >> 3) + g) & 7); };
+
+    // wave-uniform role (a scalar branch: every wave meets the same barriers)
+    if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0) {
+        // the summing wave: columns c0 + lane (and half + c0 + lane for int4)
+        const int col_lo = c0 + lane, col_hi = half + c0 + lane;
+        const bool live_lo = KIND == 0 ? col_lo < n : col_lo < half;
+        const bool live_hi = KIND == 1 && col_hi < n;
+        float acc_lo = bias && live_lo ? bias[col_lo] : 0.0f;
+        float acc_hi = bias && live_hi ? bias[col_hi] : 0.0f;
+        __syncthreads();  // chunk 0 is in LDS
+        for (int c = 0; c < chunks; c++) {
+            const float4* pb = prod[c & 1];
+            const int pn = min(kRows, k - c * kRows);
+            const int gn = pn >> 2;
+            auto add4 = [](float acc, float4 v) __attribute__((always_inline)) {
+                return (((acc + v.x) + v.y) + v.z) + v.w;
+            };
+            if (gn == kGroups) {
+#pragma unroll
+                for (int g = 0; g < kGroups; g++) {
+                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lane, g)]);
+                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(kTile + lane, g)]);
+                }
+            } else {
+                for (int g = 0; g < gn; g++) {
+                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lane, g)]);
+                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(kTile + lane, g)]);
+                }
+                const int rest = pn & 3;  // rows of a last, partial group
+                if (rest) {
+                    const float4 v = pb[gn * kCols + slot(lane, gn)];
+                    acc_lo = acc_lo + v.x;
+                    if (rest > 1) acc_lo = acc_lo + v.y;
+                    if (rest > 2) acc_lo = acc_lo + v.z;
+                    if (KIND == 1) {
+                        const float4 h = pb[gn * kCols + slot(kTile + lane, gn)];
+                        acc_hi = acc_hi + h.x;
+                        if (rest > 1) acc_hi = acc_hi + h.y;
+                        if (rest > 2) acc_hi = acc_hi + h.z;
+                    }
+                }
+            }
+            __syncthreads();  // chunk c + 1 is in LDS; buffer c & 1 is free
+        }
+        if (live_lo) y[col_lo] = acc_lo;
+        if (live_hi) y[col_hi] = acc_hi;
+        return;
+    }
+
+    // The producers: thread t owns rows 4g..4g+3 of a chunk and 16-byte column
+    // segment s (for int4, the low or the high nibbles of it: hs = 0 or 4).
+    const int t = tid - 64;
+    const int tj = KIND == 0 ? t : t % 96;
+    const int g = tj >> 2, s = tj & 3;
+    const int hs = KIND == 0 ? 0 : (t / 96) * 4;
+    const int colb = (KIND == 0 ? 0 : (t / 96) * kTile) + s * 16;
+    u4 wv[2][4];
+    float xv[2][4], sv[2][4];
+    // Chunk c's rows into register set S (rows past K clamp to K - 1: loaded,
+    // never summed).
+    auto fetch = [&](auto S, int c) __attribute__((always_inline)) {
+        const int p0 = c * kRows + 4 * g;
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int p = min(p0 + r, k - 1);
+            wv[S][r] = *reinterpret_cast<const u4*>(q + static_cast<size_t>(p) * pitch + c0 + s * 16);
+            xv[S][r] = x[p];
+            sv[S][r] = scales[p];
+        }
+    };
+    auto produce = [&](auto S, int b) __attribute__((always_inline)) {
+        float a[4];
+#pragma unroll
+        for (int r = 0; r < 4; r++) a[r] = xv[S][r] * sv[S][r];  // ops.rs:331-339
+        float4* pb = prod[b] + g * kCols;
+#pragma unroll
+        for (int i = 0; i < 16; i++) {
+            float lv[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const uint32_t byte = (wv[S][r][i >> 2] >> (8 * (i & 3))) & 0xFFu;
+                lv[r] = KIND == 0 ? static_cast<float>(static_cast<int8_t>(static_cast<uint8_t>(byte)))
+                                  : level4(byte >> hs, false);
+            }
+            pb[slot(colb + i, g)] = make_float4(a[0] * lv[0], a[1] * lv[1], a[2] * lv[2], a[3] * lv[3]);
+        }
+    };
+    std::integral_constant<int, 0> s0;
+    std::integral_constant<int, 1> s1;
+    fetch(s0, 0);
+    if (chunks > 1) fetch(s1, 1);
+    produce(s0, 0);
+    __syncthreads();
+    // Step c: set c & 1 held chunk c (its products are in LDS), so it takes
+    // chunk c + 2; chunk c + 1's products go to buffer (c + 1) & 1.
+    auto step = [&](auto S, int c) __attribute__((always_inline)) {
+        if (c + 2 < chunks) fetch(S, c + 2);
+        if (c + 1 < chunks) produce(std::integral_constant<int, 1 - S>{}, (c + 1) & 1);
+        __syncthreads();
+    };
+    for (int c = 0; c < chunks; c += 2) {
+        step(s0, c);
+        if (c + 1 < chunks) step(s1, c + 1);
+    }
+}
+
 template <int KIND>
 int launch(fh_ctx* ctx, const fh_qweight* w, const float* x, size_t m, const float* bias, float* y) {
     const unsigned gx = static_cast<unsigned>(w->pitch / kTile);
     const int mi = static_cast<int>(m), ki = static_cast<int>(w->k), ni = static_cast<int>(w->n);
     const int pi = static_cast<int>(w->pitch);
     if (m == 1) {
-        hipLaunchKernelGGL((k_qlinear<KIND, 1>), dim3(gx, 1), dim3(kThreads), 0, ctx->stream, w->q, w->scales, x, bias,
-                           y, mi, ki, ni, pi);
+        hipLaunchKernelGGL((k_qlinear_row<KIND>), dim3(gx), dim3(kThreads), 0, ctx->stream, w->q, w->scales, x, bias,
+                           y, ki, ni, pi);
     } else {
         hipLaunchKernelGGL((k_qlinear<KIND, 4>), dim3(gx, static_cast<unsigned>((m + 3) / 4)), dim3(kThreads), 0,
                            ctx->stream, w->q, w->scales, x, bias, y, mi, ki, ni, pi);
