@@ -145,17 +145,27 @@ __global__ void __launch_bounds__(kThreads)
 // summing lane reads 4 consecutive rows of its column at once.  Columns are
 // permuted within a group row (low 3 bits XOR ((col >> 3) + g)) so that the
 // producers' 16-byte writes spread over the banks; the summing wave reads one
-// contiguous 1 KB (or 2 KB) group row, conflict-free under any permutation.
-template <int KIND>
+// contiguous group row, conflict-free under any permutation.
+//
+// TW is the column tile in bytes (16, 32 or 64).  Every chunk is 48 KB of
+// products whatever TW is, so a narrow tile means a long chunk: for a narrow
+// output the chain then runs ~4x longer per chunk against the same LDS
+// traffic, and the producers' writes no longer hold up the summing wave's
+// reads (a dependent f32 add takes ~5.75 cycles; at TW = 64 the products'
+// write and read take ~70 % of the CU's LDS bandwidth during the chain).
+template <int KIND, int TW>
 __global__ void __launch_bounds__(kThreads)
     k_qlinear_row(const uint8_t* __restrict__ q, const float* __restrict__ scales, const float* __restrict__ x,
                   const float* __restrict__ bias, float* __restrict__ y, int k, int n, int pitch) {
-    constexpr int kRows = KIND == 0 ? 192 : 96;  // rows p per chunk
+    static_assert(TW == 16 || TW == 32 || TW == 64, "column tile of 16, 32 or 64 bytes");
+    constexpr int kSegs = TW / 16;                             // 16-byte segments per row tile
+    constexpr int kRows = (KIND == 0 ? 768 : 384) / kSegs;     // rows p per chunk: 192 producer jobs
     constexpr int kGroups = kRows / 4;
-    constexpr int kCols = KIND == 0 ? kTile : 2 * kTile;  // output columns per workgroup
+    constexpr int kCols = KIND == 0 ? TW : 2 * TW;             // output columns per workgroup
     __shared__ float4 prod[2][kGroups * kCols];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int c0 = blockIdx.x * kTile;
+    const int lr = lane % TW;  // lanes past the tile mirror lane % TW and store nothing
+    const int c0 = blockIdx.x * TW;
     const int half = (n + 1) / 2;
     const int chunks = (k + kRows - 1) / kRows;
     auto slot = [](int col, int g) __attribute__((always_inline)) { return col ^ (((col >> 3) + g) & 7); };
@@ -163,9 +173,9 @@ __global__ void __launch_bounds__(kThreads)
     // wave-uniform role (a scalar branch: every wave meets the same barriers)
     if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0) {
         // the summing wave: columns c0 + lane (and half + c0 + lane for int4)
-        const int col_lo = c0 + lane, col_hi = half + c0 + lane;
-        const bool live_lo = KIND == 0 ? col_lo < n : col_lo < half;
-        const bool live_hi = KIND == 1 && col_hi < n;
+        const int col_lo = c0 + lr, col_hi = half + c0 + lr;
+        const bool live_lo = lane < TW && (KIND == 0 ? col_lo < n : col_lo < half);
+        const bool live_hi = KIND == 1 && lane < TW && col_hi < n;
         float acc_lo = bias && live_lo ? bias[col_lo] : 0.0f;
         float acc_hi = bias && live_hi ? bias[col_hi] : 0.0f;
         __syncthreads();  // chunk 0 is in LDS
@@ -177,24 +187,24 @@ __global__ void __launch_bounds__(kThreads)
                 return (((acc + v.x) + v.y) + v.z) + v.w;
             };
             if (gn == kGroups) {
-#pragma unroll
+#pragma unroll 32
                 for (int g = 0; g < kGroups; g++) {
-                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lane, g)]);
-                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(kTile + lane, g)]);
+                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lr, g)]);
+                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(TW + lr, g)]);
                 }
             } else {
                 for (int g = 0; g < gn; g++) {
-                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lane, g)]);
-                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(kTile + lane, g)]);
+                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lr, g)]);
+                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(TW + lr, g)]);
                 }
                 const int rest = pn & 3;  // rows of a last, partial group
                 if (rest) {
-                    const float4 v = pb[gn * kCols + slot(lane, gn)];
+                    const float4 v = pb[gn * kCols + slot(lr, gn)];
                     acc_lo = acc_lo + v.x;
                     if (rest > 1) acc_lo = acc_lo + v.y;
                     if (rest > 2) acc_lo = acc_lo + v.z;
                     if (KIND == 1) {
-                        const float4 h = pb[gn * kCols + slot(kTile + lane, gn)];
+                        const float4 h = pb[gn * kCols + slot(TW + lr, gn)];
                         acc_hi = acc_hi + h.x;
                         if (rest > 1) acc_hi = acc_hi + h.y;
                         if (rest > 2) acc_hi = acc_hi + h.z;
@@ -212,9 +222,9 @@ __global__ void __launch_bounds__(kThreads)
     // segment s (for int4, the low or the high nibbles of it: hs = 0 or 4).
     const int t = tid - 64;
     const int tj = KIND == 0 ? t : t % 96;
-    const int g = tj >> 2, s = tj & 3;
+    const int g = tj / kSegs, s = tj % kSegs;
     const int hs = KIND == 0 ? 0 : (t / 96) * 4;
-    const int colb = (KIND == 0 ? 0 : (t / 96) * kTile) + s * 16;
+    const int colb = (KIND == 0 ? 0 : (t / 96) * TW) + s * 16;
     u4 wv[2][4];
     float xv[2][4], sv[2][4];
     // Chunk c's rows into register set S (rows past K clamp to K - 1: loaded,
@@ -271,8 +281,16 @@ int launch(fh_ctx* ctx, const fh_qweight* w, const float* x, size_t m, const flo
     const int mi = static_cast<int>(m), ki = static_cast<int>(w->k), ni = static_cast<int>(w->n);
     const int pi = static_cast<int>(w->pitch);
     if (m == 1) {
-        hipLaunchKernelGGL((k_qlinear_row<KIND>), dim3(gx), dim3(kThreads), 0, ctx->stream, w->q, w->scales, x, bias,
-                           y, ki, ni, pi);
+        // the narrowest tile that still keeps the grid within one workgroup per CU
+        if (gx <= 64)
+            hipLaunchKernelGGL((k_qlinear_row<KIND, 16>), dim3(gx * 4), dim3(kThreads), 0, ctx->stream, w->q,
+                               w->scales, x, bias, y, ki, ni, pi);
+        else if (gx <= 128)
+            hipLaunchKernelGGL((k_qlinear_row<KIND, 32>), dim3(gx * 2), dim3(kThreads), 0, ctx->stream, w->q,
+                               w->scales, x, bias, y, ki, ni, pi);
+        else
+            hipLaunchKernelGGL((k_qlinear_row<KIND, 64>), dim3(gx), dim3(kThreads), 0, ctx->stream, w->q, w->scales,
+                               x, bias, y, ki, ni, pi);
     } else {
         hipLaunchKernelGGL((k_qlinear<KIND, 4>), dim3(gx, static_cast<unsigned>((m + 3) / 4)), dim3(kThreads), 0,
                            ctx->stream, w->q, w->scales, x, bias, y, mi, ki, ni, pi);

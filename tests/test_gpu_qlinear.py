@@ -2,7 +2,8 @@
 bit-equal to the oracle's restatement of qaccum_cols (bias first, p
 ascending, no FMA), across int8 / int4, odd widths (the split-half nibble
 layout's last column), several rows of x, K beyond one LDS chunk, the
-one-row kernel's chunk and 4-row-group tails (K = 1, 2, 7, 389), and the
+one-row kernel's chunk and 4-row-group tails (K = 1, 2, 7, 389) and its
+16-, 32- and 64-byte column tiles (chosen by the output width), and the
 reference's dimension errors (ops.rs:316-330)."""
 import numpy as np
 import pytest
@@ -28,7 +29,8 @@ def host(fh, t):
 @pytest.mark.parametrize("m,k,n,bias", [(1, 768, 768, True), (1, 768, 50257, False), (3, 1100, 333, True),
                                         (5, 64, 7, True), (8, 3072, 768, True), (1, 513, 1, True),
                                         (1, 3072, 2304, True), (1, 389, 129, True), (1, 7, 130, False),
-                                        (1, 1, 5, True), (1, 2, 64, True)])
+                                        (1, 1, 5, True), (1, 2, 64, True), (1, 777, 5000, True),
+                                        (1, 1000, 10000, False)])
 def test_qlinear_is_bit_exact(fh, orc, kind, m, k, n, bias):
     import torch
 
