@@ -283,9 +283,11 @@ def main():
         return
 
     if args.leg in ("all", "qlinear"):
-        result["qlinear_gpu"] = qlinear_gpu_leg(ctx, fh, torch, dev, max(args.steps // 10, 10), args.replicas)
+        result["qlinear_gpu"] = qlinear_gpu_leg(ctx, fh, torch, dev, max(args.steps // 10, 10), args.replicas, fh.QINT8)
+        result["qlinear4_gpu"] = qlinear_gpu_leg(ctx, fh, torch, dev, max(args.steps // 10, 10), args.replicas, fh.QINT4)
     if args.leg == "qlinear":
-        print(json.dumps({"leg": "qlinear", "qlinear_int8_gpu": result["qlinear_gpu"]}))
+        print(json.dumps({"leg": "qlinear", "qlinear_int8_gpu": result["qlinear_gpu"],
+                          "qlinear_int4_gpu": result["qlinear4_gpu"]}))
         return
 
     if args.leg in ("all", "qwen"):
@@ -399,6 +401,7 @@ def main():
         "prefill": result["prefill"],
         "qwen2_b64": result.get("qwen2_b64"),
         "qlinear_int8_gpu": result.get("qlinear_gpu"),
+        "qlinear_int4_gpu": result.get("qlinear4_gpu"),
         "hbm_copy_GBps": round(copy_GBps, 1) if copy_GBps else None,
         "shard_head_gemv": result["shard_head"],
     }
@@ -513,18 +516,21 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
                                "numerics": "W8A8 (activations re-quantised to Q8_0), bit-exact with the reference"}}
 
 
-def qlinear_gpu_leg(ctx, fh, torch, dev, steps, replicas):
-    """The reference's per-row int8 path on the GPU: the 49 ops::qlinear calls
-    of a GPT-2-124M decode step (m = 1, bias-first ascending-p sums, the
+def qlinear_gpu_leg(ctx, fh, torch, dev, steps, replicas, kind):
+    """The reference's per-row int8 / int4 path on the GPU: the 49 ops::qlinear
+    calls of a GPT-2-124M decode step (m = 1, bias-first ascending-p sums, the
     reference's bits), random levels and scales, `replicas` weight sets (HBM-
-    forced), one graph per set."""
+    forced), one graph per set.  int4 is the reference's default
+    `run-gguf --quant`."""
     import numpy as np
 
     rng = np.random.default_rng(77)
+    int4 = kind == fh.QINT4
 
     def qw(k, n):
-        return fh.QWeight(ctx, np.abs(rng.standard_normal(k)).astype(np.float32) * 1e-3,
-                          rng.integers(-127, 128, size=k * n, dtype=np.int8).view(np.uint8), k, n, fh.QINT8)
+        levels = (rng.integers(0, 256, size=k * ((n + 1) // 2), dtype=np.uint8) if int4
+                  else rng.integers(-127, 128, size=k * n, dtype=np.int8).view(np.uint8))
+        return fh.QWeight(ctx, np.abs(rng.standard_normal(k)).astype(np.float32) * 1e-3, levels, k, n, kind)
 
     shapes = [(k, n) for (n, k) in LAYER_SHAPES]  # QWeight: k input rows x n outputs
     sets = [([[qw(k, n) for (k, n) in shapes] for _ in range(L)], qw(D, V)) for _ in range(replicas)]
@@ -558,7 +564,8 @@ def qlinear_gpu_leg(ctx, fh, torch, dev, steps, replicas):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
-    qbytes = L * sum(k * n + 4 * k for (k, n) in shapes) + D * V + 4 * D
+    rb = (lambda n: (n + 1) // 2) if int4 else (lambda n: n)  # level bytes per row
+    qbytes = L * sum(k * rb(n) + 4 * k for (k, n) in shapes) + D * rb(V) + 4 * D
     for ws, head in sets:
         head.free()
         for layer in ws:
@@ -568,7 +575,8 @@ def qlinear_gpu_leg(ctx, fh, torch, dev, steps, replicas):
     torch.cuda.synchronize()
     return {"ms_per_step": round(ms, 4), "tok_s": round(1000.0 / ms, 1), "weight_bytes": qbytes,
             "weight_GBps": round(qbytes / (ms * 1e-3) / 1e9, 1), "residency": f"hbm-forced ({replicas} weight sets)",
-            "what": "49 ops::qlinear (per-row int8) of a GPT-2-124M step at m = 1, bit-exact numerics"}
+            "what": f"49 ops::qlinear (per-row {'int4' if int4 else 'int8'}) of a GPT-2-124M step at m = 1, "
+                    "bit-exact numerics"}
 
 
 QWEN05 = dict(vocab=151936, d=896, n_heads=14, n_kv=2, head_dim=64, layers=24, ffn=4864, context=512,

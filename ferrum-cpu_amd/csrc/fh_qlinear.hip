@@ -164,7 +164,12 @@ __global__ void __launch_bounds__(kThreads)
     constexpr int kCols = KIND == 0 ? TW : 2 * TW;             // output columns per workgroup
     __shared__ float4 prod[2][kGroups * kCols];
     const int tid = threadIdx.x, lane = tid & 63;
-    const int lr = lane % TW;  // lanes past the tile mirror lane % TW and store nothing
+    // Summing lanes: one column each (int8; int4 at TW <= 32, lanes < TW on the
+    // low-nibble columns, the next TW on the high ones), or, for int4 at
+    // TW = 64, the low and the high column of byte lane (two chains).
+    constexpr bool kTwo = KIND == 1 && TW == 64;
+    constexpr int kLane = KIND == 0 || kTwo ? TW : 2 * TW;  // lanes that own columns
+    const int lr = lane % kLane;  // lanes past them mirror lane % kLane and store nothing
     const int c0 = blockIdx.x * TW;
     const int half = (n + 1) / 2;
     const int chunks = (k + kRows - 1) / kRows;
@@ -172,10 +177,11 @@ __global__ void __launch_bounds__(kThreads)
 
     // wave-uniform role (a scalar branch: every wave meets the same barriers)
     if (__builtin_amdgcn_readfirstlane(tid >> 6) == 0) {
-        // the summing wave: columns c0 + lane (and half + c0 + lane for int4)
-        const int col_lo = c0 + lr, col_hi = half + c0 + lr;
-        const bool live_lo = lane < TW && (KIND == 0 ? col_lo < n : col_lo < half);
-        const bool live_hi = KIND == 1 && lane < TW && col_hi < n;
+        // the summing wave: column col_lo (and col_hi for int4 at TW = 64)
+        const bool hi_lane = KIND == 1 && !kTwo && lr >= TW;
+        const int col_lo = hi_lane ? half + c0 + lr - TW : c0 + lr, col_hi = half + c0 + lr;
+        const bool live_lo = lane < kLane && col_lo < (KIND == 0 || hi_lane ? n : half);
+        const bool live_hi = kTwo && col_hi < n;
         float acc_lo = bias && live_lo ? bias[col_lo] : 0.0f;
         float acc_hi = bias && live_hi ? bias[col_hi] : 0.0f;
         __syncthreads();  // chunk 0 is in LDS
@@ -186,24 +192,37 @@ __global__ void __launch_bounds__(kThreads)
             auto add4 = [](float acc, float4 v) __attribute__((always_inline)) {
                 return (((acc + v.x) + v.y) + v.z) + v.w;
             };
+            // two chains (int4 at TW = 64) are independent; their adds
+            // alternate so each waits on its own chain only (written one chain
+            // after the other, in-order issue serialises them)
+            auto step = [&](int g) __attribute__((always_inline)) {
+                const float4 v = pb[g * kCols + slot(lr, g)];
+                if constexpr (!kTwo) {
+                    acc_lo = add4(acc_lo, v);
+                } else {
+                    const float4 h = pb[g * kCols + slot(TW + lr, g)];
+                    acc_lo = acc_lo + v.x;
+                    acc_hi = acc_hi + h.x;
+                    acc_lo = acc_lo + v.y;
+                    acc_hi = acc_hi + h.y;
+                    acc_lo = acc_lo + v.z;
+                    acc_hi = acc_hi + h.z;
+                    acc_lo = acc_lo + v.w;
+                    acc_hi = acc_hi + h.w;
+                }
+            };
             if (gn == kGroups) {
 #pragma unroll 32
-                for (int g = 0; g < kGroups; g++) {
-                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lr, g)]);
-                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(TW + lr, g)]);
-                }
+                for (int g = 0; g < kGroups; g++) step(g);
             } else {
-                for (int g = 0; g < gn; g++) {
-                    acc_lo = add4(acc_lo, pb[g * kCols + slot(lr, g)]);
-                    if (KIND == 1) acc_hi = add4(acc_hi, pb[g * kCols + slot(TW + lr, g)]);
-                }
+                for (int g = 0; g < gn; g++) step(g);
                 const int rest = pn & 3;  // rows of a last, partial group
                 if (rest) {
                     const float4 v = pb[gn * kCols + slot(lr, gn)];
                     acc_lo = acc_lo + v.x;
                     if (rest > 1) acc_lo = acc_lo + v.y;
                     if (rest > 2) acc_lo = acc_lo + v.z;
-                    if (KIND == 1) {
+                    if (kTwo) {
                         const float4 h = pb[gn * kCols + slot(TW + lr, gn)];
                         acc_hi = acc_hi + h.x;
                         if (rest > 1) acc_hi = acc_hi + h.y;
