@@ -147,19 +147,23 @@ __global__ void __launch_bounds__(kThreads)
 // producers' 16-byte writes spread over the banks; the summing wave reads one
 // contiguous group row, conflict-free under any permutation.
 //
-// TW is the column tile in bytes (16, 32 or 64).  Every chunk is 48 KB of
-// products whatever TW is, so a narrow tile means a long chunk: for a narrow
-// output the chain then runs ~4x longer per chunk against the same LDS
-// traffic, and the producers' writes no longer hold up the summing wave's
-// reads (a dependent f32 add takes ~5.75 cycles; at TW = 64 the products'
-// write and read take ~70 % of the CU's LDS bandwidth during the chain).
+// TW is the column tile in bytes (16, 32 or 64).  At 16 and 32 a chunk is
+// 48 KB of products, so a narrow tile means a long chunk: for a narrow output
+// the chain then runs ~4x longer per chunk against the same LDS traffic, and
+// the producers' writes no longer hold up the summing wave's reads (a
+// dependent f32 add takes ~5.75 cycles; with 64-byte tiles and 48 KB chunks
+// the products' write and read took ~70 % of the CU's LDS bandwidth during the
+// chain).  TW = 64 serves wide outputs (more tiles than CUs): its chunks are
+// 32 KB, so two workgroups share a CU, and two producer waves fill a chunk
+// (the third repeats their work, writing the same values).
 template <int KIND, int TW>
 __global__ void __launch_bounds__(kThreads)
     k_qlinear_row(const uint8_t* __restrict__ q, const float* __restrict__ scales, const float* __restrict__ x,
                   const float* __restrict__ bias, float* __restrict__ y, int k, int n, int pitch) {
     static_assert(TW == 16 || TW == 32 || TW == 64, "column tile of 16, 32 or 64 bytes");
     constexpr int kSegs = TW / 16;                             // 16-byte segments per row tile
-    constexpr int kRows = (KIND == 0 ? 768 : 384) / kSegs;     // rows p per chunk: 192 producer jobs
+    constexpr int kRows = TW == 64 ? (KIND == 0 ? 128 : 64)     // rows p per chunk: 128 producer jobs
+                                   : (KIND == 0 ? 768 : 384) / kSegs;  // 192 producer jobs
     constexpr int kGroups = kRows / 4;
     constexpr int kCols = KIND == 0 ? TW : 2 * TW;             // output columns per workgroup
     __shared__ float4 prod[2][kGroups * kCols];
@@ -239,11 +243,12 @@ __global__ void __launch_bounds__(kThreads)
 
     // The producers: thread t owns rows 4g..4g+3 of a chunk and 16-byte column
     // segment s (for int4, the low or the high nibbles of it: hs = 0 or 4).
+    constexpr int kHalfJobs = kGroups * kSegs;  // jobs per nibble half (int4) or per chunk (int8)
     const int t = tid - 64;
-    const int tj = KIND == 0 ? t : t % 96;
+    const int tj = t % kHalfJobs, h = KIND == 0 ? 0 : (t / kHalfJobs) % 2;
     const int g = tj / kSegs, s = tj % kSegs;
-    const int hs = KIND == 0 ? 0 : (t / 96) * 4;
-    const int colb = (KIND == 0 ? 0 : (t / 96) * TW) + s * 16;
+    const int hs = h * 4;
+    const int colb = h * TW + s * 16;
     u4 wv[2][4];
     float xv[2][4], sv[2][4];
     // Chunk c's rows into register set S (rows past K clamp to K - 1: loaded,
