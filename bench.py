@@ -100,7 +100,7 @@ def main():
     ap.add_argument("--leg", choices=["all", "head", "prefill", "qwen", "qlinear"], default="all",
                     help="'head': only the lm_head GEMV roofline leg (for counter runs); "
                          "'prefill': only the GPT-2-medium prefill GEMMs; 'qwen': only the Qwen2-shaped "
-                         "batch-64 step; 'qlinear': only the per-row int8 qlinear step")
+                         "batch-64 step; 'qlinear': only the per-row int8 and int4 qlinear steps")
     ap.add_argument("--prefill-steps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
