@@ -30,7 +30,7 @@ def host(fh, t):
                                         (5, 64, 7, True), (8, 3072, 768, True), (1, 513, 1, True),
                                         (1, 3072, 2304, True), (1, 389, 129, True), (1, 7, 130, False),
                                         (1, 1, 5, True), (1, 2, 64, True), (1, 777, 5000, True),
-                                        (1, 1000, 10000, False)])
+                                        (1, 1000, 10000, False), (1, 1001, 9000, True)])
 def test_qlinear_is_bit_exact(fh, orc, kind, m, k, n, bias):
     import torch
 
