@@ -315,7 +315,7 @@ def main():
     achieved = head_bytes / (head_us * 1e-6) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
-                "kernel": "k_gemv_w8a32<16,3,1,4,false> (lm_head 50257x768, Q8_0, m=1)",
+                "kernel": "k_gemv_w8a32<16,3,1,4,false,false> (lm_head 50257x768, Q8_0, m=1)",
                 "avg_launch_us": round(head_us, 3), "bytes_per_launch": head_bytes}
     copy_GBps = None
     if args.leg == "all":  # (kept out of the counter runs: their copy calibration must see one size)
