@@ -73,7 +73,12 @@ static int zeroed_area(fh_ctx* ctx, void** area, size_t* area_bytes, size_t byte
             *area_bytes = 0;
         }
         FH_HIP(ctx, hipMalloc(area, bytes));
-        FH_HIP(ctx, hipMemset(*area, 0, bytes));
+        // Zeroed on the context's stream and waited for: the stream is
+        // non-blocking, so a memset on the legacy default stream would not be
+        // ordered before the kernels that use the area (a kernel could start,
+        // publish into it, and have the late memset wipe what it published).
+        FH_HIP(ctx, hipMemsetAsync(*area, 0, bytes, ctx->stream));
+        FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
         *area_bytes = bytes;
     }
     *out = *area;
@@ -97,6 +102,28 @@ static hipError_t on_device(int device) {
     return hipSetDevice(device);
 }
 #define FH_ON_DEVICE(ctx) FH_HIP((ctx), on_device((ctx)->device))
+
+int fh_take_status(fh_ctx* ctx) {
+    unsigned bits = 0;
+    FH_HIP(ctx, hipMemcpyAsync(&bits, ctx->status, sizeof(bits), hipMemcpyDeviceToHost, ctx->stream));
+    FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (bits == 0) return FH_OK;
+    FH_HIP(ctx, hipMemsetAsync(ctx->status, 0, sizeof(unsigned), ctx->stream));
+    FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+    if (bits & FH_STATUS_EXCHANGE) {
+        // A failed exchange can leave a row's survivor count or slots behind
+        // its generation: start every row over from a zeroed area (tag 0 is
+        // never a live tag, so no stale slot is taken for a fresh one).
+        if (ctx->sync) {
+            FH_HIP(ctx, hipMemsetAsync(ctx->sync, 0, ctx->sync_bytes, ctx->stream));
+            FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+        }
+        return fh_fail(ctx, FH_ERR_EXCHANGE,
+                       "a kernel's cross-workgroup wait gave up (its workgroups were not all resident at once); "
+                       "the results since the last fh_sync are unreliable");
+    }
+    return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: recent_offsets decrease");
+}
 
 extern "C" {
 
@@ -130,9 +157,20 @@ int fh_ctx_create(int device, fh_ctx** out) {
     if (hipDeviceGetAttribute(&c->num_cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess ||
         c->num_cus < 1)
         c->num_cus = 1;
+    void* st = nullptr;
+    if ((e = hipMalloc(&st, 256)) != hipSuccess || (e = hipMemsetAsync(st, 0, 256, c->own)) != hipSuccess ||
+        (e = hipStreamSynchronize(c->own)) != hipSuccess) {
+        int code = fh_hip_fail(nullptr, e, "fh_ctx_create (status word)");
+        if (st) (void)hipFree(st);
+        (void)hipStreamDestroy(c->own);
+        delete c;
+        return code;
+    }
+    c->status = static_cast<unsigned*>(st);
     *out = c;
     return FH_OK;
 }
+
 
 void fh_ctx_destroy(fh_ctx* ctx) {
     if (!ctx) return;
@@ -142,6 +180,7 @@ void fh_ctx_destroy(fh_ctx* ctx) {
     if (ctx->sync) (void)hipFree(ctx->sync);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->act) (void)hipFree(ctx->act);
+    if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
 }
@@ -165,7 +204,7 @@ int fh_sync(fh_ctx* ctx) {
     ctx->err.clear();
     FH_ON_DEVICE(ctx);
     FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
-    return FH_OK;
+    return fh_take_status(ctx);
 }
 
 const char* fh_last_error(const fh_ctx* ctx) { return ctx ? ctx->err.c_str() : g_create_err.c_str(); }
@@ -403,8 +442,6 @@ int fh_q8_0_block_dots_async(fh_ctx* ctx, const fh_q8_0* w, const int8_t* d_qx, 
 
 // ---- sampler -------------------------------------------------------------------
 
-enum { FH_MAX_RECENT = 16384 };
-
 static int check_sample(fh_ctx* ctx, size_t rows, size_t vocab, int kind, const fh_sampling_params* p) {
     if (!p) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: params is NULL");
     if (kind != FH_LOGITS_RAW && kind != FH_LOGITS_GPT2_SOFTMAX)
@@ -420,10 +457,6 @@ static int check_offsets(fh_ctx* ctx, const uint32_t* off, size_t rows, const vo
     for (size_t r = 0; r < rows; r++) {
         if (off[r + 1] < off[r])
             return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: recent_offsets decrease at row " + std::to_string(r));
-        if (off[r + 1] - off[r] > FH_MAX_RECENT)
-            return fh_fail(ctx, FH_ERR_LIMIT, "fh_sample_rows: row " + std::to_string(r) + " has " +
-                                                  std::to_string(off[r + 1] - off[r]) +
-                                                  " recent ids, above the limit of 16384");
     }
     if (off[rows] != off[0] && !recent) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: recent is NULL");
     return FH_OK;
@@ -440,8 +473,8 @@ int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t
     if (!d_logits || !d_out) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: logits or out_ids is NULL");
     if (!d_draws && !(p->temperature <= 0.0f))
         return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: draws is NULL with temperature > 0");
-    // Device offsets cannot be inspected without a copy; the kernel clamps each
-    // row's list to FH_MAX_RECENT ids and ignores decreasing offsets.
+    // Device offsets cannot be inspected without a copy: the kernels record
+    // decreasing offsets in the status word, which fh_sync reports.
     FH_ON_DEVICE(ctx);
     return fh_launch_sample(ctx, d_logits, rows, vocab, kind, p, d_recent, d_off, d_draws, d_out);
 }
@@ -493,9 +526,18 @@ int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, 
     }
     e = hipStreamSynchronize(ctx->stream);
     if (rc == FH_OK && e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_sample_rows sync");
+    if (rc == FH_OK) rc = fh_take_status(ctx);
     delete[] hoff;
     (void)hipFree(dev);
     return rc;
+}
+
+int fh_debug_sampler_faults(fh_ctx* ctx, int skip_segment, uint32_t spin_limit) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    ctx->test_skip_segment = skip_segment < 0 ? -1 : skip_segment;
+    ctx->test_spin_limit = spin_limit;
+    return FH_OK;
 }
 
 }  // extern "C"

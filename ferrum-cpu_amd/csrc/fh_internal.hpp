@@ -41,7 +41,22 @@ struct fh_ctx {
     // linear), separate from ws, which the linear itself may use.
     void* act = nullptr;
     size_t act_bytes = 0;
+    // Device status word: kernels OR in FH_STATUS_* bits (a bounded wait that
+    // gave up, decreasing recent offsets); fh_sync and the blocking calls read
+    // and clear it.
+    unsigned* status = nullptr;
+    // Workgroups of the split sampler one CU holds at once (occupancy API;
+    // -1 until asked).
+    int split_per_cu = -1;
+    // Testing hooks (fh_debug_sampler_faults): a split-sampler segment that
+    // publishes nothing, and a lower poll limit for the bounded waits.
+    int test_skip_segment = -1;
+    unsigned test_spin_limit = 0;
 };
+
+// Read and clear ctx->status after the stream has drained; FH_OK or the error
+// its bits stand for.
+int fh_take_status(fh_ctx* ctx);
 
 constexpr int8_t kFhBadRowExp = -128;
 

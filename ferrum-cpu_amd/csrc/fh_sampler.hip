@@ -52,7 +52,6 @@ constexpr int kCopies = 16;     // histogram copies (lane & 15) against same-bin
 constexpr int kSlots = 8192;    // repetition-penalty hash table
 constexpr int kChunk = 4096;    // recent ids deduplicated per table fill
 constexpr uint32_t kEmpty = 0xFFFFFFFFu;
-constexpr int kMaxRecent = 16384;
 constexpr int kMaxItems = 50;   // register-resident rows: vocab <= kMaxItems * kT (51,200; GPT-2's 50,257)
 
 struct Shared {
@@ -846,7 +845,26 @@ struct Params {
     float pen;
     int kind;
     int n;
+    // Cross-workgroup waits of the split kernel give up after this many polls
+    // (kSpinLimit unless a test lowers it).
+    unsigned spin_limit;
+    // Testing hook: the segment whose workgroup publishes nothing (-1: none),
+    // so its readers' bounded waits give up and report FH_STATUS_EXCHANGE.
+    int skip_seg;
 };
+
+// The recent list of a row: offsets[row] .. offsets[row + 1].  Decreasing
+// offsets are recorded in the status word (and the row gets no penalty).
+__device__ __forceinline__ int recent_len(const uint32_t* __restrict__ offsets, size_t row, unsigned* status,
+                                          const uint32_t** rec, const uint32_t* __restrict__ recent) {
+    const uint32_t r0 = offsets[row], r1 = offsets[row + 1];
+    *rec = recent + r0;
+    if (r1 < r0) {
+        if (threadIdx.x == 0) atomicOr(status, static_cast<unsigned>(FH_STATUS_BAD_OFFSETS));
+        return 0;
+    }
+    return static_cast<int>(min(r1 - r0, 0x7FFFFFFFu));
+}
 
 template <class Row>
 __device__ __forceinline__ void sample_row(Shared& s, Row& row, const Params& P, const float* __restrict__ z,
@@ -1013,16 +1031,12 @@ template <int ITEMS>
 __global__ void __launch_bounds__(kT)
     k_sample_regs(const float* __restrict__ logits, Params P, const uint32_t* __restrict__ recent,
                   const uint32_t* __restrict__ offsets, const uint64_t* __restrict__ draws,
-                  uint32_t* __restrict__ out) {
+                  uint32_t* __restrict__ out, unsigned* __restrict__ status) {
     __shared__ Shared s;
     const size_t row = blockIdx.x;
     int nrec = 0;
     const uint32_t* rec = nullptr;
-    if (offsets && recent) {
-        const uint32_t r0 = offsets[row], r1 = offsets[row + 1];
-        nrec = r1 > r0 ? static_cast<int>(min(r1 - r0, static_cast<uint32_t>(kMaxRecent))) : 0;
-        rec = recent + r0;
-    }
+    if (offsets && recent) nrec = recent_len(offsets, row, status, &rec, recent);
     RegRow<ITEMS> st;
     st.n = P.n;
     const bool has_draw = draws != nullptr;
@@ -1033,16 +1047,12 @@ __global__ void __launch_bounds__(kT)
 __global__ void __launch_bounds__(kT)
     k_sample_global(const float* __restrict__ logits, Params P, const uint32_t* __restrict__ recent,
                     const uint32_t* __restrict__ offsets, const uint64_t* __restrict__ draws,
-                    uint32_t* __restrict__ out, float* __restrict__ work) {
+                    uint32_t* __restrict__ out, float* __restrict__ work, unsigned* __restrict__ status) {
     __shared__ Shared s;
     const size_t row = blockIdx.x;
     int nrec = 0;
     const uint32_t* rec = nullptr;
-    if (offsets && recent) {
-        const uint32_t r0 = offsets[row], r1 = offsets[row + 1];
-        nrec = r1 > r0 ? static_cast<int>(min(r1 - r0, static_cast<uint32_t>(kMaxRecent))) : 0;
-        rec = recent + r0;
-    }
+    if (offsets && recent) nrec = recent_len(offsets, row, status, &rec, recent);
     GlobalRow st;
     st.n = P.n;
     st.w = work + row * static_cast<size_t>(P.n);
@@ -1071,9 +1081,12 @@ __global__ void __launch_bounds__(kT)
 // stale slot (the previous launch's tag) is never taken for a fresh one — which
 // keeps the state valid across HIP graph replays.  The launcher keeps rows * S
 // <= the number of CUs with one workgroup per CU (the kernel's LDS allows no
-// more), so every workgroup of a row is resident together; every poll is
-// bounded: a slot still stale after kSpinLimit polls records an error and the
-// workgroup goes on.
+// more, and checks that with the occupancy API), so every workgroup of a row
+// is resident together; every poll is bounded: a slot still stale after
+// P.spin_limit polls sets FH_STATUS_EXCHANGE in the context's status word
+// (which fh_sync and the blocking call report) and the workgroup goes on with
+// what it has.  Every index derived from exchanged data is clamped, so a
+// failed exchange gives a wrong id, never an out-of-bounds access.
 
 constexpr int kSMax = 64;
 constexpr unsigned kSpinLimit = 1u << 20;
@@ -1081,7 +1094,7 @@ enum { kPhGpt2 = 0, kPhTemp = 1, kPhGreedy = 2, kPhSeg = 3, kPhDone = 4, kPhases
 
 struct RowSync {
     unsigned gen;
-    unsigned err;
+    unsigned unused;
     unsigned n_cand;  // survivors appended so far (workgroup 0 zeroes it when done)
     unsigned pad[13];
     unsigned long long a[kPhases][kSMax];  // payload A | tag
@@ -1112,21 +1125,27 @@ __device__ __forceinline__ unsigned long long tagi(int v, unsigned tag) {
 __device__ __forceinline__ float untagf(unsigned long long x) { return __builtin_bit_cast(float, static_cast<uint32_t>(x)); }
 __device__ __forceinline__ int untagi(unsigned long long x) { return static_cast<int>(static_cast<uint32_t>(x)); }
 
+// Where a bounded wait reports that it gave up, and after how many polls.
+struct Waits {
+    unsigned* status;
+    unsigned limit;
+};
+
 // Poll one slot until it carries `tag` (bounded).
-__device__ __forceinline__ unsigned long long poll(RowSync* rs, const unsigned long long* slot, unsigned tag) {
+__device__ __forceinline__ unsigned long long poll(const Waits& wt, const unsigned long long* slot, unsigned tag) {
     unsigned spins = 0;
     while (true) {
         const unsigned long long x = cload(slot);
         if (static_cast<unsigned>(x >> 32) == tag) return x;
         __builtin_amdgcn_s_sleep(1);
-        if (++spins == kSpinLimit) {
-            atomicOr(&rs->err, 1u);
+        if (++spins >= wt.limit) {
+            atomicOr(wt.status, static_cast<unsigned>(FH_STATUS_EXCHANGE));
             return x;
         }
     }
 }
 // Poll two slots at once (both loads in flight per round).
-__device__ __forceinline__ void poll2(RowSync* rs, const unsigned long long* p, const unsigned long long* q,
+__device__ __forceinline__ void poll2(const Waits& wt, const unsigned long long* p, const unsigned long long* q,
                                       unsigned tag, unsigned long long* x, unsigned long long* y) {
     unsigned spins = 0;
     while (true) {
@@ -1134,16 +1153,18 @@ __device__ __forceinline__ void poll2(RowSync* rs, const unsigned long long* p, 
         *y = cload(q);
         if (static_cast<unsigned>(*x >> 32) == tag && static_cast<unsigned>(*y >> 32) == tag) return;
         __builtin_amdgcn_s_sleep(1);
-        if (++spins == kSpinLimit) {
-            atomicOr(&rs->err, 1u);
+        if (++spins >= wt.limit) {
+            atomicOr(wt.status, static_cast<unsigned>(FH_STATUS_EXCHANGE));
             return;
         }
     }
 }
 
-// Thread 0 publishes this workgroup's pair for `phase`.
-__device__ __forceinline__ void publish(RowSync* rs, int phase, int w, unsigned long long a, unsigned long long b) {
-    if (threadIdx.x == 0) {
+// Thread 0 publishes this workgroup's pair for `phase` (the testing hook
+// P.skip_seg silences one segment).
+__device__ __forceinline__ void publish(RowSync* rs, int phase, int w, unsigned long long a, unsigned long long b,
+                                        int skip_seg) {
+    if (threadIdx.x == 0 && w != skip_seg) {
         cstore(&rs->a[phase][w], a);
         cstore(&rs->b[phase][w], b);
     }
@@ -1151,11 +1172,11 @@ __device__ __forceinline__ void publish(RowSync* rs, int phase, int w, unsigned 
 
 // Every workgroup's pair for `phase` into s.pa / s.pb (float view) and
 // s.qa / s.qb (int view); whole-workgroup call.
-__device__ __forceinline__ void gather(Shared& s, RowSync* rs, int phase, int S, unsigned tag) {
+__device__ __forceinline__ void gather(Shared& s, const Waits& wt, RowSync* rs, int phase, int S, unsigned tag) {
     const int tid = threadIdx.x;
     if (tid < S) {
         unsigned long long x, y;
-        poll2(rs, &rs->a[phase][tid], &rs->b[phase][tid], tag, &x, &y);
+        poll2(wt, &rs->a[phase][tid], &rs->b[phase][tid], tag, &x, &y);
         s.pa[tid] = untagf(x);
         s.pb[tid] = untagf(y);
         s.qa[tid] = untagi(x);
@@ -1199,12 +1220,14 @@ template <int ITEMS>
 __global__ void __launch_bounds__(kT)
     k_sample_split(const float* __restrict__ logits, Params P, const uint32_t* __restrict__ recent,
                    const uint32_t* __restrict__ offsets, const uint64_t* __restrict__ draws,
-                   uint32_t* __restrict__ out, RowSync* __restrict__ sync, float* __restrict__ pbuf, int S) {
+                   uint32_t* __restrict__ out, RowSync* __restrict__ sync, float* __restrict__ pbuf, int S,
+                   unsigned* __restrict__ status) {
     __shared__ Shared s;
     const int tid = threadIdx.x;
     const int row = blockIdx.x / S, w = blockIdx.x % S;
     const int n = P.n;
     RowSync* rs = sync + row;
+    const Waits wt{status, P.spin_limit};
     const unsigned gen = cload(&rs->gen);
     const unsigned tag = gen + 1;
     const float* z = logits + static_cast<size_t>(row) * n;
@@ -1228,11 +1251,7 @@ __global__ void __launch_bounds__(kT)
     const float pen = P.pen;
     int nrec = 0;
     const uint32_t* rec = nullptr;
-    if (offsets && recent) {
-        const uint32_t r0 = offsets[row], r1 = offsets[row + 1];
-        nrec = r1 > r0 ? static_cast<int>(min(r1 - r0, static_cast<uint32_t>(kMaxRecent))) : 0;
-        rec = recent + r0;
-    }
+    if (offsets && recent) nrec = recent_len(offsets, row, status, &rec, recent);
     const bool use_pen = fabsf(pen - 1.0f) > FLT_EPSILON && pen > 0.0f && nrec > 0;
     auto fill = [&](int b0) __attribute__((always_inline)) {
         for (int i = tid; i < kSlots; i += kT) {
@@ -1277,8 +1296,8 @@ __global__ void __launch_bounds__(kT)
     if (P.kind == FH_LOGITS_GPT2_SOFTMAX) {
         float m, sm;
         block_softmax_stats(s, st, 1.0f, false, &m, &sm);
-        publish(rs, kPhGpt2, w, tagf(m, tag), tagf(sm, tag));
-        gather(s, rs, kPhGpt2, S, tag);
+        publish(rs, kPhGpt2, w, tagf(m, tag), tagf(sm, tag), P.skip_seg);
+        gather(s, wt, rs, kPhGpt2, S, tag);
         float M, Z;
         merge_segments(s, S, 1.0f, false, &M, &Z);
         st.map([&](float x, int) { return logf(fmaxf(expf(x - M) / Z, 1e-12f)); });
@@ -1303,9 +1322,9 @@ __global__ void __launch_bounds__(kT)
         });
         const int best = block_max_i(s, bk);
         const int first = block_min_i(s, bk == best ? bi : INT_MAX);
-        publish(rs, kPhGreedy, w, tagi(best, tag), tagi(first, tag));
+        publish(rs, kPhGreedy, w, tagi(best, tag), tagi(first, tag), P.skip_seg);
         if (w != 0) return;
-        gather(s, rs, kPhGreedy, S, tag);
+        gather(s, wt, rs, kPhGreedy, S, tag);
         if (tid == 0) {
             int gk = INT_MIN, gi = INT_MAX;
             for (int v = 0; v < S; v++) {  // segments in index order: strict '>' keeps the first
@@ -1328,9 +1347,9 @@ __global__ void __launch_bounds__(kT)
     {
         float m, sm;
         block_softmax_stats(s, st, t, true, &m, &sm);
-        publish(rs, kPhTemp, w, tagf(m, tag), tagf(sm, tag));
+        publish(rs, kPhTemp, w, tagf(m, tag), tagf(sm, tag), P.skip_seg);
     }
-    gather(s, rs, kPhTemp, S, tag);
+    gather(s, wt, rs, kPhTemp, S, tag);
     float mx, sum;
     merge_segments(s, S, t, true, &mx, &sum);
     if (sum != sum || sum <= 1e-10f) {
@@ -1371,18 +1390,20 @@ __global__ void __launch_bounds__(kT)
                 c += s.hist[k][tid];
                 ms += s.mass[k][tid];
             }
-            if (!use_k) {
-                cstore(&rs->mass[w][tid], ms);
-                stores_done();
+            if (w != P.skip_seg) {
+                if (!use_k) {
+                    cstore(&rs->mass[w][tid], ms);
+                    stores_done();
+                }
+                cstore(&rs->hist[w][tid], tagi(static_cast<int>(c), tag));
             }
-            cstore(&rs->hist[w][tid], tagi(static_cast<int>(c), tag));
         }
         // every segment's histogram, summed in segment order
         uint32_t* hc = reinterpret_cast<uint32_t*>(s.u.cand);                     // [S][kBuckets]
         unsigned long long* hm = s.u.cand + (kSMax * kBuckets) / 2;                 // [S][kBuckets]
         for (int i = tid; i < S * kBuckets; i += kT) {
             const int v = i / kBuckets, b = i % kBuckets;
-            hc[i] = static_cast<uint32_t>(poll(rs, &rs->hist[v][b], tag));
+            hc[i] = static_cast<uint32_t>(poll(wt, &rs->hist[v][b], tag));
             if (!use_k) hm[i] = cload(&rs->mass[v][b]);
         }
         __syncthreads();
@@ -1411,22 +1432,29 @@ __global__ void __launch_bounds__(kT)
                 unsigned base = 0;
                 if (lane == leader) base = atomicAdd(&rs->n_cand, static_cast<unsigned>(__popcll(mask)));
                 base = __builtin_amdgcn_readlane(base, leader);
-                if (take) cstore(&rs->cand[base + __popcll(mask & ((1ull << lane) - 1ull))], cand_key(p, i));
+                // (at most kCap survivors when the histograms were exchanged
+                // intact; the bound only matters after a failed exchange)
+                const unsigned at = base + static_cast<unsigned>(__popcll(mask & ((1ull << lane) - 1ull)));
+                if (take && at < static_cast<unsigned>(kCap)) cstore(&rs->cand[at], cand_key(p, i));
             });
         }
         stores_done();
         __syncthreads();
-        publish(rs, kPhDone, w, tagi(0, tag), tagi(0, tag));
+        publish(rs, kPhDone, w, tagi(0, tag), tagi(0, tag), P.skip_seg);
         if (w != 0) return;
-        gather(s, rs, kPhDone, S, tag);
+        gather(s, wt, rs, kPhDone, S, tag);
         int n_list = -1;
         bool done = false;
         if (depth >= 0) {
             // the count and the first 64 keys in one round trip
             unsigned long long key = 0;
             if (tid < 64) key = cload(&rs->cand[tid]);
-            const int nc = static_cast<int>(cload(&rs->n_cand));
-            if (nc <= 64) {
+            const unsigned nc_all = cload(&rs->n_cand);
+            const int nc = static_cast<int>(min(nc_all, static_cast<unsigned>(kCap)));
+            if (nc_all > static_cast<unsigned>(kCap)) {
+                // only after a failed exchange: the list is incomplete, take
+                // the general path over the row
+            } else if (nc <= 64) {
                 if (tid < 64) {
                     const bool ok = wave_tail(key, nc, P.top_k, P.top_p, use_k, use_p, r, o);
                     if (tid == 0) s.bi[2] = ok;
@@ -1464,9 +1492,9 @@ __global__ void __launch_bounds__(kT)
         });
         loc = block_sum(s, loc);
         lastid = block_max_i(s, lastid);
-        publish(rs, kPhSeg, w, tagf(loc, tag), tagi(lastid, tag));
+        publish(rs, kPhSeg, w, tagf(loc, tag), tagi(lastid, tag), P.skip_seg);
     }
-    gather(s, rs, kPhSeg, S, tag);
+    gather(s, wt, rs, kPhSeg, S, tag);
     float sum2 = 0.0f, before = 0.0f;
     for (int v = 0; v < S; v++) {
         if (v == w) before = sum2;
@@ -1480,13 +1508,13 @@ __global__ void __launch_bounds__(kT)
     const float mine = s.pa[w] / sum2;
     int first = INT_MAX;
     if (r <= cum0 + mine || w == S - 1) first = draw_scan_from(s, st, sum2, r, cum0);
-    publish(rs, kPhDone, w, tagi(first, tag), tagi(0, tag));
+    publish(rs, kPhDone, w, tagi(first, tag), tagi(0, tag), P.skip_seg);
     if (w != 0) return;
     // s.qb still holds every segment's last id with mass (gathered above)
     int lastg = -1;
     for (int v = 0; v < S; v++) lastg = max(lastg, s.qb[v]);
     __syncthreads();
-    gather(s, rs, kPhDone, S, tag);
+    gather(s, wt, rs, kPhDone, S, tag);
     if (tid == 0) {
         int pick = INT_MAX;
         for (int v = 0; v < S; v++) pick = min(pick, s.qa[v]);
@@ -1499,7 +1527,7 @@ template <int ITEMS>
 int launch_split(fh_ctx* ctx, size_t rows, int S, const float* logits, const Params& P, const uint32_t* recent,
                  const uint32_t* offsets, const uint64_t* draws, uint32_t* out, void* sync, float* pbuf) {
     hipLaunchKernelGGL(k_sample_split<ITEMS>, dim3(static_cast<unsigned>(rows * S)), dim3(kT), 0, ctx->stream,
-                       logits, P, recent, offsets, draws, out, static_cast<RowSync*>(sync), pbuf, S);
+                       logits, P, recent, offsets, draws, out, static_cast<RowSync*>(sync), pbuf, S, ctx->status);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -1508,7 +1536,7 @@ template <int ITEMS>
 int launch_regs(fh_ctx* ctx, size_t rows, const float* logits, const Params& P, const uint32_t* recent,
                 const uint32_t* offsets, const uint64_t* draws, uint32_t* out) {
     hipLaunchKernelGGL(k_sample_regs<ITEMS>, dim3(static_cast<unsigned>(rows)), dim3(kT), 0, ctx->stream, logits, P,
-                       recent, offsets, draws, out);
+                       recent, offsets, draws, out, ctx->status);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -1526,17 +1554,32 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
     P.pen = p->repetition_penalty;
     P.kind = kind;
     P.n = static_cast<int>(vocab);
-    // Split rows over S workgroups while a launch's rows * S fit one
-    // workgroup per CU (the kernel's LDS allows one per CU, so all workgroups
+    P.spin_limit = ctx->test_spin_limit ? ctx->test_spin_limit : kSpinLimit;
+    P.skip_seg = ctx->test_skip_segment;
+    // Split rows over S workgroups while a launch's rows * S fit the device
+    // at once: the occupancy API gives how many of the split kernel's
+    // workgroups a CU holds (one: its LDS allows no more), so all workgroups
     // of a launch are resident together and their exchanges cannot wait on an
-    // undispatched one): for rows of at least 8192 ids, the fewest ids per
+    // undispatched one.  For rows of at least 8192 ids, the fewest ids per
     // thread that fits all rows in one launch; when none does, consecutive
     // launches of as many rows as fit (fewest launches, at most 8), each row
     // keeping its own exchange slots.
     const size_t items = (vocab + kT - 1) / kT;
-    if (vocab >= 8192 && rows <= 1024) {
+    if (ctx->split_per_cu < 0) {  // the least over the instances below
+        const void* ks[] = {reinterpret_cast<const void*>(k_sample_split<2>), reinterpret_cast<const void*>(k_sample_split<4>),
+                            reinterpret_cast<const void*>(k_sample_split<8>), reinterpret_cast<const void*>(k_sample_split<16>),
+                            reinterpret_cast<const void*>(k_sample_split<32>)};
+        int least = 1 << 30;
+        for (const void* k : ks) {
+            int per = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, k, kT, 0) != hipSuccess) per = 0;
+            least = per < least ? per : least;
+        }
+        ctx->split_per_cu = least;
+    }
+    if (vocab >= 8192 && rows <= 1024 && ctx->split_per_cu > 0) {
         static const int kOpts[] = {2, 4, 8, 16, 32};
-        const size_t cus = static_cast<size_t>(ctx->num_cus);
+        const size_t cus = static_cast<size_t>(ctx->num_cus) * static_cast<size_t>(ctx->split_per_cu);
         int pick = 0;
         size_t pick_rows = 0, pick_launches = 9;
         for (int it : kOpts) {
@@ -1585,7 +1628,7 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
     int rc = fh_workspace(ctx, rows * vocab * sizeof(float), &ws);
     if (rc) return rc;
     hipLaunchKernelGGL(k_sample_global, dim3(static_cast<unsigned>(rows)), dim3(kT), 0, ctx->stream, logits, P, recent,
-                       offsets, draws, out, static_cast<float*>(ws));
+                       offsets, draws, out, static_cast<float*>(ws), ctx->status);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }

@@ -33,7 +33,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libferrum_hip.so")
 
-FH_OK, FH_ERR_DIM, FH_ERR_INVALID, FH_ERR_OOM, FH_ERR_HIP, FH_ERR_LIMIT, FH_ERR_FORMAT = range(7)
+FH_OK, FH_ERR_DIM, FH_ERR_INVALID, FH_ERR_OOM, FH_ERR_HIP, FH_ERR_LIMIT, FH_ERR_FORMAT, FH_ERR_EXCHANGE = range(8)
 W8A32, W8A8 = 0, 1
 LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
 
@@ -42,7 +42,7 @@ EXPORTS = (
     "fh_device_count", "fh_q8_0_upload", "fh_q8_0_upload_device", "fh_q8_0_download",
     "fh_q8_0_dims", "fh_q8_0_free", "fh_q8_0_linear", "fh_q8_0_linear_async",
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
-    "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async",
+    "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async", "fh_debug_sampler_faults",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
     "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
@@ -163,6 +163,7 @@ def lib():
         L.fh_q8_0_block_dots_async.argtypes = [vp, vp, vp, sz, vp]
         L.fh_sample_rows.argtypes = [vp, vp, sz, sz, i32, C.POINTER(SamplingParams), vp, vp, vp, vp]
         L.fh_sample_rows_async.argtypes = [vp, vp, sz, sz, i32, C.POINTER(SamplingParams), vp, vp, vp, vp]
+        L.fh_debug_sampler_faults.argtypes = [vp, i32, C.c_uint32]
         L.fh_embed_one_async.argtypes = [vp, vp, vp, sz, sz, sz, vp, sz, vp]
         L.fh_layernorm_async.argtypes = [vp, vp, sz, sz, vp, vp, vp]
         L.fh_gelu_async.argtypes = [vp, vp, sz]
@@ -248,7 +249,14 @@ class Context:
             self.check(lib().fh_ctx_set_stream(self.h, stream_handle))
 
     def sync(self):
+        """Wait for the context's stream; raises what its kernels recorded since
+        the last sync (FH_ERR_EXCHANGE for a bounded wait that gave up)."""
         self.check(lib().fh_sync(self.h))
+
+    def debug_sampler_faults(self, skip_segment: int = -1, spin_limit: int = 0):
+        """Testing hook: one split-sampler segment publishes nothing and the
+        bounded waits give up after spin_limit polls (0: the default)."""
+        self.check(lib().fh_debug_sampler_faults(self.h, int(skip_segment), int(spin_limit)))
 
     def close(self):
         if getattr(self, "h", None):

@@ -53,7 +53,17 @@ enum {
     FH_ERR_OOM = 3,     /* device or host allocation failed */
     FH_ERR_HIP = 4,     /* a HIP runtime call failed (message carries hipGetErrorString) */
     FH_ERR_LIMIT = 5,   /* a size beyond a documented kernel limit */
-    FH_ERR_FORMAT = 6   /* a malformed GGUF file: ferrum_core's InferError::Format (gguf/cursor.rs) */
+    FH_ERR_FORMAT = 6,  /* a malformed GGUF file: ferrum_core's InferError::Format (gguf/cursor.rs) */
+    FH_ERR_EXCHANGE = 7 /* a kernel's bounded cross-workgroup wait gave up (its workgroups were not all
+                           resident at once, e.g. the GPU was shared): the results of the calls since
+                           the last fh_sync are unreliable; no reference counterpart */
+};
+
+/* Bits kernels record in a context's device status word, reported (and
+ * cleared) by fh_sync and by the blocking calls. */
+enum {
+    FH_STATUS_EXCHANGE = 1,   /* -> FH_ERR_EXCHANGE */
+    FH_STATUS_BAD_OFFSETS = 2 /* a device recent_offsets list decreased -> FH_ERR_INVALID */
 };
 
 /* Numerics of a Q8_0 linear.
@@ -99,7 +109,10 @@ void fh_ctx_destroy(fh_ctx* ctx);
  * context's own stream. */
 int fh_ctx_set_stream(fh_ctx* ctx, void* hip_stream);
 int fh_ctx_reset_stream(fh_ctx* ctx);
-/* Wait for all work enqueued on the context stream. */
+/* Wait for all work enqueued on the context stream, then report what its
+ * kernels recorded since the last fh_sync (and clear it): FH_ERR_EXCHANGE when a
+ * bounded wait gave up, FH_ERR_INVALID when a device-form sampler call found
+ * decreasing recent_offsets; FH_OK otherwise. */
 int fh_sync(fh_ctx* ctx);
 /* Message of the last failed call on `ctx` ("" if none); valid until the next
  * call on `ctx`.  fh_ctx_create failures are reported with ctx == NULL. */
@@ -169,16 +182,28 @@ int fh_q8_0_block_dots_async(fh_ctx* ctx, const fh_q8_0* w, const int8_t* d_qx, 
  * rng.rs:39-41), or draws[r] % vocab on the degenerate-softmax fallback
  * (sampling.rs:156-168).  The RNG stays on the host so the sequence is exactly
  * the reference's; draws may be NULL for greedy.  logits_kind: FH_LOGITS_*.
- * vocab == 0 -> FH_ERR_INVALID; a row with more than 16384 recent ids ->
- * FH_ERR_LIMIT.  Host pointers; blocks until out_ids is written. */
+ * A recent list may be of any length (the Llama path passes the whole prompt
+ * and everything generated, llm.rs:740-750).  vocab == 0 or decreasing
+ * recent_offsets -> FH_ERR_INVALID.  Rows of 8192 ids or more are split over
+ * several workgroups that exchange partial results; if a bounded wait of that
+ * exchange gives up (the GPU did not hold all of a launch's workgroups at
+ * once), the call returns FH_ERR_EXCHANGE.  Host pointers; blocks until
+ * out_ids is written. */
 int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, int logits_kind,
                    const fh_sampling_params* params, const uint32_t* recent,
                    const uint32_t* recent_offsets, const uint64_t* draws, uint32_t* out_ids);
-/* Device-pointer form of fh_sample_rows (params by value, on the host). */
+/* Device-pointer form of fh_sample_rows (params by value, on the host).  The
+ * offsets are not read on the host: decreasing offsets and a failed exchange
+ * are recorded on the device and reported by the next fh_sync. */
 int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t vocab,
                          int logits_kind, const fh_sampling_params* params,
                          const uint32_t* d_recent, const uint32_t* d_recent_offsets,
                          const uint64_t* d_draws, uint32_t* d_out_ids);
+/* Testing hook, no reference counterpart: make the split sampler's segment
+ * `skip_segment` (-1: none) publish nothing and its bounded waits give up after
+ * `spin_limit` polls (0: the default, 2^20), for later calls on ctx, so a test
+ * can drive the failure path from the host while every kernel still ends. */
+int fh_debug_sampler_faults(fh_ctx* ctx, int skip_segment, uint32_t spin_limit);
 
 /* ---- the rest of a GPT-2 decode step ------------------------------------- */
 /* Activation applied to a linear's output before it is stored. */

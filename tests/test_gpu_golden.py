@@ -1,8 +1,12 @@
 """The HIP path against the committed fixtures (tests/golden/), with the
 tolerances of BASELINE.json's north star: Q8_0 encode, dequant and int32
 block dots bit-exact; f32 outputs within 1e-5 of the output's term mass
-sum |x w|; sampled ids identical except where the oracle recorded a decision
-margin below 1e-5."""
+sum |x w| and, for W8A32, at most 1.5x the fixture's own mean error against
+the float64 product of the fixture's weights (decoded here from the GGUF
+bytes); ids identical except where the oracle recorded a decision margin
+below 1e-6 (a sampled row; the fixture keeps the smallest gap, so the top-p
+cut's own 2e-5 allowance of tests/test_gpu_sampler.py is not applied here)
+or a top-2 gap below 1e-5 (a greedy row)."""
 import os
 
 import numpy as np
@@ -11,7 +15,7 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-RTOL, MARGIN = 1e-5, 1e-5
+RTOL, MARGIN_SAMPLED, MARGIN_GREEDY = 1e-5, 1e-6, 1e-5
 
 
 def load(name):
@@ -23,6 +27,17 @@ def close(got, want, mass):
     got, want = np.asarray(got, np.float64), np.asarray(want, np.float64)
     err = np.abs(got - want)
     assert np.all(err <= RTOL * np.maximum(np.abs(want), np.asarray(mass, np.float64))), err.max()
+
+
+def exact_from_gguf(raw, n, k, x, b):
+    """float64 x . W^T + b with W decoded from the GGUF Q8_0 bytes (f16 scale,
+    then 32 int8 per block; the product d * q is exact)."""
+    blocks = np.asarray(raw, np.uint8).reshape(n, k // 32, 34)
+    d = blocks[:, :, :2].copy().view(np.float16)[:, :, 0].astype(np.float64)
+    q = blocks[:, :, 2:].view(np.int8).astype(np.float64)
+    w = (d[:, :, None] * q).reshape(n, k)
+    y = np.asarray(x, np.float64) @ w.T
+    return y + np.asarray(b, np.float64) if b is not None and b.size else y
 
 
 def test_codec_matches_fixture(fh):
@@ -43,7 +58,12 @@ def test_linear_matches_fixture(fh):
         raw, x, b = g[f"c{c}_gguf"], g[f"c{c}_x"], g[f"c{c}_bias"]
         bias = b if b.size else None
         w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
-        close(ferrum_hip.linear_forward(fh, x, w, bias), g[f"c{c}_y"], g[f"c{c}_mass"])
+        got = ferrum_hip.linear_forward(fh, x, w, bias)
+        close(got, g[f"c{c}_y"], g[f"c{c}_mass"])
+        exact = exact_from_gguf(raw, n, k, x, b)
+        e_gpu = np.abs(got - exact).mean()
+        e_fix = np.abs(g[f"c{c}_y"] - exact).mean()
+        assert e_gpu <= 1.5 * e_fix + 2.0**-23 * np.abs(exact).mean(), (c, e_gpu, e_fix)
         close(ferrum_hip.linear_forward(fh, x, w, bias, numerics=ferrum_hip.W8A8), g[f"c{c}_y8"], g[f"c{c}_mass"])
         if f"c{c}_dots" in g:
             dq = torch.from_numpy(g[f"c{c}_qx"]).cuda()
@@ -71,6 +91,8 @@ def test_sampler_matches_fixture(fh):
                                              kind)[0]
                 total += 1
                 if got != g["ids"][pi, kind, i]:
-                    assert g["margins"][pi, kind, i] < MARGIN, (pi, kind, i, got, g["ids"][pi, kind, i])
+                    margin = MARGIN_GREEDY if t <= 0 else MARGIN_SAMPLED
+                    assert g["margins"][pi, kind, i] < margin, (pi, kind, i, got, g["ids"][pi, kind, i])
                     exempt += 1
+    print(f"sampler fixture: {exempt} of {total} rows exempt")
     assert exempt <= max(1, total // 50), f"{exempt} of {total} rows exempt"

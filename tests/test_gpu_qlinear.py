@@ -3,7 +3,9 @@ bit-equal to the oracle's restatement of qaccum_cols (bias first, p
 ascending, no FMA), across int8 / int4, odd widths (the split-half nibble
 layout's last column), several rows of x, K beyond one LDS chunk, the
 one-row kernel's chunk and 4-row-group tails (K = 1, 2, 7, 389) and its
-16-, 32- and 64-byte column tiles (chosen by the output width), and the
+16-, 32- and 64-byte column tiles (chosen by the output width; int4 takes
+the 64-byte tile, where a lane owns two nibble columns, only above 16,384
+outputs, so two such cases end on partial chunks and row groups), and the
 reference's dimension errors (ops.rs:316-330)."""
 import numpy as np
 import pytest
@@ -30,7 +32,8 @@ def host(fh, t):
                                         (5, 64, 7, True), (8, 3072, 768, True), (1, 513, 1, True),
                                         (1, 3072, 2304, True), (1, 389, 129, True), (1, 7, 130, False),
                                         (1, 1, 5, True), (1, 2, 64, True), (1, 777, 5000, True),
-                                        (1, 1000, 10000, False), (1, 1001, 9000, True)])
+                                        (1, 1000, 10000, False), (1, 1001, 9000, True),
+                                        (1, 1001, 20001, True), (1, 389, 50257, False)])
 def test_qlinear_is_bit_exact(fh, orc, kind, m, k, n, bias):
     import torch
 

@@ -2,18 +2,43 @@
 (slm/sampling.rs:124-210).
 
 Parity rule: token ids identical given the same
-uniform draws, except where the oracle reports a decision margin below 1e-5 —
-a top-2 gap for greedy, or for sampling the smallest of |r - cumsum boundary|,
-|cum - top_p| at the cut and the p gap at the k-th place — because the GPU's
-exp/log and its parallel softmax sum may move a probability by about 1e-7
-relative.  Such exempt rows must stay rare (counted and bounded per test).
+uniform draws, except at a decision the oracle reports as within the
+precision both sides carry (exempt()):
+  * greedy: the top-2 gap below 1e-5 (the north star's rule);
+  * the p gap at the k-th place, or |r - cumsum| at the draw, below 1e-6:
+    the GPU's exp/log (ocml, <= 1 ulp from glibc) move each p by ~1e-7
+    relative, and the draw's sum2 / cumsum replay the reference's sequential
+    order on those p;
+  * the top-p cut (|cum - top_p| relative to top_p, or the relative p gap
+    between the crossing id and the next) below 2e-5, or a p tie there: the
+    reference normalises with a sequential f32 sum over the whole vocabulary
+    (sampling.rs:154-167), whose own rounding error is ~1e-5 relative at
+    50,257 ids (round-off of ~sqrt(n) adds, each up to half an ulp of a
+    partial sum near the total); it scales every p by one common factor, which
+    moves cum against top_p by that much.  The GPU's tree sum is closer to
+    the exact normaliser, so a cut within that distance can fall on either
+    side, and near-flat rows (GPT-2 bridge, thousands of ids at nearly equal
+    p) put their cut between nearly tied ids.
+Every call prints how many rows fall within these margins and how many were
+exempt (ids differ); each test bounds the exempt share.
 """
 import numpy as np
 import pytest
 
 pytestmark = pytest.mark.gpu
 
-MARGIN = 1e-5
+MARGIN_GREEDY = 1e-5
+MARGIN_SAMPLED = 1e-6
+MARGIN_TOP_P = 2e-5
+
+
+def exempt(info, greedy):
+    """True where the oracle's decision lies within the precision both sides
+    carry (see the module docstring)."""
+    if greedy:
+        return info.greedy_gap < MARGIN_GREEDY
+    return (info.topk_gap < MARGIN_SAMPLED or info.draw_gap < MARGIN_SAMPLED or info.topp_gap < MARGIN_TOP_P
+            or bool(info.topp_tie))
 
 
 def run_and_compare(fh, orc, logits, params_kw, recents=None, draws=None, kind=0, max_exempt=0.01):
@@ -29,17 +54,25 @@ def run_and_compare(fh, orc, logits, params_kw, recents=None, draws=None, kind=0
     gp = ferrum_hip.SamplingParams(**params_kw)
     got = ferrum_hip.sample_rows(fh, logits, gp, recents, draws, kind)
     op = orc.SamplingParams(**params_kw)
-    exempt = 0
+    greedy = params_kw.get("temperature", 1.0) <= 0.0
+    n_exempt, near, bad = 0, 0, []
     for r in range(rows):
         row = logits[r]
         if kind == ferrum_hip.LOGITS_GPT2_SOFTMAX:
             row = orc.ln_bridge(orc.softmax_rows(row)[0])
         want, info = orc.sample(row, op, recents[r], int(draws[r]))
+        near += exempt(info, greedy)
         if got[r] != want:
-            assert info.margin < MARGIN, (f"row {r}: gpu {got[r]} vs oracle {want}, margin {info.margin:.3e}, "
-                                          f"path {info.path}, kept {info.n_kept}")
-            exempt += 1
-    assert exempt <= max(1, int(max_exempt * rows)), f"{exempt} exempt rows of {rows}"
+            if exempt(info, greedy):
+                n_exempt += 1
+            else:
+                bad.append(f"row {r}: gpu {got[r]} vs oracle {want}; gaps greedy {info.greedy_gap:.2e} top-k "
+                           f"{info.topk_gap:.2e} top-p {info.topp_gap:.2e} draw {info.draw_gap:.2e}, "
+                           f"path {info.path}, kept {info.n_kept}")
+    print(f"sampler parity {params_kw} kind {kind}: {rows} rows, {near} within the margins, "
+          f"{n_exempt} exempt (ids differ)")
+    assert not bad, "; ".join(bad)
+    assert n_exempt <= max(1, int(max_exempt * rows)), f"{n_exempt} exempt rows of {rows}"
     return got
 
 
@@ -129,10 +162,12 @@ def test_gpt2_softmax_bridge_parity(fh, orc, name):
     lg = normal_logits(rows, vocab, 99, scale=2.0)
     rng = np.random.default_rng(5)
     recents = [list(rng.integers(0, vocab, size=256)) for _ in range(rows)]
-    # GPT-2-bridged rows are flat (|z| ~ 2): the kept set runs to thousands of
-    # ids spaced ~1e-4 apart in cumulative mass, so a draw lands within 1e-5 of
-    # a boundary in a sizeable share of rows; each mismatch must still be one.
-    run_and_compare(fh, orc, lg, PARAMS[name], recents, kind=ferrum_hip.LOGITS_GPT2_SOFTMAX, max_exempt=0.25)
+    # GPT-2-bridged rows are flat (|z| ~ 2): with top-p alone the kept set is
+    # ~10,000 ids at nearly equal p, so almost every row's top-p cut falls
+    # between ids whose p differ by ~1e-6 relative (all 16 rows are within
+    # the top-p margin); each mismatch must still be such a row.
+    run_and_compare(fh, orc, lg, PARAMS[name], recents, kind=ferrum_hip.LOGITS_GPT2_SOFTMAX,
+                    max_exempt=0.25 if name == "topp" else 0.1)
 
 
 def test_repeated_ids_penalised_once_per_occurrence(fh, orc):
@@ -191,11 +226,99 @@ def test_sampler_errors(fh):
 
     with pytest.raises(ferrum_hip.FerrumHipError, match="vocab is 0"):
         ferrum_hip.sample_rows(fh, np.zeros((1, 0), np.float32), ferrum_hip.SamplingParams(0.0))
-    with pytest.raises(ferrum_hip.FerrumHipError, match="above the limit"):
-        ferrum_hip.sample_rows(fh, np.zeros((1, 10), np.float32), ferrum_hip.SamplingParams(0.0, repetition_penalty=1.1),
-                               [[1] * 16385])
     with pytest.raises(ferrum_hip.FerrumHipError, match="draws is NULL"):
         ferrum_hip.sample_rows(fh, np.zeros((1, 10), np.float32), ferrum_hip.SamplingParams(0.5))
+
+
+@pytest.mark.parametrize("vocab", [4096, 50257])
+def test_histories_longer_than_any_table(fh, orc, vocab):
+    """A Llama-path history is the whole prompt plus every generated id
+    (llm.rs:740-750): 40,000 recent ids, no cut-off, through the blocking call
+    and through the device form."""
+    import torch
+
+    import ferrum_hip
+
+    rows = 3
+    lg = normal_logits(rows, vocab, 17)
+    rng = np.random.default_rng(18)
+    rec = [list(rng.integers(0, 300, size=40000)) for _ in range(rows)]
+    lg[:, :300] += 1.0
+    kw = dict(temperature=0.7, top_k=30, top_p=0.9, repetition_penalty=1.0005)
+    got = run_and_compare(fh, orc, lg, kw, rec)
+    run_and_compare(fh, orc, lg, dict(temperature=0.0, repetition_penalty=1.0005), rec)
+    flat, off = ferrum_hip._recent_lists(rec, rows)
+    draws = np.random.default_rng(rows * 977 + vocab).integers(0, 2**64, size=rows, dtype=np.uint64)
+    d_out = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ferrum_hip.sample_rows_async(fh, torch.from_numpy(lg).cuda(), rows, vocab, ferrum_hip.SamplingParams(**kw),
+                                 torch.from_numpy(flat.astype(np.int32)).cuda(),
+                                 torch.from_numpy(off.astype(np.int32)).cuda(),
+                                 torch.from_numpy(draws.view(np.int64)).cuda(), d_out)
+    fh.sync()
+    assert np.array_equal(d_out.cpu().numpy().astype(np.uint32), got)
+
+
+def test_decreasing_device_offsets_are_reported(fh):
+    """The device form cannot read its offsets on the host: a decreasing list
+    is recorded by the kernel and raised by the next sync."""
+    import torch
+
+    import ferrum_hip
+
+    rows, vocab = 2, 50257
+    lg = torch.from_numpy(normal_logits(rows, vocab, 4)).cuda()
+    rec = torch.zeros(8, dtype=torch.int32, device="cuda")
+    off = torch.tensor([4, 2, 6], dtype=torch.int32, device="cuda")
+    out = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    for params in (ferrum_hip.SamplingParams(0.0, repetition_penalty=1.2),
+                   ferrum_hip.SamplingParams(0.8, 40, 0.95, 1.2)):
+        draws = torch.zeros(rows, dtype=torch.int64, device="cuda")
+        ferrum_hip.sample_rows_async(fh, lg, rows, vocab, params, rec, off, draws, out)
+        with pytest.raises(ferrum_hip.FerrumHipError, match="recent_offsets decrease") as e:
+            fh.sync()
+        assert e.value.code == ferrum_hip.FH_ERR_INVALID
+    fh.sync()  # cleared
+
+
+@pytest.mark.parametrize("params", [dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1),
+                                    dict(temperature=0.0), dict(temperature=0.9)])
+def test_a_failed_exchange_is_reported_and_recovered(fh, orc, params):
+    """One segment of a split row publishes nothing (a host-set testing hook)
+    and the bounded waits give up after 64 polls: every workgroup still ends,
+    the blocking call returns FH_ERR_EXCHANGE, the device form reports it at
+    the next sync, and later calls are exact again."""
+    import torch
+
+    import ferrum_hip
+
+    rows, vocab = 3, 50257
+    lg = normal_logits(rows, vocab, 61)
+    rng = np.random.default_rng(62)
+    rec = [list(rng.integers(0, vocab, size=128)) for _ in range(rows)]
+    draws = rng.integers(0, 2**63, size=rows, dtype=np.uint64)
+    gp = ferrum_hip.SamplingParams(**params)
+    fh.debug_sampler_faults(1, 64)
+    try:
+        with pytest.raises(ferrum_hip.FerrumHipError) as e:
+            ferrum_hip.sample_rows(fh, lg, gp, rec, draws)
+        assert e.value.code == ferrum_hip.FH_ERR_EXCHANGE
+        flat, off = ferrum_hip._recent_lists(rec, rows)
+        out = torch.zeros(rows, dtype=torch.int32, device="cuda")
+        d_lg = torch.from_numpy(lg).cuda()
+        d_rec = torch.from_numpy(flat.astype(np.int32)).cuda()
+        d_off = torch.from_numpy(off.astype(np.int32)).cuda()
+        d_dr = torch.from_numpy(draws.view(np.int64)).cuda()
+        torch.cuda.synchronize()
+        ferrum_hip.sample_rows_async(fh, d_lg, rows, vocab, gp, d_rec, d_off, d_dr, out)
+        with pytest.raises(ferrum_hip.FerrumHipError) as e:
+            fh.sync()
+        assert e.value.code == ferrum_hip.FH_ERR_EXCHANGE
+    finally:
+        fh.debug_sampler_faults(-1, 0)
+    fh.sync()
+    run_and_compare(fh, orc, lg, params, rec, draws=draws)
 
 
 def test_split_rows_replay_in_a_graph(fh, orc):
