@@ -897,8 +897,14 @@ int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const f
 // (their sums fit 64 KiB of LDS, two workgroups per CU) and 8 (256 VGPRs per lane).  Column tiles per
 // wave (NT): up to 4 while that still leaves >= 256 workgroups, so wide
 // outputs split each activation block once per 128 columns.
+__global__ void k_zero_counters(unsigned* __restrict__ c, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) c[i] = 0u;
+}
+
 template <int MT, int NT, int BPW>
-int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                    const fh_scratch* scratch) {
     constexpr size_t kMaxWaves = 16 / (MT * NT) < 8 ? 16 / (MT * NT) : 8;
     const size_t kb = w->k / 32, tiles = (w->n + 32 * NT - 1) / (32 * NT);
     size_t splits = 1;
@@ -913,14 +919,32 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     float* part = nullptr;
     unsigned* counters = nullptr;
     if (splits > 1) {
-        void* ws = nullptr;
-        int rc = fh_workspace(ctx, splits * tiles * MT * NT * 1024 * sizeof(float), &ws);
-        if (rc) return rc;
-        part = static_cast<float*>(ws);
-        void* cnt = nullptr;
-        rc = fh_counter_area(ctx, tiles * sizeof(unsigned), &cnt);
-        if (rc) return rc;
-        counters = static_cast<unsigned*>(cnt);
+        const size_t part_bytes = splits * tiles * MT * NT * 1024 * sizeof(float);
+        if (scratch) {
+            // The caller's fixed scratch: partials, then the arrival counters,
+            // which are cleared here (a kernel, not a memset, so the call can
+            // be captured into a graph).
+            const size_t cnt_at = fh_align256(part_bytes);
+            if (cnt_at + tiles * sizeof(unsigned) > scratch->bytes)
+                return fh_fail(ctx, FH_ERR_LIMIT,
+                               "fh_q8_0_linear_noalloc: this shape needs " +
+                                   std::to_string(cnt_at + tiles * sizeof(unsigned)) +
+                                   " bytes of scratch, above the fixed " + std::to_string(scratch->bytes));
+            part = static_cast<float*>(scratch->ptr);
+            counters = reinterpret_cast<unsigned*>(static_cast<char*>(scratch->ptr) + cnt_at);
+            hipLaunchKernelGGL(k_zero_counters, dim3(static_cast<unsigned>((tiles + 255) / 256)), dim3(256), 0,
+                               ctx->stream, counters, static_cast<int>(tiles));
+            FH_HIP(ctx, hipGetLastError());
+        } else {
+            void* ws = nullptr;
+            int rc = fh_workspace(ctx, part_bytes, &ws);
+            if (rc) return rc;
+            part = static_cast<float*>(ws);
+            void* cnt = nullptr;
+            rc = fh_counter_area(ctx, tiles * sizeof(unsigned), &cnt);
+            if (rc) return rc;
+            counters = static_cast<unsigned*>(cnt);
+        }
     }
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: too many output columns");
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), block(static_cast<unsigned>(64 * kw));
@@ -939,18 +963,19 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
 // 32 and 64 outputs narrower than 2048 take one block per wave batch (more K
 // splits, so more workgroups: 896 x 896 7.9 -> 6.9 us at m = 32, 10.4 -> 9.2
 // us at m = 64; a 3072-wide one slows down).
-int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                  const fh_scratch* scratch = nullptr) {
     const size_t t32 = (w->n + 31) / 32;
     if (m <= 32) {
-        if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y);
-        if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y);
-        if (t32 >= 64) return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y);
-        return launch_skinny_t<1, 1, 1>(ctx, w, x, m, bias, y);
+        if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y, scratch);
+        if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y, scratch);
+        if (t32 >= 64) return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y, scratch);
+        return launch_skinny_t<1, 1, 1>(ctx, w, x, m, bias, y, scratch);
     }
-    if (t32 >= 4 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y);
-    if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y);
-    if (t32 >= 64) return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y);
-    return launch_skinny_t<2, 1, 1>(ctx, w, x, m, bias, y);  // 896 x 896: 10.4 -> 9.2 us
+    if (t32 >= 4 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y, scratch);
+    if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y, scratch);
+    if (t32 >= 64) return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y, scratch);
+    return launch_skinny_t<2, 1, 1>(ctx, w, x, m, bias, y, scratch);  // 896 x 896: 10.4 -> 9.2 us
 }
 
 }  // namespace
@@ -986,6 +1011,11 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                            static_cast<int>(tiles_n), static_cast<int>(tiles));
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
+}
+
+int fh_launch_skinny_scratch(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                             const fh_scratch& scratch) {
+    return launch_skinny(ctx, w, x, m, bias, y, &scratch);
 }
 
 // Tile choice: m <= 64 takes the skinny kernel; otherwise the 256 x 256

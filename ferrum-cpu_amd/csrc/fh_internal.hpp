@@ -114,6 +114,19 @@ int fh_launch_linear_ln_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, siz
                               const float* bias, float* y, int act);
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                          const float* bias, float* y);
+// The decode GEMV alone (m <= 2, W8A32, no workspace); -1 when the row is too
+// long for it (the caller then takes the GEMM).
+int fh_launch_gemv_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y);
+// A device scratch area a caller owns (no allocation by the launcher).
+struct fh_scratch {
+    void* ptr;
+    size_t bytes;
+};
+// The skinny GEMM (3 <= m <= 64) with its split-K partials and arrival
+// counters in `scratch` (counters cleared by a kernel first); FH_ERR_LIMIT when
+// the shape needs more than scratch.bytes.
+int fh_launch_skinny_scratch(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                             const fh_scratch& scratch);
 int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                         const float* bias, float* y);
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,

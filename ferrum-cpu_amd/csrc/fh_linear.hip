@@ -454,6 +454,12 @@ int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t
     return rc;
 }
 
+int fh_launch_gemv_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    if (m == 1) return dispatch_gemv<1>(ctx, w, x, bias, y, FH_ACT_NONE);
+    if (m == 2) return dispatch_gemv<2>(ctx, w, x, bias, y, FH_ACT_NONE);
+    return -1;
+}
+
 int fh_launch_linear_ln_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_ln_args& ln,
                               const float* bias, float* y, int act) {
     const bool aligned = !((reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(ln.r) |

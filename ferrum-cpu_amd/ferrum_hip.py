@@ -40,7 +40,7 @@ LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
 EXPORTS = (
     "fh_ctx_create", "fh_ctx_destroy", "fh_ctx_set_stream", "fh_ctx_reset_stream", "fh_sync", "fh_last_error",
     "fh_device_count", "fh_q8_0_upload", "fh_q8_0_upload_device", "fh_q8_0_download",
-    "fh_q8_0_dims", "fh_q8_0_free", "fh_q8_0_linear", "fh_q8_0_linear_async",
+    "fh_q8_0_dims", "fh_q8_0_free", "fh_q8_0_linear", "fh_q8_0_linear_async", "fh_q8_0_linear_noalloc_async",
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async", "fh_debug_sampler_faults",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
@@ -157,6 +157,7 @@ def lib():
         L.fh_q8_0_free.restype = None
         L.fh_q8_0_linear.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32]
         L.fh_q8_0_linear_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32]
+        L.fh_q8_0_linear_noalloc_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32]
         L.fh_q8_0_encode.argtypes = [vp, vp, sz, vp]
         L.fh_q8_0_encode_async.argtypes = [vp, vp, sz, vp]
         L.fh_q8_0_dequant_async.argtypes = [vp, vp, sz, vp]

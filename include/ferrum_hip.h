@@ -151,6 +151,19 @@ int fh_q8_0_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, size
 int fh_q8_0_linear_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
                          const float* d_bias, size_t bias_len, float* d_y, int numerics);
 
+/* No reference counterpart: for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  fh_q8_0_linear_async for FH_W8A32 at m <= 64 (the decode and
+ * batched-decode shapes: the same kernels, the same results bit for bit), with
+ * no allocation of any kind: the skinny GEMM's split-K partial sums and
+ * arrival counters live in a fixed 12 MiB device array that each GPU holds
+ * for the life of the process.  m > 64, FH_W8A8, or a shape whose K split
+ * would need more than 12 MiB -> FH_ERR_LIMIT.  All calls on one GPU share that
+ * array: calls that overlap on one GPU (two streams, two threads) race;
+ * calls in one stream order are safe. */
+int fh_q8_0_linear_noalloc_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                                 const float* d_bias, size_t bias_len, float* d_y, int numerics);
+
 /* ---- Q8_0 encode -------------------------------------------------------- */
 /* n floats -> n/32 GGUF Q8_0 blocks of 34 bytes, bit-exact with enc_q8_0
  * (gguf_write/blocks.rs:132-140) over q8_0_block (quant.rs:271-280) and
