@@ -1,32 +1,37 @@
-"""Benchmark of the MI355X Q8_0 decode-step hot path (one JSON line on stdout).
+"""Benchmark of the MI355X Q8_0 decode path (one JSON line on stdout).
 
-Workload (GPT-2-124M shape, batch 1): one decode
-step of the hot path = the 49 Q8_0 linear layers of a GPT-2-124M forward
-(12 x [QKV 2304x768, attn-out 768x768, MLP-up 3072x768, MLP-down 768x3072],
-bias added; tied lm_head 50257x768, no bias) followed by the fused sampler on
-the 50257 head outputs (GPT-2 softmax -> ln bridge, temperature 0.8, top-k 40,
-top-p 0.95, repetition penalty 1.1 over a 128-id window, one host draw).
-Random-init N(0, 0.02) weights, Q8_0-encoded on the GPU; synthetic N(0,1)
-activations resident in HBM.  The adjacent LayerNorm/attention/GELU ops are not
-part of the hot path and are not timed.
+Workload (GPT-2-124M shape, batch 1): one whole
+decode step on the device at position 255 (mid-run of the configuration's
+128-token prompt + 256 steps) — Embedding::embed_one, 12 blocks of
+forward_with_cache (LayerNorm, fused Q|K|V Q8_0 linear, KV-cache attention,
+out projection, residual, LayerNorm, up + GELU, down, residual), the final
+LayerNorm, the tied Q8_0 head (50257 x 768) and the fused sampler (GPT-2
+softmax -> ln bridge, temperature 0.8, top-k 40, top-p 0.95, repetition
+penalty 1.1 over a 128-id window, one host draw), whose id feeds the next
+step's embedding on the device.  The 12 blocks run as one launch
+(k_gpt2_stack), then the LayerNorm-prologue head GEMV and the sampler: three
+launches per token.  Random-init N(0, 0.02) weights, Q8_0-encoded on the GPU.
 
-Residency: three replicas of the whole weight set (3 x 131 MB = 394 MB, above
-the 256 MB MALL) are used in rotation, so every step streams its weights from
-HBM ("hbm-forced").  A MALL-resident figure (one replica) is reported beside it.
+Residency: three model replicas (3 x 131 MB of Q8_0 + their caches, above the
+256 MB MALL) are used in rotation, so every step streams its weights from HBM
+("hbm-forced").  The step is captured once per replica into a HIP graph
+(torch.cuda.CUDAGraph) and replayed; K timed steps are bracketed by
+synchronisations and HIP events.
 
-The step is captured once per replica into a HIP graph (torch.cuda.CUDAGraph)
-and replayed; K timed steps are bracketed by synchronisations and HIP events.
-
-roofline: the dominant kernel is the Q8_0 GEMV; it is measured on the lm_head
-shape (50257 x 768, the largest launch) in back-to-back launches over 32 head
-replicas (1.3 GB, HBM-forced), timed with HIP events on the launch stream.
-Algorithmic bytes per launch = 50257*768*34/32 (Q8_0 weight) + 768*4 (x)
-+ 50257*4 (y).
+roofline: the step's dominant kernel, k_gpt2_stack (all 12 blocks), timed
+alone (graphs of 10 launches per replica, HIP events on its stream);
+algorithmic bytes per launch = the 48 layer weights' Q8_0 bytes + the K and V
+cache rows it reads (2 x 12 x 256 x 768 x 4 at position 255).  The kernel is
+bound by its 60 dependent exchanges between workgroups, not by HBM; the
+fraction says how far from the HBM roofline that leaves it.  The lm_head GEMV
+roofline (41.2 MB per launch, the largest HBM stream of the step) is reported
+beside it.
 
 cpu_baseline: the CPU oracle (oracle/, ferrum_core's arithmetic restated in C,
 "port") on one host core — ferrum_core runs the m=1 linear serially at any
-thread count (parallel.rs:90-92) — over f32-expanded weights as the reference's
-loader builds them, for a bounded number of decode steps.
+thread count (parallel.rs:90-92) — running the same whole decode step over
+f32-expanded weights as the reference's loader builds them, at position 255
+of a randomly filled KV cache, for a bounded number of steps.
 """
 from __future__ import annotations
 
@@ -55,18 +60,19 @@ HEADS, CTX, FULL_POS = 12, 1024, 255  # GPT-2-124M attention; the whole-step leg
 
 COPY_BYTES = 256 << 20
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q8_0_lm_head_pmc.json")
+STACK_PMC = os.path.join(ROOT, "profiles", "gpt2_stack_124m_pmc.json")
 
 
 def q8_bytes(n, k):
     return n * k // 32 * 34
 
 
-def measured_traffic():
-    """HBM bytes per lm_head GEMV launch from the committed counter runs
+def measured_traffic(path):
+    """HBM bytes per launch of a kernel from its committed counter runs
     (FETCH_SIZE + WRITE_SIZE, scaled by a plain copy of known size); None when
     that summary is absent."""
     try:
-        with open(PMC_SUMMARY) as f:
+        with open(path) as f:
             return json.load(f)["traffic_bytes_per_launch"]
     except (OSError, KeyError, ValueError):
         return None
@@ -92,15 +98,16 @@ class Replica:
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=2000)
+    ap.add_argument("--steps", type=int, default=1000)
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--leg", choices=["all", "head", "prefill", "qwen", "qlinear"], default="all",
-                    help="'head': only the lm_head GEMV roofline leg (for counter runs); "
-                         "'prefill': only the GPT-2-medium prefill GEMMs; 'qwen': only the Qwen2-shaped "
-                         "batch-64 step; 'qlinear': only the per-row int8 and int4 qlinear steps")
+    ap.add_argument("--leg", choices=["all", "stack", "head", "prefill", "qwen", "qlinear"], default="all",
+                    help="'stack': only the whole decode step and its one-launch block stack (for profiles and "
+                         "counter runs); 'head': only the lm_head GEMV roofline leg; 'prefill': only the "
+                         "GPT-2-medium prefill GEMMs; 'qwen': only the Qwen2-shaped batch-64 step; 'qlinear': only "
+                         "the per-row int8 and int4 qlinear steps")
     ap.add_argument("--prefill-steps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -125,7 +132,9 @@ def main():
     x_d = torch.randn((1, D), generator=gen, device=dev)
     x_f = torch.randn((1, FFN), generator=gen, device=dev)
     y_big = torch.empty((1, max(3 * D, FFN)), device=dev)
-    logits = torch.empty((1, V), device=dev)
+    # the head's scores as the hot path produces them: N(0,1) activations
+    # through N(0, 0.02) weights give scores of spread 0.02 * sqrt(768)
+    logits = torch.randn((1, V), generator=gen, device=dev) * (0.02 * D ** 0.5)
     biases = {n: torch.randn(n, generator=gen, device=dev) * 0.1 for n in {s[0] for s in LAYER_SHAPES}}
     rec = torch.from_numpy(np.random.default_rng(3).integers(0, V, size=N_RECENT).astype(np.uint32)).to(dev)
     rec_off = torch.tensor([0, N_RECENT], dtype=torch.int32, device=dev)
@@ -144,37 +153,75 @@ def main():
         fh.sample_rows_async(ctx, logits, 1, V, params, rec, rec_off, draws, out_id, fh.LOGITS_GPT2_SOFTMAX)
 
     result = {}
-    if args.leg == "all":
-        reps = [Replica(ctx, fh, torch, gen) for _ in range(args.replicas)]
-        for r in reps:  # eager pass: grows the context workspace before capture
-            step(r)
+
+    def timed(gs, steps, warmup):
+        for i in range(warmup):
+            gs[i % len(gs)].replay()
         torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0 = time.perf_counter()
+        e0.record()
+        for i in range(steps):
+            gs[i % len(gs)].replay()
+        e1.record()
+        torch.cuda.synchronize()
+        wall = (time.perf_counter() - t0) * 1e3
+        return e0.elapsed_time(e1) / steps, wall / steps
+
+    def capture(fn, items):
+        """One HIP graph per item: fn(item) run once eagerly (grows the
+        context's areas outside capture), then captured."""
+        for it in items:
+            fn(it)
+        torch.cuda.synchronize()
+        ctx.sync()
         graphs = []
-        for r in reps:
+        for it in items:
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
                 ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-                step(r)
+                fn(it)
             ctx.set_stream(stream.cuda_stream)
             graphs.append(g)
         torch.cuda.synchronize()
+        return graphs
 
-        def timed(gs, steps, warmup):
-            for i in range(warmup):
-                gs[i % len(gs)].replay()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            t0 = time.perf_counter()
-            e0.record()
-            for i in range(steps):
-                gs[i % len(gs)].replay()
-            e1.record()
-            torch.cuda.synchronize()
-            wall = (time.perf_counter() - t0) * 1e3
-            return e0.elapsed_time(e1) / steps, wall / steps
+    if args.leg in ("all", "stack"):
+        # ---- the whole decode step (the headline) ----------------------------------
+        models = [fh.GPT2Device.random(ctx, V, D, HEADS, L, FFN, CTX, gen) for _ in range(args.replicas)]
+        assert all(m.stack is not None for m in models), "the one-launch block stack is not available"
 
-        ms_step, wall_step = timed(graphs, args.steps, args.warmup)
-        ms_mall, _ = timed(graphs[:1], args.steps, args.warmup)
+        def full_step(mdl):
+            mdl.feed_async(mdl.token, FULL_POS)
+            fh.sample_rows_async(ctx, mdl.z, 1, V, params, rec, rec_off, draws, mdl.token, fh.LOGITS_GPT2_SOFTMAX)
+
+        graphs_f = capture(full_step, models)
+        ms_full, wall_full = timed(graphs_f, args.steps, args.warmup)
+        ms_full_mall, _ = timed(graphs_f[:1], args.steps, args.warmup)
+        del graphs_f
+        ctx.sync()  # raises if any exchange of the timed steps gave up
+
+        # the dominant kernel alone: k_gpt2_stack, 10 launches per graph
+        def stack_only(mdl):
+            for _ in range(10):
+                ctx.check(fh.lib().fh_gpt2_stack_forward_async(ctx.h, mdl.stack, mdl.token.data_ptr(), FULL_POS,
+                                                               mdl.x.data_ptr()))
+
+        graphs_s = capture(stack_only, models)
+        ms_stack, _ = timed(graphs_s, max(args.steps // 10, 5), max(args.warmup // 10, 2))
+        stack_us = ms_stack / 10 * 1e3
+        del graphs_s
+        ctx.sync()
+
+        # the same step one launch per op (64 launches), for comparison
+        for mdl in models:
+            mdl.fused = False
+        graphs_p = capture(full_step, models)
+        ms_perop, _ = timed(graphs_p, max(args.steps // 4, 10), args.warmup)
+        del graphs_p
+        for mdl in models:
+            mdl.fused = True
+
         # Sampler alone: one 50257-wide row (GPT-2 bridge, config-3 params),
         # 50 launches captured in one graph so the host's launch rate is not
         # what is timed.
@@ -193,53 +240,46 @@ def main():
             gs.replay()
         e1.record()
         torch.cuda.synchronize()
-        result["sampler_us_per_row"] = round(e0.elapsed_time(e1) / (ns * nrep) * 1e3, 2)
+        sampler_us = e0.elapsed_time(e1) / (ns * nrep) * 1e3
         del gs
-        step_bytes = sum(q8_bytes(n, k) for (n, k) in LAYER_SHAPES) * L + q8_bytes(V, D)
-        result.update(ms_per_step=ms_step, wall_ms_per_step=wall_step, ms_per_step_mall=ms_mall,
-                      step_weight_bytes=step_bytes)
-        del graphs
-        torch.cuda.synchronize()
-
-        # The whole decode step on the device (GPT-2-124M, b1): embed_one, 12
-        # blocks (LayerNorm, fused QKV, KV-cache attention, out projection,
-        # residual, LayerNorm, up, GELU, down, residual), the final LayerNorm,
-        # the head and the sampler, whose id feeds the next replay's embedding
-        # on the device.  At position FULL_POS (mid-run of the 128-token prompt
-        # + 256 steps); one model per replica (HBM-forced).
-        models = [fh.GPT2Device.random(ctx, V, D, HEADS, L, FFN, CTX, gen) for _ in range(args.replicas)]
-
-        def full_step(mdl):
-            mdl.feed_async(mdl.token, FULL_POS)
-            fh.sample_rows_async(ctx, mdl.z, 1, V, params, rec, rec_off, draws, mdl.token, fh.LOGITS_GPT2_SOFTMAX)
-
-        for mdl in models:
-            full_step(mdl)
-        torch.cuda.synchronize()
-        graphs_f = []
-        for mdl in models:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-                full_step(mdl)
-            ctx.set_stream(stream.cuda_stream)
-            graphs_f.append(g)
-        torch.cuda.synchronize()
-        ms_full, _ = timed(graphs_f, max(args.steps // 4, 10), args.warmup)
-        kv_bytes = 2 * L * (FULL_POS + 1) * D * 4
-        result["full_step"] = {
-            "tok_s": round(1000.0 / ms_full, 1), "ms_per_step": round(ms_full, 5), "position": FULL_POS,
-            "launches_per_step": models[0].launches_per_step() + 1, "kv_cache_bytes_read": kv_bytes,
-            "residency": f"hbm-forced ({args.replicas} model replicas)",
-            "what": "embed_one + LayerNorm + QKV, then 12 x (attention, out, add+LayerNorm+up+GELU, down, "
-                    "add+LayerNorm+next QKV or head) + sampler, all on the device"}
-        del graphs_f
         for mdl in models:
             mdl.free()
         del models
         torch.cuda.synchronize()
 
-        # ---- batch 32: the same step for 32 sequences (BASELINE's b32 decode) ----
+        layer_bytes = sum(q8_bytes(n, k) for (n, k) in LAYER_SHAPES) * L
+        kv_bytes = 2 * L * (FULL_POS + 1) * D * 4
+        head_bytes_ln = q8_bytes(V, D) + 4 * D + 4 * V
+        step_bytes = layer_bytes + kv_bytes + head_bytes_ln + 4 * V  # + the sampler's logits read
+        stack_bytes = layer_bytes + kv_bytes
+        stack_gbps = stack_bytes / (stack_us * 1e-6) / 1e9
+        result.update(ms_full=ms_full, wall_full=wall_full, ms_full_mall=ms_full_mall, ms_perop=ms_perop,
+                      stack_us=stack_us, stack_bytes=stack_bytes, stack_gbps=stack_gbps, step_bytes=step_bytes,
+                      sampler_us=sampler_us, kv_bytes=kv_bytes)
+        if args.leg == "stack":
+            # A plain device copy of known size, for scaling the PMC byte
+            # counters (FETCH_SIZE / WRITE_SIZE) of the same run.
+            src = torch.empty(COPY_BYTES // 4, device=dev)
+            dst = torch.empty_like(src)
+            for _ in range(5):
+                dst.copy_(src)
+            torch.cuda.synchronize()
+            print(json.dumps({"leg": "stack", "stack_us": round(stack_us, 3), "stack_bytes": stack_bytes,
+                              "stack_GBps": round(stack_gbps, 1), "ms_per_step": round(ms_full, 5),
+                              "per_op_ms_per_step": round(ms_perop, 5), "copy_bytes_per_launch": COPY_BYTES}))
+            return
+
+    if args.leg == "all":
+        # ---- the hot path alone, unchained: the 49 Q8_0 linears on fixed
+        # inputs + the sampler (no dependence between the linears) -------------
+        reps = [Replica(ctx, fh, torch, gen) for _ in range(args.replicas)]
+        graphs = capture(step, reps)
+        ms_step, _ = timed(graphs, args.steps, args.warmup)
+        del graphs
+        result["hot_unchained"] = ms_step
+        torch.cuda.synchronize()
+
+        # ---- batch 32: the same hot path for 32 sequences (BASELINE's b32 decode) ----
         B = B32
         xb_d = torch.randn((B, D), generator=gen, device=dev)
         xb_f = torch.randn((B, FFN), generator=gen, device=dev)
@@ -257,21 +297,11 @@ def main():
             fh.linear_forward_async(ctx, rep.head, xb_d, B, D, None, 0, logits_b)
             fh.sample_rows_async(ctx, logits_b, B, V, params, rec_b, off_b, draws_b, out_b, fh.LOGITS_GPT2_SOFTMAX)
 
-        for r in reps:
-            step_b(r)
-        torch.cuda.synchronize()
-        graphs_b = []
-        for r in reps:
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g):
-                ctx.set_stream(torch.cuda.current_stream().cuda_stream)
-                step_b(r)
-            ctx.set_stream(stream.cuda_stream)
-            graphs_b.append(g)
-        torch.cuda.synchronize()
+        graphs_b = capture(step_b, reps)
         ms_b, _ = timed(graphs_b, max(args.steps // 4, 10), args.warmup)
         result["b32"] = {"tok_s": round(B * 1000.0 / ms_b, 1), "ms_per_step": round(ms_b, 5), "batch": B,
-                         "sampler_rows": B, "residency": f"hbm-forced ({args.replicas} weight replicas)"}
+                         "sampler_rows": B, "residency": f"hbm-forced ({args.replicas} weight replicas)",
+                         "what": "49 Q8_0 skinny GEMMs at m = 32 + head + 32 sampler rows (unchained inputs)"}
         del graphs_b, reps
         torch.cuda.synchronize()
 
@@ -313,8 +343,8 @@ def main():
     head_us = e0.elapsed_time(e1) / launches * 1e3
     head_bytes = q8_bytes(V, D) + 4 * D + 4 * V
     achieved = head_bytes / (head_us * 1e-6) / 1e9
-    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
+    head_roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(PMC_SUMMARY),
                 "kernel": "k_gemv_w8a32<16,3,1,4,false,false> (lm_head 50257x768, Q8_0, m=1)",
                 "avg_launch_us": round(head_us, 3), "bytes_per_launch": head_bytes}
     copy_GBps = None
@@ -364,7 +394,7 @@ def main():
         for _ in range(5):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"leg": "head", "roofline": roofline, "copy_bytes_per_launch": COPY_BYTES}))
+        print(json.dumps({"leg": "head", "roofline": head_roofline, "copy_bytes_per_launch": COPY_BYTES}))
         return
 
     # ---- CPU baseline: the oracle on this host, one core ----------------------------
@@ -372,9 +402,9 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline(args.cpu_seconds)
 
-    ms = result["ms_per_step"]
+    ms = result["ms_full"]
     line = {
-        "metric": "decode tok/s GPT-2-124M Q8_0 b1 (hot path: Q8_0 linears + fused sampler)",
+        "metric": "decode tok/s GPT-2-124M Q8_0 b1 (whole step: embedding, 12 blocks, head, fused sampler)",
         "value": round(1000.0 / ms, 1),
         "unit": "tok/s",
         "n_gpus": 1,
@@ -385,18 +415,29 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic (random-init N(0,0.02) Q8_0 weights, N(0,1) activations, random logits history)",
-        "config": {"workload": "gpt2-124m-q8_0-decode-step-hotpath", "batch": 1, "layers": L, "d_model": D,
-                   "ffn": FFN, "vocab": V, "numerics": "W8A32 (ferrum_core)", "sampler": SAMPLER,
-                   "residency": f"hbm-forced ({args.replicas} weight replicas, "
-                                f"{args.replicas * result['step_weight_bytes'] / 1e6:.0f} MB > 256 MB MALL)"},
-        "roofline": roofline,
+        "data": "synthetic (random-init N(0,0.02) Q8_0 weights, random token history)",
+        "config": {"workload": "gpt2-124m-q8_0-decode-step", "batch": 1, "layers": L, "d_model": D, "heads": HEADS,
+                   "ffn": FFN, "vocab": V, "position": FULL_POS, "numerics": "W8A32 (ferrum_core)",
+                   "sampler": SAMPLER, "launches_per_step": 3,
+                   "residency": f"hbm-forced ({args.replicas} model replicas, "
+                                f"{args.replicas * result['step_bytes'] / 1e6:.0f} MB > 256 MB MALL)"},
+        "roofline": {"bound": "hbm", "achieved": round(result["stack_gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(result["stack_gbps"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(STACK_PMC),
+                     "kernel": "k_gpt2_stack<768,64,64> (12 GPT-2 blocks, one launch)",
+                     "avg_launch_us": round(result["stack_us"], 3), "bytes_per_launch": result["stack_bytes"],
+                     "note": "bound by 60 dependent exchanges between workgroups (~2 us each), not by HBM"},
+        "step_roofline": {"bytes_per_step": result["step_bytes"],
+                          "achieved_GBps": round(result["step_bytes"] / (ms * 1e-3) / 1e9, 1),
+                          "frac": round(result["step_bytes"] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)},
+        "roofline_lm_head": head_roofline,
         "cpu_baseline": cpu,
-        "mall_resident_tok_s": round(1000.0 / result["ms_per_step_mall"], 1),
-        "step_weight_GBps": round(result["step_weight_bytes"] / (ms * 1e-3) / 1e9, 1),
-        "sampler_us_per_row": result["sampler_us_per_row"],
-        "wall_ms_per_step": round(result["wall_ms_per_step"], 5),
-        "full_decode_step": result["full_step"],
+        "mall_resident_tok_s": round(1000.0 / result["ms_full_mall"], 1),
+        "per_op_launches_tok_s": round(1000.0 / result["ms_perop"], 1),
+        "hot_path_unchained": {"tok_s": round(1000.0 / result["hot_unchained"], 1),
+                               "ms_per_step": round(result["hot_unchained"], 5),
+                               "what": "the 49 Q8_0 linears on fixed inputs (no dependence between them) + sampler"},
+        "sampler_us_per_row": round(result["sampler_us"], 2),
+        "wall_ms_per_step": round(result["wall_full"], 5),
         "b32": result["b32"],
         "prefill": result["prefill"],
         "qwen2_b64": result.get("qwen2_b64"),
@@ -662,7 +703,10 @@ def qwen_leg(ctx, fh, torch, gen, dev, steps, warmup):
 
 
 def cpu_baseline(budget_s):
-    """ferrum_core's decode-step hot path on the host CPU (the oracle, one core)."""
+    """ferrum_core's whole decode step on the host CPU (the oracle, one core):
+    CachedTransformer::feed at position 255 (embed_one, 12 x forward_with_cache,
+    final LayerNorm, the tied head over the f32-expanded weights as the
+    reference's loader builds them) + the softmax/ln bridge and the sampler."""
     import numpy as np
 
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
@@ -672,28 +716,44 @@ def cpu_baseline(budget_s):
         oracle.build()
     t_setup = time.perf_counter()
     rng = np.random.default_rng(7)
+    f32 = lambda a: np.asarray(a, np.float32)  # noqa: E731
     layers = []
     for li in range(L):
         ws = []
         for (n, k) in LAYER_SHAPES:
             raw = oracle.quantize_weight(n, k, seed=li * 10 + n + k)
-            ws.append((oracle.q8_0_to_ferrum_weight(raw, n, k), rng.standard_normal(n).astype(np.float32) * 0.1))
-        layers.append(ws)
-    head = oracle.q8_0_to_ferrum_weight(oracle.quantize_weight(V, D, seed=99), V, D)
-    x_d = rng.standard_normal((1, D)).astype(np.float32)
-    x_f = rng.standard_normal((1, FFN)).astype(np.float32)
+            ws.append((oracle.q8_0_to_ferrum_weight(raw, n, k), f32(rng.standard_normal(n) * 0.02)))
+        ln = [f32(1.0 + rng.standard_normal(D) * 0.02), f32(rng.standard_normal(D) * 0.02),
+              f32(1.0 + rng.standard_normal(D) * 0.02), f32(rng.standard_normal(D) * 0.02)]
+        # the KV cache of positions 0 .. 254 (random rows: the step's work does not depend on them)
+        kc = f32(rng.standard_normal((CTX, D)))
+        vc = f32(rng.standard_normal((CTX, D)))
+        layers.append((ws, ln, kc, vc))
+    head_raw = oracle.quantize_weight(V, D, seed=99)
+    head = oracle.q8_0_to_ferrum_weight(head_raw, V, D)          # [D, V], the tied head's f32 expansion
+    tok_w = np.ascontiguousarray(head.T)                        # [V, D], the token table
+    pos_w = f32(rng.standard_normal((CTX, D)) * 0.02)
+    lnf = (f32(1.0 + rng.standard_normal(D) * 0.02), f32(rng.standard_normal(D) * 0.02))
     recent = list(rng.integers(0, V, size=N_RECENT))
     params = oracle.SamplingParams(**SAMPLER)
     orng = oracle.Rng(7)
     setup = time.perf_counter() - t_setup
+    token = [int(recent[-1])]
 
     def one_step():
-        for ws in layers:
-            for (w_kn, b), (n, k) in zip(ws, LAYER_SHAPES):
-                oracle.linear_forward(x_d if k == D else x_f, w_kn, b, threads=1)
-        z = oracle.linear_forward(x_d, head, None, threads=1)
+        x = oracle.embed_one(tok_w, pos_w, token[0], FULL_POS)[None, :]
+        for (ws, ln, kc, vc) in layers:
+            (wq, bq), (wo, bo), (wu, bu), (wd, bd) = ws
+            h = oracle.layernorm(x, ln[0], ln[1])
+            qkv = oracle.linear_forward(h, wq, bq, threads=1)[0]
+            att = oracle.attention_decode(qkv, kc, vc, HEADS, FULL_POS)
+            x = (x + oracle.linear_forward(att[None, :], wo, bo, threads=1)).astype(np.float32)
+            h = oracle.layernorm(x, ln[2], ln[3])
+            up = oracle.gelu(oracle.linear_forward(h, wu, bu, threads=1))
+            x = (x + oracle.linear_forward(up, wd, bd, threads=1)).astype(np.float32)
+        z = oracle.linear_forward(oracle.layernorm(x, *lnf), head, None, threads=1)
         l = oracle.ln_bridge(oracle.softmax_rows(z)[0])
-        oracle.sample_with_params(l, params, recent, orng)
+        token[0] = oracle.sample_with_params(l, params, recent, orng)
 
     one_step()  # warm-up
     times = []
@@ -704,17 +764,22 @@ def cpu_baseline(budget_s):
         times.append(time.perf_counter() - t0)
     best, med = min(times), float(np.median(times))
     out = {"value": round(1.0 / med, 3), "unit": "tok/s", "cores": 1, "kind": "port",
-           "sample": f"{len(times)} GPT-2-124M decode steps of the hot path (49 f32-expanded linears, serial "
-                     f"m=1 as ferrum_core runs them, + softmax/ln bridge + sampler) in {sum(times):.1f} s; "
+           "sample": f"{len(times)} whole GPT-2-124M decode steps at position {FULL_POS} (embed_one, 12 blocks with "
+                     f"attention over a randomly filled KV cache, final LayerNorm, tied head; f32-expanded weights, "
+                     f"serial m=1 as ferrum_core runs them; softmax/ln bridge + sampler) in {sum(times):.1f} s; "
                      f"median {med * 1e3:.1f} ms/step, best {best * 1e3:.1f} ms; setup {setup:.1f} s",
            "best_tok_s": round(1.0 / best, 3)}
+    layers_w = [ws for (ws, _, _, _) in layers]
+    x_d = f32(rng.standard_normal((1, D)))
+    x_f = f32(rng.standard_normal((1, FFN)))
 
     # Second figure: the reference's only multi-core m = 1 decode, ops::qlinear
     # on per-row int8 QWeights (column split over T threads, min chunk 64).
     # Not the GPU path's numerics (those are GGUF Q8_0); a CPU bandwidth figure.
-    threads = max(1, min(os.cpu_count() or 1, 16))
+    nproc = os.cpu_count() or 1
+    threads = max(1, min(nproc, 16))  # a one-GPU box's CPU share is 16 cores whatever nproc shows
     qlayers = [[(oracle.QWeight(w_kn, w_kn.shape[0], w_kn.shape[1], oracle.INT8), b) for (w_kn, b) in ws]
-               for ws in layers]
+               for ws in layers_w]
     qhead = oracle.QWeight(head, head.shape[0], head.shape[1], oracle.INT8)
     zero_v = np.zeros(V, np.float32)
 
@@ -735,9 +800,10 @@ def cpu_baseline(budget_s):
         qt.append(time.perf_counter() - t0)
     qmed = float(np.median(qt))
     qbytes = sum(qw.q.size + qw.scales.size * 4 for ws in qlayers for (qw, _) in ws) + qhead.q.size + qhead.scales.size * 4
+    out["host_nproc"] = nproc
     out["qlinear_int8"] = {"value": round(1.0 / qmed, 3), "unit": "tok/s", "cores": threads, "kind": "port",
                            "weight_GBps": round(qbytes / qmed / 1e9, 2),
-                           "sample": f"{len(qt)} GPT-2-124M decode steps through ops::qlinear (per-row int8, "
+                           "sample": f"{len(qt)} GPT-2-124M hot-path steps (the 49 linears + head through ops::qlinear, per-row int8, "
                                      f"{qbytes / 1e6:.0f} MB/token, m = 1 column split over {threads} threads); "
                                      f"median {qmed * 1e3:.1f} ms/step"}
     return out

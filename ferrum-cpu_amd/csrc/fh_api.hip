@@ -654,7 +654,7 @@ int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, con
     if (k > 2048) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_ln: rows wider than 2048");
     if (m > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_ln: m is above 2^31 - 1");
     FH_ON_DEVICE(ctx);
-    if (numerics == FH_W8A32 && d_r) {
+    if (numerics == FH_W8A32) {
         const fh_ln_args ln{d_r, d_gamma, d_beta, d_s};
         return fh_launch_linear_ln_w8a32(ctx, w, d_x, m, ln, d_bias, d_y, activation);
     }

@@ -176,6 +176,41 @@ __device__ __forceinline__ float wave_sum(float v) {
     return v;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+__device__ __forceinline__ float rdlane(float v, int lane) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over each group of G consecutive lanes (G a power of two <= 16), every
+// lane of the group ending with the same total: quad_perm [1,0,3,2],
+// quad_perm [2,3,0,1], row_half_mirror, row_mirror.
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+    if (G >= 2) v += dpp<0xB1>(v);
+    if (G >= 4) v += dpp<0x4E>(v);
+    if (G >= 8) v += dpp<0x141>(v);
+    if (G >= 16) v += dpp<0x140>(v);
+    return v;
+}
+
+// Sum over each group of G lanes for any power of two G <= 64 (every lane of
+// the group gets the total): 16-lane rows by DPP, then across rows with
+// readlane.
+template <int G>
+__device__ __forceinline__ float group_total(float v) {
+    if constexpr (G <= 16) {
+        return group_sum<G>(v);
+    } else {
+        const float r16 = group_sum<16>(v);
+        const float lo = rdlane(r16, 0) + rdlane(r16, 16);
+        const float hi = rdlane(r16, 32) + rdlane(r16, 48);
+        return G == 64 ? lo + hi : ((threadIdx.x & 63) < 32 ? lo : hi);
+    }
+}
+
 // Sum over the workgroup in a fixed order (wave sums, then waves in order);
 // red holds one float per wave.
 __device__ __forceinline__ float block_sum(float v, float* red) {

@@ -45,6 +45,7 @@ EXPORTS = (
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async", "fh_debug_sampler_faults",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
+    "fh_gpt2_stack_create", "fh_gpt2_stack_free", "fh_gpt2_stack_forward_async",
     "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
     "fh_gguf_open", "fh_gguf_close", "fh_gguf_error", "fh_gguf_version", "fh_gguf_tensor_count", "fh_gguf_find_tensor",
     "fh_gguf_tensor_info", "fh_gguf_tensor_data", "fh_gguf_meta_type", "fh_gguf_meta_u64", "fh_gguf_meta_f64",
@@ -115,6 +116,13 @@ class Rng:
         return float(np.float32(self.next_u64() >> 40) / np.float32(1 << 24))
 
 
+class GPT2Block(C.Structure):
+    """fh_gpt2_block: one transformer block's device weights and caches."""
+
+    _fields_ = [(n, C.c_void_p) for n in ("qkv", "out", "up", "down", "qkv_b", "out_b", "up_b", "down_b", "ln1_g",
+                                           "ln1_b", "ln2_g", "ln2_b", "k_cache", "v_cache")]
+
+
 _lib = None
 
 
@@ -173,6 +181,11 @@ def lib():
         L.fh_q8_0_linear_act_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32, i32]
         L.fh_add_layernorm_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         L.fh_q8_0_linear_ln_async.argtypes = [vp, vp, vp, vp, vp, sz, sz, vp, vp, vp, sz, vp, i32, i32]
+        L.fh_gpt2_stack_create.argtypes = [vp, C.POINTER(GPT2Block), sz, sz, sz, sz, sz, vp, vp, sz, sz,
+                                           C.POINTER(vp)]
+        L.fh_gpt2_stack_free.argtypes = [vp]
+        L.fh_gpt2_stack_free.restype = None
+        L.fh_gpt2_stack_forward_async.argtypes = [vp, vp, vp, sz, vp]
         f32 = C.c_float
         L.fh_rmsnorm_async.argtypes = [vp, vp, vp, vp, sz, sz, vp, f32, vp]
         L.fh_rope_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, f32, i32, vp, f32]
@@ -910,6 +923,25 @@ class GPT2Device:
         self.token = torch.zeros(1, dtype=torch.int32, device=dev)
         self.pos = 0
         self.blocks = []
+        self.stack = None  # fh_gpt2_stack: the whole block stack as one launch (when the shape has a kernel)
+        self.fused = True
+
+    def _make_stack(self):
+        """The one-launch block stack (fh_gpt2_stack_create); shapes without a
+        kernel keep the one-launch-per-op path (FH_ERR_LIMIT)."""
+        blocks = (GPT2Block * self.layers)()
+        for i, b in enumerate(self.blocks):
+            blocks[i] = GPT2Block(b["qkv"].h, b["out"].h, b["up"].h, b["down"].h, _ptr(b["qkv_b"]), _ptr(b["out_b"]),
+                                  _ptr(b["up_b"]), _ptr(b["down_b"]), _ptr(b["ln1_g"]), _ptr(b["ln1_b"]),
+                                  _ptr(b["ln2_g"]), _ptr(b["ln2_b"]), _ptr(b["k"]), _ptr(b["v"]))
+        h = C.c_void_p()
+        rc = lib().fh_gpt2_stack_create(self.ctx.h, blocks, self.layers, self.d, self.heads, self.ffn, self.cap,
+                                        _ptr(self.tok_w), _ptr(self.pos_w), self.vocab, self.pos_w.shape[0],
+                                        C.byref(h))
+        if rc == FH_ERR_LIMIT:
+            return
+        self.ctx.check(rc)
+        self.stack = h
 
     def _block(self, ln, qkv, qkv_b, out, out_b, up, up_b, down, down_b):
         import torch
@@ -941,6 +973,7 @@ class GPT2Device:
         m.lnf_g, m.lnf_b = f(weights["lnf_g"]), f(weights["lnf_b"])
         torch.cuda.synchronize()  # uploads ran on torch's stream
         ctx.sync()
+        m._make_stack()
         return m
 
     @classmethod
@@ -978,6 +1011,7 @@ class GPT2Device:
             m.lnf_g, m.lnf_b = f("output_norm.weight"), f("output_norm.bias")
             torch.cuda.synchronize()
             ctx.sync()
+        m._make_stack()
         return m
 
     @classmethod
@@ -1008,11 +1042,19 @@ class GPT2Device:
         m.lnf_g, m.lnf_b = vec(d, 1.0), vec(d)
         torch.cuda.synchronize()
         ctx.sync()
+        m._make_stack()
         return m
 
     def feed_async(self, d_token, pos: int):
-        """One position: the head's scores for the next token land in self.z."""
+        """One position: the head's scores for the next token land in self.z.
+        With the one-launch stack: the stack (embedding and every block) into
+        self.x, then the final LayerNorm fused into the head GEMV (two
+        launches); otherwise one launch per op."""
         ctx, d = self.ctx, self.d
+        if self.stack is not None and self.fused:
+            ctx.check(lib().fh_gpt2_stack_forward_async(ctx.h, self.stack, _ptr(d_token), int(pos), _ptr(self.x)))
+            linear_ln_async(ctx, self.head, self.x, None, None, 1, d, self.lnf_g, self.lnf_b, None, 0, self.z)
+            return
         embed_one_async(ctx, self.tok_w, self.pos_w, self.vocab, self.pos_w.shape[0], d, d_token, pos, self.x)
         cur, other = self.x, self.x2
         for i, b in enumerate(self.blocks):
@@ -1035,6 +1077,8 @@ class GPT2Device:
 
     def launches_per_step(self) -> int:
         """Kernel launches of feed_async (the sampler not included)."""
+        if self.stack is not None and self.fused:
+            return 2
         return 2 + 5 * self.layers + 1
 
     def forward(self, ids, reprime: bool):
@@ -1058,6 +1102,9 @@ class GPT2Device:
         return self.z.cpu().numpy()
 
     def free(self):
+        if self.stack is not None:
+            lib().fh_gpt2_stack_free(self.stack)
+            self.stack = None
         self.head.free()
         for b in self.blocks:
             for key in ("qkv", "out", "up", "down"):

@@ -212,10 +212,11 @@ int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t
                          int logits_kind, const fh_sampling_params* params,
                          const uint32_t* d_recent, const uint32_t* d_recent_offsets,
                          const uint64_t* d_draws, uint32_t* d_out_ids);
-/* Testing hook, no reference counterpart: make the split sampler's segment
- * `skip_segment` (-1: none) publish nothing and its bounded waits give up after
- * `spin_limit` polls (0: the default, 2^20), for later calls on ctx, so a test
- * can drive the failure path from the host while every kernel still ends. */
+/* Testing hook, no reference counterpart: for later calls on ctx, the split
+ * sampler's segment `skip_segment` and workgroup `skip_segment` of
+ * fh_gpt2_stack_forward_async publish nothing (-1: none), and their bounded
+ * waits give up after `spin_limit` polls (0: the default, 2^20), so a test can
+ * drive the failure path from the host while every kernel still ends. */
 int fh_debug_sampler_faults(fh_ctx* ctx, int skip_segment, uint32_t spin_limit);
 
 /* ---- the rest of a GPT-2 decode step ------------------------------------- */
@@ -261,6 +262,44 @@ int fh_add_layernorm_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t row
 int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, const float* d_r, float* d_s,
                             size_t m, size_t k, const float* d_gamma, const float* d_beta, const float* d_bias,
                             size_t bias_len, float* d_y, int numerics, int activation);
+
+/* ---- a GPT-2 decode position's block stack in one launch --------------------
+ * CachedTransformer::feed for one token up to the final LayerNorm
+ * (slm/cached.rs:100-125): embed_one (layer/embedding.rs:70-90), then every
+ * block's forward_with_cache (layer/transformer.rs:221-290: LayerNorm, fused
+ * Q|K|V, KV-cache append and attention, out projection, residual, LayerNorm,
+ * up + GELU, down, residual), as ONE kernel launch whose workgroups exchange
+ * each phase's outputs through device memory (bounded waits; a wait that gives
+ * up is FH_ERR_EXCHANGE at the next fh_sync).  The same arithmetic as the
+ * separate calls above, within the 1e-5 rule.  The final LayerNorm, the head
+ * (fh_q8_0_linear_ln_async) and the sampler follow as usual. */
+typedef struct {
+    const fh_q8_0* qkv;   /* [3d x d] */
+    const fh_q8_0* out;   /* [d x d] */
+    const fh_q8_0* up;    /* [ffn x d] */
+    const fh_q8_0* down;  /* [d x ffn] */
+    const float *qkv_b, *out_b, *up_b, *down_b;  /* device */
+    const float *ln1_g, *ln1_b, *ln2_g, *ln2_b;  /* device, d each */
+    float* k_cache;       /* device, [capacity, d] */
+    float* v_cache;
+} fh_gpt2_block;
+typedef struct fh_gpt2_stack fh_gpt2_stack;
+/* Builds the device state of a stack of `layers` blocks (the block table,
+ * exchange slots, launch counters); weights, caches and the token / position
+ * tables stay the caller's and must outlive the stack.  d = 768 or 1024 with
+ * head width 64, or d = 128 with head width 32; ffn = 4 d; capacity <= 4096
+ * (and within the device's LDS: 1024 at d = 768) -> else FH_ERR_LIMIT; a
+ * weight of the wrong shape -> FH_ERR_DIM. */
+int fh_gpt2_stack_create(fh_ctx* ctx, const fh_gpt2_block* blocks, size_t layers, size_t d, size_t heads,
+                         size_t ffn, size_t capacity, const float* d_tok_w, const float* d_pos_w, size_t vocab,
+                         size_t max_seq, fh_gpt2_stack** out);
+void fh_gpt2_stack_free(fh_gpt2_stack* s);
+/* One position: the token id is read from device memory (a sampled id feeds
+ * the next step without a copy); k and v of every block are written at cache
+ * row pos; the final residual stream [d] goes to d_x.  pos >= max_seq or pos >=
+ * capacity -> FH_ERR_DIM with the reference's messages.  Calls on one stack
+ * must not overlap. */
+int fh_gpt2_stack_forward_async(fh_ctx* ctx, fh_gpt2_stack* s, const uint32_t* d_token, size_t pos, float* d_x);
 
 /* ---- Llama / Qwen block pieces (ferrum_core llm.rs), batched over rows ------
  * Each row is one sequence of a batched decode.  Positions live on the device

@@ -8,11 +8,14 @@ import numpy as np
 VOCAB, D, HEADS, LAYERS, FFN, CTX = 4096, 128, 4, 4, 512, 256
 
 
-def make_weights(orc, seed=11, vocab=VOCAB, d=D, layers=LAYERS, ffn=FFN, ctx=CTX):
+def make_weights(orc, seed=11, vocab=VOCAB, d=D, layers=LAYERS, ffn=FFN, ctx=CTX, std=None):
+    """Random weights in GgufOut::gpt2's naming.  std=None gives each matrix its
+    own spread (0.05-0.3, so the tiny model's scores are not flat); a number
+    draws every Q8_0 matrix from N(0, std), as BASELINE's configs do (0.02)."""
     rng = np.random.default_rng(seed)
 
     def q8(n, k, scale):
-        return orc.q8_0_encode((rng.standard_normal(n * k) * scale).astype(np.float32))
+        return orc.q8_0_encode((rng.standard_normal(n * k) * (scale if std is None else std)).astype(np.float32))
 
     def vec(n, scale, base=0.0):
         return (base + rng.standard_normal(n) * scale).astype(np.float32)

@@ -1,0 +1,170 @@
+"""The one-launch GPT-2 block stack (fh_gpt2_stack_*, csrc/fh_decode.hip)
+against the oracle's CachedTransformer::feed (slm/cached.rs:100-125,
+layer/transformer.rs:221-290) and against the one-launch-per-op device path:
+the tiny configuration and the GPT-2-124M shape (12
+blocks, d = 768, 12 heads, N(0, 0.02) Q8_0 weights) across positions that
+span several 64-position attention items per head; HIP graph replays (the
+stack's launch counters); the reference's position errors; a failed exchange
+forced from the host, reported and recovered from."""
+import numpy as np
+import pytest
+
+import gpt2_tiny
+
+pytestmark = pytest.mark.gpu
+
+G124 = dict(vocab=50257, d=768, heads=12, layers=12, ffn=3072, ctx=1024)
+
+
+def device_model(fh, w, cfg):
+    import ferrum_hip
+
+    return ferrum_hip.GPT2Device.from_weights(fh, w, cfg["vocab"], cfg["d"], cfg["heads"], cfg["layers"], cfg["ffn"],
+                                              cfg["ctx"])
+
+
+def feed(model, tok, pos, fused):
+    import torch
+
+    model.fused = fused
+    model.token.fill_(int(tok))
+    torch.cuda.synchronize()
+    model.feed_async(model.token, pos)
+    model.ctx.sync()
+    torch.cuda.synchronize()
+    return model.z.cpu().numpy().copy()
+
+
+def assert_scores_close(got, want, what):
+    err = np.abs(np.asarray(got, np.float64) - want).max()
+    scale = np.abs(want).max()
+    assert err <= 2e-5 * scale, f"{what}: max |diff| {err:.3e} against max |score| {scale:.3e}"
+
+
+@pytest.fixture(scope="module")
+def tiny_pair(fh, orc):
+    w = gpt2_tiny.make_weights(orc)
+    m = device_model(fh, w, dict(vocab=gpt2_tiny.VOCAB, d=gpt2_tiny.D, heads=gpt2_tiny.HEADS,
+                                 layers=gpt2_tiny.LAYERS, ffn=gpt2_tiny.FFN, ctx=gpt2_tiny.CTX))
+    yield w, m
+    m.free()
+
+
+def test_tiny_stack_matches_oracle_and_per_op_path(fh, orc, tiny_pair):
+    """Positions 0 .. 149 (three attention items per head at the end): the
+    stack's scores against the oracle's, and against the one-launch-per-op
+    path fed the same tokens into its own cache."""
+    w, m = tiny_pair
+    assert m.stack is not None and m.launches_per_step() == 2
+    ref = gpt2_tiny.OracleGPT2(orc, w)
+    ids = np.random.default_rng(21).integers(0, gpt2_tiny.VOCAB, 150)
+    per_op = [feed(m, t, p, False) for p, t in enumerate(ids)]  # fills the cache the per-op way
+    for p, t in enumerate(ids):
+        z = feed(m, t, p, True)                                   # rewrites row p, reads rows < p
+        want = ref.feed(t)
+        assert_scores_close(z, want, f"stack at position {p}")
+        assert_scores_close(z, per_op[p], f"stack vs per-op at position {p}")
+
+
+@pytest.fixture(scope="module")
+def g124(fh, orc):
+    w = gpt2_tiny.make_weights(orc, seed=3, vocab=G124["vocab"], d=G124["d"], layers=G124["layers"],
+                               ffn=G124["ffn"], ctx=G124["ctx"], std=0.02)
+    m = device_model(fh, w, G124)
+    yield w, m
+    m.free()
+
+
+def test_gpt2_124m_stack_matches_oracle(fh, orc, g124):
+    """GPT-2-124M shape with N(0, 0.02) weights: 130 positions through the
+    stack (three 64-position attention items per head at the end), the scores
+    at every tenth position and the last against the oracle's."""
+    w, m = g124
+    assert m.stack is not None
+    ref = gpt2_tiny.OracleGPT2(orc, w, **{k: G124[k] for k in ("vocab", "d", "heads", "layers", "ffn")},
+                               ctx=G124["ctx"])
+    ids = np.random.default_rng(5).integers(0, G124["vocab"], 130)
+    for p, t in enumerate(ids):
+        z = feed(m, t, p, True)
+        want = ref.feed(t)
+        if p % 10 == 0 or p == len(ids) - 1:
+            assert_scores_close(z, want, f"124M stack at position {p}")
+
+
+def test_gpt2_124m_stack_agrees_with_per_op_path(fh, orc, g124):
+    """The same positions through both device paths (each re-primed from 0)."""
+    w, m = g124
+    ids = np.random.default_rng(6).integers(0, G124["vocab"], 70)
+    a = [feed(m, t, p, True) for p, t in enumerate(ids)]
+    b = [feed(m, t, p, False) for p, t in enumerate(ids)]
+    for p in (0, 1, 63, 64, 65, 69):
+        assert_scores_close(a[p], b[p], f"position {p}")
+
+
+def test_stack_replays_in_a_graph(fh, orc, tiny_pair):
+    """The launch counters advance per replay: replays of a captured step give
+    the eager result, with eager work between them."""
+    import torch
+
+    import ferrum_hip
+
+    w, m = tiny_pair
+    ids = np.random.default_rng(8).integers(0, gpt2_tiny.VOCAB, 40)
+    for p, t in enumerate(ids[:-1]):
+        feed(m, t, p, True)
+    pos = len(ids) - 1
+    want = feed(m, ids[-1], pos, True)
+    s = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    m.token.fill_(int(ids[-1]))
+    torch.cuda.synchronize()
+    with torch.cuda.graph(g, stream=s):
+        fh.set_stream(torch.cuda.current_stream().cuda_stream)
+        m.feed_async(m.token, pos)
+    fh.set_stream(None)
+    try:
+        for rep in range(4):
+            m.z.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            fh.sync()
+            assert np.array_equal(m.z.cpu().numpy(), want), rep
+            feed(m, ids[-1], pos, True)  # eager launches between replays
+    finally:
+        del g
+    assert isinstance(ferrum_hip.GPT2Device, type)
+
+
+def test_stack_position_errors(fh, tiny_pair):
+    import ferrum_hip
+
+    _, m = tiny_pair
+    with pytest.raises(ferrum_hip.DimMismatch, match="exceeds max_seq_len|KvCache full"):
+        m.feed_async(m.token, gpt2_tiny.CTX)
+
+
+def test_a_failed_stack_exchange_is_reported_and_recovered(fh, orc, tiny_pair):
+    """Workgroup 5 publishes none of its outputs (testing hook) and the waits
+    give up after 64 polls: every workgroup ends, fh_sync reports
+    FH_ERR_EXCHANGE, and a re-primed run is exact again."""
+    import ferrum_hip
+
+    w, m = tiny_pair
+    ids = np.random.default_rng(9).integers(0, gpt2_tiny.VOCAB, 6)
+    fh.debug_sampler_faults(5, 64)
+    try:
+        m.fused = True
+        m.token.fill_(int(ids[0]))
+        import torch
+
+        torch.cuda.synchronize()
+        m.feed_async(m.token, 0)
+        with pytest.raises(ferrum_hip.FerrumHipError) as e:
+            fh.sync()
+        assert e.value.code == ferrum_hip.FH_ERR_EXCHANGE
+    finally:
+        fh.debug_sampler_faults(-1, 0)
+    fh.sync()
+    ref = gpt2_tiny.OracleGPT2(orc, w)
+    for p, t in enumerate(ids):
+        assert_scores_close(feed(m, t, p, True), ref.feed(t), f"after recovery, position {p}")
