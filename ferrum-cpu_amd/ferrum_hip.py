@@ -1081,6 +1081,51 @@ class GPT2Device:
             return 2
         return 2 + 5 * self.layers + 1
 
+    def generate(self, prompt, max_tokens: int, params: SamplingParams, rng: Rng, eos=None, bos: int = 0):
+        """GenerativeSLM::token_stream + stream_next (slm/token_stream.rs:66-190)
+        with every step on the device: the prompt is fed position by position,
+        then each step runs the block stack, the head and the fused sampler,
+        which writes its id straight into the device history (the penalty
+        window) where the next step's embedding reads it.  The draws are the
+        ones gpt2_decode takes from rng (one next_u64 per sampled step, none
+        when greedy), generated up front.  Same kernels and order as
+        gpt2_decode over forward(), so the same ids; the host only sees the ids
+        at the end (an EOS ends the returned list as in the reference; the
+        steps computed past it are discarded).  A run that would outgrow the
+        window (prompt + max_tokens > context: the reference cuts and
+        re-primes) takes the host loop instead."""
+        import torch
+
+        win = GPT2Window(self.cap, prompt, bos)
+        n0 = len(win.ids)
+        if n0 + max_tokens > self.cap or self.stack is None or not self.fused:
+            return gpt2_decode(self.ctx, self.forward, prompt, max_tokens, params, rng, self.cap, eos, bos)
+        ctx, dev = self.ctx, "cuda"
+        greedy = params.temperature <= 0.0
+        hist = torch.zeros(n0 + max_tokens, dtype=torch.int32, device=dev)
+        hist[:n0] = torch.tensor(win.ids, dtype=torch.int32, device=dev)
+        offs = torch.tensor([[0, n0 + k] for k in range(max_tokens)], dtype=torch.int32, device=dev)
+        draws = None
+        if not greedy:
+            d = np.array([rng.next_u64() for _ in range(max_tokens)], dtype=np.uint64)
+            draws = torch.from_numpy(d.view(np.int64)).to(dev)
+        torch.cuda.synchronize()
+        ctx.sync()
+        # prime: positions 0 .. n0 - 1 (the head only after the last)
+        for p in range(n0 - 1):
+            ctx.check(lib().fh_gpt2_stack_forward_async(ctx.h, self.stack, hist.data_ptr() + 4 * p, p, _ptr(self.x)))
+        for k in range(max_tokens):
+            p = n0 - 1 + k
+            self.feed_async(hist.data_ptr() + 4 * p, p)
+            sample_rows_async(ctx, self.z, 1, self.vocab, params, hist, offs[k], None if greedy else draws[k:],
+                              hist.data_ptr() + 4 * (n0 + k), LOGITS_GPT2_SOFTMAX)
+        ctx.sync()
+        self.pos = n0 + max_tokens - 1
+        out = [int(t) for t in hist[n0:].cpu().numpy()]
+        if eos is not None and eos in out:
+            out = out[:out.index(eos)]
+        return out
+
     def forward(self, ids, reprime: bool):
         """gpt2_decode's forward: re-feed the whole window from position 0, or
         feed its last id at the next position.  Returns the scores (host)."""

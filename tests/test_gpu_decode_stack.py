@@ -168,3 +168,42 @@ def test_a_failed_stack_exchange_is_reported_and_recovered(fh, orc, tiny_pair):
     ref = gpt2_tiny.OracleGPT2(orc, w)
     for p, t in enumerate(ids):
         assert_scores_close(feed(m, t, p, True), ref.feed(t), f"after recovery, position {p}")
+
+
+CONFIG3 = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
+
+
+def test_config3_run_replays_on_the_oracle(fh, orc, g124):
+    """BASELINE configs[2] end to end: GPT-2-124M (N(0, 0.02) Q8_0 weights), a
+    128-token random prompt, then 32 steps sampled with temperature 0.8,
+    top-k 40, top-p 0.95 and repetition penalty 1.1 over the window, the draws
+    from Rng (slm/token_stream.rs:66-190, slm/cached.rs:100-137).  The
+    device-resident run (GPT2Device.generate: the sampler's id feeds the next
+    step on the device) equals the host loop over forward() id for id, and
+    every step replays on the oracle's model and sampler with the same window
+    and draw; a differing id must be one the oracle reports within the
+    sampler's margins, and the replay continues from the device's id."""
+    import ferrum_hip
+    from sampler_margins import exempt
+
+    w, m = g124
+    prompt = [int(t) for t in np.random.default_rng(128).integers(0, G124["vocab"], 128)]
+    params = ferrum_hip.SamplingParams(**CONFIG3)
+    ids = m.generate(prompt, 32, params, ferrum_hip.Rng(11))
+    assert len(ids) == 32
+    host = ferrum_hip.gpt2_decode(fh, m.forward, prompt, 32, params, ferrum_hip.Rng(11), G124["ctx"])
+    assert host == ids
+    ref = gpt2_tiny.OracleGPT2(orc, w, **{k: G124[k] for k in ("vocab", "d", "heads", "layers", "ffn")},
+                               ctx=G124["ctx"])
+    win, rng, op = ferrum_hip.GPT2Window(G124["ctx"], prompt), orc.Rng(11), orc.SamplingParams(**CONFIG3)
+    z = ref.forward(win.ids, True)
+    n_exempt = 0
+    for step, tok in enumerate(ids):
+        want, info = orc.sample(orc.ln_bridge(orc.softmax_rows(z)[0]), op, win.ids, rng.next_u64())
+        if want != tok:
+            assert exempt(info, False), (step, tok, want, info.topk_gap, info.topp_gap, info.draw_gap)
+            n_exempt += 1
+        win.push(tok)
+        z = ref.forward(win.ids, False)
+    print(f"config-3 run: 32 steps, {n_exempt} exempt")
+    assert n_exempt <= 2
