@@ -103,11 +103,12 @@ def main():
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--leg", choices=["all", "stack", "head", "prefill", "qwen", "qlinear"], default="all",
+    ap.add_argument("--leg", choices=["all", "stack", "head", "prefill", "qwen", "qlinear", "dropin"], default="all",
                     help="'stack': only the whole decode step and its one-launch block stack (for profiles and "
                          "counter runs); 'head': only the lm_head GEMV roofline leg; 'prefill': only the "
                          "GPT-2-medium prefill GEMMs; 'qwen': only the Qwen2-shaped batch-64 step; 'qlinear': only "
-                         "the per-row int8 and int4 qlinear steps")
+                         "the per-row int8 and int4 qlinear steps; 'dropin': the blocking per-call linear and the "
+                         "exact mode")
     ap.add_argument("--prefill-steps", type=int, default=3)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -327,6 +328,12 @@ def main():
         del graphs_b, reps
         torch.cuda.synchronize()
 
+    if args.leg in ("all", "dropin"):
+        result["dropin"] = dropin_leg(ctx, fh, torch, gen, dev)
+    if args.leg == "dropin":
+        print(json.dumps({"leg": "dropin", "dropin": result["dropin"]}))
+        return
+
     if args.leg in ("all", "prefill"):
         result["prefill"] = prefill_leg(ctx, fh, torch, gen, dev, args.prefill_steps)
 
@@ -464,12 +471,56 @@ def main():
         "b32": result["b32"],
         "prefill": result["prefill"],
         "qwen2_b64": result.get("qwen2_b64"),
+        "dropin_linear": result.get("dropin"),
         "qlinear_int8_gpu": result.get("qlinear_gpu"),
         "qlinear_int4_gpu": result.get("qlinear4_gpu"),
         "hbm_copy_GBps": round(copy_GBps, 1) if copy_GBps else None,
         "shard_head_gemv": result["shard_head"],
     }
     print(json.dumps(line))
+
+
+def dropin_leg(ctx, fh, torch, gen, dev, calls=200):
+    """The drop-in boundary as ferrum_core's Linear would call it: the blocking
+    fh_q8_0_linear (host x and bias in, host y out; it allocates device
+    buffers, copies in, runs, copies out and synchronises per call), timed on
+    the host per call at m = 1 for the GPT-2-124M shapes, beside the device
+    form's kernel time (HIP events, one weight: MALL-resident) and the opt-in
+    bit-exact mode (FH_W8A32_EXACT, device form)."""
+    import numpy as np
+
+    out = {}
+    for (n, k) in LAYER_SHAPES + [(V, D)]:
+        w = make_weight(ctx, fh, torch, n, k, gen)
+        x = np.random.default_rng(n + k).standard_normal((1, k), dtype=np.float32)
+        b = np.random.default_rng(n).standard_normal(n, dtype=np.float32) if n != V else None
+        for _ in range(5):
+            fh.linear_forward(ctx, x, w, b)
+        t0 = time.perf_counter()
+        for _ in range(calls):
+            fh.linear_forward(ctx, x, w, b)
+        blocking_us = (time.perf_counter() - t0) / calls * 1e6
+        dx = torch.from_numpy(x).to(dev)
+        db = None if b is None else torch.from_numpy(b).to(dev)
+        dy = torch.empty((1, n), device=dev)
+        row = {"blocking_us": round(blocking_us, 2)}
+        for name, mode in (("async_us", fh.W8A32), ("exact_async_us", fh.W8A32_EXACT)):
+            for _ in range(5):
+                fh.linear_forward_async(ctx, w, dx, 1, k, db, 0 if b is None else n, dy, mode)
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(calls):
+                fh.linear_forward_async(ctx, w, dx, 1, k, db, 0 if b is None else n, dy, mode)
+            e1.record()
+            torch.cuda.synchronize()
+            row[name] = round(e0.elapsed_time(e1) / calls * 1e3, 3)
+        ctx.sync()
+        w.free()
+        out[f"{n}x{k}"] = row
+    out["what"] = ("m = 1, one weight per shape (MALL-resident); blocking = host wall clock per fh_q8_0_linear call "
+                   "(host arrays), async = the device form's time per launch (HIP events, back to back)")
+    return out
 
 
 def prefill_leg(ctx, fh, torch, gen, dev, steps):

@@ -3,6 +3,7 @@
 // Argument checking and error text follow the reference entry points each
 // function replaces (cited per function); kernels live in the other
 // translation units and are reached through the fh_launch_* launchers.
+#include <algorithm>
 #include <cstdio>
 #include <cstring>
 #include <new>
@@ -54,6 +55,34 @@ static int grow_area(fh_ctx* ctx, void** area, size_t* area_bytes, size_t bytes,
 int fh_workspace(fh_ctx* ctx, size_t bytes, void** out) { return grow_area(ctx, &ctx->ws, &ctx->ws_bytes, bytes, out); }
 
 int fh_act_area(fh_ctx* ctx, size_t bytes, void** out) { return grow_area(ctx, &ctx->act, &ctx->act_bytes, bytes, out); }
+
+// Pinned host staging of the blocking calls (grown with hipHostMalloc; only
+// touched by blocking calls, which synchronise before they return).
+constexpr size_t kPinMax = size_t(8) << 20;  // larger arguments are copied from the caller's memory directly
+static int pin_area(fh_ctx* ctx, size_t bytes, char** out) {
+    bytes = fh_align256(bytes ? bytes : 256);
+    if (ctx->pin_bytes < bytes) {
+        if (ctx->pin) {
+            FH_HIP(ctx, hipStreamSynchronize(ctx->stream));
+            FH_HIP(ctx, hipHostFree(ctx->pin));
+            ctx->pin = nullptr;
+            ctx->pin_bytes = 0;
+        }
+        FH_HIP(ctx, hipHostMalloc(&ctx->pin, bytes, hipHostMallocDefault));
+        ctx->pin_bytes = bytes;
+    }
+    *out = static_cast<char*>(ctx->pin);
+    return FH_OK;
+}
+
+// The blocking calls' device buffers: kept on the context, so a call in steady
+// state allocates nothing (no hipMalloc / hipFree per call).
+static int io_area(fh_ctx* ctx, size_t bytes, char** out) {
+    void* p = nullptr;
+    const int rc = grow_area(ctx, &ctx->io, &ctx->io_bytes, bytes, &p);
+    *out = static_cast<char*>(p);
+    return rc;
+}
 
 // Grow a zero-initialised area (kernels leave it zeroed again).  Growing
 // synchronises the stream and is refused under graph capture.
@@ -180,6 +209,8 @@ void fh_ctx_destroy(fh_ctx* ctx) {
     if (ctx->sync) (void)hipFree(ctx->sync);
     if (ctx->counters) (void)hipFree(ctx->counters);
     if (ctx->act) (void)hipFree(ctx->act);
+    if (ctx->io) (void)hipFree(ctx->io);
+    if (ctx->pin) (void)hipHostFree(ctx->pin);
     if (ctx->status) (void)hipFree(ctx->status);
     if (ctx->own) (void)hipStreamDestroy(ctx->own);
     delete ctx;
@@ -319,7 +350,7 @@ void fh_q8_0_free(fh_q8_0* w) {
 static int check_linear(fh_ctx* ctx, const fh_q8_0* w, size_t k, const void* bias, size_t bias_len,
                         int numerics) {
     if (!w) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight is NULL");
-    if (numerics != FH_W8A32 && numerics != FH_W8A8)
+    if (numerics != FH_W8A32 && numerics != FH_W8A8 && numerics != FH_W8A32_EXACT)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: unknown numerics " + std::to_string(numerics));
     if (w->device != ctx->device)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight lives on another device");
@@ -332,6 +363,17 @@ static int check_linear(fh_ctx* ctx, const fh_q8_0* w, size_t k, const void* bia
     return FH_OK;
 }
 
+// The linear in one numerics mode; the W8A32 kernels apply the activation
+// themselves, the other modes by a GELU pass after the linear.
+static int launch_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                         int numerics, int act = FH_ACT_NONE) {
+    if (numerics == FH_W8A32) return fh_launch_linear_w8a32(ctx, w, x, m, bias, y, act);
+    int rc = numerics == FH_W8A8 ? fh_launch_linear_w8a8(ctx, w, x, m, bias, y)
+                                 : fh_launch_linear_exact(ctx, w, x, m, bias, y);
+    if (rc == FH_OK && act == FH_ACT_GELU) rc = fh_launch_gelu(ctx, y, m * w->n);
+    return rc;
+}
+
 int fh_q8_0_linear_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
                          const float* d_bias, size_t bias_len, float* d_y, int numerics) {
     if (!ctx) return FH_ERR_INVALID;
@@ -341,8 +383,7 @@ int fh_q8_0_linear_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t
     if (m == 0) return FH_OK;
     if (!d_x || !d_y) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x or y is NULL");
     FH_ON_DEVICE(ctx);
-    return numerics == FH_W8A32 ? fh_launch_linear_w8a32(ctx, w, d_x, m, d_bias, d_y)
-                                : fh_launch_linear_w8a8(ctx, w, d_x, m, d_bias, d_y);
+    return launch_linear(ctx, w, d_x, m, d_bias, d_y, numerics);
 }
 
 int fh_q8_0_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, size_t k,
@@ -355,25 +396,38 @@ int fh_q8_0_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, size
     if (!x || !y) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x or y is NULL");
     FH_ON_DEVICE(ctx);
     size_t xb = fh_align256(m * k * 4), bb = fh_align256(bias_len * 4), yb = fh_align256(m * w->n * 4);
-    // Device buffers of the blocking call sit past the kernels' own workspace
-    // needs, so allocate them separately from ctx->ws.
+    // Device copies of the arguments live in the context's io area, apart
+    // from ctx->ws, which the kernels themselves may use.
     char* dev = nullptr;
-    FH_HIP(ctx, hipMalloc(&dev, xb + bb + yb));
+    if ((rc = io_area(ctx, xb + bb + yb, &dev))) return rc;
     float* dx = reinterpret_cast<float*>(dev);
     float* db = bias_len ? reinterpret_cast<float*>(dev + xb) : nullptr;
     float* dy = reinterpret_cast<float*>(dev + xb + bb);
-    hipError_t e = hipMemcpyAsync(dx, x, m * k * 4, hipMemcpyHostToDevice, ctx->stream);
-    if (e == hipSuccess && db) e = hipMemcpyAsync(db, bias, bias_len * 4, hipMemcpyHostToDevice, ctx->stream);
+    // Small calls (the decode shapes) go through pinned staging: x and bias
+    // in one copy, y out in one; large ones copy the caller's memory directly.
+    char* pin = nullptr;
+    const bool staged = xb + bb <= kPinMax && yb <= kPinMax;
+    if (staged && (rc = pin_area(ctx, std::max(xb + bb, yb), &pin))) return rc;
+    hipError_t e;
+    if (staged) {
+        std::memcpy(pin, x, m * k * 4);
+        if (bias_len) std::memcpy(pin + xb, bias, bias_len * 4);
+        e = hipMemcpyAsync(dx, pin, xb + bias_len * 4, hipMemcpyHostToDevice, ctx->stream);
+    } else {
+        e = hipMemcpyAsync(dx, x, m * k * 4, hipMemcpyHostToDevice, ctx->stream);
+        if (e == hipSuccess && db) e = hipMemcpyAsync(db, bias, bias_len * 4, hipMemcpyHostToDevice, ctx->stream);
+    }
     if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_linear copy-in");
-    if (rc == FH_OK) rc = numerics == FH_W8A32 ? fh_launch_linear_w8a32(ctx, w, dx, m, db, dy)
-                                               : fh_launch_linear_w8a8(ctx, w, dx, m, db, dy);
+    if (rc == FH_OK) rc = launch_linear(ctx, w, dx, m, db, dy, numerics);
     if (rc == FH_OK) {
-        e = hipMemcpyAsync(y, dy, m * w->n * 4, hipMemcpyDeviceToHost, ctx->stream);
+        // (stream order: the staging's copy-in has finished before this reuses it)
+        e = hipMemcpyAsync(staged ? static_cast<void*>(pin) : static_cast<void*>(y), dy, m * w->n * 4,
+                           hipMemcpyDeviceToHost, ctx->stream);
         if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_linear copy-out");
     }
     e = hipStreamSynchronize(ctx->stream);
     if (rc == FH_OK && e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_linear sync");
-    (void)hipFree(dev);
+    if (rc == FH_OK && staged) std::memcpy(y, pin, m * w->n * 4);
     return rc;
 }
 
@@ -402,8 +456,8 @@ int fh_q8_0_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out) {
     FH_ON_DEVICE(ctx);
     size_t xb = fh_align256(n * 4), ob = n / 32 * 34;
     char* dev = nullptr;
-    FH_HIP(ctx, hipMalloc(&dev, xb + ob));
-    int rc = FH_OK;
+    int rc = io_area(ctx, xb + ob, &dev);
+    if (rc) return rc;
     hipError_t e = hipMemcpyAsync(dev, x, n * 4, hipMemcpyHostToDevice, ctx->stream);
     if (e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_encode copy-in");
     if (rc == FH_OK) rc = fh_launch_encode(ctx, reinterpret_cast<float*>(dev), n, reinterpret_cast<uint8_t*>(dev + xb));
@@ -413,7 +467,6 @@ int fh_q8_0_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out) {
     }
     e = hipStreamSynchronize(ctx->stream);
     if (rc == FH_OK && e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_q8_0_encode sync");
-    (void)hipFree(dev);
     return rc;
 }
 
@@ -496,7 +549,7 @@ int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, 
     size_t lb = fh_align256(rows * vocab * 4), rb = fh_align256(n_recent * 4 + 4),
            ob = fh_align256((rows + 1) * 4), db = fh_align256(rows * 8), yb = fh_align256(rows * 4);
     char* dev = nullptr;
-    FH_HIP(ctx, hipMalloc(&dev, lb + rb + ob + db + yb));
+    if ((rc = io_area(ctx, lb + rb + ob + db + yb, &dev))) return rc;
     float* d_logits = reinterpret_cast<float*>(dev);
     uint32_t* d_recent = reinterpret_cast<uint32_t*>(dev + lb);
     uint32_t* d_off = reinterpret_cast<uint32_t*>(dev + lb + rb);
@@ -528,7 +581,6 @@ int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, 
     if (rc == FH_OK && e != hipSuccess) rc = fh_hip_fail(ctx, e, "fh_sample_rows sync");
     if (rc == FH_OK) rc = fh_take_status(ctx);
     delete[] hoff;
-    (void)hipFree(dev);
     return rc;
 }
 
@@ -618,10 +670,7 @@ int fh_q8_0_linear_act_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, si
     if (m == 0) return FH_OK;
     if (!d_x || !d_y) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x or y is NULL");
     FH_ON_DEVICE(ctx);
-    if (numerics == FH_W8A32) return fh_launch_linear_w8a32(ctx, w, d_x, m, d_bias, d_y, activation);
-    rc = fh_launch_linear_w8a8(ctx, w, d_x, m, d_bias, d_y);
-    if (rc == FH_OK && activation == FH_ACT_GELU) rc = fh_launch_gelu(ctx, d_y, m * w->n);
-    return rc;
+    return launch_linear(ctx, w, d_x, m, d_bias, d_y, numerics, activation);
 }
 
 int fh_add_layernorm_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t rows, size_t d, const float* d_gamma,
@@ -664,10 +713,7 @@ int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, con
     float* hf = static_cast<float*>(h);
     rc = fh_launch_add_layernorm(ctx, d_x, d_r, d_s, m, k, d_gamma, d_beta, hf);
     if (rc) return rc;
-    if (numerics == FH_W8A32) return fh_launch_linear_w8a32(ctx, w, hf, m, d_bias, d_y, activation);
-    rc = fh_launch_linear_w8a8(ctx, w, hf, m, d_bias, d_y);
-    if (rc == FH_OK && activation == FH_ACT_GELU) rc = fh_launch_gelu(ctx, d_y, m * w->n);
-    return rc;
+    return launch_linear(ctx, w, hf, m, d_bias, d_y, numerics, activation);
 }
 
 // ---- Llama / Qwen block pieces ---------------------------------------------------

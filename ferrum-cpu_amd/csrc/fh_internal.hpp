@@ -41,6 +41,15 @@ struct fh_ctx {
     // linear), separate from ws, which the linear itself may use.
     void* act = nullptr;
     size_t act_bytes = 0;
+    // Grow-on-demand device copies of the blocking calls' host arguments and
+    // results (each blocking call synchronises before it returns, so one
+    // area serves them all).
+    void* io = nullptr;
+    size_t io_bytes = 0;
+    // Pinned host staging for the blocking calls' small arguments (one DMA
+    // copy each way instead of one pageable copy per argument).
+    void* pin = nullptr;
+    size_t pin_bytes = 0;
     // Device status word: kernels OR in FH_STATUS_* bits (a bounded wait that
     // gave up, decreasing recent offsets); fh_sync and the blocking calls read
     // and clear it.
@@ -131,6 +140,8 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                         const float* bias, float* y);
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                           const float* bias, float* y);
+// FH_W8A32_EXACT: ferrum_core's sequential sums, bit for bit (no K split).
+int fh_launch_linear_exact(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y);
 int fh_launch_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out);
 int fh_launch_embed_one(fh_ctx* ctx, const float* tok_w, const float* pos_w, size_t vocab, size_t d,
                         const uint32_t* token, size_t pos, float* out);

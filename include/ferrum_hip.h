@@ -74,8 +74,14 @@ enum {
  *  FH_W8A8:  llama.cpp's semantics, which the reference names as the
  *            behaviour it does NOT follow (MANUAL.md:1609-1611): activations
  *            Q8_0-encoded per 32 with q8_0_block, exact int32 block dots,
- *            then y = sum_b f32(dot_b) * (d_w * d_x) + bias. */
-enum { FH_W8A32 = 0, FH_W8A8 = 1 };
+ *            then y = sum_b f32(dot_b) * (d_w * d_x) + bias.
+ *  FH_W8A32_EXACT: FH_W8A32 bit for bit as ferrum_core computes it over the
+ *            expanded weights: each output is 0 + x[0] w[0] + x[1] w[1] + ...
+ *            in ascending k, every product and add rounded (no FMA), then
+ *            + bias (ops.rs:29-148, 233-256) — the contract the reference's
+ *            roadmap names q8_0_packed_forward_equals_expanded.  K is never
+ *            split, so it runs at a fraction of FH_W8A32's speed; opt-in. */
+enum { FH_W8A32 = 0, FH_W8A8 = 1, FH_W8A32_EXACT = 2 };
 
 /* What fh_sample_* receives in `logits`.
  *  FH_LOGITS_RAW:          the sampler input itself (the Llama/Qwen path,
@@ -143,8 +149,8 @@ void fh_q8_0_free(fh_q8_0* w);
  * (ops.rs:233-256; bias_len == n) and ops::matmul (ops.rs:197-223; bias NULL,
  * bias_len 0) on a Q8_0-backed Linear (layer/linear.rs:191-194).
  * k != W's k, or bias_len not in {0 (with bias NULL), n} -> FH_ERR_DIM, with the
- * reference's message.  m == 0 is a valid empty call.  numerics: FH_W8A32 or
- * FH_W8A8.  Host pointers; blocks until y is written. */
+ * reference's message.  m == 0 is a valid empty call.  numerics: FH_W8A32,
+ * FH_W8A8 or FH_W8A32_EXACT.  Host pointers; blocks until y is written. */
 int fh_q8_0_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, size_t k,
                    const float* bias, size_t bias_len, float* y, int numerics);
 /* Device-pointer form of fh_q8_0_linear, enqueued on the context stream. */
