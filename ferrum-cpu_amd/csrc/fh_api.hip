@@ -308,9 +308,50 @@ int fh_q8_0_upload(fh_ctx* ctx, const uint8_t* gguf, size_t n_rows, size_t k, fh
     return rc;
 }
 
+int fh_weight_upload_f32(fh_ctx* ctx, const float* rows, size_t n_rows, size_t k, fh_q8_0** out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (!out) return fh_fail(ctx, FH_ERR_INVALID, "fh_weight_upload_f32: out is NULL");
+    *out = nullptr;
+    if (!rows) return fh_fail(ctx, FH_ERR_INVALID, "fh_weight_upload_f32: rows is NULL");
+    if (n_rows == 0 || k == 0) return fh_fail(ctx, FH_ERR_INVALID, "fh_weight_upload_f32: empty matrix");
+    if (n_rows > 0x7FFFFFFFu || k > 0x7FFFFFFFu)
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_weight_upload_f32: a dimension is above 2^31 - 1");
+    FH_ON_DEVICE(ctx);
+    fh_q8_0* w = new (std::nothrow) fh_q8_0();
+    if (!w) return fh_fail(ctx, FH_ERR_OOM, "fh_weight_upload_f32: out of host memory");
+    w->device = ctx->device;
+    w->kind = FH_WEIGHT_F32;
+    w->n = n_rows;
+    w->k = k;
+    w->pitch = (k + 15) / 16 * 16;
+    hipError_t e = hipMalloc(&w->base, fh_align256(n_rows * w->pitch * sizeof(float)));
+    if (e != hipSuccess) {
+        delete w;
+        return fh_hip_fail(ctx, e, "hipMalloc(F32 weight)");
+    }
+    w->f32 = static_cast<float*>(w->base);
+    // rows padded to the pitch with zeros, in one strided copy
+    e = hipMemsetAsync(w->f32, 0, n_rows * w->pitch * sizeof(float), ctx->stream);
+    if (e == hipSuccess)
+        e = hipMemcpy2DAsync(w->f32, w->pitch * sizeof(float), rows, k * sizeof(float), k * sizeof(float), n_rows,
+                             hipMemcpyHostToDevice, ctx->stream);
+    if (e == hipSuccess) e = hipStreamSynchronize(ctx->stream);
+    if (e != hipSuccess) {
+        (void)hipFree(w->base);
+        delete w;
+        return fh_hip_fail(ctx, e, "fh_weight_upload_f32 copy");
+    }
+    *out = w;
+    return FH_OK;
+}
+
+int fh_weight_kind(const fh_q8_0* w) { return w ? w->kind : -1; }
+
 int fh_q8_0_download(fh_ctx* ctx, const fh_q8_0* w, uint8_t* gguf) {
     if (!ctx || !w || !gguf) return ctx ? fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_download: NULL argument") : FH_ERR_INVALID;
     ctx->err.clear();
+    if (w->kind != FH_WEIGHT_Q8_0) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_download: the weight is F32, not Q8_0");
     FH_ON_DEVICE(ctx);
     size_t raw = w->n * w->kb * 34;
     void* d_raw = nullptr;
@@ -354,6 +395,8 @@ static int check_linear(fh_ctx* ctx, const fh_q8_0* w, size_t k, const void* bia
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: unknown numerics " + std::to_string(numerics));
     if (w->device != ctx->device)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight lives on another device");
+    if (w->kind == FH_WEIGHT_F32 && numerics == FH_W8A8)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: FH_W8A8 needs a Q8_0 weight (this one is F32)");
     if (k != w->k)
         return fh_fail(ctx, FH_ERR_DIM, "linear_forward: input width " + std::to_string(k) +
                                             " \xe2\x89\xa0 weight rows " + std::to_string(w->k));
@@ -365,8 +408,11 @@ static int check_linear(fh_ctx* ctx, const fh_q8_0* w, size_t k, const void* bia
 
 // The linear in one numerics mode; the W8A32 kernels apply the activation
 // themselves, the other modes by a GELU pass after the linear.
+// F32 weights take the exact kernel whatever the numerics (W8A32 and
+// W8A32_EXACT agree there: the reference's f32 sums, bit for bit).
 static int launch_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
                          int numerics, int act = FH_ACT_NONE) {
+    if (w->kind == FH_WEIGHT_F32) numerics = FH_W8A32_EXACT;
     if (numerics == FH_W8A32) return fh_launch_linear_w8a32(ctx, w, x, m, bias, y, act);
     int rc = numerics == FH_W8A8 ? fh_launch_linear_w8a8(ctx, w, x, m, bias, y)
                                  : fh_launch_linear_exact(ctx, w, x, m, bias, y);
@@ -487,6 +533,7 @@ int fh_q8_0_block_dots_async(fh_ctx* ctx, const fh_q8_0* w, const int8_t* d_qx, 
     if (!ctx) return FH_ERR_INVALID;
     ctx->err.clear();
     if (!w) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_block_dots: weight is NULL");
+    if (w->kind != FH_WEIGHT_Q8_0) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_block_dots: the weight is F32, not Q8_0");
     if (m == 0) return FH_OK;
     if (!d_qx || !d_dots) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_block_dots: NULL buffer");
     FH_ON_DEVICE(ctx);
@@ -703,7 +750,7 @@ int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, con
     if (k > 2048) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_ln: rows wider than 2048");
     if (m > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_ln: m is above 2^31 - 1");
     FH_ON_DEVICE(ctx);
-    if (numerics == FH_W8A32) {
+    if (numerics == FH_W8A32 && w->kind == FH_WEIGHT_Q8_0) {
         const fh_ln_args ln{d_r, d_gamma, d_beta, d_s};
         return fh_launch_linear_ln_w8a32(ctx, w, d_x, m, ln, d_bias, d_y, activation);
     }

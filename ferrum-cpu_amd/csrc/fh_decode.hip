@@ -631,6 +631,8 @@ int fh_gpt2_stack_create(fh_ctx* ctx, const fh_gpt2_block* blocks, size_t layers
                                                     std::to_string(shapes[i][0]) + " x " + std::to_string(shapes[i][1]));
             if (ws[i]->device != ctx->device)
                 return fh_fail(ctx, FH_ERR_INVALID, "fh_gpt2_stack_create: a weight lives on another device");
+            if (ws[i]->kind != FH_WEIGHT_Q8_0)
+                return fh_fail(ctx, FH_ERR_LIMIT, "fh_gpt2_stack_create: F32 weights run one op at a time");
         }
         if (!b.ln1_g || !b.ln1_b || !b.ln2_g || !b.ln2_b || !b.k_cache || !b.v_cache)
             return fh_fail(ctx, FH_ERR_INVALID, "fh_gpt2_stack_create: block " + std::to_string(l) +

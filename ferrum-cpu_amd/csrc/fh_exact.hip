@@ -45,22 +45,30 @@ struct Geo {
     static_assert(kSegs % kProducers == 0 && kProducers % kSegRow == 0, "producer geometry");
 };
 
-// A producer thread's share of one chunk: kPer 16-byte quant segments of rows
+// A producer thread's share of one chunk: kPer 16-value row segments of rows
 // r = s / kSegRow (s = pt + i * kProducers), all at the same positions
 // p = c * P + (pt % kSegRow) * 16, so one 16-float slice of x serves every
-// segment.
-template <int P>
+// segment.  Q8_0 weights: 16 quants and their block's f16 scale per segment;
+// F32 weights: the 16 values.
+template <int P, bool F32>
 struct Share {
-    uint4 q[Geo<P>::kPer];
+    uint4 q[Geo<P>::kPer][F32 ? 4 : 1];
     uint32_t d[Geo<P>::kPer];
     float4 x[4];
 };
 
+struct WeightPtrs {
+    const int8_t* qs;      // Q8_0 quant plane [n][k]
+    const uint16_t* dsc;   // its f16 scales [n][k / 32]
+    const float* f32;      // or F32 rows [n][pitch] (pitch = k rounded up to 16, zero-padded)
+    int pitch;
+};
+
 // Issue the loads of chunk c (rows past n clamped: computed, never stored;
 // positions past k skipped).
-template <int P>
-__device__ __forceinline__ void load(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
-                                     const float* __restrict__ xr, int j0, int n, int k, int c, int pt, Share<P>& sh) {
+template <int P, bool F32>
+__device__ __forceinline__ void load(const WeightPtrs& wp, const float* __restrict__ xr, int j0, int n, int k, int c,
+                                     int pt, Share<P, F32>& sh) {
     using G = Geo<P>;
     const int p = c * P + (pt % G::kSegRow) * 16;
     if (p >= k) return;
@@ -69,45 +77,61 @@ __device__ __forceinline__ void load(const int8_t* __restrict__ qs, const uint16
     for (int i = 0; i < G::kPer; i++) {
         const int r = (pt + i * kProducers) / G::kSegRow;
         const size_t row = static_cast<size_t>(min(j0 + r, n - 1));
-        sh.q[i] = *reinterpret_cast<const uint4*>(qs + row * static_cast<size_t>(k) + p);
-        sh.d[i] = dsc[row * kb + static_cast<size_t>(p >> 5)];
+        if constexpr (F32) {
+            const uint4* src = reinterpret_cast<const uint4*>(wp.f32 + row * static_cast<size_t>(wp.pitch) + p);
+#pragma unroll
+            for (int v = 0; v < 4; v++) sh.q[i][v] = src[v];
+        } else {
+            sh.q[i][0] = *reinterpret_cast<const uint4*>(wp.qs + row * static_cast<size_t>(k) + p);
+            sh.d[i] = wp.dsc[row * kb + static_cast<size_t>(p >> 5)];
+        }
     }
 #pragma unroll
-    for (int v = 0; v < 4; v++) sh.x[v] = make_float4(xr[p + 4 * v], xr[p + 4 * v + 1], xr[p + 4 * v + 2], xr[p + 4 * v + 3]);
+    for (int v = 0; v < 4; v++) {
+        // (positions past k: clamped loads whose products are never summed)
+        const int e = p + 4 * v;
+        sh.x[v] = make_float4(xr[min(e, k - 1)], xr[min(e + 1, k - 1)], xr[min(e + 2, k - 1)], xr[min(e + 3, k - 1)]);
+    }
 }
 
 // The products of chunk c into buf[r * kStride + p - c * P].
-template <int P>
-__device__ __forceinline__ void produce(int k, int c, int pt, const Share<P>& sh, float* buf) {
+template <int P, bool F32>
+__device__ __forceinline__ void produce(int k, int c, int pt, const Share<P, F32>& sh, float* buf) {
     using G = Geo<P>;
     const int q = pt % G::kSegRow;
     if (c * P + q * 16 >= k) return;
 #pragma unroll
     for (int i = 0; i < G::kPer; i++) {
         const int r = (pt + i * kProducers) / G::kSegRow;
-        const float d = fh_h2f(static_cast<uint16_t>(sh.d[i]));
-        const uint32_t words[4] = {sh.q[i].x, sh.q[i].y, sh.q[i].z, sh.q[i].w};
         float* o = buf + r * G::kStride + q * 16;
 #pragma unroll
         for (int v = 0; v < 4; v++) {
             const float xs[4] = {sh.x[v].x, sh.x[v].y, sh.x[v].z, sh.x[v].w};
             float4 pr;
             float* e = &pr.x;
+            if constexpr (F32) {
+                const uint32_t ws[4] = {sh.q[i][v].x, sh.q[i][v].y, sh.q[i][v].z, sh.q[i][v].w};
 #pragma unroll
-            for (int b = 0; b < 4; b++) {
-                const float level = static_cast<float>(static_cast<int8_t>((words[v] >> (8 * b)) & 0xFFu));
-                const float wv = d * level;  // exact: an f16 value times an 8-bit integer
-                e[b] = xs[b] * wv;
+                for (int b = 0; b < 4; b++) e[b] = xs[b] * __builtin_bit_cast(float, ws[b]);
+            } else {
+                const float d = fh_h2f(static_cast<uint16_t>(sh.d[i]));
+                const uint32_t word = v == 0 ? sh.q[i][0].x : v == 1 ? sh.q[i][0].y : v == 2 ? sh.q[i][0].z : sh.q[i][0].w;
+#pragma unroll
+                for (int b = 0; b < 4; b++) {
+                    const float level = static_cast<float>(static_cast<int8_t>((word >> (8 * b)) & 0xFFu));
+                    const float wv = d * level;  // exact: an f16 value times an 8-bit integer
+                    e[b] = xs[b] * wv;
+                }
             }
             *reinterpret_cast<float4*>(o + v * 4) = pr;
         }
     }
 }
 
-template <int P>
+template <int P, bool F32>
 __global__ void __launch_bounds__(kThreads)
-    k_q8_0_exact(const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const float* __restrict__ x,
-                 const float* __restrict__ bias, float* __restrict__ y, int m, int n, int k) {
+    k_linear_exact(WeightPtrs wp, const float* __restrict__ x, const float* __restrict__ bias, float* __restrict__ y,
+                   int m, int n, int k) {
     constexpr int kStride = Geo<P>::kStride;
     __shared__ __align__(16) float prod[2][kRows * kStride];
     const int tid = threadIdx.x;
@@ -125,8 +149,9 @@ __global__ void __launch_bounds__(kThreads)
             __syncthreads();  // chunk 0 is in LDS
             for (int c = 0; c < chunks; c++) {
                 own = prod[c & 1] + tid * kStride;
-                const int pn = min(P, k - c * P);  // a multiple of 32
-                for (int g = 0; g < pn; g += 32) {
+                const int pn = min(P, k - c * P);  // a multiple of 32 for Q8_0 weights
+                int g = 0;
+                for (; g + 32 <= pn; g += 32) {
                     // all eight reads in flight before the chain of 32 adds
                     float4 v[8];
 #pragma unroll
@@ -139,6 +164,7 @@ __global__ void __launch_bounds__(kThreads)
                         acc = acc + v[u].w;
                     }
                 }
+                for (; g < pn; g++) acc = acc + own[g];  // (F32 rows whose k is not a multiple of 32)
                 __syncthreads();  // chunk c + 1 is in LDS; buffer c & 1 is free again
             }
             if (j < n) y[static_cast<size_t>(i) * n + j] = bias ? acc + bias[j] : acc;
@@ -146,17 +172,17 @@ __global__ void __launch_bounds__(kThreads)
             // Loads run two chunks ahead of the products: `a` holds the even
             // chunks, `b` the odd ones.
             const int pt = tid - 64;
-            Share<P> a, b;
-            load(qs, dsc, xr, j0, n, k, 0, pt, a);
-            if (chunks > 1) load(qs, dsc, xr, j0, n, k, 1, pt, b);
+            Share<P, F32> a, b;
+            load(wp, xr, j0, n, k, 0, pt, a);
+            if (chunks > 1) load(wp, xr, j0, n, k, 1, pt, b);
             produce(k, 0, pt, a, prod[0]);
             __syncthreads();
             for (int c = 0; c < chunks; c += 2) {
-                if (c + 2 < chunks) load(qs, dsc, xr, j0, n, k, c + 2, pt, a);
+                if (c + 2 < chunks) load(wp, xr, j0, n, k, c + 2, pt, a);
                 if (c + 1 < chunks) produce(k, c + 1, pt, b, prod[1]);
                 __syncthreads();
                 if (c + 1 < chunks) {
-                    if (c + 3 < chunks) load(qs, dsc, xr, j0, n, k, c + 3, pt, b);
+                    if (c + 3 < chunks) load(wp, xr, j0, n, k, c + 3, pt, b);
                     if (c + 2 < chunks) produce(k, c + 2, pt, a, prod[0]);
                     __syncthreads();
                 }
@@ -175,12 +201,17 @@ int fh_launch_linear_exact(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t
     if (w->n == 0 || m == 0) return FH_OK;
     const unsigned gx = static_cast<unsigned>((w->n + kRows - 1) / kRows);
     const unsigned gy = static_cast<unsigned>(m < 65535 ? m : 65535);
-    if (w->n >= 16384)
-        hipLaunchKernelGGL(k_q8_0_exact<96>, dim3(gx, gy), dim3(kThreads), 0, ctx->stream, w->qs, w->d, x, bias, y,
-                           static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k));
+    const WeightPtrs wp{w->qs, w->d, w->f32, static_cast<int>(w->pitch)};
+    const int mi = static_cast<int>(m), ni = static_cast<int>(w->n), ki = static_cast<int>(w->k);
+    if (w->kind == FH_WEIGHT_F32)
+        hipLaunchKernelGGL((k_linear_exact<96, true>), dim3(gx, gy), dim3(kThreads), 0, ctx->stream, wp, x, bias, y, mi,
+                           ni, ki);
+    else if (w->n >= 16384)
+        hipLaunchKernelGGL((k_linear_exact<96, false>), dim3(gx, gy), dim3(kThreads), 0, ctx->stream, wp, x, bias, y, mi,
+                           ni, ki);
     else
-        hipLaunchKernelGGL(k_q8_0_exact<192>, dim3(gx, gy), dim3(kThreads), 0, ctx->stream, w->qs, w->d, x, bias, y,
-                           static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k));
+        hipLaunchKernelGGL((k_linear_exact<192, false>), dim3(gx, gy), dim3(kThreads), 0, ctx->stream, wp, x, bias, y,
+                           mi, ni, ki);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }

@@ -69,9 +69,18 @@ int fh_take_status(fh_ctx* ctx);
 
 constexpr int8_t kFhBadRowExp = -128;
 
+// Weight storage kinds behind an fh_q8_0 handle.
+enum { FH_WEIGHT_Q8_0 = 0, FH_WEIGHT_F32 = 1 };
+
 struct fh_q8_0 {
     int device = 0;
+    int kind = FH_WEIGHT_Q8_0;
     size_t n = 0, k = 0, kb = 0;
+    // FH_WEIGHT_F32: rows [n][pitch] f32, pitch = k rounded up to 16 floats,
+    // the padding zero (a tensor the reference stores as F32: ne0 % 32 != 0,
+    // or an unquantized file).  qs / d / rexp unused.
+    float* f32 = nullptr;
+    size_t pitch = 0;
     int8_t* qs = nullptr;
     uint16_t* d = nullptr;
     // Per row j, e_j with 127 * max_b |d_jb| * 2^e_j in [2^14, 2^15) (0 for a

@@ -68,8 +68,8 @@ extern "C" int fh_q8_0_linear_noalloc_async(fh_ctx* ctx, const fh_q8_0* w, const
     if ((d_bias == nullptr) != (bias_len == 0) || (bias_len != 0 && bias_len != w->n))
         return fh_fail(ctx, FH_ERR_DIM, "linear_forward: bias length " + std::to_string(bias_len) +
                                             " \xe2\x89\xa0 out_features " + std::to_string(w->n));
-    if (numerics != FH_W8A32)
-        return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_noalloc: only FH_W8A32 runs without allocation");
+    if (numerics != FH_W8A32 || w->kind != FH_WEIGHT_Q8_0)
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_noalloc: only FH_W8A32 on a Q8_0 weight runs without allocation");
     if (m > 64)
         return fh_fail(ctx, FH_ERR_LIMIT,
                        "fh_q8_0_linear_noalloc: m = " + std::to_string(m) + " is above 64 (the decode shapes)");

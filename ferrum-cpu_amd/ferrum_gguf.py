@@ -118,15 +118,36 @@ def synthetic_bpe(vocab: int):
     return tokens, merges, types
 
 
+def q8_0_rows_to_f32(raw, n_rows: int, k: int) -> np.ndarray:
+    """GGUF Q8_0 bytes [n_rows of k] expanded to f32 [n_rows, k] (exact: an f16
+    scale times an 8-bit integer)."""
+    blk = np.asarray(raw, np.uint8).reshape(-1, 34)
+    sc = blk[:, :2].copy().view(np.float16).astype(np.float32)
+    return (sc * blk[:, 2:].copy().view(np.int8).astype(np.float32)).reshape(n_rows, k)
+
+
 def gpt2_gguf(weights: dict, vocab: int, d: int, heads: int, layers: int, ffn: int, ctx: int,
-              eps: float = 1e-5, name: str = "synthetic") -> GGUFBuilder:
+              eps: float = 1e-5, name: str = "synthetic", file_order=None, output=None) -> GGUFBuilder:
     """GgufOut::gpt2's layout (loader/gpt2.rs:61-146, loader/encode.rs:60-93)
     from Q8_0 bytes and f32 arrays keyed as tests/gpt2_tiny.make_weights makes
     them: token_embd_q8 [vocab rows of d], position_embd [ctx, d], per block
     ln1/ln2 gamma and beta, qkv_q8 [3d rows] + qkv_b, out_q8 [d rows] + out_b,
     up_q8 [ffn rows] + up_b, down_q8 [d rows of ffn] + down_b; lnf_g / lnf_b.
-    The head is tied (no output.weight)."""
+    A matrix may instead be given as f32 rows under the same name with _f32
+    for _q8 (token_embd_f32, blk{i}.qkv_f32, ...): it is written as F32, as the
+    reference's writer stores a matrix whose ne0 is not a multiple of 32
+    (loader/mod.rs:147-152).  The head is tied (no output.weight) unless
+    `output` (Q8_0 bytes of [vocab rows of d]) is given.
+
+    file_order (a permutation of the vocabulary, ferrum ids in file order)
+    writes the tokens, their types and the token-table (and output) rows in
+    that order instead of ferrum's -- a foreign GPT-2 vocab, as a llama.cpp
+    conversion orders it."""
     tokens, merges, types = synthetic_bpe(vocab)
+    order = list(range(vocab)) if file_order is None else [int(i) for i in file_order]
+    if sorted(order) != list(range(vocab)):
+        raise ValueError("file_order must be a permutation of the vocabulary")
+    tokens, types = [tokens[i] for i in order], [types[i] for i in order]
     b = GGUFBuilder()
     b.str("general.architecture", "gpt2").str("general.name", name)
     for k, v in (("context_length", ctx), ("embedding_length", d), ("block_count", layers),
@@ -143,23 +164,85 @@ def gpt2_gguf(weights: dict, vocab: int, d: int, heads: int, layers: int, ffn: i
     b.u32("general.file_type", 7).u32("general.quantization_version", 2)
     f32 = lambda a: np.ascontiguousarray(a, np.float32).tobytes()  # noqa: E731
     q8 = lambda a: np.asarray(a, np.uint8).tobytes()  # noqa: E731
-    b.tensor("token_embd.weight", [d, vocab], GGML_Q8_0, q8(weights["token_embd_q8"]))
+
+    def matrix(tname, key, rows, ne0, perm=None):
+        """A [rows x ne0] matrix, Q8_0 from key_q8 or F32 from key_f32, rows
+        optionally reordered."""
+        if key + "_f32" in weights:
+            a = np.asarray(weights[key + "_f32"], np.float32).reshape(rows, ne0)
+            b.tensor(tname, [ne0, rows], GGML_F32, f32(a if perm is None else a[perm]))
+        else:
+            a = np.asarray(weights[key + "_q8"], np.uint8).reshape(rows, -1)
+            b.tensor(tname, [ne0, rows], GGML_Q8_0, q8(a if perm is None else a[perm]))
+
+    matrix("token_embd.weight", "token_embd", vocab, d, order)
+    if output is not None:
+        b.tensor("output.weight", [d, vocab], GGML_Q8_0, q8(np.asarray(output, np.uint8).reshape(vocab, -1)[order]))
     b.tensor("position_embd.weight", [d, ctx], GGML_F32, f32(weights["position_embd"]))
     for i in range(layers):
         w = lambda k: weights[f"blk{i}.{k}"]  # noqa: E731
         n = lambda s: f"blk.{i}.{s}"  # noqa: E731
         b.tensor(n("attn_norm.weight"), [d], GGML_F32, f32(w("ln1_g")))
         b.tensor(n("attn_norm.bias"), [d], GGML_F32, f32(w("ln1_b")))
-        b.tensor(n("attn_qkv.weight"), [d, 3 * d], GGML_Q8_0, q8(w("qkv_q8")))
+        matrix(n("attn_qkv.weight"), f"blk{i}.qkv", 3 * d, d)
         b.tensor(n("attn_qkv.bias"), [3 * d], GGML_F32, f32(w("qkv_b")))
-        b.tensor(n("attn_output.weight"), [d, d], GGML_Q8_0, q8(w("out_q8")))
+        matrix(n("attn_output.weight"), f"blk{i}.out", d, d)
         b.tensor(n("attn_output.bias"), [d], GGML_F32, f32(w("out_b")))
         b.tensor(n("ffn_norm.weight"), [d], GGML_F32, f32(w("ln2_g")))
         b.tensor(n("ffn_norm.bias"), [d], GGML_F32, f32(w("ln2_b")))
-        b.tensor(n("ffn_up.weight"), [d, ffn], GGML_Q8_0, q8(w("up_q8")))
+        matrix(n("ffn_up.weight"), f"blk{i}.up", ffn, d)
         b.tensor(n("ffn_up.bias"), [ffn], GGML_F32, f32(w("up_b")))
-        b.tensor(n("ffn_down.weight"), [ffn, d], GGML_Q8_0, q8(w("down_q8")))
+        matrix(n("ffn_down.weight"), f"blk{i}.down", d, ffn)
         b.tensor(n("ffn_down.bias"), [d], GGML_F32, f32(w("down_b")))
     b.tensor("output_norm.weight", [d], GGML_F32, f32(weights["lnf_g"]))
     b.tensor("output_norm.bias", [d], GGML_F32, f32(weights["lnf_b"]))
+    return b
+
+
+def llama_gguf(weights: dict, cfg: dict, arch: str = "qwen2", f32_names=(), extra=None) -> GGUFBuilder:
+    """A llama.cpp-layout llama / qwen2 GGUF (the keys and tensor names
+    Gguf::load_llama_prec reads, gguf/llama.rs:171-340) from a weights dict
+    keyed as LlamaDevice.from_weights takes it (token_embd, optional output,
+    output_norm, blk.i.attn_norm / attn_q / attn_k / attn_v (+ .bias) /
+    attn_output / ffn_norm / ffn_gate / ffn_up / ffn_down; matrices as Q8_0
+    bytes) and its cfg.  Matrices named in f32_names (dict keys) are written
+    as F32 (their Q8_0 rows expanded exactly).  extra(builder) adds further
+    metadata or tensors (rope scaling keys, rope_freqs.weight)."""
+    d, nh, nkv, hd, L, ffn = cfg["d"], cfg["n_heads"], cfg["n_kv"], cfg["head_dim"], cfg["layers"], cfg["ffn"]
+    qd, kvd, V = nh * hd, nkv * hd, cfg["vocab"]
+    b = GGUFBuilder()
+    b.str("general.architecture", arch).str("general.name", "synthetic")
+    for k, v in (("embedding_length", d), ("block_count", L), ("attention.head_count", nh),
+                 ("attention.head_count_kv", nkv), ("feed_forward_length", ffn), ("context_length", cfg["context"]),
+                 ("attention.key_length", hd), ("rope.dimension_count", cfg.get("rope_dim", hd))):
+        b.u32(f"{arch}.{k}", v)
+    b.f32(f"{arch}.rope.freq_base", cfg["rope_base"])
+    b.f32(f"{arch}.attention.layer_norm_rms_epsilon", cfg["eps"])
+    f32 = lambda a: np.ascontiguousarray(a, np.float32).tobytes()  # noqa: E731
+
+    def mat(tname, key, rows, ne0):
+        raw = np.asarray(weights[key], np.uint8)
+        if key in f32_names:
+            b.tensor(tname, [ne0, rows], GGML_F32, f32(q8_0_rows_to_f32(raw, rows, ne0)))
+        else:
+            b.tensor(tname, [ne0, rows], GGML_Q8_0, raw.tobytes())
+
+    mat("token_embd.weight", "token_embd", V, d)
+    if "output" in weights:
+        mat("output.weight", "output", V, d)
+    b.tensor("output_norm.weight", [d], GGML_F32, f32(weights["output_norm"]))
+    for i in range(L):
+        p = f"blk.{i}."
+        b.tensor(p + "attn_norm.weight", [d], GGML_F32, f32(weights[p + "attn_norm"]))
+        for s, n in (("q", qd), ("k", kvd), ("v", kvd)):
+            mat(p + f"attn_{s}.weight", p + f"attn_{s}", n, d)
+            if p + f"attn_{s}.bias" in weights:
+                b.tensor(p + f"attn_{s}.bias", [n], GGML_F32, f32(weights[p + f"attn_{s}.bias"]))
+        mat(p + "attn_output.weight", p + "attn_output", d, qd)
+        b.tensor(p + "ffn_norm.weight", [d], GGML_F32, f32(weights[p + "ffn_norm"]))
+        mat(p + "ffn_gate.weight", p + "ffn_gate", ffn, d)
+        mat(p + "ffn_up.weight", p + "ffn_up", ffn, d)
+        mat(p + "ffn_down.weight", p + "ffn_down", d, ffn)
+    if extra is not None:
+        extra(b)
     return b

@@ -40,7 +40,8 @@ LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
 EXPORTS = (
     "fh_ctx_create", "fh_ctx_destroy", "fh_ctx_set_stream", "fh_ctx_reset_stream", "fh_sync", "fh_last_error",
     "fh_device_count", "fh_q8_0_upload", "fh_q8_0_upload_device", "fh_q8_0_download",
-    "fh_q8_0_dims", "fh_q8_0_free", "fh_q8_0_linear", "fh_q8_0_linear_async", "fh_q8_0_linear_noalloc_async",
+    "fh_q8_0_dims", "fh_q8_0_free", "fh_weight_upload_f32", "fh_weight_kind", "fh_q8_0_linear", "fh_q8_0_linear_async",
+    "fh_q8_0_linear_noalloc_async",
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async", "fh_debug_sampler_faults",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
@@ -161,6 +162,8 @@ def lib():
         L.fh_q8_0_upload_device.argtypes = [vp, vp, sz, sz, C.POINTER(vp)]
         L.fh_q8_0_download.argtypes = [vp, vp, vp]
         L.fh_q8_0_dims.argtypes = [vp, C.POINTER(sz), C.POINTER(sz)]
+        L.fh_weight_upload_f32.argtypes = [vp, vp, sz, sz, C.POINTER(vp)]
+        L.fh_weight_kind.argtypes = [vp]
         L.fh_q8_0_free.argtypes = [vp]
         L.fh_q8_0_free.restype = None
         L.fh_q8_0_linear.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32]
@@ -299,6 +302,23 @@ class Q8_0Weight:
         h = C.c_void_p()
         ctx.check(lib().fh_q8_0_upload(ctx.h, raw.ctypes.data, n_rows, k, C.byref(h)))
         return cls(ctx, h, n_rows, k)
+
+    @classmethod
+    def upload_f32(cls, ctx: Context, rows) -> "Q8_0Weight":
+        """An F32 weight [n_rows, k] (host rows, GGUF order: k = ne0) behind the
+        same handle: a tensor the reference stores as F32 (ne0 % 32 != 0, or an
+        unquantized file).  Linears on it run the reference's f32 sums bit for
+        bit (the exact kernel)."""
+        a = np.ascontiguousarray(rows, dtype=np.float32)
+        if a.ndim != 2:
+            raise FerrumHipError(FH_ERR_INVALID, f"expected a matrix, got shape {a.shape}")
+        h = C.c_void_p()
+        ctx.check(lib().fh_weight_upload_f32(ctx.h, a.ctypes.data, a.shape[0], a.shape[1], C.byref(h)))
+        return cls(ctx, h, a.shape[0], a.shape[1])
+
+    @property
+    def is_f32(self) -> bool:
+        return lib().fh_weight_kind(self.h) == 1
 
     @classmethod
     def upload_device(cls, ctx: Context, d_bytes, n_rows: int, k: int) -> "Q8_0Weight":
@@ -620,6 +640,13 @@ class GGUFFile:
     def __exit__(self, *a):
         self.close()
 
+    def meta_kind(self, key: str):
+        """(GGUF value type, array element type, array length) of a key, None if absent."""
+        ty, el, cnt = C.c_uint32(), C.c_uint32(), C.c_uint64()
+        if lib().fh_gguf_meta_type(self.h, key.encode(), C.byref(ty), C.byref(el), C.byref(cnt)) != FH_OK:
+            return None
+        return ty.value, el.value, cnt.value
+
     def meta(self, key: str):
         """The value of a metadata key (int, float, str, or list), None if absent."""
         k = key.encode()
@@ -685,6 +712,281 @@ class GGUFFile:
         return Q8_0Weight(ctx, h, n, k)
 
 
+# ---- GGUF import: the reference's loader checks, before anything is uploaded ----
+
+GGML_F32, GGML_F16, GGML_Q8_0 = 0, 1, 8
+_VT_INTS = {0: False, 1: True, 2: False, 3: True, 4: False, 5: True, 10: False, 11: True}  # type -> signed
+_VT_F32, _VT_BOOL, _VT_STRING, _VT_ARRAY, _VT_F64 = 6, 7, 8, 9, 12
+LN_EPS = 1e-5  # GPT-2's LayerNorm epsilon, which ferrum_core's LayerNorm uses (loader/mod.rs:135-136)
+
+
+def _fmt(msg: str) -> "GGUFFormatError":
+    return GGUFFormatError(FH_ERR_FORMAT, msg)
+
+
+def _rust_str(s: str) -> str:
+    """A string as Rust's {:?} prints it (quoted, with its escapes)."""
+    esc = {'"': '\\"', "\\": "\\\\", "\n": "\\n", "\r": "\\r", "\t": "\\t", "\0": "\\0"}
+    return '"' + "".join(esc.get(ch, ch) for ch in s) + '"'
+
+
+def _rust_f32(v: float) -> str:
+    """An f32 as Rust's {} prints it (shortest round trip, no exponent)."""
+    return np.format_float_positional(np.float32(v), trim="-")
+
+
+def _dims(dims) -> str:
+    return "[" + ", ".join(str(int(x)) for x in dims) + "]"
+
+
+class GgufMeta:
+    """Typed metadata reads as ferrum_core's MetaValue converts them
+    (gguf/mod.rs:96-116): as_usize takes any integer type holding a
+    non-negative value, as_f32 takes F32/F64 or such an integer; booleans
+    and strings are neither."""
+
+    def __init__(self, g: "GGUFFile"):
+        self.g = g
+
+    def usize(self, key: str):
+        k = self.g.meta_kind(key)
+        if k is None or k[0] not in _VT_INTS:
+            return None
+        v = int(self.g.meta(key))
+        return v if v >= 0 else None
+
+    def f32(self, key: str):
+        k = self.g.meta_kind(key)
+        if k is None:
+            return None
+        if k[0] in (_VT_F32, _VT_F64):
+            return float(np.float32(self.g.meta(key)))
+        u = self.usize(key)
+        return None if u is None else float(np.float32(u))
+
+    def string(self, key: str):
+        k = self.g.meta_kind(key)
+        return self.g.meta(key) if k is not None and k[0] == _VT_STRING else None
+
+    def array(self, key: str, elem: int):
+        k = self.g.meta_kind(key)
+        if k is None or k[0] != _VT_ARRAY or k[1] != elem:
+            return None
+        return self.g.meta(key)
+
+
+def ferrum_vocab(tokens, merges, types):
+    """loader/gpt2.rs:149-191: map a GGUF BPE vocabulary onto ferrum_core's id
+    layout -- the 256 byte tokens in byte order, one token per merge in rank
+    order, then every other token in file order -- so a foreign GPT-2 file
+    (which orders its byte tokens differently) loads too.  Returns perm with
+    perm[ferrum_id] = file_id."""
+    from ferrum_gguf import byte_to_unicode
+
+    if len(types) != len(tokens):
+        raise _fmt(f"gguf vocab: {len(tokens)} tokens but {len(types)} token types")
+    ids = {}
+    for i, t in enumerate(tokens):  # (a repeated token keeps its last id, as a HashMap collect does)
+        ids[t] = i
+    b2u = byte_to_unicode()
+    used = [False] * len(tokens)
+    perm = []
+    for w in [b2u[b] for b in range(256)] + [m.replace(" ", "", 1) for m in merges]:
+        i = ids.get(w)
+        if i is None or used[i]:
+            raise _fmt(f"gguf vocab: no unique token {_rust_str(w)}")
+        used[i] = True
+        perm.append(i)
+    perm.extend(i for i in range(len(tokens)) if not used[i])
+    return perm
+
+
+def _check_dims(g: "GGUFFile", name: str, want):
+    """GgufIn::tensor's checks (loader/decode.rs:44-56)."""
+    if name not in g.tensors:
+        raise _fmt(f"missing tensor '{name}'")
+    dims = g.tensors[name][0]
+    if tuple(int(x) for x in dims) != tuple(int(x) for x in want):
+        raise _fmt(f"tensor '{name}' has dims {_dims(dims)}, expected {_dims(want)}")
+
+
+def gpt2_gguf_plan(g: "GGUFFile"):
+    """gpt2_from's reading of a GPT-2 GGUF (loader/gpt2.rs:201-232 and the
+    tensor shapes it asks for, 233-275), before any upload: the
+    hyperparameters, the layer_norm_epsilon check, the vocabulary permutation
+    and every tensor's dims.  Returns (cfg dict, perm, tied)."""
+    meta = GgufMeta(g)
+    arch = meta.string("general.architecture")
+    if arch != "gpt2":
+        shown = "None" if arch is None else f"Some({_rust_str(arch)})"
+        raise _fmt(f"not a GPT-2 model: architecture {shown} (need gpt2)")
+
+    def usize(key):
+        v = meta.usize(key)
+        if v is None:
+            raise _fmt(f"GGUF key '{key}' missing or not an integer")
+        return v
+
+    ctx_len, d, n_layer = usize("gpt2.context_length"), usize("gpt2.embedding_length"), usize("gpt2.block_count")
+    ff, heads = usize("gpt2.feed_forward_length"), usize("gpt2.attention.head_count")
+    eps = meta.f32("gpt2.attention.layer_norm_epsilon")
+    if eps is None:
+        raise _fmt("GGUF key 'gpt2.attention.layer_norm_epsilon' missing or not a number")
+    if np.abs(np.float32(eps) - np.float32(LN_EPS)) > np.float32(1e-9):
+        raise _fmt(f"gpt2.attention.layer_norm_epsilon is {_rust_f32(eps)}; Ferrum's LayerNorm uses "
+                   f"{_rust_f32(LN_EPS)}")
+    arrays = {}
+    for key, elem in (("tokenizer.ggml.tokens", _VT_STRING), ("tokenizer.ggml.merges", _VT_STRING),
+                      ("tokenizer.ggml.token_type", 5)):
+        arrays[key] = meta.array(key, elem)
+        if arrays[key] is None:
+            raise _fmt(f"GGUF key '{key}' missing or of the wrong type")
+    perm = ferrum_vocab(arrays["tokenizer.ggml.tokens"], arrays["tokenizer.ggml.merges"],
+                        [int(t) for t in arrays["tokenizer.ggml.token_type"]])
+    v = len(perm)
+    _check_dims(g, "token_embd.weight", (d, v))
+    tied = "output.weight" not in g.tensors
+    if not tied:
+        _check_dims(g, "output.weight", (d, v))
+    _check_dims(g, "position_embd.weight", (d, ctx_len))
+    for i in range(n_layer):
+        for stem, dims in (("attn_norm.weight", (d,)), ("attn_norm.bias", (d,)), ("attn_qkv.weight", (d, 3 * d)),
+                           ("attn_qkv.bias", (3 * d,)), ("attn_output.weight", (d, d)), ("attn_output.bias", (d,)),
+                           ("ffn_norm.weight", (d,)), ("ffn_norm.bias", (d,)), ("ffn_up.weight", (d, ff)),
+                           ("ffn_up.bias", (ff,)), ("ffn_down.weight", (ff, d)), ("ffn_down.bias", (d,))):
+            _check_dims(g, f"blk.{i}.{stem}", dims)
+    _check_dims(g, "output_norm.weight", (d,))
+    _check_dims(g, "output_norm.bias", (d,))
+    return dict(vocab=v, d=d, heads=heads, layers=n_layer, ffn=ff, context=ctx_len), perm, tied
+
+
+def llama_gguf_plan(g: "GGUFFile"):
+    """Gguf::load_llama_prec's reading of a llama / qwen2 GGUF
+    (gguf/llama.rs:171-340, rope scaling 51-103), before any upload: the
+    architecture and its rope type, the hyperparameters with the reference's
+    defaults, the rope scaling rules, the bias rules and every tensor's dims.
+    Returns (cfg dict for LlamaDevice, {name: (n_out, n_in)} of the matrices,
+    tied)."""
+    meta = GgufMeta(g)
+    arch = meta.string("general.architecture")
+    if arch is None:
+        raise _fmt("GGUF missing general.architecture")
+    if arch not in ("llama", "qwen2"):
+        raise _fmt(f"architecture '{arch}' is not supported by load_llama (llama / qwen2 only)")
+    rope_type = ROPE_NEOX if arch == "qwen2" else ROPE_NORM
+
+    def req(key):
+        v = meta.usize(key)
+        if v is None:
+            raise _fmt(f"GGUF missing/invalid metadata '{key}'")
+        return v
+
+    def opt(key, default):
+        v = meta.usize(key)
+        return default if v is None else v
+
+    def f32_or(key, default):
+        v = meta.f32(key)
+        return float(np.float32(default)) if v is None else v
+
+    dim = req(f"{arch}.embedding_length")
+    n_layers = req(f"{arch}.block_count")
+    if n_layers > len(g.tensors):
+        raise _fmt(f"GGUF block_count = {n_layers} exceeds what the file can hold ({len(g.tensors)})")
+    n_heads = req(f"{arch}.attention.head_count")
+    n_kv = opt(f"{arch}.attention.head_count_kv", n_heads)
+    ffn = req(f"{arch}.feed_forward_length")
+    head_dim = opt(f"{arch}.attention.key_length", dim // max(n_heads, 1))
+    rope_dim = opt(f"{arch}.rope.dimension_count", head_dim)
+    rope_base = f32_or(f"{arch}.rope.freq_base", 10000.0)
+    # rope scaling (gguf/llama.rs:51-103)
+    key = lambda k: f"{arch}.rope.{k}"  # noqa: E731
+    if g.meta_kind(key("scaling.factor")) is not None:
+        factor = meta.f32(key("scaling.factor"))
+    else:
+        factor = meta.f32(key("scale_linear"))
+    if g.meta_kind(key("scaling.type")) is not None:
+        ty = meta.string(key("scaling.type"))
+        if ty is None:
+            raise _fmt(f"'{key('scaling.type')}' is not a string")
+    else:
+        ty = "linear"
+    factor = factor if factor is not None and factor != 0.0 else 1.0
+    if ty == "linear":
+        linear_factor = factor
+    elif ty == "none":
+        if factor != 1.0:
+            raise _fmt(f"'{key('scaling.type')}' is \"none\" but the scaling factor is {_rust_f32(factor)}")
+        linear_factor = 1.0
+    else:
+        raise _fmt(f"RoPE scaling type '{ty}' is not supported: Ferrum implements none, linear and "
+                   "rope_freqs.weight (yarn and longrope are refused)")
+    attn = f32_or(key("scaling.attn_factor"), 1.0)
+    if attn != 1.0:
+        raise _fmt(f"RoPE scaling attn_factor {_rust_f32(attn)} is not supported (only 1.0)")
+    has_freqs = "rope_freqs.weight" in g.tensors
+    if has_freqs and tuple(int(x) for x in g.tensors["rope_freqs.weight"][0]) != (rope_dim // 2,):
+        raise _fmt(f"rope_freqs.weight has dims {_dims(g.tensors['rope_freqs.weight'][0])}, expected "
+                   f"[{rope_dim // 2}] (rope_dim / 2)")
+    eps = f32_or(f"{arch}.attention.layer_norm_rms_epsilon", 1e-5)
+    ctx_len = opt(f"{arch}.context_length", 2048)
+    if "token_embd.weight" not in g.tensors:
+        raise _fmt("GGUF missing token_embd.weight")
+    edims = tuple(int(x) for x in g.tensors["token_embd.weight"][0])
+    vocab = edims[1] if len(edims) == 2 else req(f"{arch}.vocab_size")
+    n_el = int(np.prod(edims)) if edims else 1
+    emb_ok = edims == (dim, vocab) if len(edims) == 2 else vocab * dim == n_el
+    if not emb_ok or vocab == 0 or dim == 0:
+        raise _fmt("token_embd.weight size does not match vocab × dim")
+    q_dim, kv_dim = n_heads * head_dim, n_kv * head_dim
+    mats = {}
+
+    def norm(name):
+        if name not in g.tensors:
+            raise _fmt(f"GGUF tensor '{name}' not found")
+        n = int(np.prod(g.tensors[name][0])) if g.tensors[name][0] else 1
+        if n != dim:
+            raise _fmt(f"tensor '{name}' length is not {dim}")
+
+    def linear(name, n_in, n_out, bias=None):
+        if name not in g.tensors:
+            raise _fmt(f"GGUF tensor '{name}' not found")
+        dims = tuple(int(x) for x in g.tensors[name][0])
+        if dims != (n_in, n_out):
+            raise _fmt(f"tensor '{name}' has dims {_dims(dims)}, expected [{n_in}, {n_out}] from the metadata")
+        if bias is not None and bias in g.tensors:
+            nb = int(np.prod(g.tensors[bias][0])) if g.tensors[bias][0] else 1
+            if nb != n_out:
+                raise _fmt(f"bias for '{name}' has wrong length")
+        mats[name] = (n_out, n_in)
+
+    for i in range(n_layers):
+        p = f"blk.{i}"
+        for stem in ("attn_output", "ffn_gate", "ffn_up", "ffn_down"):
+            if f"{p}.{stem}.bias" in g.tensors:
+                raise _fmt(f"GGUF tensor '{p}.{stem}.bias' is not supported: Ferrum loads biases only for "
+                           "attn_q/attn_k/attn_v")
+        norm(f"{p}.attn_norm.weight")
+        linear(f"{p}.attn_q.weight", dim, q_dim, f"{p}.attn_q.bias")
+        linear(f"{p}.attn_k.weight", dim, kv_dim, f"{p}.attn_k.bias")
+        linear(f"{p}.attn_v.weight", dim, kv_dim, f"{p}.attn_v.bias")
+        linear(f"{p}.attn_output.weight", q_dim, dim)
+        norm(f"{p}.ffn_norm.weight")
+        linear(f"{p}.ffn_gate.weight", dim, ffn)
+        linear(f"{p}.ffn_up.weight", dim, ffn)
+        linear(f"{p}.ffn_down.weight", ffn, dim)
+    norm("output_norm.weight")
+    if "output.bias" in g.tensors:
+        raise _fmt("GGUF tensor 'output.bias' is not supported: Ferrum loads biases only for attn_q/attn_k/attn_v")
+    tied = "output.weight" not in g.tensors
+    if not tied:
+        linear("output.weight", dim, vocab)
+    cfg = dict(arch=arch, vocab=vocab, d=dim, n_heads=n_heads, n_kv=n_kv, head_dim=head_dim, layers=n_layers,
+               ffn=ffn, context=ctx_len, rope_dim=rope_dim, rope_base=rope_base, rope_type=rope_type, eps=eps,
+               rope_linear=linear_factor, rope_freqs=has_freqs)
+    return cfg, mats, tied
+
+
 # ---- Llama / Qwen block pieces (llm.rs), batched over rows --------------------
 
 ROPE_NORM, ROPE_NEOX = 0, 1
@@ -748,6 +1050,9 @@ class LlamaDevice:
         self.layers, self.ffn, self.cap = c["layers"], c["ffn"], c["context"]
         self.rope_dim, self.rope_base = c.get("rope_dim", self.hd), c.get("rope_base", 10000.0)
         self.rope_type, self.eps = c.get("rope_type", ROPE_NEOX), c.get("eps", 1e-5)
+        # RopeScaling (llm.rs): a linear position factor and optional per-pair
+        # frequency factors (a device tensor of rope_dim / 2 floats, or None)
+        self.rope_linear, self.rope_freqs = float(c.get("rope_linear", 1.0)), None
         self.q_dim, self.kv_dim = self.nh * self.hd, self.nkv * self.hd
         self.qkv_dim = self.q_dim + 2 * self.kv_dim
         dev, B = torch.device("cuda"), rows
@@ -799,6 +1104,88 @@ class LlamaDevice:
         m.out_norm = f(weights["output_norm"])
         torch.cuda.synchronize()
         ctx.sync()
+        return m
+
+    @classmethod
+    def from_gguf(cls, ctx: Context, path, rows: int = 1, capacity=None) -> "LlamaDevice":
+        """A llama / qwen2 GGUF read as Gguf::load_llama_prec(None) reads it
+        (gguf/llama.rs:171-340; the checks, llama_gguf_plan): rope type by
+        architecture (NORM for llama, NEOX for qwen2), the metadata defaults,
+        linear rope scaling and rope_freqs.weight, q/k/v biases when present,
+        the head tied to the token table when output.weight is absent.  The
+        q|k|v and gate|up matrices are stacked into one weight each (row
+        concatenation: Q8_0 rows stay Q8_0 bytes; a group holding an F32 / F16
+        matrix becomes one F32 weight, the Q8_0 rows expanded exactly).  Each
+        row's KV cache holds `capacity` positions (default: the file's
+        context_length)."""
+        import torch
+
+        with GGUFFile(path) as g:
+            cfg, mats, tied = llama_gguf_plan(g)
+            if capacity is not None:
+                cfg["context"] = int(capacity)
+            m = cls(ctx, cfg, rows)
+            d = m.d
+            f = lambda name: torch.from_numpy(np.ascontiguousarray(g.read_f32(ctx, name), np.float32).ravel()).cuda()  # noqa: E731
+
+            def kind(name):
+                ty = g.tensors[name][1]
+                if ty not in (GGML_Q8_0, GGML_F32, GGML_F16):
+                    raise FerrumHipError(FH_ERR_LIMIT, f"tensor '{name}' is GGML type {ty}; the device path takes "
+                                                       "Q8_0, F32 or F16 matrices")
+                return ty
+
+            def shape(name):
+                """(rows, row length) of a 2-D tensor: GGML dims are (ne0, ne1)."""
+                dims = g.tensors[name][0]
+                return int(dims[1]), int(dims[0])
+
+            def dense(name):
+                """The matrix's rows as f32 (Q8_0 expanded exactly: f16 scale times int8)."""
+                n_out, n_in = shape(name)
+                if kind(name) == GGML_Q8_0:
+                    blk = np.frombuffer(g.raw(name), np.uint8).reshape(-1, 34)
+                    sc = blk[:, :2].copy().view(np.float16).astype(np.float32)
+                    return (sc * blk[:, 2:].copy().view(np.int8).astype(np.float32)).reshape(n_out, n_in)
+                return g.read_f32(ctx, name).reshape(n_out, n_in)
+
+            def weight(names):
+                """One device weight holding the rows of `names` in order."""
+                shapes = [shape(n) for n in names]
+                n_in = shapes[0][1]
+                if all(kind(n) == GGML_Q8_0 for n in names):
+                    raw = np.concatenate([np.frombuffer(g.raw(n), np.uint8) for n in names])
+                    return Q8_0Weight.upload(ctx, raw, sum(s[0] for s in shapes), n_in)
+                return Q8_0Weight.upload_f32(ctx, np.concatenate([dense(n) for n in names]))
+
+            if kind("token_embd.weight") == GGML_Q8_0:
+                traw = torch.from_numpy(np.frombuffer(g.raw("token_embd.weight"), np.uint8).copy()).cuda()
+                m.tok_w = torch.empty((m.vocab, d), device="cuda")
+                torch.cuda.synchronize()
+                q8_0_dequant_async(ctx, traw, m.vocab * d, m.tok_w)
+                ctx.sync()
+            else:
+                m.tok_w = f("token_embd.weight").reshape(m.vocab, d)
+            m.head = weight(["token_embd.weight" if tied else "output.weight"])
+            for i in range(m.layers):
+                p = f"blk.{i}."
+                names = [p + "attn_q.weight", p + "attn_k.weight", p + "attn_v.weight"]
+                biases = [p + f"attn_{s}.bias" for s in "qkv"]
+                qkv_b = None
+                if any(b in g.tensors for b in biases):
+                    qkv_b = torch.cat([f(b) if b in g.tensors else torch.zeros(n, device="cuda")
+                                       for b, n in zip(biases, (m.q_dim, m.kv_dim, m.kv_dim))])
+                k, v = m._alloc_cache()
+                m.blocks.append({
+                    "attn_norm": f(p + "attn_norm.weight"), "ffn_norm": f(p + "ffn_norm.weight"),
+                    "qkv": weight(names), "qkv_b": qkv_b, "o": weight([p + "attn_output.weight"]),
+                    "gate_up": weight([p + "ffn_gate.weight", p + "ffn_up.weight"]),
+                    "down": weight([p + "ffn_down.weight"]), "k": k, "v": v})
+            m.out_norm = f("output_norm.weight")
+            if cfg["rope_freqs"]:
+                m.rope_freqs = f("rope_freqs.weight")
+            torch.cuda.synchronize()
+            ctx.sync()
         return m
 
     @classmethod
@@ -870,9 +1257,10 @@ class LlamaDevice:
             else:  # the previous block's second residual add, then attn_norm
                 rmsnorm_async(ctx, cur, self.proj, other, B, d, b["attn_norm"], self.eps, self.h)
                 cur, other = other, cur
-            linear_forward_async(ctx, b["qkv"], self.h, B, d, b["qkv_b"], self.qkv_dim, self.qkv)
+            qkv_b = b.get("qkv_b")  # (None: a file without q/k/v biases, whose linears are bias-free)
+            linear_forward_async(ctx, b["qkv"], self.h, B, d, qkv_b, 0 if qkv_b is None else self.qkv_dim, self.qkv)
             rope_async(ctx, self.qkv, B, self.qkv_dim, self.nh + self.nkv, self.hd, self.rope_dim, self.pos,
-                       self.rope_base, self.rope_type)
+                       self.rope_base, self.rope_type, self.rope_freqs, self.rope_linear)
             gqa_attention_decode_async(ctx, self.qkv, self.qkv_dim, B, self.nh, self.nkv, self.hd, b["k"], b["v"],
                                        self.cap, self.pos, max_pos, self.att)
             linear_forward_async(ctx, b["o"], self.att, B, self.q_dim, None, 0, self.proj)
@@ -978,37 +1366,78 @@ class GPT2Device:
 
     @classmethod
     def from_gguf(cls, ctx: Context, path) -> "GPT2Device":
-        """A GPT-2 GGUF in GgufOut::gpt2's layout (loader/gpt2.rs:61-146, read
-        back by gpt2_from, loader/gpt2.rs:201-295): hyperparameters from the
-        gpt2.* keys, Q8_0 matrices uploaded straight from the file's mapping,
-        f32 vectors copied; the head is output.weight when present, else the
-        token table (tied)."""
+        """A GPT-2 GGUF read as gpt2_from reads it (loader/gpt2.rs:201-295;
+        the checks, gpt2_gguf_plan): hyperparameters from the gpt2.* keys, the
+        layer_norm_epsilon check, the token table's rows (and an untied
+        output.weight's) reordered to ferrum_core's vocabulary order
+        (ferrum_vocab / permute_rows, loader/gpt2.rs:149-199); Q8_0 matrices
+        uploaded straight from the file's mapping (a row permutation of Q8_0
+        rows is exact), F32 / F16 ones (the reference's writer stores a matrix
+        as F32 when ne0 % 32 != 0, loader/mod.rs:147-152) as F32 weights; the
+        head is output.weight when present, else the token table (tied).  A
+        model with an F32 matrix runs one op at a time (the one-launch stack
+        takes Q8_0 only)."""
         import torch
 
         with GGUFFile(path) as g:
-            if g.meta("general.architecture") != "gpt2":
-                raise FerrumHipError(FH_ERR_INVALID, f"{path}: general.architecture is not gpt2")
-            d, layers = g.meta("gpt2.embedding_length"), g.meta("gpt2.block_count")
-            heads, ffn, context = g.meta("gpt2.attention.head_count"), g.meta("gpt2.feed_forward_length"), \
-                g.meta("gpt2.context_length")
-            vocab = g.tensors["token_embd.weight"][0][1]
-            m = cls(ctx, vocab, d, heads, layers, ffn, context)
+            cfg, perm, tied = gpt2_gguf_plan(g)
+            vocab, d = cfg["vocab"], cfg["d"]
+            m = cls(ctx, vocab, d, cfg["heads"], cfg["layers"], cfg["ffn"], cfg["context"])
+            identity = perm == list(range(vocab))
             f = lambda name: torch.from_numpy(g.read_f32(ctx, name).copy()).cuda()  # noqa: E731
-            tok = torch.from_numpy(np.frombuffer(g.raw("token_embd.weight"), np.uint8).copy()).cuda()
-            m.tok_w = torch.empty((vocab, d), device="cuda")
-            torch.cuda.synchronize()
-            q8_0_dequant_async(ctx, tok, vocab * d, m.tok_w)
-            m.head = g.upload_q8_0(ctx, "output.weight" if "output.weight" in g.tensors else "token_embd.weight")
+
+            def rows_q8(name):
+                raw = np.frombuffer(g.raw(name), np.uint8).reshape(vocab, -1)
+                return raw if identity else raw[perm]
+
+            def rows_f32(name):
+                a = g.read_f32(ctx, name).reshape(vocab, d)
+                return a if identity else a[perm]
+
+            def table(name):
+                """(device Q8_0-or-F32 weight of the vocab rows, f32 rows on the device)."""
+                ty = g.tensors[name][1]
+                if ty == GGML_Q8_0:
+                    raw = np.ascontiguousarray(rows_q8(name))
+                    w = Q8_0Weight.upload(ctx, raw, vocab, d)
+                    dense = torch.empty((vocab, d), device="cuda")
+                    traw = torch.from_numpy(raw.ravel().copy()).cuda()
+                    torch.cuda.synchronize()
+                    q8_0_dequant_async(ctx, traw, vocab * d, dense)
+                    ctx.sync()
+                    return w, dense
+                if ty in (GGML_F32, GGML_F16):
+                    a = np.ascontiguousarray(rows_f32(name))
+                    return Q8_0Weight.upload_f32(ctx, a), torch.from_numpy(a.copy()).cuda()
+                raise FerrumHipError(FH_ERR_LIMIT, f"tensor '{name}' is GGML type {ty}; the device path takes "
+                                                   "Q8_0, F32 or F16 matrices")
+
+            def mat(name):
+                ty = g.tensors[name][1]
+                if ty == GGML_Q8_0:
+                    return g.upload_q8_0(ctx, name)
+                if ty in (GGML_F32, GGML_F16):
+                    return Q8_0Weight.upload_f32(ctx, g.read_f32(ctx, name))
+                raise FerrumHipError(FH_ERR_LIMIT, f"tensor '{name}' is GGML type {ty}; the device path takes "
+                                                   "Q8_0, F32 or F16 matrices")
+
+            tok_w, m.tok_w = table("token_embd.weight")
+            if tied:
+                m.head = tok_w
+            else:
+                tok_w.free()
+                m.head = table("output.weight")[0]
             m.pos_w = f("position_embd.weight")
-            for i in range(layers):
+            for i in range(cfg["layers"]):
                 n = lambda s: f"blk.{i}.{s}"  # noqa: E731
                 m.blocks.append(m._block([f(n("attn_norm.weight")), f(n("attn_norm.bias")), f(n("ffn_norm.weight")),
                                           f(n("ffn_norm.bias"))],
-                                         g.upload_q8_0(ctx, n("attn_qkv.weight")), f(n("attn_qkv.bias")),
-                                         g.upload_q8_0(ctx, n("attn_output.weight")), f(n("attn_output.bias")),
-                                         g.upload_q8_0(ctx, n("ffn_up.weight")), f(n("ffn_up.bias")),
-                                         g.upload_q8_0(ctx, n("ffn_down.weight")), f(n("ffn_down.bias"))))
+                                         mat(n("attn_qkv.weight")), f(n("attn_qkv.bias")),
+                                         mat(n("attn_output.weight")), f(n("attn_output.bias")),
+                                         mat(n("ffn_up.weight")), f(n("ffn_up.bias")),
+                                         mat(n("ffn_down.weight")), f(n("ffn_down.bias"))))
             m.lnf_g, m.lnf_b = f("output_norm.weight"), f("output_norm.bias")
+            m.vocab_perm = None if identity else perm
             torch.cuda.synchronize()
             ctx.sync()
         m._make_stack()

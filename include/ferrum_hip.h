@@ -139,6 +139,16 @@ int fh_q8_0_upload(fh_ctx* ctx, const uint8_t* gguf_bytes, size_t n_rows, size_t
 /* The same from a device buffer holding the GGUF bytes. */
 int fh_q8_0_upload_device(fh_ctx* ctx, const uint8_t* d_gguf_bytes, size_t n_rows, size_t k,
                           fh_q8_0** out);
+/* An F32 weight [n_rows x k] behind the same handle, from host rows (GGUF
+ * order: k = ne0 values per row, any k): a matrix the reference stores as F32
+ * (loader/mod.rs:147-152: ne0 % 32 != 0, or an unquantized save), read back
+ * by Gguf::dequantize.  Every linear entry point takes it and computes the
+ * reference's f32 linear_forward bit for bit (the FH_W8A32_EXACT kernel, for
+ * FH_W8A32 too); FH_W8A8, the block dots, download, the no-allocation linear
+ * and the one-launch GPT-2 stack need Q8_0 (FH_ERR_INVALID / FH_ERR_LIMIT). */
+int fh_weight_upload_f32(fh_ctx* ctx, const float* rows, size_t n_rows, size_t k, fh_q8_0** out);
+/* 0 for a Q8_0 weight, 1 for F32, -1 for NULL. */
+int fh_weight_kind(const fh_q8_0* w);
 /* Write the tensor back as GGUF bytes (host buffer of n_rows * k / 32 * 34). */
 int fh_q8_0_download(fh_ctx* ctx, const fh_q8_0* w, uint8_t* gguf_bytes);
 int fh_q8_0_dims(const fh_q8_0* w, size_t* n_rows, size_t* k);

@@ -38,10 +38,20 @@ class OracleGPT2:
     def __init__(self, orc, w, vocab=VOCAB, d=D, heads=HEADS, layers=LAYERS, ffn=FFN, ctx=CTX):
         self.orc, self.w, self.vocab, self.d, self.heads, self.layers, self.ffn, self.cap = (
             orc, w, vocab, d, heads, layers, ffn, ctx)
-        self.tok_w = orc.q8_0_dequant(w["token_embd_q8"], vocab * d).reshape(vocab, d)
+        self.tok_w = (np.asarray(w["token_embd_f32"], np.float32).reshape(vocab, d) if "token_embd_f32" in w
+                      else orc.q8_0_dequant(w["token_embd_q8"], vocab * d).reshape(vocab, d))
         self.k = [np.zeros((ctx, d), np.float32) for _ in range(layers)]
         self.v = [np.zeros((ctx, d), np.float32) for _ in range(layers)]
         self.pos = 0
+
+    def lin(self, x, key, n, bias):
+        """ops::linear_forward on the key's matrix: Q8_0 rows (key_q8) as the
+        reference expands them, or F32 rows (key_f32) as stored."""
+        x = np.atleast_2d(np.asarray(x, np.float32))
+        if key + "_f32" in self.w:
+            rows = np.asarray(self.w[key + "_f32"], np.float32).reshape(n, -1)
+            return self.orc.linear_forward(x, np.ascontiguousarray(rows.T), bias)
+        return self.orc.q8_0_linear(x, self.w[key + "_q8"], n, bias)
 
     def feed(self, token):
         orc, w, d = self.orc, self.w, self.d
@@ -49,15 +59,15 @@ class OracleGPT2:
         for i in range(self.layers):
             g = lambda name: w[f"blk{i}.{name}"]  # noqa: E731
             h = orc.layernorm(x, g("ln1_g"), g("ln1_b"))
-            qkv = orc.q8_0_linear(h, g("qkv_q8"), 3 * d, g("qkv_b"))[0]
+            qkv = self.lin(h, f"blk{i}.qkv", 3 * d, g("qkv_b"))[0]
             att = orc.attention_decode(qkv, self.k[i], self.v[i], self.heads, self.pos)
-            x = (x + orc.q8_0_linear(att[None, :], g("out_q8"), d, g("out_b"))[0]).astype(np.float32)
+            x = (x + self.lin(att, f"blk{i}.out", d, g("out_b"))[0]).astype(np.float32)
             h = orc.layernorm(x, g("ln2_g"), g("ln2_b"))
-            up = orc.gelu(orc.q8_0_linear(h, g("up_q8"), self.ffn, g("up_b")))
-            x = (x + orc.q8_0_linear(up, g("down_q8"), d, g("down_b"))[0]).astype(np.float32)
+            up = orc.gelu(self.lin(h, f"blk{i}.up", self.ffn, g("up_b")))
+            x = (x + self.lin(up, f"blk{i}.down", d, g("down_b"))[0]).astype(np.float32)
         self.pos += 1
         h = orc.layernorm(x, w["lnf_g"], w["lnf_b"])
-        return orc.q8_0_linear(h, w["token_embd_q8"], self.vocab, None)[0]
+        return self.lin(h, "token_embd", self.vocab, None)[0]
 
     def forward(self, ids, reprime):
         """gpt2_decode's forward: reprime re-feeds the window from position 0."""

@@ -59,8 +59,9 @@ class OracleLlamaRow:
         for i in range(c["layers"]):
             p = f"blk.{i}."
             h = orc.rmsnorm(x, w[p + "attn_norm"], eps)
-            q = orc.rope(lin(h, p + "attn_q", nh * hd), nh, hd, rd, self.pos, base, rt)
-            k = orc.rope(lin(h, p + "attn_k", nkv * hd), nkv, hd, rd, self.pos, base, rt)
+            ff, lf = c.get("rope_freqs"), c.get("rope_linear", 1.0)  # RopeScaling (gguf/llama.rs:51-103)
+            q = orc.rope(lin(h, p + "attn_q", nh * hd), nh, hd, rd, self.pos, base, rt, ff, lf)
+            k = orc.rope(lin(h, p + "attn_k", nkv * hd), nkv, hd, rd, self.pos, base, rt, ff, lf)
             v = lin(h, p + "attn_v", nkv * hd)
             att = orc.gqa_attention_decode(np.concatenate([q, k, v]), self.k[i], self.v[i], nh, nkv, hd, self.pos)
             x = (x + lin(att, p + "attn_output", d)).astype(np.float32)
