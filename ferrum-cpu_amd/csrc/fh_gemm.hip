@@ -20,9 +20,12 @@
 // does.  Non-finite activations keep l = 0, so inf and NaN propagate as they
 // do in the reference's products (inf * 0 = NaN, inf * q = inf).
 //
-// Work split: k_split_rows writes the h/l terms once per call into a panel
-// laid out for the GEMM's staging ([row tile][block][row][h 32 | l 32], 128 B
-// per row and block, so a stage is one contiguous read).  k_gemm_mfma stages
+// Work split: for the mid-size tiles k_split_rows writes the h/l terms once
+// per call into a panel laid out for the GEMM's staging ([row tile][block]
+// [row][h 32 | l 32], 128 B per row and block, so a stage is one contiguous
+// read); the large-m weight-split kernel instead takes only the row scales
+// (k_row_scales, one read of x) and splits the activations while staging
+// them, which saves the panel's write and re-read.  k_gemm_mfma stages
 // KW Q8_0 blocks of the activation panel and of the weight rows per step into
 // LDS (double buffered, one barrier per step), converting the int8 quants to
 // f16 on the way in; each wave owns TM x TN 32x32 output tiles, and with
@@ -151,6 +154,46 @@ __global__ void __launch_bounds__(256)
         uint4* dst = dst_row + static_cast<size_t>(c >> 2) * bm * 8;
         dst[c & 3] = __builtin_bit_cast(uint4, hv);
         dst[4 + (c & 3)] = __builtin_bit_cast(uint4, lv);
+    }
+}
+
+// The row scales and flags of k_split_rows without the panel: the weight-split
+// GEMM splits the activations itself while staging them (one read of x here
+// instead of a read and a write of the whole panel).  Rows m .. m_pad - 1 get
+// scale 1 and no flag.
+__global__ void __launch_bounds__(256)
+    k_row_scales(const float* __restrict__ x, int m, int m_pad, int k, float* __restrict__ xinv,
+                 uint8_t* __restrict__ xbad) {
+    const int row = blockIdx.x * 4 + static_cast<int>(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (row >= m_pad) return;
+    const int chunks = k >> 3;
+    float mx = 0.0f;
+    bool bad = false;
+    if (row < m) {
+        const float4* xr = reinterpret_cast<const float4*>(x + static_cast<size_t>(row) * k);
+        for (int c = lane; c < chunks; c += 64) {
+            const float4 a = xr[2 * c], b = xr[2 * c + 1];
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int t = 0; t < 8; t++) {
+                if (finite(v[t])) mx = fmaxf(mx, fabsf(v[t]));
+                else bad = true;
+            }
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
+    const bool any_bad = __ballot(bad) != 0;
+    // the same scale as k_split_rows: 2^(15 - E) for mx = f * 2^E, f in [0.5, 1)
+    int e = 0;
+    if (mx > 0.0f) {
+        const int E = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 126;
+        e = min(max(15 - E, -126), 126);
+    }
+    if (lane == 0) {
+        xbad[row] = any_bad;
+        xinv[row] = __builtin_bit_cast(float, static_cast<uint32_t>(127 - e) << 23);
     }
 }
 
@@ -347,7 +390,7 @@ __global__ void __launch_bounds__(64 * WM * WN * KW)
 // only rounding beyond the f32 sums is the activations' 22-bit split.
 // Workgroup tile 256 x 256, eight waves of 128 x 64 (4 x 2 MFMA tiles), one
 // Q8_0 block per stage, two LDS stages of 72 KiB.
-template <int BM, int BN, int WM, int WN>
+template <int BM, int BN, int WM, int WN, bool FROM_X>
 __global__ void __launch_bounds__(64 * WM * WN)
     k_gemm_wsplit(const uint4* __restrict__ panel, const float* __restrict__ xinv, const uint8_t* __restrict__ xbad,
                   const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
@@ -380,11 +423,34 @@ __global__ void __launch_bounds__(64 * WM * WN)
     const int ejw = rexp[jw] == kFhBadRowExp ? 0 : rexp[jw];  // flagged rows: recomputed at the end
     const float wscale = __builtin_bit_cast(float, static_cast<uint32_t>(ejw + 127) << 23);
 
+    // FROM_X: the activations come straight from x (f32, row-major) and are
+    // split here, with the row scales of k_row_scales: each thread stages
+    // four 4-value pieces (rows piece / 8, values 4 * (piece % 8) of the
+    // block) as the h and l terms k_split_rows writes to the panel.
+    constexpr int XP = BM * 8 / NTH;  // (also AP) pieces per thread
+    float xsc[FROM_X ? XP : 1];
+    const float* xrow[FROM_X ? XP : 1];
+    if constexpr (FROM_X) {
+        const int i0x = (tile / tiles_n) * BM;
+#pragma unroll
+        for (int p = 0; p < XP; p++) {
+            const int r = (tid + NTH * p) / 8, i = min(i0x + r, m - 1);  // rows past m: clamped, never stored
+            // 2^e from the stored 2^-e (both exact powers of two)
+            xsc[p] = __builtin_bit_cast(float, (254u << 23) - __builtin_bit_cast(uint32_t, xinv[i0x + r]));
+            xrow[p] = x + static_cast<size_t>(i) * k + ((tid + NTH * p) % 8) * 4;
+        }
+    }
     u4 ra[AP], rq;
     uint16_t rd;
     auto load = [&](int b) __attribute__((always_inline)) {
+        if constexpr (FROM_X) {
 #pragma unroll
-        for (int p = 0; p < AP; p++) ra[p] = reinterpret_cast<const u4*>(pan)[static_cast<size_t>(b) * BM * 8 + tid + NTH * p];
+            for (int p = 0; p < AP; p++) ra[p] = *reinterpret_cast<const u4*>(xrow[p] + b * 32);
+        } else {
+#pragma unroll
+            for (int p = 0; p < AP; p++)
+                ra[p] = reinterpret_cast<const u4*>(pan)[static_cast<size_t>(b) * BM * 8 + tid + NTH * p];
+        }
         rq = *reinterpret_cast<const u4*>(wsrc + b * 32);
         rd = dsrc[b];
     };
@@ -393,7 +459,25 @@ __global__ void __launch_bounds__(64 * WM * WN)
 #pragma unroll
         for (int p = 0; p < AP; p++) {
             const int piece = tid + NTH * p;
-            *reinterpret_cast<u4*>(st + (piece / 8) * kArow * 2 + (piece % 8) * 16) = ra[p];
+            if constexpr (FROM_X) {
+                const f4 sv = __builtin_bit_cast(f4, ra[p]) * xsc[p];  // exact (power of two)
+                const f2 s01 = {sv.x, sv.y}, s23 = {sv.z, sv.w};
+                const h2 h01 = __builtin_convertvector(s01, h2), h23 = __builtin_convertvector(s23, h2);
+                f2 r01 = {sv.x - static_cast<float>(h01.x), sv.y - static_cast<float>(h01.y)};
+                f2 r23 = {sv.z - static_cast<float>(h23.x), sv.w - static_cast<float>(h23.y)};
+                r01.x = finite(sv.x) ? r01.x : 0.0f;
+                r01.y = finite(sv.y) ? r01.y : 0.0f;
+                r23.x = finite(sv.z) ? r23.x : 0.0f;
+                r23.y = finite(sv.w) ? r23.y : 0.0f;
+                char* rowp = st + (piece / 8) * kArow * 2 + (piece % 8) * 8;
+                *reinterpret_cast<uint2*>(rowp) =
+                    make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+                *reinterpret_cast<uint2*>(rowp + 64) =
+                    make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(r01, h2)),
+                               __builtin_bit_cast(uint32_t, __builtin_convertvector(r23, h2)));
+            } else {
+                *reinterpret_cast<u4*>(st + (piece / 8) * kArow * 2 + (piece % 8) * 16) = ra[p];
+            }
         }
         const float ds = fh_h2f(rd) * wscale;  // exact (power of two)
         uint32_t hi[8], lo[8];
@@ -863,6 +947,29 @@ __global__ void __launch_bounds__(512)
 
 namespace {
 
+// The weight-split GEMM fed straight from x: row scales first (one read of
+// x), then the GEMM, which splits the activations while staging them.
+template <int BM, int BN, int WM, int WN>
+int launch_wsplit_x(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    const size_t m_pad = (m + BM - 1) / BM * BM;
+    const size_t ibytes = fh_align256(m_pad * 4), fbytes = fh_align256(m_pad);
+    void* ws = nullptr;
+    int rc = fh_workspace(ctx, ibytes + fbytes, &ws);
+    if (rc) return rc;
+    float* xinv = static_cast<float*>(ws);
+    uint8_t* xbad = reinterpret_cast<uint8_t*>(static_cast<char*>(ws) + ibytes);
+    hipLaunchKernelGGL(k_row_scales, dim3(static_cast<unsigned>((m_pad + 3) / 4)), dim3(256), 0, ctx->stream, x,
+                       static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(w->k), xinv, xbad);
+    FH_HIP(ctx, hipGetLastError());
+    const size_t tiles_n = (w->n + BN - 1) / BN, tiles = tiles_n * (m_pad / BM);
+    if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
+    hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN, true>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN),
+                       0, ctx->stream, nullptr, xinv, xbad, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
+                       static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n));
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
 template <int BM, int BN, int WM, int WN, int KW>
 int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
     const size_t m_pad = (m + BM - 1) / BM * BM;
@@ -879,7 +986,7 @@ int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const f
     const size_t tiles_n = (w->n + BN - 1) / BN, tiles = tiles_n * (m_pad / BM);
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
     if constexpr (KW == 0)  // the weight-split kernel
-        hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN), 0,
+        hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN, false>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN), 0,
                            ctx->stream, panel, xinv, xbad, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
                            static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n));
     else
@@ -1024,7 +1131,7 @@ int fh_launch_skinny_scratch(fh_ctx* ctx, const fh_q8_0* w, const float* x, size
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
     const size_t cus = static_cast<size_t>(ctx->num_cus);
     if (m <= 64) return launch_skinny(ctx, w, x, m, bias, y);
-    if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus) return launch_gemm<256, 256, 2, 4, 0>(ctx, w, x, m, bias, y);
+    if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus) return launch_wsplit_x<256, 256, 2, 4>(ctx, w, x, m, bias, y);
     if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) return launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
     if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) return launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
     return launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);
