@@ -201,6 +201,15 @@ def main():
         ms_full_mall, _ = timed(graphs_f[:1], args.steps, args.warmup)
         del graphs_f
         ctx.sync()  # raises if any exchange of the timed steps gave up
+        # The same steps with one graph holding a step per replica (three
+        # consecutive steps): what a decode loop that keeps its token on the
+        # device gets by capturing several steps at once (no host launch and
+        # graph boundary between them).
+        graphs_3 = capture(lambda _: [full_step(mdl) for mdl in models], [None])
+        ms_g3, _ = timed(graphs_3, max(args.steps // len(models), 1), max(args.warmup // len(models), 1))
+        ms_full_multi = ms_g3 / len(models)
+        del graphs_3
+        ctx.sync()
 
         # Config 3 as a run: a 128-token random prompt fed position by
         # position, then 256 steps sampled on the device (the sampler's id
@@ -216,12 +225,24 @@ def main():
         t0 = time.perf_counter()
         run_ids = m3.generate(prompt, 256, params, fh.Rng(3))
         t_run = time.perf_counter() - t0
+        # the same run with the prompt primed in one pass (prefill=True: its
+        # 127 positions as rows of GEMMs and one attention launch per block)
+        m3.generate(prompt, 8, params, fh.Rng(1), prefill=True)
+        t0 = time.perf_counter()
+        m3.generate(prompt, 1, params, fh.Rng(2), prefill=True)
+        t_prime_pf = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        run_ids_pf = m3.generate(prompt, 256, params, fh.Rng(3), prefill=True)
+        t_run_pf = time.perf_counter() - t0
         result["config3_run"] = {
             "prompt": 128, "steps": len(run_ids), "run_ms": round(t_run * 1e3, 2), "prime_ms": round(t_prime * 1e3, 2),
             "decode_tok_s": round(255 / max(t_run - t_prime, 1e-9), 1), "run_tok_s": round(len(run_ids) / t_run, 1),
+            "prefill": {"run_ms": round(t_run_pf * 1e3, 2), "prime_ms": round(t_prime_pf * 1e3, 2),
+                        "run_tok_s": round(len(run_ids_pf) / t_run_pf, 1),
+                        "same_ids": run_ids_pf == run_ids},
             "residency": "one model (131 MB, MALL-resident)", "sampler": SAMPLER,
-            "what": "GPT2Device.generate: prompt fed position by position, then stack + head + sampler per step, "
-                    "wall clock around the whole run (host launches included)"}
+            "what": "GPT2Device.generate: prompt fed position by position (prefill: in one pass), then stack + "
+                    "head + sampler per step, wall clock around the whole run (host launches included)"}
 
         # the dominant kernel alone: k_gpt2_stack, 10 launches per graph
         def stack_only(mdl):
@@ -276,6 +297,7 @@ def main():
         stack_bytes = layer_bytes + kv_bytes
         stack_gbps = stack_bytes / (stack_us * 1e-6) / 1e9
         result.update(ms_full=ms_full, wall_full=wall_full, ms_full_mall=ms_full_mall, ms_perop=ms_perop,
+                      ms_full_multi=ms_full_multi,
                       stack_us=stack_us, stack_bytes=stack_bytes, stack_gbps=stack_gbps, step_bytes=step_bytes,
                       sampler_us=sampler_us, kv_bytes=kv_bytes)
         if args.leg == "stack":
@@ -289,6 +311,7 @@ def main():
             print(json.dumps({"leg": "stack", "stack_us": round(stack_us, 3), "stack_bytes": stack_bytes,
                               "stack_GBps": round(stack_gbps, 1), "ms_per_step": round(ms_full, 5),
                               "per_op_ms_per_step": round(ms_perop, 5), "copy_bytes_per_launch": COPY_BYTES,
+                              "multi_step_graph_ms_per_step": round(ms_full_multi, 5),
                               "config3_run": result["config3_run"]}))
             return
 
@@ -461,6 +484,9 @@ def main():
         "roofline_lm_head": head_roofline,
         "cpu_baseline": cpu,
         "mall_resident_tok_s": round(1000.0 / result["ms_full_mall"], 1),
+        "multi_step_graph": {"tok_s": round(1000.0 / result["ms_full_multi"], 1),
+                             "ms_per_step": round(result["ms_full_multi"], 5),
+                             "what": "the same HBM-forced steps, three consecutive steps (one per replica) per graph"},
         "per_op_launches_tok_s": round(1000.0 / result["ms_perop"], 1),
         "hot_path_unchained": {"tok_s": round(1000.0 / result["hot_unchained"], 1),
                                "ms_per_step": round(result["hot_unchained"], 5),

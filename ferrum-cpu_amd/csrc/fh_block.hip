@@ -78,6 +78,21 @@ __global__ void __launch_bounds__(kThreads) k_add(float* __restrict__ x, const f
     if (i < n) x[i] = x[i] + y[i];
 }
 
+// Rows r of a prompt block: their k and v slices (qkv + r * ld + k_off / v_off,
+// kv_dim values each) into cache rows pos0 + r, before the block's attention
+// reads them (one sequence: every row shares the cache).
+__global__ void __launch_bounds__(kThreads) k_kv_store(const float* __restrict__ qkv, int ld, int k_off, int v_off,
+                                                      int kv_dim, int pos0, float* __restrict__ kc,
+                                                      float* __restrict__ vc) {
+    const int r = blockIdx.y;
+    const float* src = qkv + static_cast<size_t>(r) * ld;
+    const size_t dst = static_cast<size_t>(pos0 + r) * kv_dim;
+    for (int c = blockIdx.x * kThreads + threadIdx.x; c < kv_dim; c += gridDim.x * kThreads) {
+        kc[dst + c] = src[k_off + c];
+        vc[dst + c] = src[v_off + c];
+    }
+}
+
 // Grid (chunks, heads, rows); a workgroup covers S sub-chunks of 32
 // positions of one query head of one row (sequence).  Row r's q|k|v sits at
 // qkv + r * ld (q heads, then kv heads at k_off and v_off); its caches at
@@ -99,6 +114,7 @@ struct AttnArgs {
     int kv_dim, group;
     const uint32_t* dpos;
     int pos, cap;
+    int pos_step;  // without dpos, row r's position is pos + pos_step * r
     float scale;
     float* part;
     unsigned* counters;
@@ -119,7 +135,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_chunk(AttnArgs a) {
     const int chunk = blockIdx.x, head = blockIdx.y, row = blockIdx.z;
     const int hs = head * hd, tid = threadIdx.x;
     const int kvs = (head / a.group) * hd;  // this head's kv slice
-    const int pos = a.dpos ? static_cast<int>(min(a.dpos[row], 0x7FFFFFFFu)) : a.pos;
+    const int pos = a.dpos ? static_cast<int>(min(a.dpos[row], 0x7FFFFFFFu)) : a.pos + a.pos_step * row;
     float* out = a.out + static_cast<size_t>(row) * a.out_ld + hs;
     if (pos >= a.cap) {  // a position the cache cannot hold
         if (chunk == 0 && tid < hd) out[tid] = __builtin_nanf("");
@@ -447,6 +463,34 @@ int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* 
     a.out = out;
     a.out_ld = static_cast<int>(d);
     return launch_attention(ctx, a, 1, heads, d / heads, pos + 1);
+}
+
+int fh_launch_attention_prefill(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
+                                size_t pos0, size_t rows, float* out) {
+    // Every row's k and v are in the cache before any row reads them; each
+    // attention workgroup then writes its own row again (the same bits).
+    const unsigned gx = static_cast<unsigned>((d + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL(k_kv_store, dim3(gx, static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, qkv,
+                       static_cast<int>(3 * d), static_cast<int>(d), static_cast<int>(2 * d), static_cast<int>(d),
+                       static_cast<int>(pos0), kc, vc);
+    FH_HIP(ctx, hipGetLastError());
+    AttnArgs a{};
+    a.qkv = qkv;
+    a.ld = static_cast<int>(3 * d);
+    a.k_off = static_cast<int>(d);
+    a.v_off = static_cast<int>(2 * d);
+    a.kc = kc;
+    a.vc = vc;
+    a.seq_stride = 0;  // one sequence: the rows share the cache
+    a.kv_dim = static_cast<int>(d);
+    a.group = 1;
+    a.dpos = nullptr;
+    a.pos = static_cast<int>(pos0);
+    a.pos_step = 1;
+    a.cap = 0x7FFFFFFF;  // checked by the caller
+    a.out = out;
+    a.out_ld = static_cast<int>(d);
+    return launch_attention(ctx, a, rows, heads, d / heads, pos0 + rows);
 }
 
 int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,

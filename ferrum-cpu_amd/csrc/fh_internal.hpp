@@ -162,6 +162,10 @@ int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n);
 // receives x + y.  d <= 2048.
 int fh_launch_add_layernorm(fh_ctx* ctx, const float* x, const float* y, float* s, size_t rows, size_t d,
                             const float* gamma, const float* beta, float* ln);
+// A prompt block of `rows` consecutive positions pos0 .. pos0 + rows - 1 of
+// one sequence: their k / v rows into the cache, then each row's attention.
+int fh_launch_attention_prefill(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
+                                size_t pos0, size_t rows, float* out);
 int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
                                size_t pos, float* out);
 int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,

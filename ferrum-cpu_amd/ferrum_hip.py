@@ -45,6 +45,7 @@ EXPORTS = (
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async", "fh_debug_sampler_faults",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
+    "fh_attention_prefill_async",
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
     "fh_gpt2_stack_create", "fh_gpt2_stack_free", "fh_gpt2_stack_forward_async",
     "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
@@ -181,6 +182,7 @@ def lib():
         L.fh_gelu_async.argtypes = [vp, vp, sz]
         L.fh_add_async.argtypes = [vp, vp, vp, sz]
         L.fh_attention_decode_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, vp]
+        L.fh_attention_prefill_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, sz, vp]
         L.fh_q8_0_linear_act_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32, i32]
         L.fh_add_layernorm_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         L.fh_q8_0_linear_ln_async.argtypes = [vp, vp, vp, vp, vp, sz, sz, vp, vp, vp, sz, vp, i32, i32]
@@ -567,6 +569,14 @@ def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d
     """The KV-cache attention of forward_with_cache (layer/transformer.rs:242-279)."""
     ctx.check(lib().fh_attention_decode_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
                                               pos, _ptr(out)))
+
+
+def attention_prefill_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d: int, heads: int, pos0: int,
+                            rows: int, out):
+    """The same attention for `rows` consecutive positions pos0 .. pos0 + rows - 1
+    of one sequence at once (row r of qkv is position pos0 + r)."""
+    ctx.check(lib().fh_attention_prefill_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
+                                               pos0, rows, _ptr(out)))
 
 
 # ---- packed per-row int8 / int4 weights: ops::qlinear ---------------------------
@@ -1510,7 +1520,47 @@ class GPT2Device:
             return 2
         return 2 + 5 * self.layers + 1
 
-    def generate(self, prompt, max_tokens: int, params: SamplingParams, rng: Rng, eos=None, bos: int = 0):
+    def prefill_async(self, d_tokens, pos0: int, n: int):
+        """Positions pos0 .. pos0 + n - 1 (tokens on the device) through every
+        block at once, as n rows of one sequence: the same ops as feed_async's
+        per-op path with m = n (GEMMs for the linears, the block's attention
+        with every row's k / v in the cache first), the final LayerNorm and
+        the head for the last position only.  What CachedTransformer::feed
+        computes one token at a time (slm/cached.rs:100-125), within the 1e-5
+        rule (the GEMMs and the attention chunks sum in another order).  The
+        last position's scores land in self.z; the caches hold every row."""
+        import torch
+
+        ctx, d, ffn = self.ctx, self.d, self.ffn
+        if n <= 0:
+            return
+        if pos0 + n > self.cap:
+            raise DimMismatch(FH_ERR_DIM, f"KvCache full ({self.cap} positions): clear and re-prime to continue")
+        dev = "cuda"
+        x, x2, h = (torch.empty((n, d), device=dev) for _ in range(3))
+        qkv, att, proj = torch.empty((n, 3 * d), device=dev), torch.empty((n, d), device=dev), \
+            torch.empty((n, d), device=dev)
+        mid = torch.empty((n, ffn), device=dev)
+        embed_rows_async(ctx, self.tok_w, self.vocab, d, d_tokens, n, x)
+        add_async(ctx, x, self.pos_w[pos0:pos0 + n], n * d)  # tok + pos, as embed_one adds them
+        cur, other = x, x2
+        for i, b in enumerate(self.blocks):
+            if i == 0:
+                layernorm_async(ctx, cur, n, d, b["ln1_g"], b["ln1_b"], h)
+                linear_forward_async(ctx, b["qkv"], h, n, d, b["qkv_b"], 3 * d, qkv)
+            else:
+                linear_ln_async(ctx, b["qkv"], cur, proj, other, n, d, b["ln1_g"], b["ln1_b"], b["qkv_b"], 3 * d, qkv)
+                cur, other = other, cur
+            attention_prefill_async(ctx, qkv, b["k"], b["v"], self.cap, d, self.heads, pos0, n, att)
+            linear_forward_async(ctx, b["out"], att, n, d, b["out_b"], d, proj)
+            linear_ln_async(ctx, b["up"], cur, proj, other, n, d, b["ln2_g"], b["ln2_b"], b["up_b"], ffn, mid, ACT_GELU)
+            cur, other = other, cur
+            linear_forward_async(ctx, b["down"], mid, n, ffn, b["down_b"], d, proj)
+        linear_ln_async(ctx, self.head, cur[n - 1:], proj[n - 1:], None, 1, d, self.lnf_g, self.lnf_b, None, 0, self.z)
+        self._keep = (x, x2, h, qkv, att, proj, mid)  # alive until the stream has used them
+
+    def generate(self, prompt, max_tokens: int, params: SamplingParams, rng: Rng, eos=None, bos: int = 0,
+                 prefill: bool = False):
         """GenerativeSLM::token_stream + stream_next (slm/token_stream.rs:66-190)
         with every step on the device: the prompt is fed position by position,
         then each step runs the block stack, the head and the fused sampler,
@@ -1522,7 +1572,12 @@ class GPT2Device:
         at the end (an EOS ends the returned list as in the reference; the
         steps computed past it are discarded).  A run that would outgrow the
         window (prompt + max_tokens > context: the reference cuts and
-        re-primes) takes the host loop instead."""
+        re-primes) takes the host loop instead.
+
+        prefill=True primes the prompt in one pass (prefill_async: its
+        positions as rows of GEMMs) instead of position by position: much
+        faster for long prompts, and the same run within the 1e-5 rule
+        rather than bit for bit."""
         import torch
 
         win = GPT2Window(self.cap, prompt, bos)
@@ -1540,9 +1595,13 @@ class GPT2Device:
             draws = torch.from_numpy(d.view(np.int64)).to(dev)
         torch.cuda.synchronize()
         ctx.sync()
-        # prime: positions 0 .. n0 - 1 (the head only after the last)
-        for p in range(n0 - 1):
-            ctx.check(lib().fh_gpt2_stack_forward_async(ctx.h, self.stack, hist.data_ptr() + 4 * p, p, _ptr(self.x)))
+        # prime: positions 0 .. n0 - 2 (the last prompt position is the first step's)
+        if prefill and n0 > 1:
+            self.prefill_async(hist, 0, n0 - 1)
+        else:
+            for p in range(n0 - 1):
+                ctx.check(lib().fh_gpt2_stack_forward_async(ctx.h, self.stack, hist.data_ptr() + 4 * p, p,
+                                                            _ptr(self.x)))
         for k in range(max_tokens):
             p = n0 - 1 + k
             self.feed_async(hist.data_ptr() + 4 * p, p)

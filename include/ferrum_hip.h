@@ -367,6 +367,16 @@ int fh_add_async(fh_ctx* ctx, float* d_x, const float* d_y, size_t n);
  * 16, 32, 64, 128 -> FH_ERR_LIMIT. */
 int fh_attention_decode_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
                               size_t capacity, size_t d, size_t heads, size_t pos, float* d_out);
+/* The same for a block of `rows` consecutive positions pos0 .. pos0 + rows - 1
+ * of one sequence (a prompt fed at once instead of position by position, as
+ * CachedTransformer::feed does one token at a time, slm/cached.rs:100-125):
+ * row r of qkv ([rows, 3d]) is position pos0 + r; every row's k and v go to
+ * the caches first, then row r attends over rows 0 .. pos0 + r.  The same
+ * per-row arithmetic as fh_attention_decode_async (within the 1e-5 rule: the
+ * chunking of the positions may differ).  pos0 + rows > capacity ->
+ * FH_ERR_DIM ("KvCache full"); rows <= 65535. */
+int fh_attention_prefill_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
+                               size_t capacity, size_t d, size_t heads, size_t pos0, size_t rows, float* d_out);
 
 /* ---- packed per-row int8 / int4 weights: ops::qlinear (ops.rs:268-377) ------
  * QWeight (quant.rs:130-217): k rows (input features) x n columns (outputs),

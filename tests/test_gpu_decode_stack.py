@@ -101,6 +101,29 @@ def test_gpt2_124m_stack_agrees_with_per_op_path(fh, orc, g124):
         assert_scores_close(a[p], b[p], f"position {p}")
 
 
+def test_gpt2_medium_stack_agrees_with_per_op_path(fh):
+    """The d = 1024 instance (GPT-2-medium: 24 blocks, 16 heads, FFN 4096;
+    N(0, 0.02) weights made on the device): the stack against the
+    one-launch-per-op path over 70 positions (two attention items per head at
+    the end)."""
+    import torch
+
+    import ferrum_hip
+
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(17)
+    m = ferrum_hip.GPT2Device.random(fh, 50257, 1024, 16, 24, 4096, 256, gen)
+    try:
+        assert m.stack is not None
+        ids = np.random.default_rng(8).integers(0, 50257, 70)
+        a = [feed(m, t, p, True) for p, t in enumerate(ids)]
+        b = [feed(m, t, p, False) for p, t in enumerate(ids)]
+        for p in (0, 1, 31, 63, 64, 65, 69):
+            assert_scores_close(a[p], b[p], f"medium, position {p}")
+    finally:
+        m.free()
+
+
 def test_stack_replays_in_a_graph(fh, orc, tiny_pair):
     """The launch counters advance per replay: replays of a captured step give
     the eager result, with eager work between them."""
@@ -173,26 +196,14 @@ def test_a_failed_stack_exchange_is_reported_and_recovered(fh, orc, tiny_pair):
 CONFIG3 = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
 
 
-def test_config3_run_replays_on_the_oracle(fh, orc, g124):
-    """BASELINE configs[2] end to end: GPT-2-124M (N(0, 0.02) Q8_0 weights), a
-    128-token random prompt, then 32 steps sampled with temperature 0.8,
-    top-k 40, top-p 0.95 and repetition penalty 1.1 over the window, the draws
-    from Rng (slm/token_stream.rs:66-190, slm/cached.rs:100-137).  The
-    device-resident run (GPT2Device.generate: the sampler's id feeds the next
-    step on the device) equals the host loop over forward() id for id, and
-    every step replays on the oracle's model and sampler with the same window
-    and draw; a differing id must be one the oracle reports within the
-    sampler's margins, and the replay continues from the device's id."""
+def replay_config3(orc, w, prompt, ids):
+    """Every step of a config-3 run replayed on the oracle's model and sampler
+    with the same window and draw; a differing id must be one the oracle
+    reports within the sampler's margins, and the replay continues from the
+    device's id.  Returns the number of such steps."""
     import ferrum_hip
     from sampler_margins import exempt
 
-    w, m = g124
-    prompt = [int(t) for t in np.random.default_rng(128).integers(0, G124["vocab"], 128)]
-    params = ferrum_hip.SamplingParams(**CONFIG3)
-    ids = m.generate(prompt, 32, params, ferrum_hip.Rng(11))
-    assert len(ids) == 32
-    host = ferrum_hip.gpt2_decode(fh, m.forward, prompt, 32, params, ferrum_hip.Rng(11), G124["ctx"])
-    assert host == ids
     ref = gpt2_tiny.OracleGPT2(orc, w, **{k: G124[k] for k in ("vocab", "d", "heads", "layers", "ffn")},
                                ctx=G124["ctx"])
     win, rng, op = ferrum_hip.GPT2Window(G124["ctx"], prompt), orc.Rng(11), orc.SamplingParams(**CONFIG3)
@@ -205,5 +216,103 @@ def test_config3_run_replays_on_the_oracle(fh, orc, g124):
             n_exempt += 1
         win.push(tok)
         z = ref.forward(win.ids, False)
+    return n_exempt
+
+
+def test_config3_run_replays_on_the_oracle(fh, orc, g124):
+    """BASELINE configs[2] end to end: GPT-2-124M (N(0, 0.02) Q8_0 weights), a
+    128-token random prompt, then 32 steps sampled with temperature 0.8,
+    top-k 40, top-p 0.95 and repetition penalty 1.1 over the window, the draws
+    from Rng (slm/token_stream.rs:66-190, slm/cached.rs:100-137).  The
+    device-resident run (GPT2Device.generate: the sampler's id feeds the next
+    step on the device) equals the host loop over forward() id for id, and
+    every step replays on the oracle (replay_config3)."""
+    import ferrum_hip
+
+    w, m = g124
+    prompt = [int(t) for t in np.random.default_rng(128).integers(0, G124["vocab"], 128)]
+    params = ferrum_hip.SamplingParams(**CONFIG3)
+    ids = m.generate(prompt, 32, params, ferrum_hip.Rng(11))
+    assert len(ids) == 32
+    host = ferrum_hip.gpt2_decode(fh, m.forward, prompt, 32, params, ferrum_hip.Rng(11), G124["ctx"])
+    assert host == ids
+    n_exempt = replay_config3(orc, w, prompt, ids)
     print(f"config-3 run: 32 steps, {n_exempt} exempt")
     assert n_exempt <= 2
+
+
+def test_config3_run_with_prefill_replays_on_the_oracle(fh, orc, g124):
+    """The same run with the prompt primed in one pass (generate(prefill=True):
+    127 positions as rows of GEMMs and one attention launch per block): every
+    step replays on the oracle within the sampler's margins."""
+    import ferrum_hip
+
+    w, m = g124
+    prompt = [int(t) for t in np.random.default_rng(128).integers(0, G124["vocab"], 128)]
+    ids = m.generate(prompt, 32, ferrum_hip.SamplingParams(**CONFIG3), ferrum_hip.Rng(11), prefill=True)
+    assert len(ids) == 32
+    n_exempt = replay_config3(orc, w, prompt, ids)
+    print(f"config-3 run with prefill: 32 steps, {n_exempt} exempt")
+    assert n_exempt <= 2
+
+
+def prefill(model, ids, pos0):
+    import torch
+
+    d_ids = torch.tensor(np.asarray(ids, np.int32), device="cuda")
+    torch.cuda.synchronize()
+    model.prefill_async(d_ids, pos0, len(ids))
+    model.ctx.sync()
+    torch.cuda.synchronize()
+    return model.z.cpu().numpy().copy()
+
+
+def test_tiny_prefill_matches_oracle(fh, orc, tiny_pair):
+    """A 150-position prompt as one block of rows, and as two (100 + 50: the
+    second block's attention reads the first's cache rows): the last
+    position's scores against the oracle fed position by position
+    (CachedTransformer::feed), and the next position through the stack and
+    through the per-op path, reading the caches the prefill filled."""
+    w, m = tiny_pair
+    ref = gpt2_tiny.OracleGPT2(orc, w)
+    ids = np.random.default_rng(31).integers(0, gpt2_tiny.VOCAB, 151)
+    want = [ref.feed(t) for t in ids]
+    assert_scores_close(prefill(m, ids[:150], 0), want[149], "one block of 150")
+    assert_scores_close(feed(m, ids[150], 150, True), want[150], "stack after the prefill")
+    assert_scores_close(prefill(m, ids[:100], 0), want[99], "first block of 100")
+    assert_scores_close(prefill(m, ids[100:150], 100), want[149], "second block of 50")
+    assert_scores_close(feed(m, ids[150], 150, False), want[150], "per-op after two blocks")
+    assert_scores_close(prefill(m, ids[:1], 0), want[0], "a block of one")
+
+
+def test_prefill_errors(fh, tiny_pair):
+    import torch
+
+    import ferrum_hip
+
+    _, m = tiny_pair
+    d_ids = torch.zeros(8, dtype=torch.int32, device="cuda")
+    with pytest.raises(ferrum_hip.DimMismatch, match="KvCache full"):
+        m.prefill_async(d_ids, gpt2_tiny.CTX - 4, 8)
+    with pytest.raises(ferrum_hip.DimMismatch, match="KvCache full"):
+        ferrum_hip.attention_prefill_async(fh, m.qkv, m.blocks[0]["k"], m.blocks[0]["v"], gpt2_tiny.CTX,
+                                           gpt2_tiny.D, gpt2_tiny.HEADS, gpt2_tiny.CTX - 1, 2, m.att)
+    with pytest.raises(ferrum_hip.DimMismatch, match="must divide"):
+        ferrum_hip.attention_prefill_async(fh, m.qkv, m.blocks[0]["k"], m.blocks[0]["v"], gpt2_tiny.CTX,
+                                           gpt2_tiny.D, 3, 0, 1, m.att)
+    m.prefill_async(d_ids, 0, 0)  # nothing to do
+    fh.sync()
+
+
+def test_gpt2_124m_prefill_matches_oracle(fh, orc, g124):
+    """GPT-2-124M: a 128-position prompt in one block (every GEMM at m = 128,
+    two attention items per head for the last rows), its last scores against
+    the oracle's, then three stack positions on from the prefilled caches."""
+    w, m = g124
+    ref = gpt2_tiny.OracleGPT2(orc, w, **{k: G124[k] for k in ("vocab", "d", "heads", "layers", "ffn")},
+                               ctx=G124["ctx"])
+    ids = np.random.default_rng(12).integers(0, G124["vocab"], 131)
+    want = [ref.feed(t) for t in ids]
+    assert_scores_close(prefill(m, ids[:128], 0), want[127], "124M prefill of 128")
+    for p in range(128, 131):
+        assert_scores_close(feed(m, ids[p], p, True), want[p], f"124M stack at {p} after the prefill")
