@@ -326,6 +326,17 @@ __device__ __forceinline__ void layer_norm(const float* x, const LnParams<D>& lp
     __syncthreads();
 }
 
+// Max over the 64 lanes of a wave, every lane getting it: DPP within 16-lane
+// rows (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then
+// the four rows by readlane.
+__device__ __forceinline__ float group_max64(float v) {
+    v = fmaxf(v, fh::dpp<0xB1>(v));
+    v = fmaxf(v, fh::dpp<0x4E>(v));
+    v = fmaxf(v, fh::dpp<0x141>(v));
+    v = fmaxf(v, fh::dpp<0x140>(v));
+    return fmaxf(fmaxf(fh::rdlane(v, 0), fh::rdlane(v, 16)), fmaxf(fh::rdlane(v, 32), fh::rdlane(v, 48)));
+}
+
 // One attention item: head h, cached positions [j0, j0 + kPos) of 0 .. pos.
 // Thread t scores position t / TPP over HD / TPP dims of the head and holds,
 // for the V sum, dim t % HD of positions t / HD, t / HD + kT / HD, ...
@@ -356,40 +367,37 @@ struct AttnItem {
     }
 
     // qkv: this head's [q | k_new | v_new] (3 HD floats, LDS); writes (max,
-    // sum of exp, weighted V sum) of the item to `out` (HD + 2 slots).
-    __device__ __forceinline__ void compute(const float* qkv, int j0, int pos, float scale, float* sc, float* acc,
-                                            float* stat, u64* __restrict__ out, unsigned tag, bool publish) {
-        const int tid = threadIdx.x, len = pos + 1, jn = min(kPos, len - j0);
+    // sum of exp, weighted V sum) of the item to `out` (HD + 2 slots).  sc:
+    // kPos scores; esc: kWaves x kPos (each wave's own copy of the weights);
+    // acc: kT floats.  Two barriers: the scores, then the V partial sums.
+    __device__ __forceinline__ void compute(const float* qkv, int j0, int pos, float scale, float* sc, float* esc,
+                                            float* acc, u64* __restrict__ out, unsigned tag, bool publish) {
+        const int tid = threadIdx.x, lane = tid & 63, len = pos + 1, jn = min(kPos, len - j0);
         const int jl = tid / TPP, qt = tid % TPP;
         const bool fresh = j0 + jl >= pos;  // position pos (or past it, masked): the new k row
         float dot = 0.0f;
 #pragma unroll
         for (int i = 0; i < QD; i++) dot += qkv[qt * QD + i] * (fresh ? qkv[HD + qt * QD + i] : kr[i]);
-#pragma unroll
-        for (int off = 1; off < TPP; off <<= 1) dot += __shfl_xor(dot, off, 64);
+        dot = fh::group_sum<TPP>(dot);
         if (qt == 0) sc[jl] = jl < jn ? dot * scale : -INFINITY;
         __syncthreads();
-        if (tid < 64) {
-            const float s = sc[tid];
-            float mx = s;
-#pragma unroll
-            for (int off = 32; off > 0; off >>= 1) mx = fmaxf(mx, __shfl_xor(mx, off, 64));
-            const float e = tid < jn ? expf(s - mx) : 0.0f;
-            sc[tid] = e;
-            const float se = fh::group_total<64>(e);
-            if (tid == 0) {
-                stat[0] = mx;
-                stat[1] = se;
-            }
-        }
-        __syncthreads();
+        // every wave forms the chunk's max and exponentials itself (no
+        // barrier between the softmax and the V sum); kPos == 64: lane j
+        // holds position j
+        const float s = sc[lane];
+        const float mx = group_max64(s);
+        const float e = lane < jn ? expf(s - mx) : 0.0f;
+        const float se = fh::group_total<64>(e);
+        float* ew = esc + (tid >> 6) * kPos;
+        ew[lane] = e;
+        __builtin_amdgcn_wave_barrier();
         const int dv = tid % HD, g = tid / HD;
         float o = 0.0f;
 #pragma unroll
         for (int i = 0; i < VP; i++) {
             const int jc = g + i * VG;
             const float v = j0 + jc >= pos ? qkv[2 * HD + dv] : vr[i];
-            if (jc < jn) o += sc[jc] * v;
+            if (jc < jn) o += ew[jc] * v;
         }
         acc[tid] = o;
         __syncthreads();
@@ -400,10 +408,11 @@ struct AttnItem {
             cstore64(out + 2 + tid, tagged(r, tag));
         }
         if (tid == 0 && publish) {
-            cstore64(out, tagged(stat[0], tag));
-            cstore64(out + 1, tagged(stat[1], tag));
+            cstore64(out, tagged(mx, tag));
+            cstore64(out + 1, tagged(se, tag));
         }
-        __syncthreads();
+        // (no trailing barrier: every later write to sc, esc, acc or the
+        // q|k|v buffer comes after at least one more barrier)
     }
 };
 
@@ -418,7 +427,8 @@ __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
     __shared__ __align__(16) float xres[D];  // the residual stream (every workgroup's own copy)
     __shared__ __align__(16) float hbuf[F];  // LayerNorm output / merged attention / up outputs
     __shared__ __align__(16) float hq[3 * HD];
-    __shared__ float sc[kPos], acc[kT], stat[2], red[2 * kWaves];
+    __shared__ float sc[kPos], esc[kWaves * kPos], acc[kT], red[2 * kWaves];
+    static_assert(kPos == 64, "the softmax maps lane j to position j");
     extern __shared__ __align__(16) float part[];  // polled attention partials [H][nch][HD + 2], then [H][nch] factors
     float* fac = part + H * a.nch_max * kAttnSlots;
 
@@ -501,7 +511,7 @@ __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
                 gstore(B.kc + static_cast<size_t>(pos) * D + h * HD + tid, hq[HD + tid]);
                 gstore(B.vc + static_cast<size_t>(pos) * D + h * HD + tid, hq[2 * HD + tid]);
             }
-            ai.compute(hq, j0, pos, scale, sc, acc, stat, s_att + static_cast<size_t>(it) * kAttnSlots, tag, pub);
+            ai.compute(hq, j0, pos, scale, sc, esc, acc, s_att + static_cast<size_t>(it) * kAttnSlots, tag, pub);
         }
 
         // ---- out projection: merge every item (head by head), then the GEMV
@@ -579,12 +589,18 @@ struct fh_gpt2_stack {
 
 namespace {
 
-// The workgroups one launch uses: 64, all resident at once (one per CU).
-constexpr int kGrid = 64;
+// The workgroups one launch uses, all resident at once (one per CU): fewer
+// workgroups make each exchange cheaper (fewer pollers), more make each
+// phase's GEMV slice smaller.  At d = 768, 48 give every wave whole passes of
+// rows (Q|K|V 6 rows, up 8, out and down 2: no more VALU work per lane than
+// 64) and one attention item per workgroup at position 255 (12 heads x 4
+// items); measured 194 us per position against 204 us with 64 and 294 us with
+// 32.  At d = 1024, 48 would add a Q|K|V pass per wave: 64.
+constexpr int grid_for(int d) { return d == 768 ? 48 : 64; }
 
 template <int D, int HD>
 const void* stack_kernel() {
-    return reinterpret_cast<const void*>(k_gpt2_stack<D, HD, kGrid>);
+    return reinterpret_cast<const void*>(k_gpt2_stack<D, HD, grid_for(D)>);
 }
 
 }  // namespace
@@ -642,13 +658,14 @@ int fh_gpt2_stack_create(fh_ctx* ctx, const fh_gpt2_block* blocks, size_t layers
     if (hipGetDevice(&cur) != hipSuccess || cur != ctx->device) FH_HIP(ctx, hipSetDevice(ctx->device));
     const int nch = static_cast<int>((capacity + kPos - 1) / kPos);
     const size_t dyn = static_cast<size_t>(heads) * nch * (hd + 3) * sizeof(float);
+    const int grid = grid_for(static_cast<int>(d));
     int per_cu = 0;
     FH_HIP(ctx, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kT, dyn));
-    if (per_cu < 1 || static_cast<size_t>(per_cu) * ctx->num_cus < static_cast<size_t>(kGrid))
+    if (per_cu < 1 || static_cast<size_t>(per_cu) * ctx->num_cus < static_cast<size_t>(grid))
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_gpt2_stack_create: the device cannot hold the stack kernel's " +
-                                              std::to_string(kGrid) + " workgroups at once");
+                                              std::to_string(grid) + " workgroups at once");
     const size_t stride = 3 * d + heads * nch * (hd + 2) + d + ffn + d;
-    const size_t ebytes = fh_align256(kGrid * sizeof(unsigned));
+    const size_t ebytes = fh_align256(grid * sizeof(unsigned));
     const size_t sbytes = layers * stride * sizeof(u64);
     fh_gpt2_stack* s = new (std::nothrow) fh_gpt2_stack();
     if (!s) return fh_fail(ctx, FH_ERR_OOM, "fh_gpt2_stack_create: out of host memory");
@@ -693,7 +710,7 @@ int fh_gpt2_stack_create(fh_ctx* ctx, const fh_gpt2_block* blocks, size_t layers
     s->nch_max = nch;
     s->tok_w = d_tok_w;
     s->pos_w = d_pos_w;
-    s->grid = kGrid;
+    s->grid = grid;
     s->dyn_lds = dyn;
     s->kernel = kern;
     *out = s;
