@@ -326,6 +326,47 @@ __device__ __forceinline__ void layer_norm(const float* x, const LnParams<D>& lp
     __syncthreads();
 }
 
+// The residual update and LayerNorm in one pass: x += delta, y =
+// LayerNorm(x), with the same arithmetic as the residual add followed by
+// layer_norm.  Every thread reads its columns of x and delta (and column 0,
+// for the shift c0) before the reduction's barriers and writes its updated
+// columns of x after them, so no thread reads a column another has already
+// updated.  y may be delta (every read of it precedes the barriers).
+template <int D>
+__device__ __forceinline__ void add_layer_norm(float* x, const float* delta, const LnParams<D>& lp, float* y,
+                                               float* red) {
+    constexpr int PER = LnParams<D>::PER;
+    const int tid = threadIdx.x;
+    const float c0 = x[0] + delta[0];
+    float v[PER];
+    float s1 = 0.0f, s2 = 0.0f;
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = tid + i * kT;
+        const int cc = min(c, D - 1);
+        v[i] = x[cc] + delta[cc];
+        if (c < D) {
+            const float dv = v[i] - c0;
+            s1 += dv;
+            s2 += dv * dv;
+        }
+    }
+    block_total2(s1, s2, red);
+    const float m1 = s1 / static_cast<float>(D);
+    const float mean = c0 + m1;
+    const float var = fmaxf(s2 / static_cast<float>(D) - m1 * m1, 0.0f);
+    const float sd = sqrtf(var + 1e-5f);
+#pragma unroll
+    for (int i = 0; i < PER; i++) {
+        const int c = tid + i * kT;
+        if (c < D) {
+            x[c] = v[i];
+            y[c] = ((v[i] - mean) / sd) * lp.g[i] + lp.b[i];
+        }
+    }
+    __syncthreads();
+}
+
 // Max over the 64 lanes of a wave, every lane getting it: DPP within 16-lane
 // rows (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then
 // the four rows by readlane.
@@ -477,10 +518,10 @@ __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
         if (l > 0) {
             poll_into<(D + kT - 1) / kT>(a.slots + (l - 1) * stride + 3 * D + H * a.nch_max * kAttnSlots + D + F, D,
                                          tag, hbuf, wt);
-            for (int c = tid; c < D; c += kT) xres[c] = xres[c] + hbuf[c];
-            __syncthreads();
+            add_layer_norm<D>(xres, hbuf, ln1, hbuf, red);
+        } else {
+            layer_norm<D>(xres, ln1, hbuf, red);
         }
-        layer_norm<D>(xres, ln1, hbuf, red);
         wqkv.template compute<false>(hbuf, s_qkv, tag, gw, pub);
 
         // ---- attention items; the out projection's weights are issued first
@@ -544,9 +585,7 @@ __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
         // ---- up (+GELU): residual += attention output, LayerNorm 2
         wdown.issue(B.q[3], B.d[3], B.b[3], gw);
         poll_into<(D + kT - 1) / kT>(s_proj, D, tag, hbuf, wt);
-        for (int c = tid; c < D; c += kT) xres[c] = xres[c] + hbuf[c];
-        __syncthreads();
-        layer_norm<D>(xres, ln2, hbuf, red);
+        add_layer_norm<D>(xres, hbuf, ln2, hbuf, red);
         wup.template compute<true>(hbuf, s_up, tag, gw, pub);
 
         // ---- down; the next block's Q|K|V weights are issued first
