@@ -390,6 +390,13 @@ __global__ void __launch_bounds__(64 * WM * WN * KW)
 // only rounding beyond the f32 sums is the activations' 22-bit split.
 // Workgroup tile 256 x 256, eight waves of 128 x 64 (4 x 2 MFMA tiles), one
 // Q8_0 block per stage, two LDS stages of 72 KiB.
+// Activation staging pieces (4 values of a row's 32-value block) for the
+// large-m GEMM: each 64-piece group covers 8 rows x 8 pieces, 16 consecutive
+// lanes taking 8 rows x 2 adjacent pieces, so their 8-byte LDS stores (the
+// 144-byte row pitch) fall on disjoint banks of the 32.
+__device__ __forceinline__ int piece_row(int q) { return (q >> 6) * 8 + ((q & 15) >> 1); }
+__device__ __forceinline__ int piece_col(int q) { return ((q & 63) >> 4) * 2 + (q & 1); }
+
 template <int BM, int BN, int WM, int WN, bool FROM_X>
 __global__ void __launch_bounds__(64 * WM * WN)
     k_gemm_wsplit(const uint4* __restrict__ panel, const float* __restrict__ xinv, const uint8_t* __restrict__ xbad,
@@ -416,7 +423,9 @@ __global__ void __launch_bounds__(64 * WM * WN)
 
     // This thread's weight half-row (rows past n repeat row n - 1: their
     // output columns are never stored, and a column depends only on its row).
-    const int jr = tid >> 1, jhalf = tid & 1;
+    // (lanes 8t .. 8t + 7 take eight consecutive rows, one half each: their
+    // 16-byte LDS stores fall on disjoint banks)
+    const int jr = ((tid >> 4) << 3) | (tid & 7), jhalf = (tid >> 3) & 1;
     const int jw = min(j0 + jr, n - 1);
     const int8_t* wsrc = qs + static_cast<size_t>(jw) * k + jhalf * 16;
     const uint16_t* dsrc = dsc + static_cast<size_t>(jw) * kb;
@@ -434,10 +443,10 @@ __global__ void __launch_bounds__(64 * WM * WN)
         const int i0x = (tile / tiles_n) * BM;
 #pragma unroll
         for (int p = 0; p < XP; p++) {
-            const int r = (tid + NTH * p) / 8, i = min(i0x + r, m - 1);  // rows past m: clamped, never stored
+            const int r = piece_row(tid + NTH * p), i = min(i0x + r, m - 1);  // rows past m: clamped, never stored
             // 2^e from the stored 2^-e (both exact powers of two)
             xsc[p] = __builtin_bit_cast(float, (254u << 23) - __builtin_bit_cast(uint32_t, xinv[i0x + r]));
-            xrow[p] = x + static_cast<size_t>(i) * k + ((tid + NTH * p) % 8) * 4;
+            xrow[p] = x + static_cast<size_t>(i) * k + piece_col(tid + NTH * p) * 4;
         }
     }
     u4 ra[AP], rq;
@@ -469,7 +478,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
                 r01.y = finite(sv.y) ? r01.y : 0.0f;
                 r23.x = finite(sv.z) ? r23.x : 0.0f;
                 r23.y = finite(sv.w) ? r23.y : 0.0f;
-                char* rowp = st + (piece / 8) * kArow * 2 + (piece % 8) * 8;
+                char* rowp = st + piece_row(piece) * kArow * 2 + piece_col(piece) * 8;
                 *reinterpret_cast<uint2*>(rowp) =
                     make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
                 *reinterpret_cast<uint2*>(rowp + 64) =
@@ -526,24 +535,44 @@ __global__ void __launch_bounds__(64 * WM * WN)
             wl[c][0] = *reinterpret_cast<const h8*>(q + 32);
             wl[c][1] = *reinterpret_cast<const h8*>(q + 48);
         }
+        auto mfma_rows = [&](int r0, int r1) __attribute__((always_inline)) {
 #pragma unroll
-        for (int r = 0; r < TM; r++) {
-            const _Float16* a = As + ((wm * TM + r) * 32 + arow) * kArow + koff;
-            const h8 ah0 = *reinterpret_cast<const h8*>(a), ah1 = *reinterpret_cast<const h8*>(a + 16);
-            const h8 al0 = *reinterpret_cast<const h8*>(a + 32), al1 = *reinterpret_cast<const h8*>(a + 48);
+            for (int r = r0; r < r1; r++) {
+                const _Float16* a = As + ((wm * TM + r) * 32 + arow) * kArow + koff;
+                const h8 ah0 = *reinterpret_cast<const h8*>(a), ah1 = *reinterpret_cast<const h8*>(a + 16);
+                const h8 al0 = *reinterpret_cast<const h8*>(a + 32), al1 = *reinterpret_cast<const h8*>(a + 48);
 #pragma unroll
-            for (int c = 0; c < TN; c++) {
-                f16x p = acc[r][c];
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wh[c][0], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wl[c][0], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, wh[c][0], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wh[c][1], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wl[c][1], p, 0, 0, 0);
-                p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, wh[c][1], p, 0, 0, 0);
-                acc[r][c] = p;
+                for (int c = 0; c < TN; c++) {
+                    f16x p = acc[r][c];
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wh[c][0], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wl[c][0], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, wh[c][0], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wh[c][1], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wl[c][1], p, 0, 0, 0);
+                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, wh[c][1], p, 0, 0, 0);
+                    acc[r][c] = p;
+                }
             }
+        };
+        // The next block's split and stores go between the two halves of
+        // this block's MFMAs (its loads have landed by then; the other LDS
+        // buffer is free since the last barrier), unconditionally, so they
+        // share a scheduling region with the MFMAs (at the last block they
+        // rewrite the unused buffer with the same block, before the barrier
+        // that precedes the epilogue's use of the LDS), and the scheduler
+        // interleaves them with the second half: per MFMA eight VALU
+        // operations, every other MFMA one LDS store.  (Measured: 31.8 ->
+        // 30.7 ms for the GPT-2-medium prefill; the same order without the
+        // interleave, 32.1 ms.)
+        mfma_rows(0, TM / 2);
+        store(buf ^ 1);
+        mfma_rows(TM / 2, TM);
+#pragma unroll
+        for (int i = 0; i < TM / 2 * TN * 6; i++) {
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
+            if (i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
         }
-        if (b + 1 < kb) store(buf ^ 1);
         __syncthreads();
     }
 
