@@ -660,6 +660,15 @@ __device__ __forceinline__ unsigned long long wave_sort_desc(unsigned long long 
     return bitonic_merge<64>(k);
 }
 
+// The 64 largest of two waves of keys, sorted descending: a descending and an
+// ascending run form a bitonic sequence whose lane-wise maxima are its upper
+// half (the 64 largest), and one bitonic merge sorts them.
+__device__ __forceinline__ unsigned long long wave_top64(unsigned long long a, unsigned long long b) {
+    a = wave_sort_desc(a, 64);
+    b = ~wave_sort_desc(~b, 64);  // ascending (complements reverse the order)
+    return bitonic_merge<64>(a > b ? a : b);
+}
+
 // Running f32 sum over lanes 0..len-1 in lane order (the reference's
 // sequential order): lane c gets the sum of lanes 0..c.  Each step is one
 // readlane and one dependent add; no branches.
@@ -1367,7 +1376,6 @@ __global__ void __launch_bounds__(kT)
     const bool use_p = P.top_p < 1.0f;
     if (use_k || use_p) {
         // ---- 4./5. bucket histograms, then the gathered survivors --------------------
-        st.visit([&](float p, int i) { cstore(&prow[i], p); });  // for the general path
         const int ktop = key12(pmax);
         const int copy = tid & (kCopies - 1);
         for (int i = tid; i < kCopies * kBuckets; i += kT) {
@@ -1421,6 +1429,15 @@ __global__ void __launch_bounds__(kT)
         if (tid == 0) s.bi[0] = bucket_depth(s.hist[0], s.mass[0], P.top_k, P.top_p, use_k, use_p);
         __syncthreads();
         const int depth = s.bi[0];
+        // The row's p values (pbuf) feed workgroup 0's general path, which
+        // runs when no bucket qualifies (depth < 0, known to every segment)
+        // or, with top-p alone, when the cut lies below the gathered ids;
+        // with top-k the gathered survivors always suffice (after a failed
+        // exchange the general path may read stale values: a wrong id, never
+        // an out-of-bounds read, and the failure is reported).  So they are
+        // written only when they may be read -- not before the histogram
+        // exchange, where 200 KB of device-coherent stores delayed it.
+        if (depth < 0 || !use_k) st.visit([&](float p, int i) { cstore(&prow[i], p); });
         if (depth >= 0) {
             // append this segment's survivors to the row's list, one atomic per wave
             st.visit([&](float p, int i) {
@@ -1461,6 +1478,32 @@ __global__ void __launch_bounds__(kT)
                 }
                 __syncthreads();
                 done = s.bi[2];
+            } else if (use_k && P.top_k <= 64 && nc <= 256) {
+                // Top-k keeps only ids at or above the k-th largest p, so the
+                // 64 largest keys suffice unless the 64th still ties that p:
+                // reduce up to 256 gathered keys to their top 64 in one wave
+                // (registers, no barriers) and finish there; else the block
+                // path below.
+                if (tid < 64) {
+                    unsigned long long q1 = tid + 64 < nc ? cload(&rs->cand[tid + 64]) : 0ull;
+                    unsigned long long t = wave_top64(key, q1);
+                    if (nc > 128) {
+                        const unsigned long long q2 = tid + 128 < nc ? cload(&rs->cand[tid + 128]) : 0ull;
+                        const unsigned long long q3 = tid + 192 < nc ? cload(&rs->cand[tid + 192]) : 0ull;
+                        t = wave_top64(t, wave_top64(q2, q3));
+                    }
+                    const float thr = __builtin_bit_cast(float, rlu(static_cast<unsigned>(t >> 32), P.top_k - 1));
+                    const bool fits = __builtin_bit_cast(float, rlu(static_cast<unsigned>(t >> 32), 63)) < thr;
+                    const bool ok = fits && wave_tail(t, 64, P.top_k, P.top_p, use_k, use_p, r, o);
+                    if (tid == 0) s.bi[2] = ok;
+                }
+                __syncthreads();
+                done = s.bi[2];
+                if (!done) {
+                    for (int i = tid; i < nc; i += kT) s.u.cand[i] = cload(&rs->cand[i]);
+                    __syncthreads();
+                    n_list = replay_list(s, nc, P.top_k, P.top_p, use_k, use_p);
+                }
             } else {
                 for (int i = tid; i < nc; i += kT) s.u.cand[i] = cload(&rs->cand[i]);
                 __syncthreads();

@@ -340,3 +340,32 @@ def test_split_rows_replay_in_a_graph(fh, orc):
                         ferrum_hip.sample_rows(fh, lg, params, recents, draws, kind)  # eager work between replays
                 finally:
                     fh.set_stream(None)
+
+
+@pytest.mark.parametrize("crowd,spread", [(100, 0.04), (200, 0.04), (400, 0.005)])
+def test_top_k_with_a_crowded_top(fh, orc, crowd, spread):
+    """Rows whose top holds `crowd` ids within `spread` of each other gather
+    about 100, 80-100 and 400 survivors for a top-k of 40 (the 1/8-octave
+    bucket holding the 40th largest p is crowded): up to 256 the kernel
+    reduces them to their top 64 in one wave, past that (or when ties reach
+    the 64th) it sorts them in LDS.  Every id against the oracle, with top-p on and off, raw logits and
+    the GPT-2 bridge; a second set of rows has 80 exactly equal values at the
+    top (the tie fallback)."""
+    import ferrum_hip
+
+    rows, vocab = 6, 50257
+    rng = np.random.default_rng(crowd)
+    lg = (rng.standard_normal((rows, vocab)) - 3.0).astype(np.float32)
+    for r in range(rows):
+        ids = rng.choice(vocab, size=crowd, replace=False)
+        lg[r, ids] = 4.0 + rng.uniform(0.0, spread, size=crowd).astype(np.float32)
+    for kw in (dict(temperature=1.0, top_k=40), dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1),
+               dict(temperature=1.0, top_k=64, top_p=0.5)):
+        recents = [list(rng.integers(0, vocab, size=64)) for _ in range(rows)]
+        run_and_compare(fh, orc, lg, kw, recents)
+        run_and_compare(fh, orc, lg, kw, recents, kind=ferrum_hip.LOGITS_GPT2_SOFTMAX)
+    tie = (rng.standard_normal((rows, vocab)) - 3.0).astype(np.float32)
+    for r in range(rows):
+        tie[r, rng.choice(vocab, size=80, replace=False)] = 4.0
+    run_and_compare(fh, orc, tie, dict(temperature=1.0, top_k=40))
+    run_and_compare(fh, orc, tie, dict(temperature=1.0, top_k=40, top_p=0.9))
