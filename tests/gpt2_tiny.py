@@ -32,6 +32,27 @@ def make_weights(orc, seed=11, vocab=VOCAB, d=D, layers=LAYERS, ffn=FFN, ctx=CTX
     return w
 
 
+def make_config1_weights(orc, seed=1):
+    """BASELINE configs[0] as its random init: every matrix (Q8_0, including
+    the tied token table) and the position table from N(0, 0.02), LayerNorm
+    gamma 1 and beta 0, biases 0."""
+    rng = np.random.default_rng(seed)
+
+    def q8(n, k):
+        return orc.q8_0_encode((rng.standard_normal(n * k) * 0.02).astype(np.float32))
+
+    ones, zeros = (lambda n: np.ones(n, np.float32)), (lambda n: np.zeros(n, np.float32))
+    w = {"token_embd_q8": q8(VOCAB, D),
+         "position_embd": (rng.standard_normal((CTX, D)) * 0.02).astype(np.float32),
+         "lnf_g": ones(D), "lnf_b": zeros(D)}
+    for i in range(LAYERS):
+        w.update({f"blk{i}.ln1_g": ones(D), f"blk{i}.ln1_b": zeros(D), f"blk{i}.ln2_g": ones(D),
+                  f"blk{i}.ln2_b": zeros(D), f"blk{i}.qkv_q8": q8(3 * D, D), f"blk{i}.qkv_b": zeros(3 * D),
+                  f"blk{i}.out_q8": q8(D, D), f"blk{i}.out_b": zeros(D), f"blk{i}.up_q8": q8(FFN, D),
+                  f"blk{i}.up_b": zeros(FFN), f"blk{i}.down_q8": q8(D, FFN), f"blk{i}.down_b": zeros(D)})
+    return w
+
+
 class OracleGPT2:
     """The decode on the oracle: every piece is the C restatement."""
 

@@ -351,3 +351,44 @@ def test_tiny_gpt2_sampled_decode_replays_on_the_oracle(fh, orc, tiny):
             break
         reprime = win.push(tok)
         z = ref.forward(win.ids, reprime)
+
+
+def test_config1_greedy_run_on_the_device(fh, orc):
+    """BASELINE configs[0] as configured: the tiny GPT-2 with N(0, 0.02) random
+    init (gpt2_tiny.make_config1_weights), a 16-token prompt of uniform random
+    ids, 64 greedy tokens -- run with every step on the device
+    (GPT2Device.generate: the one-launch stack, the head and the fused
+    sampler) and through the host loop over forward().  Both runs agree, and
+    every step's id is the oracle's greedy id on the same window unless the
+    oracle's top-2 gap there is below 1e-5 (then the runs may part; the steps
+    checked before that are counted)."""
+    import ferrum_hip
+
+    w = gpt2_tiny.make_config1_weights(orc, seed=1)
+    model = ferrum_hip.GPT2Device.from_weights(fh, w, gpt2_tiny.VOCAB, gpt2_tiny.D, gpt2_tiny.HEADS,
+                                               gpt2_tiny.LAYERS, gpt2_tiny.FFN, gpt2_tiny.CTX)
+    try:
+        assert model.stack is not None
+        prompt = [int(t) for t in np.random.default_rng(16).integers(0, gpt2_tiny.VOCAB, 16)]
+        greedy = ferrum_hip.SamplingParams(temperature=0.0)
+        dev = model.generate(prompt, 64, greedy, ferrum_hip.Rng(1))
+        host = ferrum_hip.gpt2_decode(fh, model.forward, prompt, 64, greedy, ferrum_hip.Rng(1), gpt2_tiny.CTX)
+        assert len(dev) == 64 and dev == host
+        ref = gpt2_tiny.OracleGPT2(orc, w)
+        win = ferrum_hip.GPT2Window(gpt2_tiny.CTX, prompt)
+        z = ref.forward(win.ids, True)
+        checked = 0
+        for step, tok in enumerate(dev):
+            p = orc.ln_bridge(orc.softmax_rows(z)[0])
+            want = int(np.argmax(p))
+            if want != tok:
+                top2 = np.sort(p)[-2:]
+                assert top2[1] - top2[0] < 1e-5, (step, tok, want)
+                break
+            checked += 1
+            reprime = win.push(tok)
+            z = ref.forward(win.ids, reprime)
+        print(f"config-1 greedy run: {checked} of 64 steps equal to the oracle's before any near-tie")
+        assert checked >= 8
+    finally:
+        model.free()
