@@ -472,12 +472,11 @@ __global__ void __launch_bounds__(64 * WM * WN)
                 const f4 sv = __builtin_bit_cast(f4, ra[p]) * xsc[p];  // exact (power of two)
                 const f2 s01 = {sv.x, sv.y}, s23 = {sv.z, sv.w};
                 const h2 h01 = __builtin_convertvector(s01, h2), h23 = __builtin_convertvector(s23, h2);
-                f2 r01 = {sv.x - static_cast<float>(h01.x), sv.y - static_cast<float>(h01.y)};
-                f2 r23 = {sv.z - static_cast<float>(h23.x), sv.w - static_cast<float>(h23.y)};
-                r01.x = finite(sv.x) ? r01.x : 0.0f;
-                r01.y = finite(sv.y) ? r01.y : 0.0f;
-                r23.x = finite(sv.z) ? r23.x : 0.0f;
-                r23.y = finite(sv.w) ? r23.y : 0.0f;
+                // (no guard for inf / NaN: such a row's outputs are
+                // recomputed at the end, and an MFMA output row depends only
+                // on its own activation row)
+                const f2 r01 = {sv.x - static_cast<float>(h01.x), sv.y - static_cast<float>(h01.y)};
+                const f2 r23 = {sv.z - static_cast<float>(h23.x), sv.w - static_cast<float>(h23.y)};
                 char* rowp = st + piece_row(piece) * kArow * 2 + piece_col(piece) * 8;
                 *reinterpret_cast<uint2*>(rowp) =
                     make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
@@ -497,9 +496,9 @@ __global__ void __launch_bounds__(64 * WM * WN)
             const f2 w = {static_cast<float>(static_cast<int8_t>((word >> sh) & 0xFF)) * ds,
                           static_cast<float>(static_cast<int8_t>((word >> (sh + 8)) & 0xFF)) * ds};
             const h2 h = __builtin_convertvector(w, h2);
-            f2 r = {w.x - static_cast<float>(h.x), w.y - static_cast<float>(h.y)};
-            r.x = finite(w.x) ? r.x : 0.0f;
-            r.y = finite(w.y) ? r.y : 0.0f;
+            // (no guard: a weight row with a non-finite scale is flagged at
+            // upload and its output column recomputed at the end)
+            const f2 r = {w.x - static_cast<float>(h.x), w.y - static_cast<float>(h.y)};
             hi[t] = __builtin_bit_cast(uint32_t, h);
             lo[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, h2));
         }
