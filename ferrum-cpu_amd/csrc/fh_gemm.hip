@@ -753,6 +753,26 @@ __device__ __forceinline__ void split16(const float* v, float sc, h8& ah0, h8& a
     }
 }
 
+// Four activations times 2^e as packed f16 h and l (split16's arithmetic).
+template <bool SAFE>
+__device__ __forceinline__ void split4(const float* v, float sc, uint2& h, uint2& l) {
+    uint32_t hw[2], lw[2];
+#pragma unroll
+    for (int q = 0; q < 4; q += 2) {
+        const f2 s = {v[q] * sc, v[q + 1] * sc};
+        const h2 hh = __builtin_convertvector(s, h2);
+        f2 r = {s.x - static_cast<float>(hh.x), s.y - static_cast<float>(hh.y)};
+        if (SAFE) {
+            r.x = finite(s.x) ? r.x : 0.0f;
+            r.y = finite(s.y) ? r.y : 0.0f;
+        }
+        hw[q / 2] = __builtin_bit_cast(uint32_t, hh);
+        lw[q / 2] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, h2));
+    }
+    h = make_uint2(hw[0], hw[1]);
+    l = make_uint2(lw[0], lw[1]);
+}
+
 // Staging row of the skinny kernel: 32 floats + 4 pad, so the 16 lanes of a
 // ds_read_b128 pass (16 rows) land on distinct banks.
 constexpr int kSkinnyRow = 36;
@@ -785,11 +805,18 @@ __global__ void __launch_bounds__(512)
     const int b_begin = split * bps, b_end = min(kb, b_begin + bps);
     const int8_t* wrow[NT];
     const uint16_t* drow[NT];
+    // The outputs this thread stores at the end are all in column r32 of the
+    // tiles, so their bias and row flags load now, beside the first weights
+    // (loaded per output in the epilogue, each would cost a round trip).
+    float bias_c[NT];
+    bool bad_c[NT];
 #pragma unroll
     for (int c = 0; c < NT; c++) {
         const int j = min((tile * NT + c) * 32 + r32, n - 1);
         wrow[c] = qs + static_cast<size_t>(j) * k + half * 16;
         drow[c] = dsc + static_cast<size_t>(j) * kb;
+        bias_c[c] = bias ? bias[j] : 0.0f;
+        bad_c[c] = rexp[j] == kFhBadRowExp;
     }
     float* inv_lds = lds + kw * SLOT + wave * (MT * BPW * 32);  // this wave's row scales
     float* xst = lds + wave * SLOT;                              // this wave's staging rows
@@ -915,27 +942,35 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
             for (int v = 0; v < 16; v++) sums[wave * SLOT + ((t * NT + c) * 16 + v) * 64 + lane] = acc[t][c][v];
     __syncthreads();
-    // Output o = ((t * NT + c) * 16 + v) * 64 + l  ->  row, column.
+    // Output o = ((t * NT + c) * 16 + v) * 64 + l  ->  row, column; the loops
+    // below walk each (t, c) tile's 1024 outputs, so its bias and flag are
+    // picked at compile time, and o & 31 == r32 (blockDim.x is a multiple of 64).
     auto row_of = [](int o) { const int t = o / (NT * 1024), v = (o / 64) % 16, l = o % 64;
                               return t * 32 + (v / 4) * 8 + (l / 32) * 4 + (v % 4); };
-    auto col_of = [&](int o) { return (tile * NT + (o / 1024) % NT) * 32 + (o & 31); };
-    auto finish = [&](int i, int jj, float s) {
-        if (__builtin_expect(rexp[jj] == kFhBadRowExp, 0))
+    auto finish = [&](int o, float s, bool bad, float bv, int jj) {
+        const int i = row_of(o);
+        if (i >= m || jj >= n) return;
+        if (__builtin_expect(bad, 0))
             s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(jj) * k,
                           dsc + static_cast<size_t>(jj) * kb);
-        y[static_cast<size_t>(i) * n + jj] = bias ? s + bias[jj] : s;
+        y[static_cast<size_t>(i) * n + jj] = bias ? s + bv : s;
     };
     const size_t tiles = gridDim.x;
-    for (int o = threadIdx.x; o < OUT; o += blockDim.x) {
-        float s = sums[o];
-        for (int w = 1; w < kw; w++) s += sums[w * SLOT + o];
-        if (splits == 1) {
-            const int i = row_of(o), jj = col_of(o);
-            if (i < m && jj < n) finish(i, jj, s);
-        } else {
-            __hip_atomic_store(part + (split * tiles + tile) * OUT + o, s, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int c = 0; c < NT; c++) {
+            const int base = (t * NT + c) * 1024, jj = (tile * NT + c) * 32 + r32;
+            for (int o = base + static_cast<int>(threadIdx.x); o < base + 1024; o += blockDim.x) {
+                float s = sums[o];
+                for (int w = 1; w < kw; w++) s += sums[w * SLOT + o];
+                if (splits == 1)
+                    finish(o, s, bad_c[c], bias_c[c], jj);
+                else
+                    __hip_atomic_store(part + (split * tiles + tile) * OUT + o, s, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
-    }
     if (splits == 1) return;
     // Publish this split; the tile's last workgroup adds all splits in order.
     // The partials go out as device-coherent stores and every thread waits for
@@ -949,28 +984,183 @@ __global__ void __launch_bounds__(512)
     if (!last) return;
     // All splits of two outputs per thread are loaded at once (clamped
     // addresses, unused values skipped in the sum), then added in split order.
-    for (int o0 = threadIdx.x; o0 < OUT; o0 += 2 * blockDim.x) {
-        float pv[2][kMaxSplits];
 #pragma unroll
-        for (int q = 0; q < 2; q++)
+    for (int t = 0; t < MT; t++)
 #pragma unroll
-            for (int sp = 0; sp < kMaxSplits; sp++) {
-                const int o = min(o0 + q * static_cast<int>(blockDim.x), OUT - 1);
-                pv[q][sp] = __hip_atomic_load(part + (min(sp, splits - 1) * tiles + tile) * OUT + o, __ATOMIC_RELAXED,
-                                              __HIP_MEMORY_SCOPE_AGENT);
+        for (int c = 0; c < NT; c++) {
+            const int base = (t * NT + c) * 1024, jj = (tile * NT + c) * 32 + r32;
+            for (int o0 = base + static_cast<int>(threadIdx.x); o0 < base + 1024; o0 += 2 * blockDim.x) {
+                float pv[2][kMaxSplits];
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+#pragma unroll
+                    for (int sp = 0; sp < kMaxSplits; sp++) {
+                        const int o = min(o0 + q * static_cast<int>(blockDim.x), base + 1023);
+                        pv[q][sp] = __hip_atomic_load(part + (min(sp, splits - 1) * tiles + tile) * OUT + o,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    }
+#pragma unroll
+                for (int q = 0; q < 2; q++) {
+                    const int o = o0 + q * static_cast<int>(blockDim.x);
+                    float s = pv[q][0];
+#pragma unroll
+                    for (int sp = 1; sp < kMaxSplits; sp++) s = sp < splits ? s + pv[q][sp] : s;
+                    if (o < base + 1024) finish(o, s, bad_c[c], bias_c[c], jj);
+                }
             }
-#pragma unroll
-        for (int q = 0; q < 2; q++) {
-            const int o = o0 + q * static_cast<int>(blockDim.x);
-            float s = pv[q][0];
-#pragma unroll
-            for (int sp = 1; sp < kMaxSplits; sp++) s = sp < splits ? s + pv[q][sp] : s;
-            if (o >= OUT) continue;
-            const int i = row_of(o), jj = col_of(o);
-            if (i < m && jj < n) finish(i, jj, s);
         }
-    }
     if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Wide outputs at m <= 32 (a vocabulary head in a batched decode step), K =
+// 32 * KB: one workgroup per CU holding a contiguous run of 32-column tiles,
+// one tile per wave over all of K.  The workgroup splits the activations once
+// into LDS, [KB][32 rows][kSkinnyRow dwords] (16 of packed f16 h, 16 of l, 4
+// pad: the 16-byte fragment reads are conflict-free) with 2^-e per (row,
+// block) beside them, so every tile of the workgroup shares one split (the
+// skinny kernel redoes it per tile).  Loads, in issue order: every wave's
+// activations (a bare barrier keeps them ahead of all weight loads: the split
+// waits on them), the row's KB scales, bias and flag, the first kWideLook
+// 16-byte quant chunks; then each block issues the chunk kWideLook ahead, so
+// block b's MFMAs wait for chunk b only (loads complete in issue order).
+// Waves past the workgroup's last tile load that tile (never used) and leave
+// after the split.
+constexpr int kWideWaves = 8;
+// Quant chunks in flight per wave ahead of the MFMAs (4 and 8 time alike; 12
+// and 24 slower: the HBM queues fill with the waves' 32-byte row pieces).
+constexpr int kWideLook = 8;
+
+template <int KB>
+__global__ void __launch_bounds__(64 * kWideWaves)
+    k_gemm_wide(const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
+                const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
+                int per_wg, int extra) {
+    constexpr int k = KB * 32;
+    constexpr int kTasks = KB * 32 * 8 / (64 * kWideWaves);  // 4-value groups per thread
+    static_assert(KB % 4 == 0 && (KB * 256) % (64 * kWideWaves) == 0, "KB");
+    extern __shared__ __attribute__((aligned(16))) float lds[];
+    uint32_t* xs = reinterpret_cast<uint32_t*>(lds);
+    float* ivs = lds + KB * 32 * kSkinnyRow;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int half = lane >> 5, r32 = lane & 31;
+    // tiles [t0, t1): per_wg each, one more for the first `extra` workgroups
+    const int g = static_cast<int>(blockIdx.x);
+    const int t0 = g * per_wg + min(g, extra), t1 = t0 + per_wg + (g < extra ? 1 : 0);
+    const int tile = min(t0 + wave, t1 - 1);
+    const bool active = t0 + wave < t1;  // wave-uniform
+    const int col = tile * 32 + r32, j = min(col, n - 1);
+
+    // Activation groups: task = (block b, row r, 4-value group q), eight
+    // consecutive lanes per (b, r) so a load covers 128 contiguous bytes.
+    f4 xv[kTasks];
+#pragma unroll
+    for (int u = 0; u < kTasks; u++) {
+        const int task = static_cast<int>(threadIdx.x) + u * 64 * kWideWaves;
+        const int b = task >> 8, r = min((task >> 3) & 31, m - 1), q = task & 7;
+        xv[u] = *reinterpret_cast<const f4*>(x + static_cast<size_t>(r) * k + b * 32 + q * 4);
+    }
+    // Every wave's activation loads go out ahead of any weight load (a bare
+    // barrier: it does not wait for the loads).
+    __builtin_amdgcn_s_barrier();
+    // (the scales, bias and flag before the quants: block b's MFMAs then wait
+    // for quant chunk b only, loads completing in issue order)
+    uint2 sc[KB / 4];
+    const uint2* srow = reinterpret_cast<const uint2*>(dsc + static_cast<size_t>(j) * KB);
+#pragma unroll
+    for (int s = 0; s < KB / 4; s++) sc[s] = srow[s];
+    const float bv = bias ? bias[j] : 0.0f;
+    const bool bad = rexp[j] == kFhBadRowExp;
+    uint4 wq[KB];
+    const int8_t* wrow = qs + static_cast<size_t>(j) * k + half * 16;
+#pragma unroll
+    for (int b = 0; b < kWideLook; b++) wq[b] = *reinterpret_cast<const uint4*>(wrow + b * 32);
+
+    // The split: 2^e from the block's largest finite |x| (eight lanes), then
+    // h = f16(x 2^e), l = f16(x 2^e - h); rows past m are zeros.
+    auto split_task = [&](int u) __attribute__((always_inline)) {
+        const int task = static_cast<int>(threadIdx.x) + u * 64 * kWideWaves;
+        const int b = task >> 8, r = (task >> 3) & 31, q = task & 7;
+        const f4 z = {};
+        const f4 v = r < m ? xv[u] : z;
+        float mx = fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+        mx = fmaxf(mx, fh::dpp<0xB1>(mx));
+        mx = fmaxf(mx, fh::dpp<0x4E>(mx));
+        mx = fmaxf(mx, fh::dpp<0x141>(mx));
+        const float vv[4] = {v.x, v.y, v.z, v.w};
+        uint2 h, l;
+        int e;
+        if (__builtin_expect(__ballot(!finite(mx)) != 0, 0)) {
+            float fm = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                if (finite(vv[i])) fm = fmaxf(fm, fabsf(vv[i]));
+            fm = fmaxf(fm, fh::dpp<0xB1>(fm));
+            fm = fmaxf(fm, fh::dpp<0x4E>(fm));
+            fm = fmaxf(fm, fh::dpp<0x141>(fm));
+            e = block_exponent(fm);
+            split4<true>(vv, __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23), h, l);
+        } else {
+            e = block_exponent(mx);
+            split4<false>(vv, __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23), h, l);
+        }
+        uint32_t* dst = xs + (b * 32 + r) * kSkinnyRow + 2 * q;
+        *reinterpret_cast<uint2*>(dst) = h;
+        *reinterpret_cast<uint2*>(dst + 16) = l;
+        if (q == 0) ivs[b * 32 + r] = __builtin_bit_cast(float, static_cast<uint32_t>(127 - e) << 23);
+    };
+
+    f16x acc = {};
+    const f16x zero = {};
+    auto block = [&](int b) __attribute__((always_inline)) {
+        if (b + kWideLook < KB) wq[b + kWideLook] = *reinterpret_cast<const uint4*>(wrow + (b + kWideLook) * 32);
+        // lane (r32, half) takes x[r32][b*32 + half*16 .. +16] as h and l
+        const uint32_t* xr = xs + (b * 32 + r32) * kSkinnyRow + half * 8;
+        const h8 ah0 = *reinterpret_cast<const h8*>(xr), ah1 = *reinterpret_cast<const h8*>(xr + 4);
+        const h8 al0 = *reinterpret_cast<const h8*>(xr + 16), al1 = *reinterpret_cast<const h8*>(xr + 20);
+        float4 iv[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++) iv[g] = *reinterpret_cast<const float4*>(ivs + b * 32 + g * 8 + half * 4);
+        const uint2 c0 = quants_to_f16(wq[b].x), c1 = quants_to_f16(wq[b].y);
+        const uint2 c2 = quants_to_f16(wq[b].z), c3 = quants_to_f16(wq[b].w);
+        const h8 bq0 = __builtin_bit_cast(h8, make_uint4(c0.x, c0.y, c1.x, c1.y));
+        const h8 bq1 = __builtin_bit_cast(h8, make_uint4(c2.x, c2.y, c3.x, c3.y));
+        const uint32_t sw = (b & 2) ? sc[b >> 2].y : sc[b >> 2].x;
+        const float dw = fh_h2f(static_cast<uint16_t>((b & 1) ? sw >> 16 : sw & 0xFFFFu));
+        f16x p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, bq0, zero, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, bq0, p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, bq1, p, 0, 0, 0);
+        p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, bq1, p, 0, 0, 0);
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            acc[4 * g + 0] = fmaf(dw, p[4 * g + 0] * iv[g].x, acc[4 * g + 0]);
+            acc[4 * g + 1] = fmaf(dw, p[4 * g + 1] * iv[g].y, acc[4 * g + 1]);
+            acc[4 * g + 2] = fmaf(dw, p[4 * g + 2] * iv[g].z, acc[4 * g + 2]);
+            acc[4 * g + 3] = fmaf(dw, p[4 * g + 3] * iv[g].w, acc[4 * g + 3]);
+        }
+        // Each block's sums are formed here, in order: without this the
+        // compiler runs every block's MFMAs first and spills their products.
+        asm volatile("" : "+v"(acc));
+    };
+
+    // Every split first (one barrier), then the blocks in order.  (Splitting
+    // and computing chunk by chunk, a barrier per chunk, ran slower.)
+#pragma unroll
+    for (int u = 0; u < kTasks; u++) split_task(u);
+    __syncthreads();
+    if (!active) return;
+#pragma unroll
+    for (int b = 0; b < KB; b++) block(b);
+    if (col >= n) return;
+#pragma unroll
+    for (int v = 0; v < 16; v++) {
+        const int i = (v >> 2) * 8 + half * 4 + (v & 3);
+        if (i >= m) continue;
+        float s = acc[v];
+        if (__builtin_expect(bad, 0))
+            s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(col) * k,
+                          dsc + static_cast<size_t>(col) * KB);
+        y[static_cast<size_t>(i) * n + col] = bias ? s + bv : s;
+    }
 }
 
 namespace {
@@ -1090,6 +1280,26 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     return FH_OK;
 }
 
+// One workgroup per CU (more only past eight tiles per CU), tiles dealt in
+// contiguous runs that differ by at most one.
+template <int KB>
+int launch_wide(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+    const size_t tiles = (w->n + 31) / 32;
+    size_t grid = static_cast<size_t>(ctx->num_cus);
+    if (grid * kWideWaves < tiles) grid = (tiles + kWideWaves - 1) / kWideWaves;
+    if (grid > tiles) grid = tiles;
+    if (tiles > 0x7FFFFFFFu / 32) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: too many output columns");
+    const size_t lds = KB * (32 * kSkinnyRow + 32) * sizeof(float);
+    hipLaunchKernelGGL(k_gemm_wide<KB>, dim3(static_cast<unsigned>(grid)), dim3(64 * kWideWaves), lds, ctx->stream, x,
+                       w->qs, w->d, w->rexp, bias, y, static_cast<int>(m), static_cast<int>(w->n),
+                       static_cast<int>(tiles / grid), static_cast<int>(tiles % grid));
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+// Outputs at least this many 32-column tiles wide take k_gemm_wide at m <= 32.
+constexpr size_t kWideMinTiles = 1024;
+
 // Tile rules from timings at m = 32 and 64 over the GPT-2 and Qwen2-0.5B
 // shapes: two column tiles per wave pay off from about 256 tiles of 32
 // columns (a 9728-wide output: 14.2 -> 11.8 us at m = 32), four only at m <=
@@ -1101,6 +1311,11 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
 int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
                   const fh_scratch* scratch = nullptr) {
     const size_t t32 = (w->n + 31) / 32;
+    if (m <= 32 && t32 >= kWideMinTiles) {
+        if (w->k == 768) return launch_wide<24>(ctx, w, x, m, bias, y);
+        if (w->k == 896) return launch_wide<28>(ctx, w, x, m, bias, y);
+        if (w->k == 1024) return launch_wide<32>(ctx, w, x, m, bias, y);
+    }
     if (m <= 32) {
         if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y, scratch);
         if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y, scratch);

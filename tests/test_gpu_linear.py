@@ -277,6 +277,52 @@ def test_gemm_rows_of_any_magnitude(fh, orc):
     assert np.all(got[4] == 0.0)
 
 
+@pytest.mark.parametrize("m,n,k", [(3, 32805, 768), (17, 40000, 896), (32, 50257, 1024), (8, 151936, 896)])
+def test_wide_outputs_at_small_batch(fh, orc, m, n, k):
+    """Outputs of at least 1024 32-column tiles at m <= 32 (vocabulary heads
+    in a batched decode step) take the kernel that splits the activations once
+    per workgroup: a ragged last tile, more tiles than eight per CU (151936),
+    rows of any magnitude, inf/NaN activations, non-finite block scales and
+    the bias, against the oracle and the float64 product."""
+    import ferrum_hip
+
+    seed = m + n + k
+    raw = orc.quantize_weight(n, k, seed, 0.02).reshape(n, k // 32, 34).copy()
+    bad_cols = [2, 7, n - 1]
+    raw[2, 0, :2] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)       # +inf scale
+    raw[7, -1, :2] = np.frombuffer(np.uint16(0xFC00).tobytes(), np.uint8)      # -inf scale
+    raw[n - 1, 1, :2] = np.frombuffer(np.uint16(0x7E00).tobytes(), np.uint8)   # NaN scale
+    raw = raw.ravel()
+    x = acts(m, k, seed)
+    x[0] *= np.float32(1e-30)
+    if m > 3:
+        x[1] *= np.float32(1e30)
+        x[2, 17] = np.float32(3e4)      # one outlier next to O(1) values
+    if m > 5:
+        x[3] = 0.0
+        x[4, 5] = np.inf
+        x[5, 100] = np.nan
+    b = bias_for(n, seed)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    got = ferrum_hip.linear_forward(fh, x, w, b)
+    w.free()
+    cols = np.unique(np.r_[bad_cols, 0, 1, 31, 32, n - 33, n - 32, n - 2,
+                           np.random.default_rng(seed).choice(n, size=min(n, 6000), replace=False)])
+    # every output column depends on its own weight row only: check the
+    # sampled columns against the oracle on those rows
+    sub = raw.reshape(n, -1)[cols].ravel()
+    ref = orc.q8_0_linear(x, sub, cols.size, b[cols])
+    g = got[:, cols]
+    assert np.array_equal(np.isnan(g), np.isnan(ref))
+    assert np.array_equal(np.isposinf(g), np.isposinf(ref)) and np.array_equal(np.isneginf(g), np.isneginf(ref))
+    fin = np.isfinite(ref)
+    assert_close(g[fin], ref[fin], term_mass(orc, x, sub, cols.size, k)[fin])
+    clean_rows = np.arange(6 if m > 5 else (3 if m > 3 else 1), m)
+    clean_cols = ~np.isin(cols, bad_cols)
+    exact = exact_linear(orc, x[clean_rows], sub, cols.size, k, b[cols])[:, clean_cols]
+    assert_as_accurate(g[clean_rows][:, clean_cols], ref[clean_rows][:, clean_cols], exact, max_factor=2.0)
+
+
 def test_gemm_propagates_inf_and_nan_like_the_reference(fh, orc):
     import ferrum_hip
 
