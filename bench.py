@@ -104,9 +104,11 @@ def main():
     ap.add_argument("--replicas", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=10.0, help="bound on the CPU baseline sample")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--leg", choices=["all", "stack", "head", "prefill", "qwen", "qlinear", "dropin"], default="all",
+    ap.add_argument("--leg", choices=["all", "stack", "head", "prefill", "qwen", "qlinear", "dropin", "b32"],
+                    default="all",
                     help="'stack': only the whole decode step and its one-launch block stack (for profiles and "
-                         "counter runs); 'head': only the lm_head GEMV roofline leg; 'prefill': only the "
+                         "counter runs); 'b32': only the batch-32 step; 'head': only the lm_head GEMV roofline leg; "
+                         "'prefill': only the "
                          "GPT-2-medium prefill GEMMs; 'qwen': only the Qwen2-shaped batch-64 step; 'qlinear': only "
                          "the per-row int8 and int4 qlinear steps; 'dropin': the blocking per-call linear and the "
                          "exact mode")
@@ -321,15 +323,17 @@ def main():
                               "config3_run": result["config3_run"]}))
             return
 
+    if args.leg in ("all", "b32"):
+        reps = [Replica(ctx, fh, torch, gen) for _ in range(args.replicas)]
     if args.leg == "all":
         # ---- the hot path alone, unchained: the 49 Q8_0 linears on fixed
         # inputs + the sampler (no dependence between the linears) -------------
-        reps = [Replica(ctx, fh, torch, gen) for _ in range(args.replicas)]
         graphs = capture(step, reps)
         ms_step, _ = timed(graphs, args.steps, args.warmup)
         del graphs
         result["hot_unchained"] = ms_step
         torch.cuda.synchronize()
+    if args.leg in ("all", "b32"):
 
         # ---- batch 32: the same hot path for 32 sequences (BASELINE's b32 decode) ----
         B = B32
@@ -351,11 +355,17 @@ def main():
 
         graphs_b = capture(step_b, reps)
         ms_b, _ = timed(graphs_b, max(args.steps // 4, 10), args.warmup)
+        b32_bytes = L * sum(q8_bytes(n, k) for (n, k) in LAYER_SHAPES) + q8_bytes(V, D)
         result["b32"] = {"tok_s": round(B * 1000.0 / ms_b, 1), "ms_per_step": round(ms_b, 5), "batch": B,
                          "sampler_rows": B, "residency": f"hbm-forced ({args.replicas} weight replicas)",
-                         "what": "49 Q8_0 skinny GEMMs at m = 32 + head + 32 sampler rows (unchained inputs)"}
+                         "weight_bytes": b32_bytes, "weight_GBps": round(b32_bytes / (ms_b * 1e-3) / 1e9, 1),
+                         "what": "48 Q8_0 skinny GEMMs at m = 32 (k_gemm_skinny) + the 50257 x 768 head "
+                                 "(k_gemm_wide) + 32 sampler rows, unchained inputs"}
         del graphs_b, reps
         torch.cuda.synchronize()
+        if args.leg == "b32":
+            print(json.dumps({"leg": "b32", "b32": result["b32"]}))
+            return
 
     if args.leg in ("all", "dropin"):
         result["dropin"] = dropin_leg(ctx, fh, torch, gen, dev)
