@@ -734,24 +734,34 @@ __device__ __forceinline__ bool wave_tail(unsigned long long key, int nc, int to
 // The shallowest bucket depth whose cumulative count reaches k (top-k) or
 // whose fixed-point mass reaches top_p, plus one bucket of margin (top-p
 // only); -1 when not found or when more than kCap ids would be gathered.
+// One wave (lane = bucket): inclusive prefix sums of the counts and the
+// fixed-point masses (exact integer sums, so the order does not matter), the
+// first bucket that reaches the target by ballot.  Every lane of the wave
+// calls and gets the result.
 __device__ __forceinline__ int bucket_depth(const uint32_t* hist, const unsigned long long* mass, int top_k,
                                             float top_p, bool use_k, bool use_p) {
-    int depth = -1, cnt = 0;
-    unsigned long long acc = 0;
-    const unsigned long long target = use_p ? fix40(top_p) : 0;
-    for (int b = 0; b < kBuckets; b++) {
-        cnt += static_cast<int>(hist[b]);
-        acc += mass[b];
-        if (use_k ? cnt >= top_k : acc >= target) {
-            depth = b;
-            break;
+    static_assert(kBuckets == 64, "one bucket per lane");
+    const int lane = lane_id();
+    unsigned cnt = hist[lane];
+    unsigned long long acc = use_k ? 0ull : mass[lane];
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const unsigned c_up = static_cast<unsigned>(__shfl_up(static_cast<int>(cnt), off, 64));
+        const unsigned lo = static_cast<unsigned>(__shfl_up(static_cast<int>(static_cast<unsigned>(acc)), off, 64));
+        const unsigned hi = static_cast<unsigned>(__shfl_up(static_cast<int>(static_cast<unsigned>(acc >> 32)), off, 64));
+        if (lane >= off) {
+            cnt += c_up;
+            acc += (static_cast<unsigned long long>(hi) << 32) | lo;
         }
     }
-    if (depth >= 0 && !use_k && depth + 1 < kBuckets) {
-        depth++;
-        cnt += static_cast<int>(hist[depth]);
-    }
-    return (depth >= 0 && cnt <= kCap) ? depth : -1;
+    const unsigned long long target = use_p ? fix40(top_p) : 0;
+    const unsigned long long reached =
+        __ballot(use_k ? static_cast<int>(cnt) >= top_k : acc >= target);
+    if (!reached) return -1;
+    int depth = __ffsll(static_cast<long long>(reached)) - 1;
+    if (!use_k && depth + 1 < kBuckets) depth++;
+    const int total = static_cast<int>(rlu(cnt, depth));
+    return total <= kCap ? depth : -1;
 }
 
 // Sort s.u.cand[0..nc) by (p desc, index asc) and replay top-k then top-p in
@@ -1006,9 +1016,12 @@ __device__ __forceinline__ void sample_row(Shared& s, Row& row, const Params& P,
             s.mass[0][tid] = ms;
         }
         __syncthreads();
-        if (tid == 0) {
-            s.bi[0] = bucket_depth(s.hist[0], s.mass[0], P.top_k, P.top_p, use_k, use_p);
-            s.n_cand = 0;
+        if (tid < 64) {
+            const int d = bucket_depth(s.hist[0], s.mass[0], P.top_k, P.top_p, use_k, use_p);
+            if (tid == 0) {
+                s.bi[0] = d;
+                s.n_cand = 0;
+            }
         }
         __syncthreads();
         const int depth = s.bi[0];
@@ -1426,7 +1439,10 @@ __global__ void __launch_bounds__(kT)
             s.mass[0][tid] = ms;
         }
         __syncthreads();
-        if (tid == 0) s.bi[0] = bucket_depth(s.hist[0], s.mass[0], P.top_k, P.top_p, use_k, use_p);
+        if (tid < 64) {
+            const int d = bucket_depth(s.hist[0], s.mass[0], P.top_k, P.top_p, use_k, use_p);
+            if (tid == 0) s.bi[0] = d;
+        }
         __syncthreads();
         const int depth = s.bi[0];
         // The row's p values (pbuf) feed workgroup 0's general path, which
