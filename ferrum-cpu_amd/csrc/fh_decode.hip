@@ -117,7 +117,7 @@ struct DecArgs {
     int pos;
     u64* slots;               // per layer: qkv [3D], attn [H][nch_max][HD + 2], proj [D], up [4D], down [D]
     int nch_max;
-    unsigned* epoch;          // [grid]: launches each workgroup has finished
+    unsigned* epoch;          // [grid + prefetch]: launches each workgroup has finished
     unsigned* status;
     unsigned spin_limit;
     int skip_wg;              // testing hook: this workgroup publishes nothing (-1: none)
@@ -457,6 +457,74 @@ struct AttnItem {
     }
 };
 
+// Past the stack's own workgroups, up to kPrefetchWGs more read each next
+// block's weights (quant and scale planes) and cached K/V rows once the
+// current block's Q|K|V outputs are out, so that the stack's own loads of that
+// block, issued a phase ahead of their use, find them in the memory-side
+// cache instead of HBM.  They only read and never publish; a wait that runs
+// out ends their work silently (the stack's own waits report).  Measured,
+// HBM-forced GPT-2-124M step at position 255: 229.7 -> 217.4 us with 24; 8
+// lag behind and slow the stack (240 us), 16-32 time alike, 64-128 a little
+// slower; warming the head as well, or two blocks ahead, did not pay.
+constexpr int kPrefetchWGs = 24;
+constexpr size_t kPrefetchKvMax = 8u << 20;  // a block's cached K/V bytes still worth warming
+
+template <int D, int HD>
+__device__ void prefetch_blocks(const DecArgs& a, int p, int np, size_t stride, unsigned tag) {
+    constexpr int F = 4 * D;
+    const int tid = threadIdx.x;
+    uint32_t sink = 0;
+    // this workgroup's share of [base, base + bytes): 16-byte pieces, eight in
+    // flight per thread (the values are folded into `sink`, kept by an asm)
+    auto touch = [&](const void* base, size_t bytes) __attribute__((always_inline)) {
+        const uint4* b4 = static_cast<const uint4*>(base);
+        const size_t n16 = bytes >> 4, step = static_cast<size_t>(np) * kT;
+        for (size_t i0 = static_cast<size_t>(p) * kT + tid; i0 < n16; i0 += 8 * step) {
+            uint4 v[8];
+#pragma unroll
+            for (int j = 0; j < 8; j++) v[j] = b4[min(i0 + j * step, n16 - 1)];
+#pragma unroll
+            for (int j = 0; j < 8; j++) sink ^= v[j].x;
+        }
+    };
+    auto touch_block = [&](const DecBlock& B) __attribute__((always_inline)) {
+        const size_t n[4] = {3 * D, D, F, D}, k[4] = {D, D, D, F};
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            touch(B.q[i], n[i] * k[i]);
+            touch(B.d[i], n[i] * (k[i] / 32) * sizeof(uint16_t));
+        }
+        const size_t kv = static_cast<size_t>(a.pos) * D * sizeof(float);
+        if (kv > 0 && 2 * kv <= kPrefetchKvMax) {
+            touch(B.kc, kv);
+            touch(B.vc, kv);
+        }
+    };
+    __shared__ int go;
+    if (a.layers > 1) touch_block(a.blk[1]);
+    for (int l = 1; l + 1 < a.layers; l++) {
+        // block l's first Q|K|V output (row 0, workgroup 0) carries this launch's tag
+        if (tid == 0) {
+            const u64* s0 = a.slots + l * stride;
+            unsigned spins = 0;
+            int ok = 1;
+            while (static_cast<unsigned>(cload64(s0) >> 32) != tag) {
+                __builtin_amdgcn_s_sleep(2);
+                if (++spins >= a.spin_limit) {
+                    ok = 0;
+                    break;
+                }
+            }
+            go = ok;
+        }
+        __syncthreads();
+        if (!go) break;
+        touch_block(a.blk[l + 1]);
+        __syncthreads();  // (go is written again next round)
+    }
+    asm volatile("" ::"v"(sink));
+}
+
 template <int D, int HD, int G>
 __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
     constexpr int H = D / HD, F = 4 * D;
@@ -474,6 +542,14 @@ __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
     float* fac = part + H * a.nch_max * kAttnSlots;
 
     const int tid = threadIdx.x, w = blockIdx.x, gw = w * kWaves + (tid >> 6);
+    if (w >= G) {  // a prefetch workgroup (its own epoch counter, like every workgroup)
+        const unsigned ptag = a.epoch[w] + 1;
+        prefetch_blocks<D, HD>(a, w - G, static_cast<int>(gridDim.x) - G,
+                               static_cast<size_t>(3 * D + H * a.nch_max * kAttnSlots + D + F + D), ptag);
+        __syncthreads();
+        if (tid == 0) a.epoch[w] = ptag;
+        return;
+    }
     const int pos = a.pos, len = pos + 1, nch = (len + kPos - 1) / kPos, items = H * nch;
     // Each workgroup keeps its own epoch counter and bumps it when it ends,
     // so all counters advance together, one per launch, with no workgroup
@@ -621,7 +697,8 @@ struct fh_gpt2_stack {
     u64* slots = nullptr;
     unsigned* epoch = nullptr;
     void* base = nullptr;        // one allocation: epoch counters, slots
-    int grid = 0;
+    int grid = 0;                // the stack's own workgroups
+    int prefetch = 0;            // prefetch workgroups launched beside them
     size_t dyn_lds = 0;
     const void* kernel = nullptr;
 };
@@ -700,11 +777,16 @@ int fh_gpt2_stack_create(fh_ctx* ctx, const fh_gpt2_block* blocks, size_t layers
     const int grid = grid_for(static_cast<int>(d));
     int per_cu = 0;
     FH_HIP(ctx, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kT, dyn));
-    if (per_cu < 1 || static_cast<size_t>(per_cu) * ctx->num_cus < static_cast<size_t>(grid))
+    const size_t resident = static_cast<size_t>(per_cu < 0 ? 0 : per_cu) * ctx->num_cus;
+    if (per_cu < 1 || resident < static_cast<size_t>(grid))
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_gpt2_stack_create: the device cannot hold the stack kernel's " +
                                               std::to_string(grid) + " workgroups at once");
+    // prefetch workgroups only where the device holds them beside the stack's
+    // (launched after them, so the stack's are never displaced)
+    const int prefetch = static_cast<int>(resident - grid < static_cast<size_t>(kPrefetchWGs) ? resident - grid
+                                                                                           : kPrefetchWGs);
     const size_t stride = 3 * d + heads * nch * (hd + 2) + d + ffn + d;
-    const size_t ebytes = fh_align256(grid * sizeof(unsigned));
+    const size_t ebytes = fh_align256((grid + prefetch) * sizeof(unsigned));
     const size_t sbytes = layers * stride * sizeof(u64);
     fh_gpt2_stack* s = new (std::nothrow) fh_gpt2_stack();
     if (!s) return fh_fail(ctx, FH_ERR_OOM, "fh_gpt2_stack_create: out of host memory");
@@ -750,6 +832,7 @@ int fh_gpt2_stack_create(fh_ctx* ctx, const fh_gpt2_block* blocks, size_t layers
     s->tok_w = d_tok_w;
     s->pos_w = d_pos_w;
     s->grid = grid;
+    s->prefetch = prefetch;
     s->dyn_lds = dyn;
     s->kernel = kern;
     *out = s;
@@ -795,7 +878,7 @@ int fh_gpt2_stack_forward_async(fh_ctx* ctx, fh_gpt2_stack* s, const uint32_t* d
     a.skip_wg = ctx->test_skip_segment;
     a.x_out = d_x;
     void* args[] = {&a};
-    FH_HIP(ctx, hipLaunchKernel(s->kernel, dim3(static_cast<unsigned>(s->grid)), dim3(kT), args, s->dyn_lds,
+    FH_HIP(ctx, hipLaunchKernel(s->kernel, dim3(static_cast<unsigned>(s->grid + s->prefetch)), dim3(kT), args, s->dyn_lds,
                                 ctx->stream));
     return FH_OK;
 }
