@@ -491,7 +491,8 @@ def main():
                                 f"{args.replicas * result['step_bytes'] / 1e6:.0f} MB > 256 MB MALL)"},
         "roofline": {"bound": "hbm", "achieved": round(result["stack_gbps"], 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(result["stack_gbps"] / HBM_PEAK_GBS, 4), "traffic": measured_traffic(STACK_PMC),
-                     "kernel": "k_gpt2_stack<768,64,48> (12 GPT-2 blocks, one launch, 48 workgroups)",
+                     "kernel": "k_gpt2_stack<768,64,48> (12 GPT-2 blocks, one launch, 48 workgroups + 24 that "
+                               "warm each next block's weights in the memory-side cache)",
                      "avg_launch_us": round(result["stack_us"], 3), "bytes_per_launch": result["stack_bytes"],
                      "note": "bound by 60 dependent phases between workgroups (an exchange of ~2 us plus each "
                              "phase's serial LDS/barrier/VALU work), not by HBM"},
