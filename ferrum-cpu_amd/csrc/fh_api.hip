@@ -544,7 +544,8 @@ int fh_q8_0_block_dots_async(fh_ctx* ctx, const fh_q8_0* w, const int8_t* d_qx, 
 
 static int check_sample(fh_ctx* ctx, size_t rows, size_t vocab, int kind, const fh_sampling_params* p) {
     if (!p) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: params is NULL");
-    if (kind != FH_LOGITS_RAW && kind != FH_LOGITS_GPT2_SOFTMAX)
+    const int base = kind & ~FH_RECENT_RANGES;
+    if (base != FH_LOGITS_RAW && base != FH_LOGITS_GPT2_SOFTMAX)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: unknown logits kind " + std::to_string(kind));
     if (vocab == 0) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: vocab is 0");
     if (vocab > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_sample_rows: vocab above 2^31 - 1");
@@ -590,6 +591,9 @@ int fh_sample_rows(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab, 
     if (!logits || !out) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: logits or out_ids is NULL");
     bool sampled = !(p->temperature <= 0.0f);
     if (!draws && sampled) return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: draws is NULL with temperature > 0");
+    if (kind & FH_RECENT_RANGES)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_sample_rows: FH_RECENT_RANGES is for fh_sample_rows_async "
+                                            "(host lists go as running offsets)");
     if ((rc = check_offsets(ctx, off, rows, recent))) return rc;
     FH_ON_DEVICE(ctx);
     size_t n_recent = off ? off[rows] - off[0] : 0;
@@ -656,6 +660,26 @@ int fh_embed_one_async(fh_ctx* ctx, const float* d_token_w, const float* d_pos_w
                                             std::to_string(max_seq));
     FH_ON_DEVICE(ctx);
     return fh_launch_embed_one(ctx, d_token_w, d_pos_w, vocab, d, d_token, pos, d_out);
+}
+
+int fh_embed_rows_pos_async(fh_ctx* ctx, const float* d_token_w, const float* d_pos_w, size_t vocab, size_t max_seq,
+                            size_t d, const uint32_t* d_tokens, const uint32_t* d_pos, size_t rows, uint32_t* d_hist,
+                            size_t hist_stride, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rows == 0) return FH_OK;
+    if (!d_token_w || !d_pos_w || !d_tokens || !d_pos || !d_out)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_embed_rows_pos: a pointer is NULL");
+    if (vocab == 0 || d == 0 || max_seq == 0 || vocab > 0x7FFFFFFFu || max_seq > 0x7FFFFFFFu || rows > 65535 ||
+        rows * d > 0x7FFFFFFFu)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_embed_rows_pos: vocab, max_seq and rows * d in 1 .. 2^31, rows "
+                                            "<= 65535");
+    if (d_hist && (hist_stride == 0 || hist_stride > 0x7FFFFFFFu || rows * hist_stride > 0xFFFFFFFFu))
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_embed_rows_pos: hist_stride in 1 .. 2^31, rows * hist_stride "
+                                            "below 2^32");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_embed_rows_pos(ctx, d_token_w, d_pos_w, vocab, max_seq, d, d_tokens, d_pos, rows, d_hist,
+                                    d_hist ? hist_stride : 0, d_out);
 }
 
 int fh_layernorm_async(fh_ctx* ctx, const float* d_x, size_t rows, size_t d, const float* d_gamma,

@@ -4,6 +4,8 @@
 // sampler (fh_sampler.hip) a whole decode step stays on the device.
 //
 //  k_embed_one   Embedding::embed_one (layer/embedding.rs:70-90).
+//  k_embed_rows_pos  the same for a batch of sequences, each row at its own
+//                position (token and position ids on the device).
 //  k_layernorm   LayerNorm::forward (layer/norm.rs:46-82), one workgroup per
 //                row; the row sums are tree reductions in a fixed order.
 //  k_gelu        activation::gelu (activation.rs:9-12), in place.
@@ -45,6 +47,27 @@ __global__ void __launch_bounds__(kThreads) k_embed_one(const float* __restrict_
     // An id past the vocabulary (never one the sampler returns) poisons the row.
     out[i] = t < static_cast<uint32_t>(vocab) ? tok_w[static_cast<size_t>(t) * d + i] + pos_w[static_cast<size_t>(pos) * d + i]
                                               : __builtin_nanf("");
+}
+
+// Embedding::embed_one for `rows` sequences at once: row r is token tokens[r]
+// at position pos[r] (both on the device).  An id past the vocabulary or a
+// position past the table poisons the row (the host checks positions before
+// the launch).  With hist set, workgroup 0 of each row also records the id at
+// hist[r * hist_stride + pos[r]] (a batched decode's per-row penalty window).
+__global__ void __launch_bounds__(kThreads) k_embed_rows_pos(const float* __restrict__ tok_w,
+                                                            const float* __restrict__ pos_w, int vocab, int max_seq,
+                                                            int d, const uint32_t* __restrict__ tokens,
+                                                            const uint32_t* __restrict__ pos, uint32_t* hist,
+                                                            int hist_stride, float* __restrict__ out) {
+    const int r = blockIdx.y, i = blockIdx.x * kThreads + threadIdx.x;
+    const uint32_t t = tokens[r], p = pos[r];
+    if (hist && blockIdx.x == 0 && threadIdx.x == 0 && p < static_cast<uint32_t>(hist_stride))
+        hist[static_cast<size_t>(r) * hist_stride + p] = t;
+    if (i >= d) return;
+    out[static_cast<size_t>(r) * d + i] =
+        t < static_cast<uint32_t>(vocab) && p < static_cast<uint32_t>(max_seq)
+            ? tok_w[static_cast<size_t>(t) * d + i] + pos_w[static_cast<size_t>(p) * d + i]
+            : __builtin_nanf("");
 }
 
 __global__ void __launch_bounds__(kThreads) k_layernorm(const float* __restrict__ x, int d,
@@ -347,6 +370,16 @@ __global__ void __launch_bounds__(kThreads) k_add_layernorm(const float* x, cons
 unsigned blocks_for(size_t n) { return static_cast<unsigned>((n + kThreads - 1) / kThreads); }
 
 }  // namespace
+
+int fh_launch_embed_rows_pos(fh_ctx* ctx, const float* tok_w, const float* pos_w, size_t vocab, size_t max_seq,
+                             size_t d, const uint32_t* tokens, const uint32_t* pos, size_t rows, uint32_t* hist,
+                             size_t hist_stride, float* out) {
+    hipLaunchKernelGGL(k_embed_rows_pos, dim3(blocks_for(d), static_cast<unsigned>(rows)), dim3(kThreads), 0,
+                       ctx->stream, tok_w, pos_w, static_cast<int>(vocab), static_cast<int>(max_seq),
+                       static_cast<int>(d), tokens, pos, hist, static_cast<int>(hist_stride), out);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
 
 int fh_launch_embed_one(fh_ctx* ctx, const float* tok_w, const float* pos_w, size_t vocab, size_t d,
                         const uint32_t* token, size_t pos, float* out) {

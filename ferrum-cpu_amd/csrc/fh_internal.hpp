@@ -152,6 +152,9 @@ int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t 
 // FH_W8A32_EXACT: ferrum_core's sequential sums, bit for bit (no K split).
 int fh_launch_linear_exact(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y);
 int fh_launch_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out);
+int fh_launch_embed_rows_pos(fh_ctx* ctx, const float* tok_w, const float* pos_w, size_t vocab, size_t max_seq,
+                             size_t d, const uint32_t* tokens, const uint32_t* pos, size_t rows, uint32_t* hist,
+                             size_t hist_stride, float* out);
 int fh_launch_embed_one(fh_ctx* ctx, const float* tok_w, const float* pos_w, size_t vocab, size_t d,
                         const uint32_t* token, size_t pos, float* out);
 int fh_launch_layernorm(fh_ctx* ctx, const float* x, size_t rows, size_t d, const float* gamma,

@@ -864,6 +864,9 @@ struct Params {
     float pen;
     int kind;
     int n;
+    // Recent lists as (begin, end) pairs per row (FH_RECENT_RANGES) rather
+    // than rows + 1 running offsets.
+    bool ranges;
     // Cross-workgroup waits of the split kernel give up after this many polls
     // (kSpinLimit unless a test lowers it).
     unsigned spin_limit;
@@ -872,11 +875,12 @@ struct Params {
     int skip_seg;
 };
 
-// The recent list of a row: offsets[row] .. offsets[row + 1].  Decreasing
-// offsets are recorded in the status word (and the row gets no penalty).
-__device__ __forceinline__ int recent_len(const uint32_t* __restrict__ offsets, size_t row, unsigned* status,
-                                          const uint32_t** rec, const uint32_t* __restrict__ recent) {
-    const uint32_t r0 = offsets[row], r1 = offsets[row + 1];
+// The recent list of a row: offsets[row] .. offsets[row + 1], or with ranges
+// offsets[2 row] .. offsets[2 row + 1].  Decreasing offsets are recorded in
+// the status word (and the row gets no penalty).
+__device__ __forceinline__ int recent_len(const uint32_t* __restrict__ offsets, size_t row, bool ranges,
+                                          unsigned* status, const uint32_t** rec, const uint32_t* __restrict__ recent) {
+    const uint32_t r0 = ranges ? offsets[2 * row] : offsets[row], r1 = ranges ? offsets[2 * row + 1] : offsets[row + 1];
     *rec = recent + r0;
     if (r1 < r0) {
         if (threadIdx.x == 0) atomicOr(status, static_cast<unsigned>(FH_STATUS_BAD_OFFSETS));
@@ -1058,7 +1062,7 @@ __global__ void __launch_bounds__(kT)
     const size_t row = blockIdx.x;
     int nrec = 0;
     const uint32_t* rec = nullptr;
-    if (offsets && recent) nrec = recent_len(offsets, row, status, &rec, recent);
+    if (offsets && recent) nrec = recent_len(offsets, row, P.ranges, status, &rec, recent);
     RegRow<ITEMS> st;
     st.n = P.n;
     const bool has_draw = draws != nullptr;
@@ -1074,7 +1078,7 @@ __global__ void __launch_bounds__(kT)
     const size_t row = blockIdx.x;
     int nrec = 0;
     const uint32_t* rec = nullptr;
-    if (offsets && recent) nrec = recent_len(offsets, row, status, &rec, recent);
+    if (offsets && recent) nrec = recent_len(offsets, row, P.ranges, status, &rec, recent);
     GlobalRow st;
     st.n = P.n;
     st.w = work + row * static_cast<size_t>(P.n);
@@ -1273,7 +1277,7 @@ __global__ void __launch_bounds__(kT)
     const float pen = P.pen;
     int nrec = 0;
     const uint32_t* rec = nullptr;
-    if (offsets && recent) nrec = recent_len(offsets, row, status, &rec, recent);
+    if (offsets && recent) nrec = recent_len(offsets, row, P.ranges, status, &rec, recent);
     const bool use_pen = fabsf(pen - 1.0f) > FLT_EPSILON && pen > 0.0f && nrec > 0;
     auto fill = [&](int b0) __attribute__((always_inline)) {
         for (int i = tid; i < kSlots; i += kT) {
@@ -1611,7 +1615,8 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
     P.top_k = p->top_k > 0x7FFFFFFFu ? 0x7FFFFFFF : static_cast<int>(p->top_k);
     P.top_p = p->top_p;
     P.pen = p->repetition_penalty;
-    P.kind = kind;
+    P.kind = kind & ~FH_RECENT_RANGES;
+    P.ranges = (kind & FH_RECENT_RANGES) != 0;
     P.n = static_cast<int>(vocab);
     P.spin_limit = ctx->test_spin_limit ? ctx->test_spin_limit : kSpinLimit;
     P.skip_seg = ctx->test_skip_segment;
@@ -1662,7 +1667,7 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
             for (size_t r0 = 0; r0 < rows; r0 += pick_rows) {
                 const size_t nr = rows - r0 < pick_rows ? rows - r0 : pick_rows;
                 const float* lg = logits + r0 * vocab;
-                const uint32_t* of = offsets ? offsets + r0 : nullptr;
+                const uint32_t* of = offsets ? offsets + (P.ranges ? 2 * r0 : r0) : nullptr;
                 const uint64_t* dr = draws ? draws + r0 : nullptr;
                 void* sy = static_cast<RowSync*>(sync) + r0;
                 float* pb = static_cast<float*>(ws) + r0 * vocab;

@@ -36,6 +36,7 @@ LIB_PATH = os.path.join(HERE, "lib", "libferrum_hip.so")
 FH_OK, FH_ERR_DIM, FH_ERR_INVALID, FH_ERR_OOM, FH_ERR_HIP, FH_ERR_LIMIT, FH_ERR_FORMAT, FH_ERR_EXCHANGE = range(8)
 W8A32, W8A8, W8A32_EXACT = 0, 1, 2
 LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
+RECENT_RANGES = 0x100  # OR'd into the logits kind: recent offsets as (begin, end) pairs per row
 
 EXPORTS = (
     "fh_ctx_create", "fh_ctx_destroy", "fh_ctx_set_stream", "fh_ctx_reset_stream", "fh_sync", "fh_last_error",
@@ -49,6 +50,7 @@ EXPORTS = (
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
     "fh_gpt2_stack_create", "fh_gpt2_stack_free", "fh_gpt2_stack_forward_async",
     "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
+    "fh_embed_rows_pos_async",
     "fh_gguf_open", "fh_gguf_close", "fh_gguf_error", "fh_gguf_version", "fh_gguf_tensor_count", "fh_gguf_find_tensor",
     "fh_gguf_tensor_info", "fh_gguf_tensor_data", "fh_gguf_meta_type", "fh_gguf_meta_u64", "fh_gguf_meta_f64",
     "fh_gguf_meta_str", "fh_gguf_meta_array_data", "fh_gguf_read_f32", "fh_gguf_upload_q8_0",
@@ -197,6 +199,7 @@ def lib():
         L.fh_gqa_attention_decode_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, sz, vp, sz, vp]
         L.fh_swiglu_async.argtypes = [vp, vp, vp, sz, sz, sz, vp]
         L.fh_embed_rows_async.argtypes = [vp, vp, sz, sz, vp, sz, vp]
+        L.fh_embed_rows_pos_async.argtypes = [vp, vp, vp, sz, sz, sz, vp, vp, sz, vp, sz, vp]
         u32, u64 = C.c_uint32, C.c_uint64
         L.fh_gguf_open.argtypes = [C.c_char_p, C.POINTER(vp)]
         L.fh_gguf_close.argtypes = [vp]
@@ -1028,6 +1031,14 @@ def swiglu_async(ctx: Context, g, u, rows: int, n: int, ld: int, out):
     ctx.check(lib().fh_swiglu_async(ctx.h, _ptr(g), _ptr(u), rows, n, ld, _ptr(out)))
 
 
+def embed_rows_pos_async(ctx: Context, tok_w, pos_w, vocab: int, max_seq: int, d: int, tokens, pos, rows: int, out,
+                         hist=None, hist_stride: int = 0):
+    """Embedding::embed_one for `rows` sequences (token and position ids on the
+    device); with hist, each row's id is also recorded at hist[r, pos[r]]."""
+    ctx.check(lib().fh_embed_rows_pos_async(ctx.h, _ptr(tok_w), _ptr(pos_w), vocab, max_seq, d, _ptr(tokens), _ptr(pos),
+                                            rows, _ptr(hist), hist_stride, _ptr(out)))
+
+
 def embed_rows_async(ctx: Context, tok_w, vocab: int, d: int, tokens, rows: int, out):
     """LlamaModel::embed for token ids on the device."""
     ctx.check(lib().fh_embed_rows_async(ctx.h, _ptr(tok_w), vocab, d, _ptr(tokens), rows, _ptr(out)))
@@ -1642,3 +1653,185 @@ class GPT2Device:
         for b in self.blocks:
             for key in ("qkv", "out", "up", "down"):
                 b[key].free()
+
+
+class GPT2Batch:
+    """`rows` GPT-2 sequences decoded together on one GPT2Device's weights.
+    Each row is its own CachedTransformer (slm/cached.rs:100-137) with its own
+    KV caches ([rows, capacity, d] per block) and token window; one step feeds
+    every row's token at its own position through the same ops as
+    GPT2Device's per-op path with the linears as GEMMs over the rows (the
+    batched decode of BASELINE's b32 figure and configs[3]), then the final
+    LayerNorm, the head and the fused sampler over the rows.  prefill_async
+    primes equal-length prompts of all rows in one pass (rows x positions as
+    the GEMMs' rows, one attention launch per sequence).  Per row the
+    arithmetic is GPT2Device's, so a row matches ferrum_core's single-sequence
+    decode within the same 1e-5 rule.  Token and position ids live on the
+    device, so a step can be captured in one graph."""
+
+    def __init__(self, model: GPT2Device, rows: int, capacity: int):
+        import torch
+
+        if rows < 1 or rows > 65535 or capacity < 1:
+            raise FerrumHipError(FH_ERR_INVALID, "GPT2Batch: rows in 1 .. 65535 and capacity >= 1")
+        if capacity > model.pos_w.shape[0]:
+            raise DimMismatch(FH_ERR_DIM, f"GPT2Batch: capacity {capacity} exceeds max_seq_len {model.pos_w.shape[0]}")
+        m, dev, B, d = model, "cuda", rows, model.d
+        self.m, self.ctx, self.rows, self.cap = m, m.ctx, rows, capacity
+        self.k = [torch.zeros(B * capacity * d, device=dev) for _ in range(m.layers)]
+        self.v = [torch.zeros(B * capacity * d, device=dev) for _ in range(m.layers)]
+        self.x, self.x2, self.h, self.att, self.proj = (torch.empty((B, d), device=dev) for _ in range(5))
+        self.qkv = torch.empty((B, 3 * d), device=dev)
+        self.mid = torch.empty((B, m.ffn), device=dev)
+        self.z = torch.empty((B, m.vocab), device=dev)
+        self.tokens = torch.zeros(B, dtype=torch.int32, device=dev)
+        self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
+
+    def launches_per_step(self) -> int:
+        """Kernel launches of feed_async (the sampler not included; a linear
+        with its LayerNorm takes two at these row counts, with GELU three)."""
+        return 3 + 8 * self.m.layers if self.rows > 2 else 3 + 6 * self.m.layers
+
+    def _cache(self, i, b):
+        n = self.cap * self.m.d
+        return self.k[i][b * n:(b + 1) * n], self.v[i][b * n:(b + 1) * n]
+
+    def feed_async(self, d_tokens, d_pos, max_pos: int, hist=None, hist_stride: int = 0):
+        """One decode step of every row: token d_tokens[r] at position d_pos[r]
+        (device ids; max_pos bounds the positions and must be below the
+        capacity).  With hist, each row's id is recorded at hist[r, pos[r]].
+        The head's scores land in self.z; nothing is advanced."""
+        m, ctx, B, d = self.m, self.ctx, self.rows, self.m.d
+        if max_pos >= self.cap:
+            raise DimMismatch(FH_ERR_DIM, f"KvCache full ({self.cap} positions): clear and re-prime to continue")
+        embed_rows_pos_async(ctx, m.tok_w, m.pos_w, m.vocab, m.pos_w.shape[0], d, d_tokens, d_pos, B, self.x, hist,
+                             hist_stride)
+        cur, other = self.x, self.x2
+        for i, b in enumerate(m.blocks):
+            if i == 0:
+                layernorm_async(ctx, cur, B, d, b["ln1_g"], b["ln1_b"], self.h)
+                linear_forward_async(ctx, b["qkv"], self.h, B, d, b["qkv_b"], 3 * d, self.qkv)
+            else:
+                linear_ln_async(ctx, b["qkv"], cur, self.proj, other, B, d, b["ln1_g"], b["ln1_b"], b["qkv_b"], 3 * d,
+                                self.qkv)
+                cur, other = other, cur
+            gqa_attention_decode_async(ctx, self.qkv, 3 * d, B, m.heads, m.heads, d // m.heads, self.k[i], self.v[i],
+                                       self.cap, d_pos, max_pos, self.att)
+            linear_forward_async(ctx, b["out"], self.att, B, d, b["out_b"], d, self.proj)
+            linear_ln_async(ctx, b["up"], cur, self.proj, other, B, d, b["ln2_g"], b["ln2_b"], b["up_b"], m.ffn,
+                            self.mid, ACT_GELU)
+            cur, other = other, cur
+            linear_forward_async(ctx, b["down"], self.mid, B, m.ffn, b["down_b"], d, self.proj)
+        linear_ln_async(ctx, m.head, cur, self.proj, None, B, d, m.lnf_g, m.lnf_b, None, 0, self.z)
+
+    def prefill_async(self, d_tokens, n: int, pos0: int = 0):
+        """Positions pos0 .. pos0 + n - 1 of every row at once: d_tokens holds
+        rows x n ids (row-major), the GEMMs run over all rows x n of them and
+        each sequence's attention reads and fills its own caches (GPT2Device.
+        prefill_async per sequence, batched).  Nothing reaches the head: the
+        first decode step feeds the next position."""
+        import torch
+
+        m, ctx, B, d = self.m, self.ctx, self.rows, self.m.d
+        if n <= 0:
+            return
+        if pos0 + n > self.cap:
+            raise DimMismatch(FH_ERR_DIM, f"KvCache full ({self.cap} positions): clear and re-prime to continue")
+        N = B * n
+        if N > 65535:
+            raise FerrumHipError(FH_ERR_LIMIT, f"GPT2Batch.prefill_async: rows x positions = {N} above 65535")
+        dev = "cuda"
+        x, x2, h, att, proj = (torch.empty((N, d), device=dev) for _ in range(5))
+        qkv, mid = torch.empty((N, 3 * d), device=dev), torch.empty((N, m.ffn), device=dev)
+        pos = torch.arange(pos0, pos0 + n, dtype=torch.int32, device=dev).repeat(B)
+        torch.cuda.synchronize()
+        embed_rows_pos_async(ctx, m.tok_w, m.pos_w, m.vocab, m.pos_w.shape[0], d, d_tokens, pos, N, x)
+        cur, other = x, x2
+        for i, b in enumerate(m.blocks):
+            if i == 0:
+                layernorm_async(ctx, cur, N, d, b["ln1_g"], b["ln1_b"], h)
+                linear_forward_async(ctx, b["qkv"], h, N, d, b["qkv_b"], 3 * d, qkv)
+            else:
+                linear_ln_async(ctx, b["qkv"], cur, proj, other, N, d, b["ln1_g"], b["ln1_b"], b["qkv_b"], 3 * d, qkv)
+                cur, other = other, cur
+            for s in range(B):
+                kc, vc = self._cache(i, s)
+                attention_prefill_async(ctx, qkv[s * n:(s + 1) * n], kc, vc, self.cap, d, m.heads, pos0, n,
+                                        att[s * n:(s + 1) * n])
+            linear_forward_async(ctx, b["out"], att, N, d, b["out_b"], d, proj)
+            linear_ln_async(ctx, b["up"], cur, proj, other, N, d, b["ln2_g"], b["ln2_b"], b["up_b"], m.ffn, mid,
+                            ACT_GELU)
+            cur, other = other, cur
+            linear_forward_async(ctx, b["down"], mid, N, m.ffn, b["down_b"], d, proj)
+        # the last block's down projection is not added in: no position here reaches the head
+        self._keep = (x, x2, h, att, proj, qkv, mid, pos)  # alive until the stream has used them
+
+    def generate(self, prompts, max_tokens: int, params: SamplingParams, rngs, eos=None, prefill: bool = True):
+        """GenerativeSLM::token_stream + stream_next (slm/token_stream.rs:66-190)
+        for every row at once, each step on the device: row r's prompt
+        (all of equal length), then max_tokens steps sampled with `params`
+        over row r's window (its prompt and everything sampled so far), the
+        draws from rngs[r] (one next_u64 per sampled step, none when greedy),
+        the sampler's ids feeding the next step's embedding on the device.
+        The prompt is primed in one pass (prefill=True) or position by
+        position.  Windows never outgrow the capacity here (prompt +
+        max_tokens <= capacity; the reference would cut and re-prime).
+        Returns one id list per row, cut at its first EOS."""
+        import torch
+
+        B, ctx = self.rows, self.ctx
+        P = np.asarray(prompts, np.int64)
+        if P.ndim != 2 or P.shape[0] != B or P.shape[1] < 1:
+            raise FerrumHipError(FH_ERR_INVALID, f"GPT2Batch.generate: {B} prompts of one length >= 1")
+        if (P < 0).any() or (P >= 2 ** 32).any():
+            raise FerrumHipError(FH_ERR_INVALID, "GPT2Batch.generate: ids must fit u32")
+        if len(rngs) != B and params.temperature > 0.0:
+            raise FerrumHipError(FH_ERR_INVALID, f"GPT2Batch.generate: {len(rngs)} generators for {B} rows")
+        n0 = P.shape[1]
+        L = n0 + max_tokens
+        if max_tokens < 1:
+            return [[] for _ in range(B)]
+        if L > self.cap:
+            raise DimMismatch(FH_ERR_DIM, f"GPT2Batch.generate: prompt + max_tokens = {L} above the capacity "
+                                          f"{self.cap}")
+        dev, greedy = "cuda", params.temperature <= 0.0
+        hist = torch.zeros((B, L), dtype=torch.int32, device=dev)
+        hist[:, :n0] = torch.from_numpy(P.astype(np.uint32).view(np.int32)).to(dev)
+        ids = torch.zeros((max_tokens + 1, B), dtype=torch.int32, device=dev)  # ids[k]: the ids step k feeds
+        ids[0] = hist[:, n0 - 1]
+        steps = torch.arange(max_tokens, dtype=torch.int32, device=dev)
+        pos = (n0 - 1 + steps)[:, None].repeat(1, B).contiguous()
+        starts = torch.arange(B, dtype=torch.int32, device=dev) * L
+        ranges = torch.stack([starts[None, :].repeat(max_tokens, 1),
+                              starts[None, :] + (n0 + steps)[:, None]], dim=2).contiguous()  # [steps, B, 2]
+        draws = None
+        if not greedy:
+            dr = np.array([[rngs[r].next_u64() for r in range(B)] for _ in range(max_tokens)], dtype=np.uint64)
+            draws = torch.from_numpy(dr.view(np.int64)).to(dev)
+        toks = hist[:, :n0 - 1].contiguous()
+        torch.cuda.synchronize()
+        ctx.sync()
+        if n0 > 1:
+            if prefill:
+                self.prefill_async(toks, n0 - 1)
+            else:
+                for p in range(n0 - 1):
+                    col = toks[:, p].contiguous()
+                    pp = torch.full((B,), p, dtype=torch.int32, device=dev)
+                    torch.cuda.synchronize()
+                    self.feed_async(col, pp, p)
+                    ctx.sync()
+        kind = LOGITS_GPT2_SOFTMAX | RECENT_RANGES
+        for k in range(max_tokens):
+            self.feed_async(ids[k], pos[k], n0 - 1 + k, hist, L)
+            sample_rows_async(ctx, self.z, B, self.m.vocab, params, hist, ranges[k], None if greedy else draws[k],
+                              ids[k + 1], kind)
+        ctx.sync()
+        out = ids[1:].cpu().numpy().astype(np.int64).T
+        res = []
+        for r in range(B):
+            row = [int(t) for t in out[r]]
+            if eos is not None and eos in row:
+                row = row[:row.index(eos)]
+            res.append(row)
+        return res

@@ -96,6 +96,7 @@ pub mod sys {
     pub const FH_W8A32_EXACT: c_int = 2;
     pub const FH_LOGITS_RAW: c_int = 0;
     pub const FH_LOGITS_GPT2_SOFTMAX: c_int = 1;
+    pub const FH_RECENT_RANGES: c_int = 0x100;
     pub const FH_ACT_NONE: c_int = 0;
     pub const FH_ACT_GELU: c_int = 1;
     pub const FH_ROPE_NORM: c_int = 0;
@@ -143,6 +144,7 @@ pub mod sys {
         pub fn fh_gqa_attention_decode_async(ctx: *mut fh_ctx, d_qkv: *const f32, ld: usize, rows: usize, n_heads: usize, n_kv: usize, head_dim: usize, d_k_cache: *mut f32, d_v_cache: *mut f32, capacity: usize, d_pos: *const u32, max_pos: usize, d_out: *mut f32) -> c_int;
         pub fn fh_swiglu_async(ctx: *mut fh_ctx, d_g: *const f32, d_u: *const f32, rows: usize, n: usize, ld: usize, d_out: *mut f32) -> c_int;
         pub fn fh_embed_rows_async(ctx: *mut fh_ctx, d_tok_w: *const f32, vocab: usize, d: usize, d_tokens: *const u32, rows: usize, d_out: *mut f32) -> c_int;
+        pub fn fh_embed_rows_pos_async(ctx: *mut fh_ctx, d_token_w: *const f32, d_pos_w: *const f32, vocab: usize, max_seq: usize, d: usize, d_tokens: *const u32, d_pos: *const u32, rows: usize, d_hist: *mut u32, hist_stride: usize, d_out: *mut f32) -> c_int;
         pub fn fh_add_async(ctx: *mut fh_ctx, d_x: *mut f32, d_y: *const f32, n: usize) -> c_int;
         pub fn fh_attention_decode_async(ctx: *mut fh_ctx, d_qkv: *const f32, d_k_cache: *mut f32, d_v_cache: *mut f32, capacity: usize, d: usize, heads: usize, pos: usize, d_out: *mut f32) -> c_int;
         pub fn fh_attention_prefill_async(ctx: *mut fh_ctx, d_qkv: *const f32, d_k_cache: *mut f32, d_v_cache: *mut f32, capacity: usize, d: usize, heads: usize, pos0: usize, rows: usize, d_out: *mut f32) -> c_int;

@@ -91,6 +91,13 @@ enum { FH_W8A32 = 0, FH_W8A8 = 1, FH_W8A32_EXACT = 2 };
  *                          l = ln(max(p, 1e-12)) (slm/token_stream.rs:134),
  *                          fused into the same kernel. */
 enum { FH_LOGITS_RAW = 0, FH_LOGITS_GPT2_SOFTMAX = 1 };
+/* OR'd into logits_kind: recent_offsets holds a (begin, end) pair per row
+ * (2 * rows entries: row r's recent list is recent[recent_offsets[2r] ..
+ * recent_offsets[2r + 1]]) instead of rows + 1 running offsets, so each row's
+ * window can sit in its own stretch of a [rows, L] buffer (a batched decode,
+ * fh_embed_rows_pos_async).  No reference counterpart: the reference samples
+ * one row at a time (slm/sampling.rs:124).  fh_sample_rows_async only. */
+enum { FH_RECENT_RANGES = 0x100 };
 
 /* slm/sampling.rs:27-38 (SamplingParams without its cancel flag, which is a
  * host-side control checked between tokens, slm/token_stream.rs:126-131). */
@@ -205,7 +212,8 @@ int fh_q8_0_block_dots_async(fh_ctx* ctx, const fh_q8_0* w, const int8_t* d_qx, 
  * renormalise and the inverse-CDF draw pick_by_mass (sampling.rs:109-122).
  *
  * Row r's recent ids are recent[recent_offsets[r] .. recent_offsets[r+1]]
- * (recent_offsets has rows + 1 entries; recent may be NULL when all are empty).
+ * (recent_offsets has rows + 1 entries; recent may be NULL when all are empty),
+ * or with FH_RECENT_RANGES recent[recent_offsets[2r] .. recent_offsets[2r+1]].
  * draws[r] is the one u64 the reference's Rng::next_u64 yields for the row
  * (rng.rs:29-36): the draw is r = (draws[r] >> 40) / 2^24 (Rng::next_f32,
  * rng.rs:39-41), or draws[r] % vocab on the degenerate-softmax fallback
@@ -247,6 +255,18 @@ enum { FH_ACT_NONE = 0, FH_ACT_GELU = 1 };
  * makes the row NaN.  pos >= max_seq -> FH_ERR_DIM, the reference's message. */
 int fh_embed_one_async(fh_ctx* ctx, const float* d_token_w, const float* d_pos_w, size_t vocab, size_t max_seq,
                        size_t d, const uint32_t* d_token, size_t pos, float* d_out);
+/* Embedding::embed_one (layer/embedding.rs:70-90) for `rows` sequences decoded
+ * together: out[r, i] = token_w[tokens[r], i] + pos_w[pos[r], i], token and
+ * position ids on the device (a batched step's sampled ids feed the next step
+ * without a copy).  An id >= vocab or a position >= max_seq makes the row NaN
+ * (the caller checks positions: the reference's error is the host's).  With
+ * d_hist set, each row's id is also recorded at d_hist[r * hist_stride +
+ * pos[r]] (skipped when pos[r] >= hist_stride): the per-row token windows a
+ * batched decode's sampler reads as its recent lists (FH_RECENT_RANGES).
+ * rows <= 65535. */
+int fh_embed_rows_pos_async(fh_ctx* ctx, const float* d_token_w, const float* d_pos_w, size_t vocab, size_t max_seq,
+                            size_t d, const uint32_t* d_tokens, const uint32_t* d_pos, size_t rows, uint32_t* d_hist,
+                            size_t hist_stride, float* d_out);
 /* LayerNorm::forward (layer/norm.rs:46-82) over `rows` rows of width d:
  * ((x - mean) / sqrt(var + 1e-5)) * gamma + beta, biased variance. */
 int fh_layernorm_async(fh_ctx* ctx, const float* d_x, size_t rows, size_t d, const float* d_gamma,

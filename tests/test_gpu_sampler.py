@@ -369,3 +369,57 @@ def test_top_k_with_a_crowded_top(fh, orc, crowd, spread):
         tie[r, rng.choice(vocab, size=80, replace=False)] = 4.0
     run_and_compare(fh, orc, tie, dict(temperature=1.0, top_k=40))
     run_and_compare(fh, orc, tie, dict(temperature=1.0, top_k=40, top_p=0.9))
+
+
+@pytest.mark.parametrize("vocab", [4096, 50257])
+def test_recent_ranges_equal_running_offsets(fh, orc, vocab):
+    """FH_RECENT_RANGES (each row's window in its own stretch of a [rows, L]
+    buffer, as the batched decode keeps them): the same ids as the running-
+    offset form and as the oracle, with an empty window, a window of a whole
+    stretch and a reversed pair (reported at the next sync, as decreasing
+    running offsets are)."""
+    import torch
+
+    import ferrum_hip
+    from sampler_margins import exempt
+
+    rows, L = 6, 300
+    lg = normal_logits(rows, vocab, 23)
+    rng = np.random.default_rng(24)
+    buf = rng.integers(0, 400, size=(rows, L)).astype(np.int32)
+    lg[:, :400] += 1.5
+    lens = [0, 1, 57, 120, 299, 300]
+    kw = dict(temperature=0.8, top_k=40, top_p=0.95, repetition_penalty=1.1)
+    params = ferrum_hip.SamplingParams(**kw)
+    draws = rng.integers(0, 2**64, size=rows, dtype=np.uint64)
+    pairs = np.array([[r * L, r * L + n] for r, n in enumerate(lens)], np.int32)
+    rec = [list(buf[r, :n]) for r, n in enumerate(lens)]
+    flat, off = ferrum_hip._recent_lists(rec, rows)
+    d_lg = torch.from_numpy(lg).cuda()
+    d_draws = torch.from_numpy(draws.view(np.int64)).cuda()
+    a = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    b = torch.zeros(rows, dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ferrum_hip.sample_rows_async(fh, d_lg, rows, vocab, params, torch.from_numpy(buf.ravel()).cuda(),
+                                 torch.from_numpy(pairs.ravel()).cuda(), d_draws, a,
+                                 ferrum_hip.LOGITS_RAW | ferrum_hip.RECENT_RANGES)
+    ferrum_hip.sample_rows_async(fh, d_lg, rows, vocab, params, torch.from_numpy(flat.astype(np.int32)).cuda(),
+                                 torch.from_numpy(off.astype(np.int32)).cuda(), d_draws, b)
+    fh.sync()
+    got = a.cpu().numpy().astype(np.uint32)
+    assert np.array_equal(got, b.cpu().numpy().astype(np.uint32))
+    op = orc.SamplingParams(**kw)
+    for r in range(rows):
+        want, info = orc.sample(lg[r], op, rec[r], int(draws[r]))
+        assert got[r] == want or exempt(info, False), (r, got[r], want)
+    # a reversed pair is reported; the blocking form refuses the flag
+    bad = torch.tensor([0, 5, 9, 3] + [0, 0] * (rows - 2), dtype=torch.int32, device="cuda")
+    torch.cuda.synchronize()
+    ferrum_hip.sample_rows_async(fh, d_lg, rows, vocab, params, torch.from_numpy(buf.ravel()).cuda(), bad, d_draws, a,
+                                 ferrum_hip.LOGITS_RAW | ferrum_hip.RECENT_RANGES)
+    with pytest.raises(ferrum_hip.FerrumHipError, match="recent_offsets decrease") as e:
+        fh.sync()
+    assert e.value.code == ferrum_hip.FH_ERR_INVALID
+    with pytest.raises(ferrum_hip.FerrumHipError, match="FH_RECENT_RANGES"):
+        ferrum_hip.sample_rows(fh, lg, params, rec, draws, ferrum_hip.LOGITS_RAW | ferrum_hip.RECENT_RANGES)
+    fh.sync()
