@@ -785,11 +785,19 @@ __device__ __forceinline__ int block_exponent(float mx) {
 
 }  // namespace
 
+// activation::gelu (activation.rs:9-12) with every product and sum rounded
+// (the kernels here are built with contraction on), so the skinny GEMM's
+// epilogue gives k_gelu's values bit for bit.
+__device__ __forceinline__ float gelu_unfused(float v) {
+#pragma clang fp contract(off)
+    return 0.5f * v * (1.0f + tanhf(0.7978846f * (v + 0.044715f * v * v * v)));
+}
+
 template <int MT, int NT, int BPW>
 __global__ void __launch_bounds__(512)
     k_gemm_skinny(const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
                   const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
-                  int k, int bps, float* __restrict__ part, unsigned* __restrict__ counters) {
+                  int k, int bps, float* __restrict__ part, unsigned* __restrict__ counters, int act) {
     constexpr int OUT = MT * NT * 1024;  // outputs of one workgroup
     // Per wave, [SLOT] floats: during the K loop one Q8_0 block of its
     // activation rows ([MT * 32][36]: the rows land there from row-contiguous
@@ -953,7 +961,9 @@ __global__ void __launch_bounds__(512)
         if (__builtin_expect(bad, 0))
             s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(jj) * k,
                           dsc + static_cast<size_t>(jj) * kb);
-        y[static_cast<size_t>(i) * n + jj] = bias ? s + bv : s;
+        float v = bias ? s + bv : s;
+        if (act == FH_ACT_GELU) v = gelu_unfused(v);
+        y[static_cast<size_t>(i) * n + jj] = v;
     };
     const size_t tiles = gridDim.x;
 #pragma unroll
@@ -1229,7 +1239,7 @@ __global__ void k_zero_counters(unsigned* __restrict__ c, int n) {
 
 template <int MT, int NT, int BPW>
 int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
-                    const fh_scratch* scratch) {
+                    const fh_scratch* scratch, int act) {
     constexpr size_t kMaxWaves = 16 / (MT * NT) < 8 ? 16 / (MT * NT) : 8;
     const size_t kb = w->k / 32, tiles = (w->n + 32 * NT - 1) / (32 * NT);
     size_t splits = 1;
@@ -1275,7 +1285,7 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), block(static_cast<unsigned>(64 * kw));
     hipLaunchKernelGGL((k_gemm_skinny<MT, NT, BPW>), grid, block, lds, ctx->stream, x, w->qs, w->d, w->rexp, bias, y,
                        static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(bps), part,
-                       counters);
+                       counters, act);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -1309,7 +1319,7 @@ constexpr size_t kWideMinTiles = 1024;
 // splits, so more workgroups: 896 x 896 7.9 -> 6.9 us at m = 32, 10.4 -> 9.2
 // us at m = 64; a 3072-wide one slows down).
 int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
-                  const fh_scratch* scratch = nullptr) {
+                  const fh_scratch* scratch = nullptr, int act = FH_ACT_NONE) {
     const size_t t32 = (w->n + 31) / 32;
     if (t32 >= kWideMinTiles && (w->k == 768 || w->k == 896 || w->k == 1024)) {
         // 32 rows per launch: at m = 64 two launches, each streaming the
@@ -1324,18 +1334,18 @@ int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const
                                          : launch_wide<32>(ctx, w, xr, mr, bias, yr);
             if (rc) return rc;
         }
-        return FH_OK;
+        return act == FH_ACT_GELU ? fh_launch_gelu(ctx, y, m * w->n) : FH_OK;
     }
     if (m <= 32) {
-        if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y, scratch);
-        if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y, scratch);
-        if (t32 >= 64) return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y, scratch);
-        return launch_skinny_t<1, 1, 1>(ctx, w, x, m, bias, y, scratch);
+        if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y, scratch, act);
+        if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y, scratch, act);
+        if (t32 >= 64) return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y, scratch, act);
+        return launch_skinny_t<1, 1, 1>(ctx, w, x, m, bias, y, scratch, act);
     }
-    if (t32 >= 4 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y, scratch);
-    if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y, scratch);
-    if (t32 >= 64) return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y, scratch);
-    return launch_skinny_t<2, 1, 1>(ctx, w, x, m, bias, y, scratch);  // 896 x 896: 10.4 -> 9.2 us
+    if (t32 >= 4 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y, scratch, act);
+    if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y, scratch, act);
+    if (t32 >= 64) return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y, scratch, act);
+    return launch_skinny_t<2, 1, 1>(ctx, w, x, m, bias, y, scratch, act);  // 896 x 896: 10.4 -> 9.2 us
 }
 
 }  // namespace
@@ -1381,11 +1391,14 @@ int fh_launch_skinny_scratch(fh_ctx* ctx, const fh_q8_0* w, const float* x, size
 // Tile choice: m <= 64 takes the skinny kernel; otherwise the 256 x 256
 // weight-split tile (eight waves) once it still yields a tile per CU, the 128 x 128 tile at two
 // tiles per CU, else 64 x 64, else 32 x 32 outputs with four waves splitting K.
-int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                         int act) {
     const size_t cus = static_cast<size_t>(ctx->num_cus);
-    if (m <= 64) return launch_skinny(ctx, w, x, m, bias, y);
-    if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus) return launch_wsplit_x<256, 256, 2, 4>(ctx, w, x, m, bias, y);
-    if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) return launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
-    if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) return launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
-    return launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);
+    if (m <= 64) return launch_skinny(ctx, w, x, m, bias, y, nullptr, act);  // GELU in its epilogue
+    int rc;
+    if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus) rc = launch_wsplit_x<256, 256, 2, 4>(ctx, w, x, m, bias, y);
+    else if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) rc = launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
+    else if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) rc = launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
+    else rc = launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);
+    return rc == FH_OK && act == FH_ACT_GELU ? fh_launch_gelu(ctx, y, m * w->n) : rc;
 }

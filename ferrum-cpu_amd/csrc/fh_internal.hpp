@@ -130,8 +130,10 @@ struct fh_ln_args {
 };
 int fh_launch_linear_ln_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_ln_args& ln,
                               const float* bias, float* y, int act);
+// act (FH_ACT_*) is applied to the outputs: in the skinny GEMM's epilogue at
+// m <= 64, else by the separate GELU kernel.
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
-                         const float* bias, float* y);
+                         const float* bias, float* y, int act = FH_ACT_NONE);
 // The decode GEMV alone (m <= 2, W8A32, no workspace); -1 when the row is too
 // long for it (the caller then takes the GEMM).
 int fh_launch_gemv_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y);

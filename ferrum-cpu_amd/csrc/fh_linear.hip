@@ -421,9 +421,7 @@ int fh_launch_linear_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t
         int rc = m == 1 ? dispatch_gemv<1>(ctx, w, x, bias, y, act) : dispatch_gemv<2>(ctx, w, x, bias, y, act);
         if (rc >= 0) return rc;
     }
-    int rc = fh_launch_gemm_w8a32(ctx, w, x, m, bias, y);
-    if (rc == FH_OK && act == FH_ACT_GELU) rc = fh_launch_gelu(ctx, y, m * w->n);
-    return rc;
+    return fh_launch_gemm_w8a32(ctx, w, x, m, bias, y, act);
 }
 
 int fh_launch_gemv_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {

@@ -1688,9 +1688,11 @@ class GPT2Batch:
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
 
     def launches_per_step(self) -> int:
-        """Kernel launches of feed_async (the sampler not included; a linear
-        with its LayerNorm takes two at these row counts, with GELU three)."""
-        return 3 + 8 * self.m.layers if self.rows > 2 else 3 + 6 * self.m.layers
+        """Kernel launches of feed_async (the sampler not included): above two
+        rows a linear with its LayerNorm takes two (the add + LayerNorm kernel,
+        then the GEMM with GELU in its epilogue); at one or two rows the
+        decode GEMV forms the LayerNorm itself."""
+        return 3 + 7 * self.m.layers if self.rows > 2 else 3 + 5 * self.m.layers
 
     def _cache(self, i, b):
         n = self.cap * self.m.d
