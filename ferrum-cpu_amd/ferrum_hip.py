@@ -473,18 +473,34 @@ class GPT2Window:
         return False
 
 
+def cancelled(cancel) -> bool:
+    """SamplingParams::is_cancelled (slm/sampling.rs:55-60) for the host-side
+    flag: None (never cancelled), an object with is_set() (threading.Event,
+    settable from any thread), a callable returning a bool, or a bool."""
+    if cancel is None:
+        return False
+    if hasattr(cancel, "is_set"):
+        return bool(cancel.is_set())
+    if callable(cancel):
+        return bool(cancel())
+    return bool(cancel)
+
+
 def gpt2_decode(ctx: Context, forward, prompt, max_tokens: int, params: SamplingParams, rng: Rng,
-                capacity: int, eos=None, bos: int = 0):
+                capacity: int, eos=None, bos: int = 0, cancel=None):
     """Token-level stream_next loop (slm/token_stream.rs:121-190).
     forward(window_ids, reprime) -> raw head scores z of the next position
     (reprime: the whole window was (re)fed, else only its last id).  Each step
-    samples with the softmax -> ln(max(p, 1e-12)) bridge fused into the
-    sampler, the window as the penalty history, and one draw from rng unless
-    greedy.  Stops at max_tokens or EOS (not appended).  Returns the ids."""
+    checks `cancel` first (stopping before it draws), then samples with the
+    softmax -> ln(max(p, 1e-12)) bridge fused into the sampler, the window as
+    the penalty history, and one draw from rng unless greedy.  Stops at
+    max_tokens or EOS (drawn, not appended).  Returns the ids."""
     win = GPT2Window(capacity, prompt, bos)
     z = forward(list(win.ids), True)
     out = []
     while len(out) < max_tokens:
+        if cancelled(cancel):
+            break
         nxt = sample_with_params(ctx, z, params, win.ids, rng, LOGITS_GPT2_SOFTMAX)
         if eos is not None and nxt == eos:
             break
@@ -495,11 +511,13 @@ def gpt2_decode(ctx: Context, forward, prompt, max_tokens: int, params: Sampling
 
 
 def llama_decode(ctx: Context, forward_one, prompt, max_new: int, params: SamplingParams, rng: Rng,
-                 context_len: int, stops=()):
+                 context_len: int, stops=(), cancel=None):
     """LlamaModel::generate_inner at the token level (llm.rs:706-754): a
     non-empty prompt shorter than the context, max_new clipped to
     context - prompt, every prompt and generated id as the penalty history, a
-    stop id returned but not fed.  forward_one(token) -> raw logits."""
+    stop id returned but not fed.  `cancel` (see cancelled) is checked before
+    every prompt position (a cancel there returns nothing) and before every
+    draw.  forward_one(token) -> raw logits."""
     prompt = [int(t) for t in prompt]
     if not prompt:
         raise DimMismatch(FH_ERR_DIM, "prompt must be non-empty")
@@ -509,9 +527,13 @@ def llama_decode(ctx: Context, forward_one, prompt, max_new: int, params: Sampli
     max_new = min(int(max_new), context_len - len(prompt))
     logits = None
     for tok in prompt:
+        if cancelled(cancel):
+            return []
         logits = forward_one(tok)
     out, recent = [], list(prompt)
     for _ in range(max_new):
+        if cancelled(cancel):
+            break
         nxt = sample_with_params(ctx, logits, params, recent, rng, LOGITS_RAW)
         out.append(nxt)
         if nxt in stops:
@@ -1571,19 +1593,26 @@ class GPT2Device:
         self._keep = (x, x2, h, qkv, att, proj, mid)  # alive until the stream has used them
 
     def generate(self, prompt, max_tokens: int, params: SamplingParams, rng: Rng, eos=None, bos: int = 0,
-                 prefill: bool = False):
+                 prefill: bool = False, cancel=None, chunk: int = 32):
         """GenerativeSLM::token_stream + stream_next (slm/token_stream.rs:66-190)
-        with every step on the device: the prompt is fed position by position,
-        then each step runs the block stack, the head and the fused sampler,
-        which writes its id straight into the device history (the penalty
-        window) where the next step's embedding reads it.  The draws are the
-        ones gpt2_decode takes from rng (one next_u64 per sampled step, none
-        when greedy), generated up front.  Same kernels and order as
-        gpt2_decode over forward(), so the same ids; the host only sees the ids
-        at the end (an EOS ends the returned list as in the reference; the
-        steps computed past it are discarded).  A run that would outgrow the
-        window (prompt + max_tokens > context: the reference cuts and
-        re-primes) takes the host loop instead.
+        with every step on the device: the prompt is primed, then each step
+        runs the block stack, the head and the fused sampler, which writes its
+        id straight into the device history (the penalty window) where the
+        next step's embedding reads it.  Same kernels and order as gpt2_decode
+        over forward(), so the same ids.
+
+        The steps run in chunks of `chunk`; between chunks the host reads the
+        chunk's ids and stops at the first EOS (drawn, not returned, as
+        stream_next does) and checks `cancel` (see cancelled): a set flag ends
+        the run before the next chunk, which is where a device-resident loop
+        can see it (the reference checks once per token; a flag set before
+        the call returns nothing).  Steps a chunk computed past an EOS are
+        discarded.  The draws are rng's (one next_u64 per sampled step, none
+        when greedy): they are taken from a copy of rng up front, and rng
+        itself is then advanced by exactly the draws of the steps returned
+        plus the EOS step, so it ends in ferrum_core's state.  A run that
+        would outgrow the window (prompt + max_tokens > context: the reference
+        cuts and re-primes) takes the host loop instead.
 
         prefill=True primes the prompt in one pass (prefill_async: its
         positions as rows of GEMMs) instead of position by position: much
@@ -1594,15 +1623,19 @@ class GPT2Device:
         win = GPT2Window(self.cap, prompt, bos)
         n0 = len(win.ids)
         if n0 + max_tokens > self.cap or self.stack is None or not self.fused:
-            return gpt2_decode(self.ctx, self.forward, prompt, max_tokens, params, rng, self.cap, eos, bos)
+            return gpt2_decode(self.ctx, self.forward, prompt, max_tokens, params, rng, self.cap, eos, bos, cancel)
+        if max_tokens <= 0 or cancelled(cancel):
+            return []
         ctx, dev = self.ctx, "cuda"
+        chunk = max(int(chunk), 1)
         greedy = params.temperature <= 0.0
         hist = torch.zeros(n0 + max_tokens, dtype=torch.int32, device=dev)
         hist[:n0] = torch.tensor(win.ids, dtype=torch.int32, device=dev)
         offs = torch.tensor([[0, n0 + k] for k in range(max_tokens)], dtype=torch.int32, device=dev)
         draws = None
         if not greedy:
-            d = np.array([rng.next_u64() for _ in range(max_tokens)], dtype=np.uint64)
+            probe = Rng.from_state(rng.state)
+            d = np.array([probe.next_u64() for _ in range(max_tokens)], dtype=np.uint64)
             draws = torch.from_numpy(d.view(np.int64)).to(dev)
         torch.cuda.synchronize()
         ctx.sync()
@@ -1613,16 +1646,32 @@ class GPT2Device:
             for p in range(n0 - 1):
                 ctx.check(lib().fh_gpt2_stack_forward_async(ctx.h, self.stack, hist.data_ptr() + 4 * p, p,
                                                             _ptr(self.x)))
-        for k in range(max_tokens):
-            p = n0 - 1 + k
-            self.feed_async(hist.data_ptr() + 4 * p, p)
-            sample_rows_async(ctx, self.z, 1, self.vocab, params, hist, offs[k], None if greedy else draws[k:],
-                              hist.data_ptr() + 4 * (n0 + k), LOGITS_GPT2_SOFTMAX)
-        ctx.sync()
-        self.pos = n0 + max_tokens - 1
-        out = [int(t) for t in hist[n0:].cpu().numpy()]
-        if eos is not None and eos in out:
-            out = out[:out.index(eos)]
+        out, used, k = [], 0, 0
+        while k < max_tokens:
+            if k > 0 and cancelled(cancel):
+                break
+            c = min(chunk, max_tokens - k)
+            for j in range(k, k + c):
+                p = n0 - 1 + j
+                self.feed_async(hist.data_ptr() + 4 * p, p)
+                sample_rows_async(ctx, self.z, 1, self.vocab, params, hist, offs[j], None if greedy else draws[j:],
+                                  hist.data_ptr() + 4 * (n0 + j), LOGITS_GPT2_SOFTMAX)
+            ctx.sync()
+            got = [int(t) for t in hist[n0 + k:n0 + k + c].cpu().numpy()]
+            k += c
+            stop = False
+            for t in got:
+                used += 1
+                if eos is not None and t == eos:
+                    stop = True
+                    break
+                out.append(t)
+            if stop:
+                break
+        if not greedy:
+            for _ in range(used):
+                rng.next_u64()
+        self.pos = n0 - 1 + k
         return out
 
     def forward(self, ids, reprime: bool):
@@ -1768,17 +1817,28 @@ class GPT2Batch:
         # the last block's down projection is not added in: no position here reaches the head
         self._keep = (x, x2, h, att, proj, qkv, mid, pos)  # alive until the stream has used them
 
-    def generate(self, prompts, max_tokens: int, params: SamplingParams, rngs, eos=None, prefill: bool = True):
+    def generate(self, prompts, max_tokens: int, params: SamplingParams, rngs, eos=None, prefill: bool = True,
+                 cancel=None, chunk: int = 32):
         """GenerativeSLM::token_stream + stream_next (slm/token_stream.rs:66-190)
         for every row at once, each step on the device: row r's prompt
-        (all of equal length), then max_tokens steps sampled with `params`
-        over row r's window (its prompt and everything sampled so far), the
-        draws from rngs[r] (one next_u64 per sampled step, none when greedy),
-        the sampler's ids feeding the next step's embedding on the device.
-        The prompt is primed in one pass (prefill=True) or position by
-        position.  Windows never outgrow the capacity here (prompt +
+        (all of equal length), then up to max_tokens steps sampled with
+        `params` over row r's window (its prompt and everything sampled so
+        far), the draws from rngs[r] (one next_u64 per sampled step, none when
+        greedy), the sampler's ids feeding the next step's embedding on the
+        device.  The prompt is primed in one pass (prefill=True) or position
+        by position.  Windows never outgrow the capacity here (prompt +
         max_tokens <= capacity; the reference would cut and re-prime).
-        Returns one id list per row, cut at its first EOS."""
+
+        Each row is its own stream: it stops at its first EOS (drawn, not
+        returned).  The steps run in chunks of `chunk`; between chunks the
+        host reads the ids, and the run ends once every row has stopped or
+        `cancel` (see cancelled) is set (checked before each chunk: the
+        granularity at which a device-resident loop sees the flag).  A row
+        that has stopped is still computed with the others until the run ends
+        and those steps are discarded (rows are independent, so the other
+        rows do not change).  rngs[r] is advanced by exactly the draws of row
+        r's returned steps plus its EOS step, so each ends in ferrum_core's
+        state.  Returns one id list per row."""
         import torch
 
         B, ctx = self.rows, self.ctx
@@ -1791,12 +1851,13 @@ class GPT2Batch:
             raise FerrumHipError(FH_ERR_INVALID, f"GPT2Batch.generate: {len(rngs)} generators for {B} rows")
         n0 = P.shape[1]
         L = n0 + max_tokens
-        if max_tokens < 1:
+        if max_tokens < 1 or cancelled(cancel):
             return [[] for _ in range(B)]
         if L > self.cap:
             raise DimMismatch(FH_ERR_DIM, f"GPT2Batch.generate: prompt + max_tokens = {L} above the capacity "
                                           f"{self.cap}")
         dev, greedy = "cuda", params.temperature <= 0.0
+        chunk = max(int(chunk), 1)
         hist = torch.zeros((B, L), dtype=torch.int32, device=dev)
         hist[:, :n0] = torch.from_numpy(P.astype(np.uint32).view(np.int32)).to(dev)
         ids = torch.zeros((max_tokens + 1, B), dtype=torch.int32, device=dev)  # ids[k]: the ids step k feeds
@@ -1808,7 +1869,8 @@ class GPT2Batch:
                               starts[None, :] + (n0 + steps)[:, None]], dim=2).contiguous()  # [steps, B, 2]
         draws = None
         if not greedy:
-            dr = np.array([[rngs[r].next_u64() for r in range(B)] for _ in range(max_tokens)], dtype=np.uint64)
+            probes = [Rng.from_state(r.state) for r in rngs]
+            dr = np.array([[probes[r].next_u64() for r in range(B)] for _ in range(max_tokens)], dtype=np.uint64)
             draws = torch.from_numpy(dr.view(np.int64)).to(dev)
         toks = hist[:, :n0 - 1].contiguous()
         torch.cuda.synchronize()
@@ -1824,16 +1886,32 @@ class GPT2Batch:
                     self.feed_async(col, pp, p)
                     ctx.sync()
         kind = LOGITS_GPT2_SOFTMAX | RECENT_RANGES
-        for k in range(max_tokens):
-            self.feed_async(ids[k], pos[k], n0 - 1 + k, hist, L)
-            sample_rows_async(ctx, self.z, B, self.m.vocab, params, hist, ranges[k], None if greedy else draws[k],
-                              ids[k + 1], kind)
-        ctx.sync()
-        out = ids[1:].cpu().numpy().astype(np.int64).T
-        res = []
-        for r in range(B):
-            row = [int(t) for t in out[r]]
-            if eos is not None and eos in row:
-                row = row[:row.index(eos)]
-            res.append(row)
+        res = [[] for _ in range(B)]
+        used = [0] * B
+        live = [True] * B
+        k = 0
+        while k < max_tokens and any(live):
+            if k > 0 and cancelled(cancel):
+                break
+            c = min(chunk, max_tokens - k)
+            for j in range(k, k + c):
+                self.feed_async(ids[j], pos[j], n0 - 1 + j, hist, L)
+                sample_rows_async(ctx, self.z, B, self.m.vocab, params, hist, ranges[j],
+                                  None if greedy else draws[j], ids[j + 1], kind)
+            ctx.sync()
+            got = ids[k + 1:k + 1 + c].cpu().numpy().astype(np.int64)  # [c, B]
+            k += c
+            for r in range(B):
+                for t in got[:, r]:
+                    if not live[r]:
+                        break
+                    used[r] += 1
+                    if eos is not None and int(t) == eos:
+                        live[r] = False
+                    else:
+                        res[r].append(int(t))
+        if not greedy:
+            for r in range(B):
+                for _ in range(used[r]):
+                    rngs[r].next_u64()
         return res

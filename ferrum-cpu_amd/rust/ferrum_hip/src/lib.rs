@@ -234,6 +234,16 @@ pub enum Numerics {
     W8A32Exact,
 }
 
+/// The drop-in default is the bit-exact mode: `ops::linear_forward`'s bits on
+/// the f32 expansion, which the reference plan's packed-Q8_0 contract
+/// (`q8_0_packed_forward_equals_expanded`) asserts.  `W8A32` is the opt-in
+/// fast mode (within the 1e-5 rule, not bit-identical).
+impl Default for Numerics {
+    fn default() -> Self {
+        Numerics::W8A32Exact
+    }
+}
+
 impl Numerics {
     fn code(self) -> c_int {
         match self {

@@ -136,6 +136,38 @@ def test_attention_decode_matches_oracle(fh, orc, d, heads, T):
     assert np.array_equal(host(fh, kc), ko, equal_nan=True) and np.array_equal(host(fh, vc), vo, equal_nan=True)
 
 
+@pytest.mark.parametrize(
+    "d,heads,blocks",
+    [(1024, 16, [(0, 511), (511, 1)]),      # configs[3]'s prime: 511 prompt positions, then the first step's row
+     (768, 12, [(0, 128), (128, 200)]),     # a second block reading the first block's cache rows
+     (128, 4, [(0, 33), (33, 64), (97, 3)]),
+     (64, 1, [(0, 70)])])
+def test_attention_prefill_matches_oracle(fh, orc, d, heads, blocks):
+    """fh_attention_prefill_async: a block of consecutive positions of one
+    sequence at once (row r of qkv is position pos0 + r; every row's k and v go
+    into the cache first, then row r attends over positions 0 .. pos0 + r).
+    Each row against the oracle's attention for that one position
+    (layer/transformer.rs:242-279, fed position by position), and the caches
+    bit-equal."""
+    import ferrum_hip
+
+    T = blocks[-1][0] + blocks[-1][1]
+    cap = T + 5
+    rng = np.random.default_rng(d * 3 + T)
+    qkv = (rng.standard_normal((T, 3 * d)) * 1.5).astype(np.float32)
+    kc, vc = dev(np.full((cap, d), np.nan, np.float32)), dev(np.full((cap, d), np.nan, np.float32))
+    ko, vo = np.full((cap, d), np.nan, np.float32), np.full((cap, d), np.nan, np.float32)
+    for pos0, n in blocks:
+        tq = dev(qkv[pos0:pos0 + n])
+        out = dev(np.zeros((n, d), np.float32))
+        ready()
+        ferrum_hip.attention_prefill_async(fh, tq, kc, vc, cap, d, heads, pos0, n, out)
+        got = host(fh, out)
+        for r in range(n):
+            close(got[r], orc.attention_decode(qkv[pos0 + r], ko, vo, heads, pos0 + r), 1e-5)
+    assert np.array_equal(host(fh, kc), ko, equal_nan=True) and np.array_equal(host(fh, vc), vo, equal_nan=True)
+
+
 def test_attention_decode_errors(fh):
     import ferrum_hip
 

@@ -291,3 +291,60 @@ def test_tiny_qwen_generate_replays_on_the_oracle(fh, orc):
         recent.append(tok)
         if step + 1 < len(got):
             z = ref.feed(tok)
+
+
+def test_qwen2_05b_step_matches_oracle(fh, orc):
+    """BASELINE configs[4] at its own depth: the Qwen2-0.5B shape (24 blocks,
+    d 896, 14 / 2 heads of 64, SwiGLU 4864, vocabulary 151936, q/k/v biases,
+    tied head; N(0, 0.02) Q8_0 weights) as LlamaModel::forward_one walks it
+    (llm.rs:606-616) for three sequences at positions 0, 97 and 255 whose
+    caches hold seeded rows before that position, two steps each (the second
+    reads the row the first wrote).  Every row's logits against the oracle's
+    within 1e-5 of the row's largest, and all of them anchored to the float64
+    step (accuracy_against_f64)."""
+    import torch
+
+    import ferrum_hip
+    from accuracy import accuracy_against_f64
+
+    cfg = llama_tiny.QWEN05
+    w = llama_tiny.make_weights(orc, cfg, 31, True, True, std=0.02)
+    rows, start, cap = 3, [0, 97, 255], cfg["context"]
+    kvd = cfg["n_kv"] * cfg["head_dim"]
+    m = ferrum_hip.LlamaDevice.from_weights(fh, w, cfg, rows)
+    try:
+        refs = [llama_tiny.OracleLlamaRow(orc, w, cfg, s) for s in start]
+        kc = [[np.zeros((cap, kvd)) for _ in range(rows)] for _ in range(cfg["layers"])]
+        vc = [[np.zeros((cap, kvd)) for _ in range(rows)] for _ in range(cfg["layers"])]
+        rng = np.random.default_rng(77)
+        for i, b in enumerate(m.blocks):
+            kd, vd = b["k"].view(rows, cap, kvd), b["v"].view(rows, cap, kvd)
+            for r, s in enumerate(start):
+                kk = rng.standard_normal((s, kvd), dtype=np.float32)
+                vv = rng.standard_normal((s, kvd), dtype=np.float32)
+                refs[r].k[i][:s], refs[r].v[i][:s] = kk, vv
+                kc[i][r][:s], vc[i][r][:s] = kk, vv
+                kd[r, :s] = torch.from_numpy(kk).cuda()
+                vd[r, :s] = torch.from_numpy(vv).cuda()
+        got_all, want_all, exact_all = [], [], []
+        for t in range(2):
+            toks = rng.integers(0, cfg["vocab"], rows)
+            pos = [s + t for s in start]
+            m.tokens.copy_(dev(toks.astype(np.int32)))
+            m.pos.copy_(dev(np.array(pos, np.int32)))
+            ready()
+            m.feed_async(max(pos))
+            got = host(fh, m.z)
+            exact = llama_tiny.step_f64(orc, w, cfg, toks, pos, kc, vc)
+            for r in range(rows):
+                want = refs[r].feed(toks[r])
+                err = float(np.abs(got[r].astype(np.float64) - want).max())
+                print(f"qwen2-0.5b step {t} row {r} (position {pos[r]}): max |diff| {err:.3e}, "
+                      f"max |logit| {np.abs(want).max():.3e}")
+                assert err <= 1e-5 * np.abs(want).max(), (t, r, err)
+                got_all.append(got[r])
+                want_all.append(want)
+                exact_all.append(exact[r])
+        accuracy_against_f64(np.stack(got_all), np.stack(want_all), np.stack(exact_all), "qwen2-0.5b step")
+    finally:
+        m.free()

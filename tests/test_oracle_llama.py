@@ -181,3 +181,32 @@ def test_swiglu_matches_the_closed_form(orc):
     np.testing.assert_allclose(orc.swiglu(g, u), want, rtol=2e-6, atol=1e-30)
     edge = orc.swiglu(np.array([0.0, 100.0, -100.0, -1e30], np.float32), np.ones(4, np.float32))
     assert edge[0] == 0.0 and edge[1] == 100.0 and edge[2] <= 0.0 and edge[3] == 0.0
+
+
+def test_float64_step_agrees_with_the_oracle(orc):
+    """llama_tiny.step_f64 (the float64 anchor of the whole-model GPU tests) is
+    an independent restatement of LlamaModel::forward_one: on the tiny Qwen2
+    and Llama shapes (NEOX and partial NORM rope, biases, tied and untied
+    heads) it agrees with the oracle's f32 decode to f32 rounding over three
+    positions, and a planted mistake (the rope pairs of the other type) does
+    not."""
+    import llama_tiny
+
+    for cfg, biases, tied in ((llama_tiny.QWEN, True, True), (llama_tiny.LLAMA, False, False)):
+        w = llama_tiny.make_weights(orc, cfg, 5, biases, tied)
+        kvd = cfg["n_kv"] * cfg["head_dim"]
+        ref = llama_tiny.OracleLlamaRow(orc, w, cfg, 0)
+        kc = [[np.zeros((cfg["context"], kvd))] for _ in range(cfg["layers"])]
+        vc = [[np.zeros((cfg["context"], kvd))] for _ in range(cfg["layers"])]
+        bad = dict(cfg, rope_type=1 - cfg["rope_type"])
+        kb = [[np.zeros((cfg["context"], kvd))] for _ in range(cfg["layers"])]
+        vb = [[np.zeros((cfg["context"], kvd))] for _ in range(cfg["layers"])]
+        worst_bad = 0.0
+        for pos, tok in enumerate((3, 77, 5)):
+            want = ref.feed(tok)
+            got = llama_tiny.step_f64(orc, w, cfg, [tok], [pos], kc, vc)[0]
+            scale = np.abs(want).max()
+            assert np.abs(got - want).max() <= 2e-5 * scale, (cfg["vocab"], pos)
+            worst_bad = max(worst_bad, float(np.abs(llama_tiny.step_f64(orc, w, bad, [tok], [pos], kb, vb)[0]
+                                                    - want).max() / scale))
+        assert worst_bad > 1e-3
