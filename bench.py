@@ -56,7 +56,7 @@ B32 = 32
 # of 32 prompts x 512 tokens = 16,384 activation rows per linear.
 MED_D, MED_L, MED_FFN, MED_M = 1024, 24, 4096, 32 * 512
 MED_SHAPES = [(3 * MED_D, MED_D), (MED_D, MED_D), (MED_FFN, MED_D), (MED_D, MED_FFN)]
-F16_DENSE_TFLOPS, I8_DENSE_TOPS = 2500.0, 5000.0
+F16_DENSE_TFLOPS, I8_DENSE_TOPS, F32_MATRIX_TFLOPS = 2500.0, 5000.0, 157.3
 HEADS, CTX, FULL_POS = 12, 1024, 255  # GPT-2-124M attention; the whole-step leg's position
 
 COPY_BYTES = 256 << 20
@@ -687,9 +687,48 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
         for w in lw:
             w.free()
     del x, y, xb, yb, lb
+    # Config 4's prompt attention alone: per block one launch for the 32
+    # prompts (fh_attention_prefill_seqs_async: 511 positions each, 16 heads of
+    # 64, fp32 matrix cores), 24 launches in a graph.  Useful flops: per
+    # (sequence, head) sum over rows r of (r + 1) keys x 64 dims x 2 products
+    # (q.k and p.v) x 2 flops.
+    pa_rows, pa_cap = 511, 576
+    pa_qkv = torch.randn((B32 * pa_rows, 3 * MED_D), generator=gen, device=dev)
+    pa_k = torch.zeros((B32, pa_cap, MED_D), device=dev)
+    pa_v = torch.zeros((B32, pa_cap, MED_D), device=dev)
+    pa_out = torch.empty((B32 * pa_rows, MED_D), device=dev)
+
+    def pa_step():
+        for _ in range(MED_L):
+            fh.attention_prefill_seqs_async(ctx, pa_qkv, pa_k, pa_v, pa_cap * MED_D, pa_cap, MED_D, 16, 0, pa_rows,
+                                            B32, pa_out)
+
+    pa_step()
+    torch.cuda.synchronize()
+    ga = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(ga):
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        pa_step()
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    ga.replay()
+    torch.cuda.synchronize()
+    e0.record()
+    for _ in range(5):
+        ga.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    pa_ms = e0.elapsed_time(e1) / 5
+    pa_flops = MED_L * B32 * 16 * (pa_rows * (pa_rows + 1) / 2) * 64 * 4
+    pa_tflops = pa_flops / (pa_ms * 1e-3) / 1e12
+    prompt_attention = {"ms": round(pa_ms, 3), "tflops": round(pa_tflops, 1),
+                        "frac_fp32_matrix_peak": round(pa_tflops / F32_MATRIX_TFLOPS, 4),
+                        "what": "configs[3]'s prompt attention: 24 blocks x 32 prompts x 511 positions x 16 heads of "
+                                "64, causal, one launch per block (k/v store + fp32-MFMA flash attention); useful "
+                                "flops of the causal triangle"}
+    del ga, pa_qkv, pa_k, pa_v, pa_out
     # Config 4 as a run: GPT-2-medium (N(0, 0.02) Q8_0 weights), 32 prompts
     # of 512 random ids primed in one pass (GPT2Batch.prefill_async: the
-    # linears at m = 32 x 511, one attention launch per prompt and block),
+    # linears at m = 32 x 511, one attention launch per block for all prompts),
     # then 64 greedy steps at batch 32 (every row's attention over its own
     # cache; the sampler's ids feed the next step on the device).  Wall clock
     # around the whole run; the prime from a one-step run.
@@ -734,7 +773,7 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
             "frac_i8_dense_peak": round(tflops / I8_DENSE_TOPS, 4),
             "mfma_f16_tflops": round(3 * tflops, 1), "mfma_frac_f16_dense_peak": round(3 * tflops / F16_DENSE_TFLOPS, 4),
             "library_f16_same_mfma_work_ms": round(lib_ms, 3), "vs_library": round(lib_ms / ms, 3),
-            "config4_run": config4,
+            "config4_run": config4, "prompt_attention": prompt_attention,
             "decode_b32": {"ms_per_step": round(dms, 4), "tok_s": round(B32 * 1000.0 / dms, 1),
                            "weight_bytes": dbytes, "weight_GBps": round(dbytes / (dms * 1e-3) / 1e9, 1),
                            "what": "gpt2-medium linears of a batch-32 step: 96 Q8_0 GEMMs + head + greedy sampler, "

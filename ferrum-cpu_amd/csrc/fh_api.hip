@@ -746,7 +746,32 @@ int fh_attention_prefill_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache
     if (d > 0x7FFFFFFFu || capacity > 0x7FFFFFFFu || capacity * d > (size_t(1) << 40) || rows > 65535)
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_attention_prefill: cache or block too large");
     FH_ON_DEVICE(ctx);
-    return fh_launch_attention_prefill(ctx, d_qkv, d_k_cache, d_v_cache, d, heads, pos0, rows, d_out);
+    return fh_launch_attention_prefill_seqs(ctx, d_qkv, d_k_cache, d_v_cache, 0, d, heads, pos0, rows, 1, d_out);
+}
+
+int fh_attention_prefill_seqs_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
+                                    size_t seq_stride, size_t capacity, size_t d, size_t heads, size_t pos0,
+                                    size_t rows, size_t seqs, float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rows == 0 || seqs == 0) return FH_OK;
+    if (!d_qkv || !d_k_cache || !d_v_cache || !d_out)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_attention_prefill: a pointer is NULL");
+    if (heads == 0 || d == 0 || d % heads != 0)
+        return fh_fail(ctx, FH_ERR_DIM, "fh_attention_prefill: heads (" + std::to_string(heads) +
+                                            ") must divide the embedding dim (" + std::to_string(d) + ")");
+    if (pos0 + rows > capacity)
+        return fh_fail(ctx, FH_ERR_DIM, "KvCache full (" + std::to_string(capacity) +
+                                            " positions): clear and re-prime to continue");
+    if (d > 0x7FFFFFFFu || capacity > 0x7FFFFFFFu || capacity * d > (size_t(1) << 40) || rows > 65535 ||
+        seqs > 65535 || seqs * rows * 3 * d > (size_t(1) << 40))
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_attention_prefill: cache or block too large");
+    if (seqs > 1 && seq_stride < capacity * d)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_attention_prefill: seq_stride " + std::to_string(seq_stride) +
+                                                " below capacity x d = " + std::to_string(capacity * d));
+    FH_ON_DEVICE(ctx);
+    return fh_launch_attention_prefill_seqs(ctx, d_qkv, d_k_cache, d_v_cache, seqs > 1 ? seq_stride : 0, d, heads,
+                                            pos0, rows, seqs, d_out);
 }
 
 int fh_q8_0_linear_act_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,

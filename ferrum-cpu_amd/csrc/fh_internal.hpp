@@ -171,6 +171,11 @@ int fh_launch_add_layernorm(fh_ctx* ctx, const float* x, const float* y, float* 
 // one sequence: their k / v rows into the cache, then each row's attention.
 int fh_launch_attention_prefill(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
                                 size_t pos0, size_t rows, float* out);
+// The same for `seqs` sequences at once (sequence s: rows s * rows .. of qkv
+// and out, caches at kc / vc + s * seq_stride): head width 64 on the fp32
+// matrix cores (fh_attn_prefill.hip), others one sequence at a time.
+int fh_launch_attention_prefill_seqs(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t seq_stride,
+                                     size_t d, size_t heads, size_t pos0, size_t rows, size_t seqs, float* out);
 int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* vc, size_t d, size_t heads,
                                size_t pos, float* out);
 int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,

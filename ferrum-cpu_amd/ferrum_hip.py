@@ -46,7 +46,7 @@ EXPORTS = (
     "fh_q8_0_encode", "fh_q8_0_encode_async", "fh_q8_0_dequant_async",
     "fh_q8_0_block_dots_async", "fh_sample_rows", "fh_sample_rows_async", "fh_debug_sampler_faults",
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
-    "fh_attention_prefill_async",
+    "fh_attention_prefill_async", "fh_attention_prefill_seqs_async",
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
     "fh_gpt2_stack_create", "fh_gpt2_stack_free", "fh_gpt2_stack_forward_async",
     "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
@@ -185,6 +185,7 @@ def lib():
         L.fh_add_async.argtypes = [vp, vp, vp, sz]
         L.fh_attention_decode_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, vp]
         L.fh_attention_prefill_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, sz, vp]
+        L.fh_attention_prefill_seqs_async.argtypes = [vp, vp, vp, vp, sz, sz, sz, sz, sz, sz, sz, vp]
         L.fh_q8_0_linear_act_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32, i32]
         L.fh_add_layernorm_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         L.fh_q8_0_linear_ln_async.argtypes = [vp, vp, vp, vp, vp, sz, sz, vp, vp, vp, sz, vp, i32, i32]
@@ -602,6 +603,15 @@ def attention_prefill_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, 
     of one sequence at once (row r of qkv is position pos0 + r)."""
     ctx.check(lib().fh_attention_prefill_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), capacity, d, heads,
                                                pos0, rows, _ptr(out)))
+
+
+def attention_prefill_seqs_async(ctx: Context, qkv, k_cache, v_cache, seq_stride: int, capacity: int, d: int,
+                                 heads: int, pos0: int, rows: int, seqs: int, out):
+    """attention_prefill_async for `seqs` sequences in one call: sequence s's
+    rows are rows s * rows .. of qkv and out, its caches start seq_stride
+    floats after sequence s - 1's (the primes of a batch of sequences)."""
+    ctx.check(lib().fh_attention_prefill_seqs_async(ctx.h, _ptr(qkv), _ptr(k_cache), _ptr(v_cache), seq_stride,
+                                                    capacity, d, heads, pos0, rows, seqs, _ptr(out)))
 
 
 # ---- packed per-row int8 / int4 weights: ops::qlinear ---------------------------
@@ -1713,7 +1723,7 @@ class GPT2Batch:
     batched decode of BASELINE's b32 figure and configs[3]), then the final
     LayerNorm, the head and the fused sampler over the rows.  prefill_async
     primes equal-length prompts of all rows in one pass (rows x positions as
-    the GEMMs' rows, one attention launch per sequence).  Per row the
+    the GEMMs' rows, one attention launch per block for all sequences).  Per row the
     arithmetic is GPT2Device's, so a row matches ferrum_core's single-sequence
     decode within the same 1e-5 rule.  Token and position ids live on the
     device, so a step can be captured in one graph."""
@@ -1805,10 +1815,8 @@ class GPT2Batch:
             else:
                 linear_ln_async(ctx, b["qkv"], cur, proj, other, N, d, b["ln1_g"], b["ln1_b"], b["qkv_b"], 3 * d, qkv)
                 cur, other = other, cur
-            for s in range(B):
-                kc, vc = self._cache(i, s)
-                attention_prefill_async(ctx, qkv[s * n:(s + 1) * n], kc, vc, self.cap, d, m.heads, pos0, n,
-                                        att[s * n:(s + 1) * n])
+            attention_prefill_seqs_async(ctx, qkv, self.k[i], self.v[i], self.cap * d, self.cap, d, m.heads, pos0, n,
+                                         B, att)
             linear_forward_async(ctx, b["out"], att, N, d, b["out_b"], d, proj)
             linear_ln_async(ctx, b["up"], cur, proj, other, N, d, b["ln2_g"], b["ln2_b"], b["up_b"], m.ffn, mid,
                             ACT_GELU)

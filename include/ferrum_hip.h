@@ -397,6 +397,18 @@ int fh_attention_decode_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache,
  * FH_ERR_DIM ("KvCache full"); rows <= 65535. */
 int fh_attention_prefill_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
                                size_t capacity, size_t d, size_t heads, size_t pos0, size_t rows, float* d_out);
+/* fh_attention_prefill_async for `seqs` independent sequences in one call: the
+ * prime of each sequence's CachedTransformer (slm/cached.rs:129-136) through
+ * forward_with_cache's attention (layer/transformer.rs:242-279), every
+ * sequence's block at positions pos0 .. pos0 + rows - 1.  Sequence s's rows are
+ * rows s * rows .. s * rows + rows - 1 of d_qkv ([seqs * rows, 3d]) and d_out
+ * ([seqs * rows, d]); its caches start at d_k_cache / d_v_cache + s *
+ * seq_stride (floats; seq_stride >= capacity * d when seqs > 1).  Head width
+ * 64 runs on the fp32 matrix cores; within the 1e-5 rule of the reference.
+ * Errors as fh_attention_prefill_async; seqs <= 65535. */
+int fh_attention_prefill_seqs_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
+                                    size_t seq_stride, size_t capacity, size_t d, size_t heads, size_t pos0,
+                                    size_t rows, size_t seqs, float* d_out);
 
 /* ---- packed per-row int8 / int4 weights: ops::qlinear (ops.rs:268-377) ------
  * QWeight (quant.rs:130-217): k rows (input features) x n columns (outputs),

@@ -168,6 +168,62 @@ def test_attention_prefill_matches_oracle(fh, orc, d, heads, blocks):
     assert np.array_equal(host(fh, kc), ko, equal_nan=True) and np.array_equal(host(fh, vc), vo, equal_nan=True)
 
 
+@pytest.mark.parametrize("d,heads,seqs,rows,pos0", [(1024, 16, 3, 300, 0), (768, 12, 2, 100, 40), (128, 4, 3, 50, 7)])
+def test_attention_prefill_seqs_matches_oracle(fh, orc, d, heads, seqs, rows, pos0):
+    """fh_attention_prefill_seqs_async: several sequences' prompt blocks in one
+    call (each with its own caches, seq_stride apart; rows before pos0 already
+    cached): every row of every sequence against the oracle's attention for
+    that position, and the caches bit-equal."""
+    import ferrum_hip
+
+    cap = pos0 + rows + 3
+    rng = np.random.default_rng(d + seqs * 7 + pos0)
+    qkv = (rng.standard_normal((seqs * rows, 3 * d)) * 1.5).astype(np.float32)
+    kc = np.full((seqs, cap, d), np.nan, np.float32)
+    vc = np.full((seqs, cap, d), np.nan, np.float32)
+    kc[:, :pos0] = rng.standard_normal((seqs, pos0, d)).astype(np.float32)
+    vc[:, :pos0] = rng.standard_normal((seqs, pos0, d)).astype(np.float32)
+    tk, tv = dev(kc), dev(vc)
+    out = dev(np.zeros((seqs * rows, d), np.float32))
+    ready()
+    ferrum_hip.attention_prefill_seqs_async(fh, dev(qkv), tk, tv, cap * d, cap, d, heads, pos0, rows, seqs, out)
+    got = host(fh, out)
+    for s in range(seqs):
+        ko, vo = kc[s].copy(), vc[s].copy()
+        for r in range(rows):
+            want = orc.attention_decode(qkv[s * rows + r], ko, vo, heads, pos0 + r)
+            close(got[s * rows + r], want, 1e-5)
+        assert np.array_equal(host(fh, tk)[s], ko, equal_nan=True) and np.array_equal(host(fh, tv)[s], vo,
+                                                                                      equal_nan=True)
+
+
+def test_attention_prefill_with_non_finite_values(fh, orc):
+    """A NaN v value at position 50 (head 0) and an inf at position 70 (head
+    3): rows before them attend only finite values and stay finite, later rows
+    of those heads turn NaN / inf exactly where the oracle's do; every other
+    output within 1e-5."""
+    import ferrum_hip
+
+    d, heads, rows = 768, 12, 100
+    rng = np.random.default_rng(99)
+    qkv = (rng.standard_normal((rows, 3 * d)) * 1.5).astype(np.float32)
+    qkv[50, 2 * d + 5] = np.nan
+    qkv[70, 2 * d + 3 * 64 + 9] = np.inf
+    kc, vc = dev(np.zeros((rows, d), np.float32)), dev(np.zeros((rows, d), np.float32))
+    out = dev(np.zeros((rows, d), np.float32))
+    ready()
+    ferrum_hip.attention_prefill_async(fh, dev(qkv), kc, vc, rows, d, heads, 0, rows, out)
+    got = host(fh, out)
+    ko, vo = np.zeros((rows, d), np.float32), np.zeros((rows, d), np.float32)
+    for r in range(rows):
+        want = orc.attention_decode(qkv[r], ko, vo, heads, r)
+        assert np.array_equal(np.isnan(got[r]), np.isnan(want)), r
+        assert np.array_equal(np.isposinf(got[r]), np.isposinf(want)), r
+        fin = np.isfinite(want)
+        close(got[r][fin], want[fin], 1e-5)
+    assert np.isfinite(got[:50]).all() and np.isnan(got[50:, 5]).all()
+
+
 def test_attention_decode_errors(fh):
     import ferrum_hip
 
