@@ -831,6 +831,71 @@ int fh_q8_0_linear_ln_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, con
     return launch_linear(ctx, w, hf, m, d_bias, d_y, numerics, activation);
 }
 
+int fh_q8_0_linear_residual_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                                  const float* d_bias, size_t bias_len, const float* d_r, float* d_y,
+                                  float* d_stats) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    int rc = check_linear(ctx, w, k, d_bias, bias_len, FH_W8A32);
+    if (rc) return rc;
+    if (m == 0) return FH_OK;
+    if (!d_x || !d_r || !d_y) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_residual: x, r or y is NULL");
+    if (d_y == d_x) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_residual: y must not alias x");
+    if (d_stats && (w->n & 31))
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_residual: row statistics need out_features % 32 == 0");
+    if (m > 0x7FFFFFFFu || w->n > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_residual: too large");
+    FH_ON_DEVICE(ctx);
+    if (d_stats && w->kind == FH_WEIGHT_Q8_0) {
+        fh_edge e{};
+        e.stats = d_stats;
+        e.r = d_r;
+        rc = fh_launch_skinny_res_out(ctx, w, d_x, m, e, d_bias, d_y);
+        if (rc >= 0) return rc;
+    }
+    // other shapes: the linear into the activation area, then the add (and statistics)
+    void* t = nullptr;
+    rc = fh_act_area(ctx, m * w->n * sizeof(float), &t);
+    if (rc) return rc;
+    rc = launch_linear(ctx, w, d_x, m, d_bias, static_cast<float*>(t), FH_W8A32);
+    if (rc) return rc;
+    return fh_launch_residual_stats(ctx, static_cast<const float*>(t), d_r, d_y, m, w->n, d_stats);
+}
+
+int fh_q8_0_linear_normed_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                                const float* d_stats, const float* d_gamma, const float* d_beta, float eps, int rms,
+                                const float* d_bias, size_t bias_len, float* d_y, int activation) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (activation != FH_ACT_NONE && activation != FH_ACT_GELU)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_normed: unknown activation " + std::to_string(activation));
+    int rc = check_linear(ctx, w, k, d_bias, bias_len, FH_W8A32);
+    if (rc) return rc;
+    if (m == 0) return FH_OK;
+    if (!d_x || !d_y || !d_stats || !d_gamma)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_normed: x, y, stats or gamma is NULL");
+    if (rms != 0 && rms != 1) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_normed: rms must be 0 or 1");
+    if (!rms && !d_beta) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_normed: LayerNorm needs beta");
+    if (k & 31) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_normed: row statistics need k % 32 == 0");
+    if (m > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear_normed: m is above 2^31 - 1");
+    FH_ON_DEVICE(ctx);
+    fh_edge e{};
+    e.stats = const_cast<float*>(d_stats);
+    e.gamma = d_gamma;
+    e.beta = rms ? nullptr : d_beta;
+    e.eps = eps;
+    e.rms = rms;
+    if (w->kind == FH_WEIGHT_Q8_0) {
+        rc = fh_launch_skinny_norm_in(ctx, w, d_x, m, e, d_bias, d_y, activation);
+        if (rc >= 0) return rc;
+    }
+    void* h = nullptr;
+    rc = fh_act_area(ctx, m * k * sizeof(float), &h);
+    if (rc) return rc;
+    rc = fh_launch_norm_from_stats(ctx, d_x, m, k, e, static_cast<float*>(h));
+    if (rc) return rc;
+    return launch_linear(ctx, w, static_cast<float*>(h), m, d_bias, d_y, FH_W8A32, activation);
+}
+
 // ---- Llama / Qwen block pieces ---------------------------------------------------
 
 int fh_rmsnorm_async(fh_ctx* ctx, const float* d_x, const float* d_r, float* d_s, size_t rows, size_t d,

@@ -414,6 +414,91 @@ int fh_launch_add(fh_ctx* ctx, float* x, const float* y, size_t n) {
     return FH_OK;
 }
 
+namespace {
+
+// The residual add after a linear, y = r + t (y may be r), and y's row
+// statistics for the next norm: per 32-column group its mean and sum of
+// squared deviations (one half-wave per group, fixed-order trees; what the
+// skinny GEMM's residual epilogue writes).  One workgroup per row; n % 32 == 0
+// when stats is set.
+__global__ void __launch_bounds__(kThreads) k_residual_stats(const float* __restrict__ t, const float* r, float* y,
+                                                            int n, float* __restrict__ stats) {
+    const size_t row = blockIdx.x;
+    const int groups = (n + 31) >> 5, tid = threadIdx.x;
+    for (int g0 = 0; g0 < groups; g0 += kThreads / 32) {
+        const int g = g0 + tid / 32, c = g * 32 + (tid & 31);
+        const bool live = c < n;
+        float v = 0.0f;
+        if (live) {
+            v = r[row * n + c] + t[row * n + c];
+            y[row * n + c] = v;
+        }
+        if (stats) {
+            const float mu = fh::group_total<32>(live ? v : 0.0f) * (1.0f / 32.0f);
+            const float dv = live ? v - mu : 0.0f;
+            const float m2 = fh::group_total<32>(dv * dv);
+            if ((tid & 31) == 0 && g < groups) {
+                stats[(row * groups + g) * 2] = mu;
+                stats[(row * groups + g) * 2 + 1] = m2;
+            }
+        }
+    }
+}
+
+// out = norm(x) from the rows' group statistics (mean = the mean of the group
+// means, M2 = sum of M2_g + 32 (mean_g - mean)^2; LayerNorm: (x - mean) * rs *
+// gamma + beta, rs = 1 / sqrt(M2 / k + eps); RmsNorm: mean 0, the same sums
+// about 0, x * rs * gamma), the skinny GEMM's normalising staging.  One
+// workgroup per row.
+__global__ void __launch_bounds__(kThreads) k_norm_from_stats(const float* __restrict__ x, int k,
+                                                             const float* __restrict__ stats,
+                                                             const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, float eps, int rms,
+                                                             float* __restrict__ out) {
+    const size_t row = blockIdx.x;
+    const int groups = k >> 5;
+    __shared__ float mr[2];
+    if (threadIdx.x == 0) {
+        const float* st = stats + row * groups * 2;
+        float sm = 0.0f;
+        for (int g = 0; g < groups; g++) sm += st[2 * g];
+        const float mu = rms ? 0.0f : sm / static_cast<float>(groups);
+        float m2 = 0.0f;
+        for (int g = 0; g < groups; g++) {
+            const float dm = st[2 * g] - mu;
+            m2 += st[2 * g + 1] + 32.0f * dm * dm;
+        }
+        mr[0] = mu;
+        mr[1] = 1.0f / sqrtf(m2 / static_cast<float>(k) + eps);
+    }
+    __syncthreads();
+    const float mu = mr[0], rsi = mr[1];
+    for (int c = threadIdx.x; c < k; c += kThreads) {
+        float v = (x[row * k + c] - mu) * rsi * gamma[c];
+        if (beta) v = v + beta[c];
+        out[row * k + c] = v;
+    }
+}
+
+}  // namespace
+
+int fh_launch_residual_stats(fh_ctx* ctx, const float* t, const float* r, float* y, size_t rows, size_t n,
+                             float* stats) {
+    if (rows == 0) return FH_OK;
+    hipLaunchKernelGGL(k_residual_stats, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, t, r, y,
+                       static_cast<int>(n), stats);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
+int fh_launch_norm_from_stats(fh_ctx* ctx, const float* x, size_t rows, size_t k, const fh_edge& e, float* out) {
+    if (rows == 0) return FH_OK;
+    hipLaunchKernelGGL(k_norm_from_stats, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, ctx->stream, x,
+                       static_cast<int>(k), e.stats, e.gamma, e.beta, e.eps, e.rms, out);
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
 int fh_launch_add_layernorm(fh_ctx* ctx, const float* x, const float* y, float* s, size_t rows, size_t d,
                             const float* gamma, const float* beta, float* ln) {
     if (d > 8 * static_cast<size_t>(kThreads))

@@ -98,6 +98,36 @@ __device__ __attribute__((noinline)) void exact_tile(const float* __restrict__ x
     }
 }
 
+// exact_dot on the normalised row (x - mean) * rs * gamma + beta (RmsNorm:
+// mean 0, no beta): the rare outputs of a weight row with a non-finite block
+// scale when the GEMM normalises its input.
+__device__ __attribute__((noinline)) float exact_dot_norm(const float* __restrict__ x, const float* __restrict__ gamma,
+                                                        const float* __restrict__ beta, const float* __restrict__ st,
+                                                        int groups, int rms, float eps, int k,
+                                                        const int8_t* __restrict__ q, const uint16_t* __restrict__ d) {
+#pragma clang fp contract(off)
+    // the row's statistics from its group statistics (sequential sums)
+    float sm = 0.0f;
+    for (int g = 0; g < groups; g++) sm += st[2 * g];
+    const float mu = rms ? 0.0f : sm / static_cast<float>(groups);
+    float m2 = 0.0f;
+    for (int g = 0; g < groups; g++) {
+        const float dm = st[2 * g] - mu;
+        m2 += st[2 * g + 1] + 32.0f * dm * dm;
+    }
+    const float rsi = 1.0f / sqrtf(m2 / static_cast<float>(k) + eps);
+    float s = 0.0f;
+    for (int b = 0; b < (k >> 5); b++) {
+        const float ds = fh_h2f(d[b]);
+        for (int t = 0; t < 32; t++) {
+            const int c = b * 32 + t;
+            const float a = (x[c] - mu) * rsi * gamma[c] + (beta ? beta[c] : 0.0f);
+            s = s + a * (ds * static_cast<float>(q[c]));
+        }
+    }
+    return s;
+}
+
 }  // namespace
 
 // One wave per activation row (rows m .. m_pad - 1 are written as zeros).
@@ -777,6 +807,9 @@ __device__ __forceinline__ void split4(const float* v, float sc, uint2& h, uint2
 // ds_read_b128 pass (16 rows) land on distinct banks.
 constexpr int kSkinnyRow = 36;
 
+// What the skinny GEMM does at its edges (k_gemm_skinny's MODE).
+enum { kSkinnyPlain = 0, kSkinnyNormIn = 1, kSkinnyResOut = 2 };
+
 __device__ __forceinline__ int block_exponent(float mx) {
     if (!(mx > 0.0f)) return 0;
     const int E = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 126;
@@ -793,11 +826,16 @@ __device__ __forceinline__ float gelu_unfused(float v) {
     return 0.5f * v * (1.0f + tanhf(0.7978846f * (v + 0.044715f * v * v * v)));
 }
 
-template <int MT, int NT, int BPW>
+// MODE kSkinnyPlain: y = act(x W^T + b).  kSkinnyNormIn: the input is
+// norm(x) (LayerNorm or RmsNorm), formed as the activations are staged from
+// the rows' statistics a kSkinnyResOut launch left (fh_edge).  kSkinnyResOut:
+// y = r + (x W^T + b) (y may be r) and, per row and 32-column group of y,
+// the group's mean and sum of squared deviations into e.stats.
+template <int MT, int NT, int BPW, int MODE>
 __global__ void __launch_bounds__(512)
     k_gemm_skinny(const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
-                  const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
-                  int k, int bps, float* __restrict__ part, unsigned* __restrict__ counters, int act) {
+                  const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* y, int m, int n,
+                  int k, int bps, float* __restrict__ part, unsigned* __restrict__ counters, int act, fh_edge e) {
     constexpr int OUT = MT * NT * 1024;  // outputs of one workgroup
     // Per wave, [SLOT] floats: during the K loop one Q8_0 block of its
     // activation rows ([MT * 32][36]: the rows land there from row-contiguous
@@ -828,6 +866,35 @@ __global__ void __launch_bounds__(512)
     }
     float* inv_lds = lds + kw * SLOT + wave * (MT * BPW * 32);  // this wave's row scales
     float* xst = lds + wave * SLOT;                              // this wave's staging rows
+    const float* nm_beta = MODE == kSkinnyNormIn && e.beta ? e.beta : e.gamma;
+    // kSkinnyNormIn: the mean and 1 / sd of the rows this lane stages (row t *
+    // 32 + lane / 8 + 8 q) from their group statistics ([rows][k / 32][2]: per
+    // 32-column group its mean and M2).  The eight lanes staging a row split
+    // its groups (lane & 7 takes groups lane & 7, + 8, ...) and sum them with
+    // an eight-lane tree in a fixed order: mean = the mean of the group means,
+    // M2 = sum of (M2_g + 32 (mean_g - mean)^2); LayerNorm: 1 / sqrt(M2 / k +
+    // eps); RmsNorm: mean 0, 1 / sqrt(sum of (M2_g + 32 mean_g^2) / k + eps).
+    // Kept per wave in LDS, [row] = (mean, 1 / sd) (registers held across the
+    // K loop would spill the wider tiles).  (Issuing the K loop's first batch
+    // before the statistics are reduced timed no faster and spilled the
+    // 64-row, two-group tiles.)
+    __shared__ float2 rowf[MODE == kSkinnyNormIn ? 8 : 1][MODE == kSkinnyNormIn ? MT * 32 : 1];
+    constexpr int kJ = 4;  // groups per lane at most (k <= 1024)
+    const int groups = k >> 5, s8 = lane & 7;
+    float2 gs[MODE == kSkinnyNormIn ? MT : 1][4][kJ];
+    if constexpr (MODE == kSkinnyNormIn) {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const size_t i = static_cast<size_t>(min(t * 32 + (lane >> 3) + 8 * q, m - 1));
+#pragma unroll
+                for (int j = 0; j < kJ; j++)
+                    if (j * 8 < groups)  // (uniform)
+                        gs[t][q][j] = *reinterpret_cast<const float2*>(
+                            e.stats + (i * groups + min(s8 + 8 * j, groups - 1)) * 2);
+            }
+    }
     f16x acc[MT][NT];
 #pragma unroll
     for (int t = 0; t < MT; t++)
@@ -835,7 +902,32 @@ __global__ void __launch_bounds__(512)
         for (int c = 0; c < NT; c++) acc[t][c] = f16x{};
     const f16x zero = {};
 
-    for (int b0 = b_begin + wave * BPW; b0 < b_end; b0 += kw * BPW) {
+    const int b_first = b_begin + wave * BPW;
+    if constexpr (MODE == kSkinnyNormIn) {
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float sm = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kJ; j++)
+                    if (j * 8 < groups && s8 + 8 * j < groups) sm += gs[t][q][j].x;
+                const float mu = e.rms ? 0.0f : fh::group_sum<8>(sm) / static_cast<float>(groups);
+                float m2 = 0.0f;
+#pragma unroll
+                for (int j = 0; j < kJ; j++)
+                    if (j * 8 < groups && s8 + 8 * j < groups) {
+                        const float dm = gs[t][q][j].x - mu;
+                        m2 += gs[t][q][j].y + 32.0f * dm * dm;
+                    }
+                m2 = fh::group_sum<8>(m2);
+                if (s8 == 0)
+                    rowf[wave][t * 32 + (lane >> 3) + 8 * q] =
+                        make_float2(mu, 1.0f / sqrtf(m2 / static_cast<float>(k) + e.eps));
+            }
+        __builtin_amdgcn_wave_barrier();
+    }
+    for (int b0 = b_first; b0 < b_end; b0 += kw * BPW) {
         // Every load is unconditional (clamped to a block of this split and a
         // valid row) so the batch is in flight at once.  Rows past m compute
         // garbage that is never stored (an MFMA output row depends only on its
@@ -843,6 +935,7 @@ __global__ void __launch_bounds__(512)
         uint4 wq[NT][BPW];
         uint16_t wd[NT][BPW];
         f4 xv[MT][BPW][4];
+        f4 gv[MODE == kSkinnyNormIn ? BPW : 1], bv[MODE == kSkinnyNormIn ? BPW : 1];
 #pragma unroll
         for (int u = 0; u < BPW; u++) {
             const int b = min(b0 + u, b_end - 1);
@@ -850,6 +943,10 @@ __global__ void __launch_bounds__(512)
             for (int c = 0; c < NT; c++) {
                 wq[c][u] = *reinterpret_cast<const uint4*>(wrow[c] + b * 32);
                 wd[c][u] = drow[c][b];
+            }
+            if constexpr (MODE == kSkinnyNormIn) {
+                gv[u] = *reinterpret_cast<const f4*>(e.gamma + b * 32 + (lane & 7) * 4);
+                bv[u] = *reinterpret_cast<const f4*>(nm_beta + b * 32 + (lane & 7) * 4);
             }
             // Activations: eight lanes per row read one block's 128 bytes,
             // eight rows per load (a load in MFMA lane order would touch 64
@@ -882,8 +979,15 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
             for (int t = 0; t < MT; t++)
 #pragma unroll
-                for (int q = 0; q < 4; q++)
-                    *reinterpret_cast<f4*>(xst + (t * 32 + (lane >> 3) + 8 * q) * kSkinnyRow + (lane & 7) * 4) = xv[t][u][q];
+                for (int q = 0; q < 4; q++) {
+                    f4 val = xv[t][u][q];
+                    if constexpr (MODE == kSkinnyNormIn) {
+                        const float2 f = rowf[wave][t * 32 + (lane >> 3) + 8 * q];
+                        val = (val - f.x) * f.y * gv[u];
+                        if (e.beta) val = val + bv[u];
+                    }
+                    *reinterpret_cast<f4*>(xst + (t * 32 + (lane >> 3) + 8 * q) * kSkinnyRow + (lane & 7) * 4) = val;
+                }
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int t = 0; t < MT; t++) {
@@ -955,15 +1059,41 @@ __global__ void __launch_bounds__(512)
     // picked at compile time, and o & 31 == r32 (blockDim.x is a multiple of 64).
     auto row_of = [](int o) { const int t = o / (NT * 1024), v = (o / 64) % 16, l = o % 64;
                               return t * 32 + (v / 4) * 8 + (l / 32) * 4 + (v % 4); };
-    auto finish = [&](int o, float s, bool bad, float bv, int jj) {
+    // One output (kSkinnyResOut: every lane of the wave calls together, so the
+    // 32 columns of a row group can be reduced across the half-wave).
+    auto finish = [&](int o, float s, bool bad, float bv, int jj, float rres = 0.0f, bool have_r = false) {
         const int i = row_of(o);
-        if (i >= m || jj >= n) return;
-        if (__builtin_expect(bad, 0))
-            s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(jj) * k,
-                          dsc + static_cast<size_t>(jj) * kb);
-        float v = bias ? s + bv : s;
-        if (act == FH_ACT_GELU) v = gelu_unfused(v);
-        y[static_cast<size_t>(i) * n + jj] = v;
+        const bool live = i < m && jj < n;
+        float v = 0.0f;
+        if (live) {
+            if (__builtin_expect(bad, 0)) {
+                if constexpr (MODE == kSkinnyNormIn)
+                    s = exact_dot_norm(x + static_cast<size_t>(i) * k, e.gamma, e.beta, e.stats + 2 * static_cast<size_t>(i) * (k >> 5),
+                                       k >> 5, e.rms, e.eps, k,
+                                       qs + static_cast<size_t>(jj) * k, dsc + static_cast<size_t>(jj) * kb);
+                else
+                    s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(jj) * k,
+                                  dsc + static_cast<size_t>(jj) * kb);
+            }
+            v = bias ? s + bv : s;
+            if constexpr (MODE == kSkinnyResOut) {
+                v = (have_r ? rres : e.r[static_cast<size_t>(i) * n + jj]) + v;
+            } else {
+                if (act == FH_ACT_GELU) v = gelu_unfused(v);
+            }
+            y[static_cast<size_t>(i) * n + jj] = v;
+        }
+        if constexpr (MODE == kSkinnyResOut) {
+            // the row group's 32 columns sit in the 32 lanes of this half-wave
+            const float mu = fh::group_total<32>(live ? v : 0.0f) * (1.0f / 32.0f);
+            const float dv = live ? v - mu : 0.0f;
+            const float m2 = fh::group_total<32>(dv * dv);
+            if (r32 == 0 && live) {
+                float* st = e.stats + (static_cast<size_t>(i) * (n >> 5) + (jj >> 5)) * 2;
+                st[0] = mu;
+                st[1] = m2;
+            }
+        }
     };
     const size_t tiles = gridDim.x;
 #pragma unroll
@@ -1000,22 +1130,29 @@ __global__ void __launch_bounds__(512)
         for (int c = 0; c < NT; c++) {
             const int base = (t * NT + c) * 1024, jj = (tile * NT + c) * 32 + r32;
             for (int o0 = base + static_cast<int>(threadIdx.x); o0 < base + 1024; o0 += 2 * blockDim.x) {
-                float pv[2][kMaxSplits];
+                float pv[2][kMaxSplits], rv[2] = {0.0f, 0.0f};
 #pragma unroll
-                for (int q = 0; q < 2; q++)
+                for (int q = 0; q < 2; q++) {
 #pragma unroll
                     for (int sp = 0; sp < kMaxSplits; sp++) {
                         const int o = min(o0 + q * static_cast<int>(blockDim.x), base + 1023);
                         pv[q][sp] = __hip_atomic_load(part + (min(sp, splits - 1) * tiles + tile) * OUT + o,
                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     }
+                    if constexpr (MODE == kSkinnyResOut) {
+                        // the residual with the partials, one round trip for both
+                        const int o = min(o0 + q * static_cast<int>(blockDim.x), base + 1023);
+                        rv[q] = e.r[static_cast<size_t>(min(row_of(o), m - 1)) * n + min(jj, n - 1)];
+                    }
+                }
 #pragma unroll
                 for (int q = 0; q < 2; q++) {
                     const int o = o0 + q * static_cast<int>(blockDim.x);
                     float s = pv[q][0];
 #pragma unroll
                     for (int sp = 1; sp < kMaxSplits; sp++) s = sp < splits ? s + pv[q][sp] : s;
-                    if (o < base + 1024) finish(o, s, bad_c[c], bias_c[c], jj);
+                    // (blockDim.x and 1024 are multiples of 64: the test is the same for the whole wave)
+                    if (o < base + 1024) finish(o, s, bad_c[c], bias_c[c], jj, rv[q], MODE == kSkinnyResOut);
                 }
             }
         }
@@ -1239,7 +1376,7 @@ __global__ void k_zero_counters(unsigned* __restrict__ c, int n) {
 
 template <int MT, int NT, int BPW>
 int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
-                    const fh_scratch* scratch, int act) {
+                    const fh_scratch* scratch, int act, const fh_edge* edge = nullptr, int mode = kSkinnyPlain) {
     constexpr size_t kMaxWaves = 16 / (MT * NT) < 8 ? 16 / (MT * NT) : 8;
     const size_t kb = w->k / 32, tiles = (w->n + 32 * NT - 1) / (32 * NT);
     size_t splits = 1;
@@ -1253,6 +1390,7 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     const size_t lds = kw * (kSlot + MT * BPW * 32) * sizeof(float);
     float* part = nullptr;
     unsigned* counters = nullptr;
+    const fh_edge ed = edge ? *edge : fh_edge{};
     if (splits > 1) {
         const size_t part_bytes = splits * tiles * MT * NT * 1024 * sizeof(float);
         if (scratch) {
@@ -1283,9 +1421,23 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     }
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: too many output columns");
     const dim3 grid(static_cast<unsigned>(tiles), static_cast<unsigned>(splits)), block(static_cast<unsigned>(64 * kw));
-    hipLaunchKernelGGL((k_gemm_skinny<MT, NT, BPW>), grid, block, lds, ctx->stream, x, w->qs, w->d, w->rexp, bias, y,
-                       static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(bps), part,
-                       counters, act);
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, lds, ctx->stream, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
+                           static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(bps), part, counters, act,
+                           ed);
+    };
+    // (the fused edges are built for the tiles of at most two 32-column
+    // groups per wave, whose registers hold them without spilling)
+    constexpr bool kEdges = NT <= 2 && !(MT == 2 && NT == 2 && BPW == 2);
+    if (mode != kSkinnyPlain && !kEdges)
+        return fh_fail(ctx, FH_ERR_LIMIT, "skinny GEMM: no fused norm or residual for this tile");
+    if constexpr (kEdges) {
+        if (mode == kSkinnyNormIn) go(k_gemm_skinny<MT, NT, BPW, kSkinnyNormIn>);
+        else if (mode == kSkinnyResOut) go(k_gemm_skinny<MT, NT, BPW, kSkinnyResOut>);
+        else go(k_gemm_skinny<MT, NT, BPW, kSkinnyPlain>);
+    } else {
+        go(k_gemm_skinny<MT, NT, BPW, kSkinnyPlain>);
+    }
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -1319,9 +1471,10 @@ constexpr size_t kWideMinTiles = 1024;
 // splits, so more workgroups: 896 x 896 7.9 -> 6.9 us at m = 32, 10.4 -> 9.2
 // us at m = 64; a 3072-wide one slows down).
 int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
-                  const fh_scratch* scratch = nullptr, int act = FH_ACT_NONE) {
+                  const fh_scratch* scratch = nullptr, int act = FH_ACT_NONE, const fh_edge* edge = nullptr,
+                  int mode = kSkinnyPlain) {
     const size_t t32 = (w->n + 31) / 32;
-    if (t32 >= kWideMinTiles && (w->k == 768 || w->k == 896 || w->k == 1024)) {
+    if (mode == kSkinnyPlain && t32 >= kWideMinTiles && (w->k == 768 || w->k == 896 || w->k == 1024)) {
         // 32 rows per launch: at m = 64 two launches, each streaming the
         // weight once, beat the skinny kernel's single pass (151936 x 896:
         // 131 -> 114 us), which re-splits the 64-row block per 64 columns
@@ -1336,16 +1489,17 @@ int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const
         }
         return act == FH_ACT_GELU ? fh_launch_gelu(ctx, y, m * w->n) : FH_OK;
     }
+    // (the fused edges never take the 4-group tiles: at t32 >= 1024 they take 2)
     if (m <= 32) {
-        if (t32 >= 4 * 256) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y, scratch, act);
-        if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y, scratch, act);
-        if (t32 >= 64) return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y, scratch, act);
-        return launch_skinny_t<1, 1, 1>(ctx, w, x, m, bias, y, scratch, act);
+        if (t32 >= 4 * 256 && mode == kSkinnyPlain) return launch_skinny_t<1, 4, 2>(ctx, w, x, m, bias, y, scratch, act);
+        if (t32 >= 256) return launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y, scratch, act, edge, mode);
+        if (t32 >= 64) return launch_skinny_t<1, 1, 3>(ctx, w, x, m, bias, y, scratch, act, edge, mode);
+        return launch_skinny_t<1, 1, 1>(ctx, w, x, m, bias, y, scratch, act, edge, mode);
     }
-    if (t32 >= 4 * 256) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y, scratch, act);
-    if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y, scratch, act);
-    if (t32 >= 64) return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y, scratch, act);
-    return launch_skinny_t<2, 1, 1>(ctx, w, x, m, bias, y, scratch, act);  // 896 x 896: 10.4 -> 9.2 us
+    if (t32 >= 4 * 256 && mode == kSkinnyPlain) return launch_skinny_t<2, 2, 2>(ctx, w, x, m, bias, y, scratch, act);
+    if (t32 >= 256) return launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y, scratch, act, edge, mode);
+    if (t32 >= 64) return launch_skinny_t<2, 1, 2>(ctx, w, x, m, bias, y, scratch, act, edge, mode);
+    return launch_skinny_t<2, 1, 1>(ctx, w, x, m, bias, y, scratch, act, edge, mode);  // 896 x 896: 10.4 -> 9.2 us
 }
 
 }  // namespace
@@ -1381,6 +1535,18 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
                            static_cast<int>(tiles_n), static_cast<int>(tiles));
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
+}
+
+int fh_launch_skinny_norm_in(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_edge& e,
+                             const float* bias, float* y, int act) {
+    if (m < 3 || m > 64 || w->kind != FH_WEIGHT_Q8_0 || w->k > 1024) return -1;
+    return launch_skinny(ctx, w, x, m, bias, y, nullptr, act, &e, kSkinnyNormIn);
+}
+
+int fh_launch_skinny_res_out(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_edge& e,
+                             const float* bias, float* y) {
+    if (m < 3 || m > 64 || w->kind != FH_WEIGHT_Q8_0) return -1;
+    return launch_skinny(ctx, w, x, m, bias, y, nullptr, FH_ACT_NONE, &e, kSkinnyResOut);
 }
 
 int fh_launch_skinny_scratch(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,

@@ -130,6 +130,31 @@ struct fh_ln_args {
 };
 int fh_launch_linear_ln_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_ln_args& ln,
                               const float* bias, float* y, int act);
+// The fused edges of the skinny GEMM (3 <= m <= 64).  Row statistics
+// ("stats"): per row and 32-column group, the group's mean and sum of squared
+// deviations (M2), [rows][groups][2] floats (k, n % 32 == 0).
+struct fh_edge {
+    float* stats;         // norm in: the input rows' statistics (read); residual out: y's (written)
+    const float* gamma;   // norm in: LayerNorm gamma / RmsNorm weight
+    const float* beta;    // norm in: LayerNorm beta (null: RmsNorm)
+    float eps;            // norm in
+    int rms;              // norm in: 1 = RmsNorm
+    const float* r;       // residual out: y = r + (x W^T + b); may be y itself
+};
+// y = act(norm(x) W^T + b), the norm formed from e.stats as the activations
+// are staged; -1 for a shape the skinny GEMM does not take.
+int fh_launch_skinny_norm_in(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_edge& e,
+                             const float* bias, float* y, int act);
+// y = r + (x W^T + b) and y's row statistics into e.stats; -1 for a shape the
+// skinny GEMM does not take (n % 32 != 0 included).
+int fh_launch_skinny_res_out(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_edge& e,
+                             const float* bias, float* y);
+// The same two edges as separate kernels (any shape): y += ... is done by
+// the caller's plain linear; these add the residual and form the statistics
+// (k_residual_stats), or normalise rows from statistics (k_norm_from_stats).
+int fh_launch_residual_stats(fh_ctx* ctx, const float* t, const float* r, float* y, size_t rows, size_t n,
+                             float* stats);
+int fh_launch_norm_from_stats(fh_ctx* ctx, const float* x, size_t rows, size_t k, const fh_edge& e, float* out);
 // act (FH_ACT_*) is applied to the outputs: in the skinny GEMM's epilogue at
 // m <= 64, else by the separate GELU kernel.
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,

@@ -48,6 +48,7 @@ EXPORTS = (
     "fh_embed_one_async", "fh_layernorm_async", "fh_gelu_async", "fh_add_async", "fh_attention_decode_async",
     "fh_attention_prefill_async", "fh_attention_prefill_seqs_async",
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
+    "fh_q8_0_linear_residual_async", "fh_q8_0_linear_normed_async",
     "fh_gpt2_stack_create", "fh_gpt2_stack_free", "fh_gpt2_stack_forward_async",
     "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
     "fh_embed_rows_pos_async",
@@ -189,6 +190,8 @@ def lib():
         L.fh_q8_0_linear_act_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, i32, i32]
         L.fh_add_layernorm_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp]
         L.fh_q8_0_linear_ln_async.argtypes = [vp, vp, vp, vp, vp, sz, sz, vp, vp, vp, sz, vp, i32, i32]
+        L.fh_q8_0_linear_residual_async.argtypes = [vp, vp, vp, sz, sz, vp, sz, vp, vp, vp]
+        L.fh_q8_0_linear_normed_async.argtypes = [vp, vp, vp, sz, sz, vp, vp, vp, C.c_float, i32, vp, sz, vp, i32]
         L.fh_gpt2_stack_create.argtypes = [vp, C.POINTER(GPT2Block), sz, sz, sz, sz, sz, vp, vp, sz, sz,
                                            C.POINTER(vp)]
         L.fh_gpt2_stack_free.argtypes = [vp]
@@ -589,6 +592,25 @@ def linear_ln_async(ctx: Context, weight: "Q8_0Weight", x, r, s, m: int, k: int,
     and the Linear that reads it, as one call."""
     ctx.check(lib().fh_q8_0_linear_ln_async(ctx.h, weight.h, _ptr(x), _ptr(r), _ptr(s), m, k, _ptr(gamma), _ptr(beta),
                                             _ptr(bias), bias_len, _ptr(y), numerics, act))
+
+
+def linear_residual_async(ctx: Context, weight: "Q8_0Weight", x, m: int, k: int, bias, bias_len: int, r, y,
+                          stats=None):
+    """y = r + linear_forward(x) (y may be r), and with `stats` ([m, n / 32,
+    2]) y's row statistics (per 32-column group: mean, sum of squared
+    deviations) for a following linear_normed_async: the residual adds of
+    forward_with_cache (layer/transformer.rs:281, 288) without a launch of
+    their own."""
+    ctx.check(lib().fh_q8_0_linear_residual_async(ctx.h, weight.h, _ptr(x), m, k, _ptr(bias), bias_len, _ptr(r),
+                                                  _ptr(y), _ptr(stats)))
+
+
+def linear_normed_async(ctx: Context, weight: "Q8_0Weight", x, m: int, k: int, stats, gamma, beta, eps: float,
+                        rms: bool, bias, bias_len: int, y, act: int = ACT_NONE):
+    """y = act(norm(x) W^T + b), norm (LayerNorm, or RmsNorm with rms) formed
+    from the row statistics linear_residual_async left for x."""
+    ctx.check(lib().fh_q8_0_linear_normed_async(ctx.h, weight.h, _ptr(x), m, k, _ptr(stats), _ptr(gamma), _ptr(beta),
+                                                float(eps), 1 if rms else 0, _ptr(bias), bias_len, _ptr(y), act))
 
 
 def attention_decode_async(ctx: Context, qkv, k_cache, v_cache, capacity: int, d: int, heads: int, pos: int, out):
@@ -1121,6 +1143,9 @@ class LlamaDevice:
         self.tokens = torch.zeros(B, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
         self.blocks = []
+        # the residual stream's row statistics between a projection and the next RmsNorm
+        self.fused = 3 <= B <= 64 and self.d % 32 == 0
+        self.st = torch.empty((B, self.d // 32, 2), device=dev) if self.fused else None
 
     def _alloc_cache(self):
         import torch
@@ -1274,8 +1299,12 @@ class LlamaDevice:
         return m
 
     def launches_per_step(self) -> int:
-        """Kernel launches of feed_async (the sampler not included)."""
-        return 1 + 9 * self.layers + 2
+        """Kernel launches of feed_async (the sampler not included): at 3 .. 64
+        rows the o and down projections add themselves to the residual stream
+        and leave its row statistics, and the q|k|v and gate|up GEMMs form the
+        RmsNorm from them as they stage their inputs (seven launches per
+        block); otherwise each RmsNorm is a launch of its own (nine)."""
+        return 1 + (7 if self.fused else 9) * self.layers + 2 + (1 if self.fused else 0)
 
     def forward_one(self, token: int):
         """LlamaModel::forward_one (llm.rs:606-616) for a single sequence (rows
@@ -1303,6 +1332,31 @@ class LlamaDevice:
         head's scores land in self.z; positions are not advanced."""
         ctx, d, B = self.ctx, self.d, self.rows
         embed_rows_async(ctx, self.tok_w, self.vocab, d, self.tokens, B, self.x)
+        if self.fused:
+            # x is updated in place by the o and down projections, which leave
+            # its row statistics in self.st for the RmsNorm the next GEMM forms
+            x, st = self.x, self.st
+            for i, b in enumerate(self.blocks):
+                qkv_b = b.get("qkv_b")
+                if i == 0:
+                    rmsnorm_async(ctx, x, None, None, B, d, b["attn_norm"], self.eps, self.h)
+                    linear_forward_async(ctx, b["qkv"], self.h, B, d, qkv_b, 0 if qkv_b is None else self.qkv_dim,
+                                         self.qkv)
+                else:
+                    linear_normed_async(ctx, b["qkv"], x, B, d, st, b["attn_norm"], None, self.eps, True, qkv_b,
+                                        0 if qkv_b is None else self.qkv_dim, self.qkv)
+                rope_async(ctx, self.qkv, B, self.qkv_dim, self.nh + self.nkv, self.hd, self.rope_dim, self.pos,
+                           self.rope_base, self.rope_type, self.rope_freqs, self.rope_linear)
+                gqa_attention_decode_async(ctx, self.qkv, self.qkv_dim, B, self.nh, self.nkv, self.hd, b["k"], b["v"],
+                                           self.cap, self.pos, max_pos, self.att)
+                linear_residual_async(ctx, b["o"], self.att, B, self.q_dim, None, 0, x, x, st)
+                linear_normed_async(ctx, b["gate_up"], x, B, d, st, b["ffn_norm"], None, self.eps, True, None, 0,
+                                    self.gu)
+                swiglu_async(ctx, self.gu, self.gu[:, self.ffn:], B, self.ffn, 2 * self.ffn, self.mid)
+                linear_residual_async(ctx, b["down"], self.mid, B, self.ffn, None, 0, x, x, st)
+            rmsnorm_async(ctx, x, None, None, B, d, self.out_norm, self.eps, self.h)
+            linear_forward_async(ctx, self.head, self.h, B, d, None, 0, self.z)
+            return
         cur, other = self.x, self.x2
         for i, b in enumerate(self.blocks):
             if i == 0:
@@ -1745,13 +1799,23 @@ class GPT2Batch:
         self.z = torch.empty((B, m.vocab), device=dev)
         self.tokens = torch.zeros(B, dtype=torch.int32, device=dev)
         self.pos = torch.zeros(B, dtype=torch.int32, device=dev)
+        # the residual stream's row statistics between a projection and the next LayerNorm
+        self.fused = 3 <= B <= 64 and d % 32 == 0
+        self.st = torch.empty((B, d // 32, 2), device=dev) if self.fused else None
 
     def launches_per_step(self) -> int:
-        """Kernel launches of feed_async (the sampler not included): above two
-        rows a linear with its LayerNorm takes two (the add + LayerNorm kernel,
-        then the GEMM with GELU in its epilogue); at one or two rows the
-        decode GEMV forms the LayerNorm itself."""
-        return 3 + 7 * self.m.layers if self.rows > 2 else 3 + 5 * self.m.layers
+        """Kernel launches of feed_async (the sampler not included).  At 3 ..
+        64 rows the out and down projections add themselves to the residual
+        stream and leave its row statistics, and the Q|K|V and up GEMMs
+        normalise from those as they stage their inputs: five launches per
+        block, plus the embedding, block 0's LayerNorm, the final LayerNorm and
+        the head.  At one or two rows the decode GEMV forms each LayerNorm
+        itself (the residual add inside it); past 64 rows each linear after a
+        LayerNorm takes two launches."""
+        L = self.m.layers
+        if self.fused:
+            return 4 + 5 * L
+        return 3 + 5 * L if self.rows <= 2 else 3 + 7 * L
 
     def _cache(self, i, b):
         n = self.cap * self.m.d
@@ -1767,6 +1831,27 @@ class GPT2Batch:
             raise DimMismatch(FH_ERR_DIM, f"KvCache full ({self.cap} positions): clear and re-prime to continue")
         embed_rows_pos_async(ctx, m.tok_w, m.pos_w, m.vocab, m.pos_w.shape[0], d, d_tokens, d_pos, B, self.x, hist,
                              hist_stride)
+        if self.fused:
+            # the residual stream x is updated in place by the out and down
+            # projections, which leave its row statistics in self.st for the
+            # LayerNorm the next GEMM forms as it stages x
+            x, st, H = self.x, self.st, m.heads
+            for i, b in enumerate(m.blocks):
+                if i == 0:
+                    layernorm_async(ctx, x, B, d, b["ln1_g"], b["ln1_b"], self.h)
+                    linear_forward_async(ctx, b["qkv"], self.h, B, d, b["qkv_b"], 3 * d, self.qkv)
+                else:
+                    linear_normed_async(ctx, b["qkv"], x, B, d, st, b["ln1_g"], b["ln1_b"], 1e-5, False, b["qkv_b"],
+                                        3 * d, self.qkv)
+                gqa_attention_decode_async(ctx, self.qkv, 3 * d, B, H, H, d // H, self.k[i], self.v[i], self.cap,
+                                           d_pos, max_pos, self.att)
+                linear_residual_async(ctx, b["out"], self.att, B, d, b["out_b"], d, x, x, st)
+                linear_normed_async(ctx, b["up"], x, B, d, st, b["ln2_g"], b["ln2_b"], 1e-5, False, b["up_b"], m.ffn,
+                                    self.mid, ACT_GELU)
+                linear_residual_async(ctx, b["down"], self.mid, B, m.ffn, b["down_b"], d, x, x, st)
+            layernorm_async(ctx, x, B, d, m.lnf_g, m.lnf_b, self.h)
+            linear_forward_async(ctx, m.head, self.h, B, d, None, 0, self.z)
+            return
         cur, other = self.x, self.x2
         for i, b in enumerate(m.blocks):
             if i == 0:

@@ -148,6 +148,8 @@ pub mod sys {
         pub fn fh_add_async(ctx: *mut fh_ctx, d_x: *mut f32, d_y: *const f32, n: usize) -> c_int;
         pub fn fh_attention_decode_async(ctx: *mut fh_ctx, d_qkv: *const f32, d_k_cache: *mut f32, d_v_cache: *mut f32, capacity: usize, d: usize, heads: usize, pos: usize, d_out: *mut f32) -> c_int;
         pub fn fh_attention_prefill_async(ctx: *mut fh_ctx, d_qkv: *const f32, d_k_cache: *mut f32, d_v_cache: *mut f32, capacity: usize, d: usize, heads: usize, pos0: usize, rows: usize, d_out: *mut f32) -> c_int;
+        pub fn fh_q8_0_linear_residual_async(ctx: *mut fh_ctx, w: *const fh_q8_0, d_x: *const f32, m: usize, k: usize, d_bias: *const f32, bias_len: usize, d_r: *const f32, d_y: *mut f32, d_stats: *mut f32) -> c_int;
+        pub fn fh_q8_0_linear_normed_async(ctx: *mut fh_ctx, w: *const fh_q8_0, d_x: *const f32, m: usize, k: usize, d_stats: *const f32, d_gamma: *const f32, d_beta: *const f32, eps: f32, rms: c_int, d_bias: *const f32, bias_len: usize, d_y: *mut f32, activation: c_int) -> c_int;
         pub fn fh_attention_prefill_seqs_async(ctx: *mut fh_ctx, d_qkv: *const f32, d_k_cache: *mut f32, d_v_cache: *mut f32, seq_stride: usize, capacity: usize, d: usize, heads: usize, pos0: usize, rows: usize, seqs: usize, d_out: *mut f32) -> c_int;
         pub fn fh_qweight_upload(ctx: *mut fh_ctx, scales: *const f32, q: *const u8, k: usize, n: usize, kind: c_int, out: *mut *mut fh_qweight) -> c_int;
         pub fn fh_qweight_free(w: *mut fh_qweight);

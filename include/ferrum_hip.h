@@ -410,6 +410,31 @@ int fh_attention_prefill_seqs_async(fh_ctx* ctx, const float* d_qkv, float* d_k_
                                     size_t seq_stride, size_t capacity, size_t d, size_t heads, size_t pos0,
                                     size_t rows, size_t seqs, float* d_out);
 
+/* ---- a batched decode step's residual adds and norms, fused into the linears ---
+ * The block of forward_with_cache (layer/transformer.rs:221-294; Llama:
+ * LlamaBlock::forward_one, llm.rs:445-456) adds each projection to the
+ * residual stream and normalises the sum before the next linear.  These two
+ * entry points carry that between two linears without a norm launch:
+ *   fh_q8_0_linear_residual_async  y = r + (x W^T + b) (y may be r: the
+ *       residual stream updated in place) and, with d_stats, y's row
+ *       statistics: per row i and 32-column group g of the n outputs, the
+ *       group's mean and sum of squared deviations at d_stats[(i * n/32 + g) * 2]
+ *       (n % 32 == 0);
+ *   fh_q8_0_linear_normed_async    y = act(norm(x) W^T + b), norm formed
+ *       from such statistics of x: LayerNorm::forward (layer/norm.rs:46-82:
+ *       rms = 0, gamma, beta, eps 1e-5 there) or RmsNorm::forward_row
+ *       (llm.rs:58-65: rms = 1, gamma = its weight, beta NULL).
+ * W8A32 numerics (the 1e-5 rule); 3 <= m <= 64 runs each as one skinny-GEMM
+ * launch, other shapes as the linear plus a small kernel.  k % 32 == 0 for the
+ * normed form.  Errors as fh_q8_0_linear_async ("linear_forward: ..."),
+ * FH_ERR_INVALID for a missing pointer or y aliasing x. */
+int fh_q8_0_linear_residual_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                                  const float* d_bias, size_t bias_len, const float* d_r, float* d_y,
+                                  float* d_stats);
+int fh_q8_0_linear_normed_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
+                                const float* d_stats, const float* d_gamma, const float* d_beta, float eps, int rms,
+                                const float* d_bias, size_t bias_len, float* d_y, int activation);
+
 /* ---- packed per-row int8 / int4 weights: ops::qlinear (ops.rs:268-377) ------
  * QWeight (quant.rs:130-217): k rows (input features) x n columns (outputs),
  * one f32 scale per row, int8 levels ([k][n] bytes) or int4 levels in the

@@ -277,11 +277,16 @@ def test_linear_with_gelu_equals_linear_then_gelu(fh, orc, m, n, k):
     [(1, 2304, 768, True, 0, 0), (1, 3072, 768, True, 1, 0), (1, 50257, 768, True, 0, 0),  # GPT-2 shapes (G = 16)
      (2, 640, 1024, True, 1, 0), (1, 512, 2048, True, 0, 0),   # 64 lanes per row, 1 and 2 chunks per lane
      (1, 96, 128, True, 0, 0), (2, 100, 896, True, 1, 0),      # narrow rows, ragged group tails
-     (5, 640, 768, True, 1, 0), (1, 384, 768, False, 0, 0),    # two-kernel path: m > 2, no residual
+     (5, 640, 768, True, 1, 0), (1, 384, 768, False, 0, 0),    # m > 2: the norm fused into the skinny GEMM
+     (32, 2304, 768, True, 0, 0), (32, 3072, 768, True, 1, 0),  # the batch-32 step's QKV and up (+GELU)
+     (64, 1152, 896, True, 0, 0), (40, 4096, 1024, False, 1, 0),  # 64-row tiles, no residual
+     (17, 9728, 1024, True, 0, 0), (100, 640, 768, True, 1, 0),  # two column tiles per wave; m > 64: two kernels
      (3, 256, 512, True, 1, 1)])                              # W8A8
 def test_linear_ln_matches_oracle(fh, orc, m, n, k, res, act, numerics):
     """y = act(LayerNorm(x + r) W^T + b) and s = x + r, against the oracle's
-    add, layernorm, Q8_0 linear and gelu."""
+    add, layernorm, Q8_0 linear and gelu (m <= 2: the GEMV's prologue;
+    3 <= m <= 64: the skinny GEMM normalising as it stages; else two
+    kernels)."""
     import torch
 
     import ferrum_hip
@@ -314,6 +319,142 @@ def test_linear_ln_matches_oracle(fh, orc, m, n, k, res, act, numerics):
         ferrum_hip.linear_act_async(fh, w, th, m, k, tb, n, y2, act, numerics)
         assert np.array_equal(got, host(fh, y2))
     w.free()
+
+
+def test_fused_layernorm_with_non_finite_scales(fh, orc):
+    """The skinny GEMM with the fused LayerNorm (m = 32): weight rows with an
+    inf or NaN block scale are recomputed on the normalised row in the
+    reference's order, so their inf / NaN pattern is the oracle's; the other
+    outputs within 1e-5."""
+    import torch
+
+    import ferrum_hip
+
+    m, n, k = 32, 768, 768
+    rng = np.random.default_rng(5)
+    raw = orc.quantize_weight(n, k, 77, 0.05).reshape(n, k // 32, 34).copy()
+    raw[2, 0, :2] = np.frombuffer(np.uint16(0x7C00).tobytes(), np.uint8)   # +inf scale
+    raw[9, 5, :2] = np.frombuffer(np.uint16(0x7E00).tobytes(), np.uint8)   # NaN scale
+    raw = raw.ravel()
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x = (rng.standard_normal((m, k)) * 2).astype(np.float32)
+    r = rng.standard_normal((m, k)).astype(np.float32)
+    g, be = rng.standard_normal(k).astype(np.float32), (rng.standard_normal(k) * 0.1).astype(np.float32)
+    y = torch.empty((m, n), device="cuda")
+    ready()
+    ferrum_hip.linear_ln_async(fh, w, dev(x), dev(r), None, m, k, dev(g), dev(be), None, 0, y, 0, 0)
+    got = host(fh, y)
+    want = orc.q8_0_linear(orc.layernorm((x + r).astype(np.float32), g, be), raw, n, None)
+    assert np.array_equal(np.isnan(got), np.isnan(want))
+    assert np.array_equal(np.isposinf(got), np.isposinf(want)) and np.array_equal(np.isneginf(got), np.isneginf(want))
+    assert not np.isfinite(want[:, 2]).any() and np.isnan(want[:, 9]).all()
+    fin = np.isfinite(want)
+    close(got[fin], want[fin], 1e-5)
+    w.free()
+
+
+def group_stats(y):
+    """Per row and 32-column group: mean and sum of squared deviations (float64)."""
+    g = np.asarray(y, np.float64).reshape(y.shape[0], -1, 32)
+    mu = g.mean(axis=2)
+    return np.stack([mu, ((g - mu[..., None]) ** 2).sum(axis=2)], axis=2)
+
+
+@pytest.mark.parametrize("m,n,k,inplace", [(32, 768, 768, True), (32, 768, 3072, True), (3, 768, 768, False),
+                                           (64, 896, 4864, True), (40, 128, 512, False),
+                                           (1, 768, 768, True), (100, 256, 768, False)])  # other shapes: two kernels
+def test_linear_residual_matches_oracle(fh, orc, m, n, k, inplace):
+    """fh_q8_0_linear_residual_async: y = r + (x W^T + b) (in place: y is r)
+    against the oracle's linear and add, and y's row statistics (per 32-column
+    group: mean, sum of squared deviations) against float64."""
+    import torch
+
+    import ferrum_hip
+
+    rng = np.random.default_rng(m * 7 + n + k)
+    raw = orc.quantize_weight(n, k, n + 3 * k, 0.05)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x = rng.standard_normal((m, k)).astype(np.float32)
+    r = (rng.standard_normal((m, n)) * 3 + 1).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    tr = dev(r)
+    y = tr if inplace else torch.empty((m, n), device="cuda")
+    st = dev(np.full((m, n // 32, 2), np.nan, np.float32))
+    ready()
+    ferrum_hip.linear_residual_async(fh, w, dev(x), m, k, dev(b), n, tr, y, st)
+    got = host(fh, y)
+    lin = orc.q8_0_linear(x, raw, n, b)
+    want = (r + lin).astype(np.float32)
+    # the linear's 1e-5 rule (relative to its terms' mass, as every linear
+    # test), plus the add's half ulp
+    mass = np.abs(x.astype(np.float64)) @ np.abs(orc.q8_0_to_ferrum_weight(raw, n, k).astype(np.float64))
+    err = np.abs(got.astype(np.float64) - want)
+    assert (err <= 1e-5 * np.maximum(np.abs(lin), mass) + 6e-8 * np.abs(want)).all(), float(err.max())
+    gs, ws = host(fh, st), group_stats(got)
+    np.testing.assert_allclose(gs[..., 0], ws[..., 0], rtol=1e-5, atol=1e-6 * np.abs(got).max())
+    np.testing.assert_allclose(gs[..., 1], ws[..., 1], rtol=2e-5)
+    w.free()
+
+
+@pytest.mark.parametrize("m,n,k,rms,act", [(32, 2304, 768, False, 0), (32, 3072, 768, False, 1),
+                                           (64, 9728, 896, True, 0), (5, 1152, 896, True, 0),
+                                           (17, 9728, 1024, False, 0), (2, 640, 768, False, 1),
+                                           (80, 384, 256, True, 0)])  # m <= 2 or > 64: two kernels
+def test_linear_normed_matches_oracle(fh, orc, m, n, k, rms, act):
+    """fh_q8_0_linear_normed_async: act(norm(x) W^T + b) with LayerNorm or
+    RmsNorm formed from the rows' group statistics (per 32 columns: mean, sum
+    of squared deviations), against the oracle's layernorm / rmsnorm, Q8_0
+    linear and gelu."""
+    import torch
+
+    import ferrum_hip
+
+    rng = np.random.default_rng(m + n * 3 + k)
+    raw = orc.quantize_weight(n, k, n + k, 0.05)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    x = (rng.standard_normal((m, k)) * 2 + 0.5).astype(np.float32)
+    g = rng.standard_normal(k).astype(np.float32)
+    be = (rng.standard_normal(k) * 0.1).astype(np.float32)
+    b = (rng.standard_normal(n) * 0.1).astype(np.float32)
+    st = group_stats(x).astype(np.float32)
+    y = torch.empty((m, n), device="cuda")
+    ready()
+    ferrum_hip.linear_normed_async(fh, w, dev(x), m, k, dev(st), dev(g), None if rms else dev(be), 1e-6 if rms else 1e-5,
+                                   rms, dev(b), n, y, act)
+    h = orc.rmsnorm(x, g, 1e-6) if rms else orc.layernorm(x, g, be)
+    want = orc.q8_0_linear(h, raw, n, b)
+    close(host(fh, y), orc.gelu(want) if act else want, 1e-5)
+    w.free()
+
+
+def test_residual_then_normed_is_add_then_layernorm(fh, orc):
+    """A block's chain at 32 rows: x += attn W_out^T + b (statistics left),
+    then up(LayerNorm(x)) with GELU from them, against the oracle's add,
+    layernorm, linear and gelu; the residual stream equals the oracle's sum."""
+    import torch
+
+    import ferrum_hip
+
+    m, d, f = 32, 768, 3072
+    rng = np.random.default_rng(3)
+    wo_raw, wu_raw = orc.quantize_weight(d, d, 1, 0.05), orc.quantize_weight(f, d, 2, 0.05)
+    wo, wu = ferrum_hip.Q8_0Weight.upload(fh, wo_raw, d, d), ferrum_hip.Q8_0Weight.upload(fh, wu_raw, f, d)
+    x = rng.standard_normal((m, d)).astype(np.float32)
+    att = rng.standard_normal((m, d)).astype(np.float32)
+    bo, bu = (rng.standard_normal(d) * 0.1).astype(np.float32), (rng.standard_normal(f) * 0.1).astype(np.float32)
+    g, be = rng.standard_normal(d).astype(np.float32), (rng.standard_normal(d) * 0.1).astype(np.float32)
+    tx, st, y = dev(x), torch.empty((m, d // 32, 2), device="cuda"), torch.empty((m, f), device="cuda")
+    ready()
+    ferrum_hip.linear_residual_async(fh, wo, dev(att), m, d, dev(bo), d, tx, tx, st)
+    ferrum_hip.linear_normed_async(fh, wu, tx, m, d, st, dev(g), dev(be), 1e-5, False, dev(bu), f, y,
+                                   ferrum_hip.ACT_GELU)
+    s_want = (x + orc.q8_0_linear(att, wo_raw, d, bo)).astype(np.float32)
+    s_got = host(fh, tx)
+    close(s_got, s_want, 1e-5)
+    want = orc.gelu(orc.q8_0_linear(orc.layernorm(s_got, g, be), wu_raw, f, bu))
+    close(host(fh, y), want, 1e-5)
+    wo.free()
+    wu.free()
 
 
 def test_linear_ln_errors(fh, orc):
