@@ -866,7 +866,7 @@ int fh_q8_0_linear_normed_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x,
                                 const float* d_bias, size_t bias_len, float* d_y, int activation) {
     if (!ctx) return FH_ERR_INVALID;
     ctx->err.clear();
-    if (activation != FH_ACT_NONE && activation != FH_ACT_GELU)
+    if (activation != FH_ACT_NONE && activation != FH_ACT_GELU && activation != FH_ACT_SWIGLU32)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear_normed: unknown activation " + std::to_string(activation));
     int rc = check_linear(ctx, w, k, d_bias, bias_len, FH_W8A32);
     if (rc) return rc;
@@ -884,6 +884,10 @@ int fh_q8_0_linear_normed_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x,
     e.beta = rms ? nullptr : d_beta;
     e.eps = eps;
     e.rms = rms;
+    if (activation == FH_ACT_SWIGLU32 && (w->kind != FH_WEIGHT_Q8_0 || w->n % 64 || m < 3 || m > 64 || k > 1024))
+        return fh_fail(ctx, FH_ERR_LIMIT,
+                       "fh_q8_0_linear_normed: FH_ACT_SWIGLU32 needs a Q8_0 weight with n % 64 == 0, "
+                       "3 <= m <= 64 and k <= 1024");
     if (w->kind == FH_WEIGHT_Q8_0) {
         rc = fh_launch_skinny_norm_in(ctx, w, d_x, m, e, d_bias, d_y, activation);
         if (rc >= 0) return rc;

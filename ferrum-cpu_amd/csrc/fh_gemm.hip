@@ -808,7 +808,10 @@ __device__ __forceinline__ void split4(const float* v, float sc, uint2& h, uint2
 constexpr int kSkinnyRow = 36;
 
 // What the skinny GEMM does at its edges (k_gemm_skinny's MODE).
-enum { kSkinnyPlain = 0, kSkinnyNormIn = 1, kSkinnyResOut = 2 };
+// kSkinnyNormGlu: kSkinnyNormIn, and the weight's rows are gate and up
+// interleaved in groups of 32, so each workgroup's two column groups are the
+// gate and the up of the same 32 outputs, which leave as silu(gate) * up.
+enum { kSkinnyPlain = 0, kSkinnyNormIn = 1, kSkinnyResOut = 2, kSkinnyNormGlu = 3 };
 
 __device__ __forceinline__ int block_exponent(float mx) {
     if (!(mx > 0.0f)) return 0;
@@ -826,11 +829,19 @@ __device__ __forceinline__ float gelu_unfused(float v) {
     return 0.5f * v * (1.0f + tanhf(0.7978846f * (v + 0.044715f * v * v * v)));
 }
 
+// FeedForward's gate (llm.rs:415-421), (g / (1 + exp(-g))) * u, rounded as
+// k_swiglu rounds it.
+__device__ __forceinline__ float swiglu_unfused(float g, float u) {
+#pragma clang fp contract(off)
+    return (g / (1.0f + expf(-g))) * u;
+}
+
 // MODE kSkinnyPlain: y = act(x W^T + b).  kSkinnyNormIn: the input is
 // norm(x) (LayerNorm or RmsNorm), formed as the activations are staged from
 // the rows' statistics a kSkinnyResOut launch left (fh_edge).  kSkinnyResOut:
 // y = r + (x W^T + b) (y may be r) and, per row and 32-column group of y,
 // the group's mean and sum of squared deviations into e.stats.
+// kSkinnyNormGlu (NT = 2): as kSkinnyNormIn, y = silu(g) * u, [m][n / 2].
 template <int MT, int NT, int BPW, int MODE>
 __global__ void __launch_bounds__(512)
     k_gemm_skinny(const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
@@ -842,6 +853,9 @@ __global__ void __launch_bounds__(512)
     // loads and leave in MFMA lane order), afterwards its OUT sums; then
     // [KW][MT][BPW][32] row scales.
     constexpr int SLOT = OUT > MT * 32 * kSkinnyRow ? OUT : MT * 32 * kSkinnyRow;
+    constexpr bool NORM = MODE == kSkinnyNormIn || MODE == kSkinnyNormGlu;
+    constexpr bool GLU = MODE == kSkinnyNormGlu;
+    static_assert(!GLU || NT == 2, "the gate and up groups are a workgroup's two column groups");
     extern __shared__ __attribute__((aligned(16))) float lds[];
     __shared__ int last;
     float* sums = lds;
@@ -866,7 +880,7 @@ __global__ void __launch_bounds__(512)
     }
     float* inv_lds = lds + kw * SLOT + wave * (MT * BPW * 32);  // this wave's row scales
     float* xst = lds + wave * SLOT;                              // this wave's staging rows
-    const float* nm_beta = MODE == kSkinnyNormIn && e.beta ? e.beta : e.gamma;
+    const float* nm_beta = NORM && e.beta ? e.beta : e.gamma;
     // kSkinnyNormIn: the mean and 1 / sd of the rows this lane stages (row t *
     // 32 + lane / 8 + 8 q) from their group statistics ([rows][k / 32][2]: per
     // 32-column group its mean and M2).  The eight lanes staging a row split
@@ -878,11 +892,11 @@ __global__ void __launch_bounds__(512)
     // K loop would spill the wider tiles).  (Issuing the K loop's first batch
     // before the statistics are reduced timed no faster and spilled the
     // 64-row, two-group tiles.)
-    __shared__ float2 rowf[MODE == kSkinnyNormIn ? 8 : 1][MODE == kSkinnyNormIn ? MT * 32 : 1];
+    __shared__ float2 rowf[NORM ? 8 : 1][NORM ? MT * 32 : 1];
     constexpr int kJ = 4;  // groups per lane at most (k <= 1024)
     const int groups = k >> 5, s8 = lane & 7;
-    float2 gs[MODE == kSkinnyNormIn ? MT : 1][4][kJ];
-    if constexpr (MODE == kSkinnyNormIn) {
+    float2 gs[NORM ? MT : 1][4][kJ];
+    if constexpr (NORM) {
 #pragma unroll
         for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -903,7 +917,7 @@ __global__ void __launch_bounds__(512)
     const f16x zero = {};
 
     const int b_first = b_begin + wave * BPW;
-    if constexpr (MODE == kSkinnyNormIn) {
+    if constexpr (NORM) {
 #pragma unroll
         for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -935,7 +949,7 @@ __global__ void __launch_bounds__(512)
         uint4 wq[NT][BPW];
         uint16_t wd[NT][BPW];
         f4 xv[MT][BPW][4];
-        f4 gv[MODE == kSkinnyNormIn ? BPW : 1], bv[MODE == kSkinnyNormIn ? BPW : 1];
+        f4 gv[NORM ? BPW : 1], bv[NORM ? BPW : 1];
 #pragma unroll
         for (int u = 0; u < BPW; u++) {
             const int b = min(b0 + u, b_end - 1);
@@ -944,7 +958,7 @@ __global__ void __launch_bounds__(512)
                 wq[c][u] = *reinterpret_cast<const uint4*>(wrow[c] + b * 32);
                 wd[c][u] = drow[c][b];
             }
-            if constexpr (MODE == kSkinnyNormIn) {
+            if constexpr (NORM) {
                 gv[u] = *reinterpret_cast<const f4*>(e.gamma + b * 32 + (lane & 7) * 4);
                 bv[u] = *reinterpret_cast<const f4*>(nm_beta + b * 32 + (lane & 7) * 4);
             }
@@ -981,7 +995,7 @@ __global__ void __launch_bounds__(512)
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
                     f4 val = xv[t][u][q];
-                    if constexpr (MODE == kSkinnyNormIn) {
+                    if constexpr (NORM) {
                         const float2 f = rowf[wave][t * 32 + (lane >> 3) + 8 * q];
                         val = (val - f.x) * f.y * gv[u];
                         if (e.beta) val = val + bv[u];
@@ -1067,7 +1081,7 @@ __global__ void __launch_bounds__(512)
         float v = 0.0f;
         if (live) {
             if (__builtin_expect(bad, 0)) {
-                if constexpr (MODE == kSkinnyNormIn)
+                if constexpr (NORM)
                     s = exact_dot_norm(x + static_cast<size_t>(i) * k, e.gamma, e.beta, e.stats + 2 * static_cast<size_t>(i) * (k >> 5),
                                        k >> 5, e.rms, e.eps, k,
                                        qs + static_cast<size_t>(jj) * k, dsc + static_cast<size_t>(jj) * kb);
@@ -1095,6 +1109,26 @@ __global__ void __launch_bounds__(512)
             }
         }
     };
+    // kSkinnyNormGlu: output o of the gate group (c = 0) and o + 1024 of the
+    // up group (c = 1) are the same row and column.
+    auto finish_glu = [&](int o, float sg, float su) {
+        const int i = row_of(o), col = tile * 32 + r32, nh = n >> 1;
+        if (i >= m || col >= nh) return;
+        if (__builtin_expect(bad_c[0] || bad_c[1], 0)) {
+            const float* xi = x + static_cast<size_t>(i) * k;
+            const float* sti = e.stats + 2 * static_cast<size_t>(i) * (k >> 5);
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+                if (bad_c[c]) {
+                    const int j = tile * 64 + c * 32 + r32;
+                    const float v = exact_dot_norm(xi, e.gamma, e.beta, sti, k >> 5, e.rms, e.eps, k,
+                                                   qs + static_cast<size_t>(j) * k, dsc + static_cast<size_t>(j) * kb);
+                    if (c == 0) sg = v; else su = v;
+                }
+        }
+        const float g = bias ? sg + bias_c[0] : sg, u = bias ? su + bias_c[1] : su;
+        y[static_cast<size_t>(i) * nh + col] = swiglu_unfused(g, u);
+    };
     const size_t tiles = gridDim.x;
 #pragma unroll
     for (int t = 0; t < MT; t++)
@@ -1104,7 +1138,13 @@ __global__ void __launch_bounds__(512)
             for (int o = base + static_cast<int>(threadIdx.x); o < base + 1024; o += blockDim.x) {
                 float s = sums[o];
                 for (int w = 1; w < kw; w++) s += sums[w * SLOT + o];
-                if (splits == 1)
+                if (GLU && splits == 1) {
+                    if (c == 0) {
+                        float su = sums[o + 1024];
+                        for (int w = 1; w < kw; w++) su += sums[w * SLOT + o + 1024];
+                        finish_glu(o, s, su);
+                    }
+                } else if (splits == 1)
                     finish(o, s, bad_c[c], bias_c[c], jj);
                 else
                     __hip_atomic_store(part + (split * tiles + tile) * OUT + o, s, __ATOMIC_RELAXED,
@@ -1124,6 +1164,31 @@ __global__ void __launch_bounds__(512)
     if (!last) return;
     // All splits of two outputs per thread are loaded at once (clamped
     // addresses, unused values skipped in the sum), then added in split order.
+    if constexpr (GLU) {
+        // gate and up partials of one output per thread at a time, each added in split order
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const int base = t * NT * 1024;
+            for (int o = base + static_cast<int>(threadIdx.x); o < base + 1024; o += blockDim.x) {
+                float pv[2][kMaxSplits];
+#pragma unroll
+                for (int q = 0; q < 2; q++)
+#pragma unroll
+                    for (int sp = 0; sp < kMaxSplits; sp++)
+                        pv[q][sp] = __hip_atomic_load(part + (min(sp, splits - 1) * tiles + tile) * OUT + o + q * 1024,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                float sg = pv[0][0], su = pv[1][0];
+#pragma unroll
+                for (int sp = 1; sp < kMaxSplits; sp++) {
+                    sg = sp < splits ? sg + pv[0][sp] : sg;
+                    su = sp < splits ? su + pv[1][sp] : su;
+                }
+                finish_glu(o, sg, su);
+            }
+        }
+        if (threadIdx.x == 0) __hip_atomic_store(counters + tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return;
+    }
 #pragma unroll
     for (int t = 0; t < MT; t++)
 #pragma unroll
@@ -1431,6 +1496,14 @@ int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     constexpr bool kEdges = NT <= 2 && !(MT == 2 && NT == 2 && BPW == 2);
     if (mode != kSkinnyPlain && !kEdges)
         return fh_fail(ctx, FH_ERR_LIMIT, "skinny GEMM: no fused norm or residual for this tile");
+    if constexpr (kEdges && NT == 2) {
+        if (mode == kSkinnyNormGlu) {
+            go(k_gemm_skinny<MT, NT, BPW, kSkinnyNormGlu>);
+            FH_HIP(ctx, hipGetLastError());
+            return FH_OK;
+        }
+    }
+    if (mode == kSkinnyNormGlu) return fh_fail(ctx, FH_ERR_LIMIT, "skinny GEMM: no fused SwiGLU for this tile");
     if constexpr (kEdges) {
         if (mode == kSkinnyNormIn) go(k_gemm_skinny<MT, NT, BPW, kSkinnyNormIn>);
         else if (mode == kSkinnyResOut) go(k_gemm_skinny<MT, NT, BPW, kSkinnyResOut>);
@@ -1474,6 +1547,10 @@ int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const
                   const fh_scratch* scratch = nullptr, int act = FH_ACT_NONE, const fh_edge* edge = nullptr,
                   int mode = kSkinnyPlain) {
     const size_t t32 = (w->n + 31) / 32;
+    // the fused SwiGLU needs each workgroup's two column groups to be a gate / up pair
+    if (mode == kSkinnyNormGlu)
+        return m <= 32 ? launch_skinny_t<1, 2, 3>(ctx, w, x, m, bias, y, scratch, act, edge, mode)
+                       : launch_skinny_t<2, 2, 1>(ctx, w, x, m, bias, y, scratch, act, edge, mode);
     if (mode == kSkinnyPlain && t32 >= kWideMinTiles && (w->k == 768 || w->k == 896 || w->k == 1024)) {
         // 32 rows per launch: at m = 64 two launches, each streaming the
         // weight once, beat the skinny kernel's single pass (151936 x 896:
@@ -1540,6 +1617,7 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
 int fh_launch_skinny_norm_in(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const fh_edge& e,
                              const float* bias, float* y, int act) {
     if (m < 3 || m > 64 || w->kind != FH_WEIGHT_Q8_0 || w->k > 1024) return -1;
+    if (act == FH_ACT_SWIGLU32) return launch_skinny(ctx, w, x, m, bias, y, nullptr, FH_ACT_NONE, &e, kSkinnyNormGlu);
     return launch_skinny(ctx, w, x, m, bias, y, nullptr, act, &e, kSkinnyNormIn);
 }
 

@@ -571,6 +571,17 @@ def add_async(ctx: Context, x, y, n: int):
 
 
 ACT_NONE, ACT_GELU = 0, 1
+# linear_normed_async only: the weight's rows are gate / up interleaved in
+# groups of 32 (interleave_gate_up), the output silu(gate) * up ([m, n / 2])
+ACT_SWIGLU32 = 2
+
+
+def interleave_gate_up(gate: np.ndarray, up: np.ndarray, rows: int) -> np.ndarray:
+    """Two row-major matrices of `rows` rows each (Q8_0 bytes or any per-row
+    layout) as one, gate and up rows interleaved in groups of 32: the weight
+    ACT_SWIGLU32 reads."""
+    g, u = np.asarray(gate).reshape(rows // 32, 32, -1), np.asarray(up).reshape(rows // 32, 32, -1)
+    return np.stack([g, u], axis=1).reshape(-1)
 
 
 def linear_act_async(ctx: Context, weight: "Q8_0Weight", x, m: int, k: int, bias, bias_len: int, y, act: int,
@@ -1146,6 +1157,8 @@ class LlamaDevice:
         # the residual stream's row statistics between a projection and the next RmsNorm
         self.fused = 3 <= B <= 64 and self.d % 32 == 0
         self.st = torch.empty((B, self.d // 32, 2), device=dev) if self.fused else None
+        # SwiGLU inside the gate|up GEMM (a Q8_0 gate|up stored interleaved, ACT_SWIGLU32)
+        self.glu = self.fused and self.ffn % 32 == 0 and self.d <= 1024
 
     def _alloc_cache(self):
         import torch
@@ -1171,14 +1184,15 @@ class LlamaDevice:
             qkv = np.concatenate([raw(p + "attn_q"), raw(p + "attn_k"), raw(p + "attn_v")])
             bias = np.concatenate([np.asarray(weights.get(p + f"attn_{s}.bias", np.zeros(n, np.float32)), np.float32)
                                    for s, n in (("q", m.q_dim), ("k", m.kv_dim), ("v", m.kv_dim))])
-            gate_up = np.concatenate([raw(p + "ffn_gate"), raw(p + "ffn_up")])
+            gate, up = raw(p + "ffn_gate"), raw(p + "ffn_up")
+            gate_up = interleave_gate_up(gate, up, m.ffn) if m.glu else np.concatenate([gate, up])
             k, v = m._alloc_cache()
             m.blocks.append({
                 "attn_norm": f(weights[p + "attn_norm"]), "ffn_norm": f(weights[p + "ffn_norm"]),
                 "qkv": Q8_0Weight.upload(ctx, qkv, m.qkv_dim, d), "qkv_b": f(bias),
                 "o": Q8_0Weight.upload(ctx, raw(p + "attn_output"), d, m.q_dim),
                 "gate_up": Q8_0Weight.upload(ctx, gate_up, 2 * m.ffn, d),
-                "down": Q8_0Weight.upload(ctx, raw(p + "ffn_down"), d, m.ffn), "k": k, "v": v})
+                "down": Q8_0Weight.upload(ctx, raw(p + "ffn_down"), d, m.ffn), "k": k, "v": v, "glu": m.glu})
         m.out_norm = f(weights["output_norm"])
         torch.cuda.synchronize()
         ctx.sync()
@@ -1227,12 +1241,14 @@ class LlamaDevice:
                     return (sc * blk[:, 2:].copy().view(np.int8).astype(np.float32)).reshape(n_out, n_in)
                 return g.read_f32(ctx, name).reshape(n_out, n_in)
 
-            def weight(names):
-                """One device weight holding the rows of `names` in order."""
+            def weight(names, glu=False):
+                """One device weight holding the rows of `names` in order (glu:
+                gate and up interleaved for ACT_SWIGLU32, Q8_0 only)."""
                 shapes = [shape(n) for n in names]
                 n_in = shapes[0][1]
                 if all(kind(n) == GGML_Q8_0 for n in names):
-                    raw = np.concatenate([np.frombuffer(g.raw(n), np.uint8) for n in names])
+                    parts = [np.frombuffer(g.raw(n), np.uint8) for n in names]
+                    raw = interleave_gate_up(parts[0], parts[1], shapes[0][0]) if glu else np.concatenate(parts)
                     return Q8_0Weight.upload(ctx, raw, sum(s[0] for s in shapes), n_in)
                 return Q8_0Weight.upload_f32(ctx, np.concatenate([dense(n) for n in names]))
 
@@ -1254,11 +1270,13 @@ class LlamaDevice:
                     qkv_b = torch.cat([f(b) if b in g.tensors else torch.zeros(n, device="cuda")
                                        for b, n in zip(biases, (m.q_dim, m.kv_dim, m.kv_dim))])
                 k, v = m._alloc_cache()
+                gu_names = [p + "ffn_gate.weight", p + "ffn_up.weight"]
+                glu = m.glu and all(kind(n) == GGML_Q8_0 for n in gu_names)
                 m.blocks.append({
                     "attn_norm": f(p + "attn_norm.weight"), "ffn_norm": f(p + "ffn_norm.weight"),
                     "qkv": weight(names), "qkv_b": qkv_b, "o": weight([p + "attn_output.weight"]),
-                    "gate_up": weight([p + "ffn_gate.weight", p + "ffn_up.weight"]),
-                    "down": weight([p + "ffn_down.weight"]), "k": k, "v": v})
+                    "gate_up": weight(gu_names, glu), "down": weight([p + "ffn_down.weight"]), "k": k, "v": v,
+                    "glu": glu})
             m.out_norm = f("output_norm.weight")
             if cfg["rope_freqs"]:
                 m.rope_freqs = f("rope_freqs.weight")
@@ -1292,7 +1310,7 @@ class LlamaDevice:
             k, v = m._alloc_cache()
             m.blocks.append({"attn_norm": vec(d, 1.0), "ffn_norm": vec(d, 1.0), "qkv": q8(m.qkv_dim, d)[0],
                              "qkv_b": vec(m.qkv_dim), "o": q8(d, m.q_dim)[0], "gate_up": q8(2 * m.ffn, d)[0],
-                             "down": q8(d, m.ffn)[0], "k": k, "v": v})
+                             "down": q8(d, m.ffn)[0], "k": k, "v": v, "glu": m.glu})
         m.out_norm = vec(d, 1.0)
         torch.cuda.synchronize()
         ctx.sync()
@@ -1303,8 +1321,10 @@ class LlamaDevice:
         rows the o and down projections add themselves to the residual stream
         and leave its row statistics, and the q|k|v and gate|up GEMMs form the
         RmsNorm from them as they stage their inputs (seven launches per
-        block); otherwise each RmsNorm is a launch of its own (nine)."""
-        return 1 + (7 if self.fused else 9) * self.layers + 2 + (1 if self.fused else 0)
+        block, six with SwiGLU in the gate|up GEMM); otherwise each RmsNorm is
+        a launch of its own (nine)."""
+        per = (6 if all(b.get("glu") for b in self.blocks) else 7) if self.fused else 9
+        return 1 + per * self.layers + 2 + (1 if self.fused else 0)
 
     def forward_one(self, token: int):
         """LlamaModel::forward_one (llm.rs:606-616) for a single sequence (rows
@@ -1350,9 +1370,13 @@ class LlamaDevice:
                 gqa_attention_decode_async(ctx, self.qkv, self.qkv_dim, B, self.nh, self.nkv, self.hd, b["k"], b["v"],
                                            self.cap, self.pos, max_pos, self.att)
                 linear_residual_async(ctx, b["o"], self.att, B, self.q_dim, None, 0, x, x, st)
-                linear_normed_async(ctx, b["gate_up"], x, B, d, st, b["ffn_norm"], None, self.eps, True, None, 0,
-                                    self.gu)
-                swiglu_async(ctx, self.gu, self.gu[:, self.ffn:], B, self.ffn, 2 * self.ffn, self.mid)
+                if b.get("glu"):
+                    linear_normed_async(ctx, b["gate_up"], x, B, d, st, b["ffn_norm"], None, self.eps, True, None, 0,
+                                        self.mid, ACT_SWIGLU32)
+                else:
+                    linear_normed_async(ctx, b["gate_up"], x, B, d, st, b["ffn_norm"], None, self.eps, True, None, 0,
+                                        self.gu)
+                    swiglu_async(ctx, self.gu, self.gu[:, self.ffn:], B, self.ffn, 2 * self.ffn, self.mid)
                 linear_residual_async(ctx, b["down"], self.mid, B, self.ffn, None, 0, x, x, st)
             rmsnorm_async(ctx, x, None, None, B, d, self.out_norm, self.eps, self.h)
             linear_forward_async(ctx, self.head, self.h, B, d, None, 0, self.z)

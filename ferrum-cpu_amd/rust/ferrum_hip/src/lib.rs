@@ -99,6 +99,7 @@ pub mod sys {
     pub const FH_RECENT_RANGES: c_int = 0x100;
     pub const FH_ACT_NONE: c_int = 0;
     pub const FH_ACT_GELU: c_int = 1;
+    pub const FH_ACT_SWIGLU32: c_int = 2;
     pub const FH_ROPE_NORM: c_int = 0;
     pub const FH_ROPE_NEOX: c_int = 1;
     pub const FH_QINT8: c_int = 0;

@@ -244,8 +244,13 @@ int fh_sample_rows_async(fh_ctx* ctx, const float* d_logits, size_t rows, size_t
 int fh_debug_sampler_faults(fh_ctx* ctx, int skip_segment, uint32_t spin_limit);
 
 /* ---- the rest of a GPT-2 decode step ------------------------------------- */
-/* Activation applied to a linear's output before it is stored. */
-enum { FH_ACT_NONE = 0, FH_ACT_GELU = 1 };
+/* Activation applied to a linear's output before it is stored.
+ * FH_ACT_SWIGLU32 (fh_q8_0_linear_normed_async only): the weight's n rows are
+ * a gate and an up projection interleaved in groups of 32 (rows 64g .. 64g + 31
+ * are gate rows 32g .. 32g + 31, rows 64g + 32 .. 64g + 63 the up rows of the
+ * same outputs), and y[i][j] = silu(gate[i][j]) * up[i][j] is stored,
+ * [m][n / 2]: FeedForward's gate (llm.rs:415-421) inside the linear. */
+enum { FH_ACT_NONE = 0, FH_ACT_GELU = 1, FH_ACT_SWIGLU32 = 2 };
 /* Device pointers, enqueued on the context's stream.  With fh_q8_0_linear_async
  * and fh_sample_rows_async these keep a whole decode step on the device.
  *
@@ -426,8 +431,11 @@ int fh_attention_prefill_seqs_async(fh_ctx* ctx, const float* d_qkv, float* d_k_
  *       (llm.rs:58-65: rms = 1, gamma = its weight, beta NULL).
  * W8A32 numerics (the 1e-5 rule); 3 <= m <= 64 runs each as one skinny-GEMM
  * launch, other shapes as the linear plus a small kernel.  k % 32 == 0 for the
- * normed form.  Errors as fh_q8_0_linear_async ("linear_forward: ..."),
- * FH_ERR_INVALID for a missing pointer or y aliasing x. */
+ * normed form.  The normed form's activation may be FH_ACT_SWIGLU32 (a Llama
+ * block's gate|up: y is [m][n / 2]) for Q8_0 weights with n % 64 == 0 at
+ * 3 <= m <= 64 and k <= 1024, FH_ERR_LIMIT elsewhere.  Errors as
+ * fh_q8_0_linear_async ("linear_forward: ..."), FH_ERR_INVALID for a missing
+ * pointer or y aliasing x. */
 int fh_q8_0_linear_residual_async(fh_ctx* ctx, const fh_q8_0* w, const float* d_x, size_t m, size_t k,
                                   const float* d_bias, size_t bias_len, const float* d_r, float* d_y,
                                   float* d_stats);

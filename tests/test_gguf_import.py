@@ -405,3 +405,18 @@ def test_llama_plan_other_errors(fhm, gg, orc, tmp_path):
         fhm.llama_gguf_plan(g)
     assert e.value.msg == (f"tensor 'blk.0.ffn_gate.weight' has dims [{c['d']}, {c['ffn']}], expected "
                            f"[{c['d']}, {c['ffn'] + 32}] from the metadata")
+
+
+def test_interleave_gate_up_layout(fhm):
+    """The gate|up weight ACT_SWIGLU32 reads: rows 64g .. 64g + 31 are gate rows
+    32g .. 32g + 31 and the next 32 the up rows of the same outputs, each row's
+    bytes (a Q8_0 row, or one bias value) kept whole."""
+    rows, width = 96, 34 * 4
+    gate = np.arange(rows * width, dtype=np.int64).reshape(rows, width)
+    up = -gate - 1
+    out = fhm.interleave_gate_up(gate.ravel(), up.ravel(), rows).reshape(2 * rows, width)
+    for g in range(rows // 32):
+        assert np.array_equal(out[64 * g:64 * g + 32], gate[32 * g:32 * g + 32])
+        assert np.array_equal(out[64 * g + 32:64 * g + 64], up[32 * g:32 * g + 32])
+    bias = fhm.interleave_gate_up(np.arange(rows), np.arange(rows) + 1000, rows)
+    assert bias.tolist()[:64] == list(range(32)) + list(range(1000, 1032))

@@ -427,6 +427,88 @@ def test_linear_normed_matches_oracle(fh, orc, m, n, k, rms, act):
     w.free()
 
 
+@pytest.mark.parametrize("m,ffn,k,rms,bias", [(64, 4864, 896, True, False), (32, 4864, 896, True, False),
+                                               (5, 256, 128, True, False), (40, 160, 1024, True, False),
+                                               (3, 96, 64, False, True), (33, 4864, 896, False, True)])
+def test_linear_normed_swiglu_matches_oracle(fh, orc, m, ffn, k, rms, bias):
+    """ACT_SWIGLU32: silu(norm(x) G^T + bg) * (norm(x) U^T + bu) from one
+    gate|up weight interleaved in groups of 32 rows, against the oracle's
+    rmsnorm / layernorm, two Q8_0 linears and swiglu (the error the two
+    linears may carry, 1e-5 of their terms' size, carried through silu and the
+    product); where the gate|up GEMM picks the same tile unfused, the result
+    equals the unfused GEMM followed by fh_swiglu bit for bit."""
+    import torch
+
+    import ferrum_hip
+
+    rng = np.random.default_rng(m * 7 + ffn + k)
+    g_raw = orc.quantize_weight(ffn, k, ffn + k, 0.05)
+    u_raw = orc.quantize_weight(ffn, k, ffn + k + 1, 0.05)
+    w = ferrum_hip.Q8_0Weight.upload(fh, ferrum_hip.interleave_gate_up(g_raw, u_raw, ffn), 2 * ffn, k)
+    x = (rng.standard_normal((m, k)) * 2 + 0.5).astype(np.float32)
+    gam = rng.standard_normal(k).astype(np.float32)
+    be = (rng.standard_normal(k) * 0.1).astype(np.float32)
+    bg = (rng.standard_normal(ffn) * 0.1).astype(np.float32) if bias else None
+    bu = (rng.standard_normal(ffn) * 0.1).astype(np.float32) if bias else None
+    b_il = ferrum_hip.interleave_gate_up(bg, bu, ffn).astype(np.float32) if bias else None
+    st = group_stats(x).astype(np.float32)
+    eps = 1e-6 if rms else 1e-5
+    y = torch.empty((m, ffn), device="cuda")
+    ready()
+    ferrum_hip.linear_normed_async(fh, w, dev(x), m, k, dev(st), dev(gam), None if rms else dev(be), eps, rms,
+                                   dev(b_il) if bias else None, 2 * ffn if bias else 0, y, ferrum_hip.ACT_SWIGLU32)
+    got = host(fh, y)
+    h = orc.rmsnorm(x, gam, eps) if rms else orc.layernorm(x, gam, be)
+    gate, up = orc.q8_0_linear(h, g_raw, ffn, bg), orc.q8_0_linear(h, u_raw, ffn, bu)
+    want = orc.swiglu(gate, up)
+    g64, u64 = gate.astype(np.float64), up.astype(np.float64)
+    sig = 1.0 / (1.0 + np.exp(-g64))
+    dsilu = np.abs(sig * (1.0 + g64 * (1.0 - sig)))
+    tol = 1e-5 * (dsilu * np.maximum(1.0, np.abs(g64)) * np.abs(u64) + np.abs(g64 * sig) * np.maximum(1.0, np.abs(u64)))
+    err = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert np.all(err <= tol + 1e-6 * np.maximum(1.0, np.abs(want))), float((err - tol).max())
+    if 2 * ffn // 32 >= 256:  # the same tile as the unfused gate|up GEMM
+        gu = torch.empty((m, 2 * ffn), device="cuda")
+        ferrum_hip.linear_normed_async(fh, w, dev(x), m, k, dev(st), dev(gam), None if rms else dev(be), eps, rms,
+                                       dev(b_il) if bias else None, 2 * ffn if bias else 0, gu)
+        gu_h = host(fh, gu).reshape(m, ffn // 32, 2, 32)
+        sep = torch.empty((m, ffn), device="cuda")
+        gg = dev(np.ascontiguousarray(gu_h[:, :, 0].reshape(m, ffn)))
+        uu = dev(np.ascontiguousarray(gu_h[:, :, 1].reshape(m, ffn)))
+        ready()
+        ferrum_hip.swiglu_async(fh, gg, uu, m, ffn, ffn, sep)
+        assert np.array_equal(host(fh, sep).view(np.uint32), got.view(np.uint32))
+    w.free()
+
+
+def test_linear_normed_swiglu_limits(fh, orc):
+    """ACT_SWIGLU32 is the skinny GEMM's epilogue: m outside 3 .. 64, a weight
+    whose rows are not whole gate / up pairs of 32, or k > 1024 is
+    FH_ERR_LIMIT; the other linear entry points refuse the activation."""
+    import torch
+
+    import ferrum_hip
+
+    k = 128
+    for m, n, kk in ((2, 128, k), (65, 128, k), (4, 96, k), (4, 128, 2048)):
+        raw = orc.quantize_weight(n, kk, 5, 0.05)
+        w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, kk)
+        x, st = torch.zeros((m, kk), device="cuda"), torch.zeros((m, kk // 32, 2), device="cuda")
+        gam, y = torch.ones(kk, device="cuda"), torch.empty((m, n), device="cuda")
+        with pytest.raises(ferrum_hip.FerrumHipError) as e:
+            ferrum_hip.linear_normed_async(fh, w, x, m, kk, st, gam, None, 1e-6, True, None, 0, y,
+                                           ferrum_hip.ACT_SWIGLU32)
+        assert e.value.code == ferrum_hip.FH_ERR_LIMIT and "SWIGLU32" in str(e.value)
+        w.free()
+    raw = orc.quantize_weight(128, k, 6, 0.05)
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, 128, k)
+    with pytest.raises(ferrum_hip.FerrumHipError) as e:
+        ferrum_hip.linear_act_async(fh, w, torch.zeros((4, k), device="cuda"), 4, k, None, 0,
+                                    torch.empty((4, 128), device="cuda"), ferrum_hip.ACT_SWIGLU32)
+    assert e.value.code == ferrum_hip.FH_ERR_INVALID
+    w.free()
+
+
 def test_residual_then_normed_is_add_then_layernorm(fh, orc):
     """A block's chain at 32 rows: x += attn W_out^T + b (statistics left),
     then up(LayerNorm(x)) with GELU from them, against the oracle's add,

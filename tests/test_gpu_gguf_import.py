@@ -193,22 +193,27 @@ def step(m, toks, pos):
     return m.z.cpu().numpy()
 
 
+@pytest.mark.parametrize("rows", [2, 3])
 @pytest.mark.parametrize("name,arch,biases,tied", [("QWEN", "qwen2", True, True), ("LLAMA", "llama", False, False)])
-def test_llama_gguf_equals_the_model_built_from_arrays(fh, orc, tmp_path, name, arch, biases, tied):
-    """Two rows, 10 steps: the file-loaded model's scores are the array-built
-    model's, bit for bit (same kernels on the same Q8_0 bytes)."""
+def test_llama_gguf_equals_the_model_built_from_arrays(fh, orc, tmp_path, name, arch, biases, tied, rows):
+    """Two rows (one launch per op) and three (the fused edges, with the
+    gate|up rows interleaved for the SwiGLU epilogue), 10 steps: the
+    file-loaded model's scores are the array-built model's, bit for bit (same
+    kernels on the same Q8_0 bytes)."""
     import ferrum_hip
 
     cfg = dict(getattr(llama_tiny, name))
     w = llama_tiny.make_weights(orc, cfg, 33, biases, tied)
-    a = ferrum_hip.LlamaDevice.from_weights(fh, w, cfg, 2)
-    b = ferrum_hip.LlamaDevice.from_gguf(fh, llama_path(tmp_path, w, cfg, arch), rows=2)
+    a = ferrum_hip.LlamaDevice.from_weights(fh, w, cfg, rows)
+    b = ferrum_hip.LlamaDevice.from_gguf(fh, llama_path(tmp_path, w, cfg, arch), rows=rows)
     try:
         assert (b.rope_type, b.nkv, b.hd, b.rope_dim, b.cap) == (cfg["rope_type"], cfg["n_kv"], cfg["head_dim"],
                                                                  cfg.get("rope_dim", cfg["head_dim"]), cfg["context"])
-        toks = np.random.default_rng(1).integers(0, cfg["vocab"], (10, 2))
+        assert all(blk["glu"] for blk in a.blocks + b.blocks) == (rows == 3)
+        toks = np.random.default_rng(1).integers(0, cfg["vocab"], (10, rows))
         for t in range(10):
-            bits_equal(step(b, toks[t], [t, t + 3]), step(a, toks[t], [t, t + 3]))
+            pos = [t + 3 * r for r in range(rows)]
+            bits_equal(step(b, toks[t], pos), step(a, toks[t], pos))
     finally:
         a.free()
         b.free()
