@@ -126,6 +126,50 @@ def test_gqa_attention_matches_oracle(fh, orc, nh, nkv, hd, T):
         assert np.array_equal(kh[r], ko[r]) and np.array_equal(vh[r], vo[r])
 
 
+@pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (32, 8, 128), (4, 2, 32), (12, 2, 64), (16, 2, 32)])
+def test_grouped_attention_equals_the_per_head_kernel(fh, orc, nh, nkv, hd):
+    """The grouped-query kernel (one workgroup per kv head's query heads, K
+    and V loaded once) gives the per-head kernel's bits: the same query heads
+    run with every kv head repeated for each of its query heads (n_kv =
+    n_heads).  Rows at positions 0, 40, 200 and 700 (a launch reaching 384
+    positions takes the grouped kernel: one chunk, several, the merge over
+    many), cache rows seeded below them; the new k / v rows land in the cache
+    as the expanded run writes them."""
+    import torch
+
+    import ferrum_hip
+
+    rows, cap, grp = 4, 720, nh // nkv
+    qd, kvd = nh * hd, nkv * hd
+    rng = np.random.default_rng(nh * hd + nkv)
+    qkv = (rng.standard_normal((rows, qd + 2 * kvd)) * 1.5).astype(np.float32)
+    kc0 = rng.standard_normal((rows, cap, nkv, hd)).astype(np.float32)
+    vc0 = rng.standard_normal((rows, cap, nkv, hd)).astype(np.float32)
+    pos = np.array([0, 40, 200, 700], np.uint32)
+    # the same inputs with kv head j repeated for its query heads j * grp ..
+    k_new = qkv[:, qd:qd + kvd].reshape(rows, nkv, hd)
+    v_new = qkv[:, qd + kvd:].reshape(rows, nkv, hd)
+    qkv_e = np.concatenate([qkv[:, :qd], np.repeat(k_new, grp, axis=1).reshape(rows, qd),
+                            np.repeat(v_new, grp, axis=1).reshape(rows, qd)], axis=1)
+    kc, vc = dev(kc0.ravel()), dev(vc0.ravel())
+    kce, vce = dev(np.repeat(kc0, grp, axis=2).ravel()), dev(np.repeat(vc0, grp, axis=2).ravel())
+    out, out_e = torch.empty((rows, qd), device="cuda"), torch.empty((rows, qd), device="cuda")
+    dpos = dev(pos.view(np.int32))
+    ready()
+    ferrum_hip.gqa_attention_decode_async(fh, dev(qkv), qd + 2 * kvd, rows, nh, nkv, hd, kc, vc, cap, dpos,
+                                          int(pos.max()), out)
+    ferrum_hip.gqa_attention_decode_async(fh, dev(qkv_e), 3 * qd, rows, nh, nh, hd, kce, vce, cap, dpos,
+                                          int(pos.max()), out_e)
+    got, want = host(fh, out), host(fh, out_e)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    kh = host(fh, kc).reshape(rows, cap, nkv, hd)
+    keh = host(fh, kce).reshape(rows, cap, nh, hd)
+    for r in range(rows):
+        assert np.array_equal(kh[r, pos[r]], k_new[r]) and np.array_equal(keh[r, pos[r]], np.repeat(k_new[r], grp, 0))
+        close(got[r], orc.gqa_attention_decode(qkv[r], kc0[r].reshape(cap, kvd), vc0[r].reshape(cap, kvd),
+                                               nh, nkv, hd, int(pos[r])), 1e-5)
+
+
 def test_gqa_attention_bad_positions_give_nan_and_leave_the_cache(fh, orc):
     import torch
 
