@@ -90,6 +90,46 @@ def make_weight(ctx, fh, torch, n, k, gen):
     return wt
 
 
+def launch_roofline(ctx, torch, calls, bytes_per_launch, launches=240):
+    """A kernel's roofline line: one HIP graph of `launches` back-to-back
+    launches cycling over `calls` (one per weight replica, so the weights
+    stream from HBM), timed with HIP events on the stream the graph replays
+    on; achieved = algorithmic bytes per launch / average launch time."""
+    for c in calls:
+        c()
+    ctx.sync()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+        for i in range(launches):
+            calls[i % len(calls)]()
+    ctx.set_stream(torch.cuda.current_stream().cuda_stream)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / launches
+    del g
+    gbps = bytes_per_launch / (us * 1e-6) / 1e9
+    return {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(gbps / HBM_PEAK_GBS, 4), "traffic": None, "avg_launch_us": round(us, 3),
+            "bytes_per_launch": bytes_per_launch}
+
+
+def copy_for_counters(torch, dev):
+    """A plain device copy of known size (COPY_BYTES), five times, for scaling
+    the PMC byte counters (FETCH_SIZE / WRITE_SIZE) of the same run."""
+    src = torch.empty(COPY_BYTES // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+
+
 class Replica:
     def __init__(self, ctx, fh, torch, gen):
         self.layers = [[make_weight(ctx, fh, torch, n, k, gen) for (n, k) in LAYER_SHAPES] for _ in range(L)]
@@ -402,8 +442,31 @@ def main():
             mdl.free()
         del bmodels
         torch.cuda.synchronize()
+
+        # ---- the step's dominant kernel family, the LayerNorm-in skinny GEMMs
+        # (24 of the 65 launches): the MLP up projection, 3072 x 768 at m = 32
+        # with GELU out, alone over 128 weight replicas (320 MB, HBM-forced)
+        ups = [make_weight(ctx, fh, torch, FFN, D, gen) for _ in range(128)]
+        xu = torch.randn((B, D), generator=gen, device=dev)
+        stu = torch.rand((B, D // 32, 2), generator=gen, device=dev)
+        gu, bu, biu = torch.ones(D, device=dev), torch.zeros(D, device=dev), torch.zeros(FFN, device=dev)
+        yu = torch.empty((B, FFN), device=dev)
+        calls = [(lambda w=w: fh.linear_normed_async(ctx, w, xu, B, D, stu, gu, bu, 1e-5, False, biu, FFN, yu,
+                                                     fh.ACT_GELU)) for w in ups]
+        up_bytes = q8_bytes(FFN, D) + 4 * B * D + 8 * B * (D // 32) + 8 * D + 4 * FFN + 4 * B * FFN
+        roof = launch_roofline(ctx, torch, calls, up_bytes)
+        roof["kernel"] = ("k_gemm_skinny<1,2,3,LayerNorm in> (MLP up 3072 x 768 at m = 32, GELU out; the step's "
+                          "24 LayerNorm-in GEMMs are its largest kernel family)")
+        roof["bytes_note"] = "Q8_0 weight + x + row statistics + gamma/beta + bias + y"
+        result["b32"]["roofline"] = roof
+        for w in ups:
+            w.free()
+        del ups, calls
+        torch.cuda.synchronize()
         if args.leg == "b32":
-            print(json.dumps({"leg": "b32", "b32": result["b32"], "b32_unchained": result["b32_unchained"]}))
+            copy_for_counters(torch, dev)
+            print(json.dumps({"leg": "b32", "b32": result["b32"], "b32_unchained": result["b32_unchained"],
+                              "copy_bytes_per_launch": COPY_BYTES}))
             return
 
     if args.leg in ("all", "dropin"):
@@ -430,7 +493,8 @@ def main():
     if args.leg in ("all", "qwen"):
         result["qwen2_b64"] = qwen_leg(ctx, fh, torch, gen, dev, max(args.steps // 20, 10), args.warmup)
     if args.leg == "qwen":
-        print(json.dumps({"leg": "qwen", "qwen2_b64": result["qwen2_b64"]}))
+        copy_for_counters(torch, dev)
+        print(json.dumps({"leg": "qwen", "qwen2_b64": result["qwen2_b64"], "copy_bytes_per_launch": COPY_BYTES}))
         return
 
     # ---- roofline leg: lm_head GEMV, back-to-back, HBM-forced ----------------------
@@ -916,11 +980,30 @@ def qwen_leg(ctx, fh, torch, gen, dev, steps, warmup):
     m.free()
     del m
     torch.cuda.synchronize()
+    # the step's dominant kernel: the gate|up GEMM (9728 x 896 at m = 64,
+    # RmsNorm in, SwiGLU out), alone over 36 weight replicas (333 MB)
+    d, f2 = c["d"], 2 * c["ffn"]
+    gus = [make_weight(ctx, fh, torch, f2, d, gen) for _ in range(36)]
+    xg = torch.randn((B, d), generator=gen, device=dev)
+    stg = torch.rand((B, d // 32, 2), generator=gen, device=dev)
+    gg = torch.ones(d, device=dev)
+    yg = torch.empty((B, c["ffn"]), device=dev)
+    calls = [(lambda w=w: fh.linear_normed_async(ctx, w, xg, B, d, stg, gg, None, 1e-6, True, None, 0, yg,
+                                                 fh.ACT_SWIGLU32)) for w in gus]
+    gu_bytes = q8_bytes(f2, d) + 4 * B * d + 8 * B * (d // 32) + 4 * d + 4 * B * c["ffn"]
+    roof = launch_roofline(ctx, torch, calls, gu_bytes)
+    roof["kernel"] = ("k_gemm_skinny<2,2,1,RmsNorm in + SwiGLU out> (gate|up 9728 x 896 at m = 64; the step's "
+                      "largest kernel)")
+    roof["bytes_note"] = "Q8_0 weight + x + row statistics + gamma + y"
+    for w in gus:
+        w.free()
+    del gus, calls
+    torch.cuda.synchronize()
     gbps = (wbytes + kv_bytes) / (ms * 1e-3) / 1e9
     return {"workload": "qwen2-0.5b-shaped Q8_0 decode step, batch 64, position 255, tied head, fused sampler",
             "tok_s": round(B * 1000.0 / ms, 1), "ms_per_step": round(ms, 4), "launches_per_step": launches,
             "weight_bytes": wbytes, "kv_cache_bytes_read": kv_bytes, "gemm_gflop": round(flops / 1e9, 1),
-            "hbm_GBps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4),
+            "hbm_GBps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4), "roofline": roof,
             "sampler_only": {"rows": B, "vocab": V, "us_per_step": round(sampler_ms * 1e3, 2),
                              "us_per_row": round(sampler_ms * 1e3 / B, 3),
                              "logits": "N(0,3) + 5 planted peaks (+12)", "history": QWEN_HIST,
