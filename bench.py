@@ -62,6 +62,8 @@ HEADS, CTX, FULL_POS = 12, 1024, 255  # GPT-2-124M attention; the whole-step leg
 COPY_BYTES = 256 << 20
 PMC_SUMMARY = os.path.join(ROOT, "profiles", "gemv_q8_0_lm_head_pmc.json")
 STACK_PMC = os.path.join(ROOT, "profiles", "gpt2_stack_124m_pmc.json")
+B32_UP_PMC = os.path.join(ROOT, "profiles", "skinny_gemm_b32_up_pmc.json")
+QWEN_GU_PMC = os.path.join(ROOT, "profiles", "skinny_gemm_qwen_gate_up_pmc.json")
 
 
 def q8_bytes(n, k):
@@ -455,8 +457,9 @@ def main():
                                                      fh.ACT_GELU)) for w in ups]
         up_bytes = q8_bytes(FFN, D) + 4 * B * D + 8 * B * (D // 32) + 8 * D + 4 * FFN + 4 * B * FFN
         roof = launch_roofline(ctx, torch, calls, up_bytes)
-        roof["kernel"] = ("k_gemm_skinny<1,2,3,LayerNorm in> (MLP up 3072 x 768 at m = 32, GELU out; the step's "
+        roof["kernel"] = ("k_gemm_skinny<1,1,3,LayerNorm in> (MLP up 3072 x 768 at m = 32, GELU out; the step's "
                           "24 LayerNorm-in GEMMs are its largest kernel family)")
+        roof["traffic"] = measured_traffic(B32_UP_PMC)
         roof["bytes_note"] = "Q8_0 weight + x + row statistics + gamma/beta + bias + y"
         result["b32"]["roofline"] = roof
         for w in ups:
@@ -995,6 +998,7 @@ def qwen_leg(ctx, fh, torch, gen, dev, steps, warmup):
     roof["kernel"] = ("k_gemm_skinny<2,2,1,RmsNorm in + SwiGLU out> (gate|up 9728 x 896 at m = 64; the step's "
                       "largest kernel)")
     roof["bytes_note"] = "Q8_0 weight + x + row statistics + gamma + y"
+    roof["traffic"] = measured_traffic(QWEN_GU_PMC)
     for w in gus:
         w.free()
     del gus, calls
