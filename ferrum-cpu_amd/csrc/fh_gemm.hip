@@ -1112,22 +1112,25 @@ __global__ void __launch_bounds__(512)
     // kSkinnyNormGlu: output o of the gate group (c = 0) and o + 1024 of the
     // up group (c = 1) are the same row and column.
     auto finish_glu = [&](int o, float sg, float su) {
-        const int i = row_of(o), col = tile * 32 + r32, nh = n >> 1;
-        if (i >= m || col >= nh) return;
-        if (__builtin_expect(bad_c[0] || bad_c[1], 0)) {
-            const float* xi = x + static_cast<size_t>(i) * k;
-            const float* sti = e.stats + 2 * static_cast<size_t>(i) * (k >> 5);
+        if constexpr (GLU) {
+            const int i = row_of(o), col = tile * 32 + r32, nh = n >> 1;
+            if (i >= m || col >= nh) return;
+            if (__builtin_expect(bad_c[0] || bad_c[1], 0)) {
+                const float* xi = x + static_cast<size_t>(i) * k;
+                const float* sti = e.stats + 2 * static_cast<size_t>(i) * (k >> 5);
 #pragma unroll
-            for (int c = 0; c < 2; c++)
-                if (bad_c[c]) {
-                    const int j = tile * 64 + c * 32 + r32;
-                    const float v = exact_dot_norm(xi, e.gamma, e.beta, sti, k >> 5, e.rms, e.eps, k,
-                                                   qs + static_cast<size_t>(j) * k, dsc + static_cast<size_t>(j) * kb);
-                    if (c == 0) sg = v; else su = v;
-                }
+                for (int c = 0; c < 2; c++)
+                    if (bad_c[c]) {
+                        const int j = tile * 64 + c * 32 + r32;
+                        const float v = exact_dot_norm(xi, e.gamma, e.beta, sti, k >> 5, e.rms, e.eps, k,
+                                                       qs + static_cast<size_t>(j) * k,
+                                                       dsc + static_cast<size_t>(j) * kb);
+                        if (c == 0) sg = v; else su = v;
+                    }
+            }
+            const float g = bias ? sg + bias_c[0] : sg, u = bias ? su + bias_c[1] : su;
+            y[static_cast<size_t>(i) * nh + col] = swiglu_unfused(g, u);
         }
-        const float g = bias ? sg + bias_c[0] : sg, u = bias ? su + bias_c[1] : su;
-        y[static_cast<size_t>(i) * nh + col] = swiglu_unfused(g, u);
     };
     const size_t tiles = gridDim.x;
 #pragma unroll
