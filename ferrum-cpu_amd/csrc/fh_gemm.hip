@@ -62,6 +62,14 @@ __device__ __forceinline__ uint2 quants_to_f16(uint32_t w) {
 
 __device__ __forceinline__ bool finite(float v) { return (__builtin_bit_cast(uint32_t, v) & 0x7F800000u) != 0x7F800000u; }
 
+// activation::gelu (activation.rs:9-12) with every product and sum rounded
+// (the kernels here are built with contraction on), so the GEMM epilogues
+// give k_gelu's values bit for bit.
+__device__ __forceinline__ float gelu_unfused(float v) {
+#pragma clang fp contract(off)
+    return 0.5f * v * (1.0f + tanhf(0.7978846f * (v + 0.044715f * v * v * v)));
+}
+
 // Outputs whose activation row holds inf/NaN (large-m kernel) or whose weight
 // row has a non-finite block scale (every kernel) are recomputed this way: the
 // reference's own arithmetic (ops.rs:29-126 on the f32 expansion), products
@@ -80,21 +88,22 @@ __device__ __attribute__((noinline)) float exact_dot(const float* __restrict__ x
 }
 
 // The outputs of one tile whose activation row is flagged (xbad, may be null)
-// or whose weight row has a non-finite scale, recomputed by exact_dot.  Every
-// thread of the workgroup calls; a barrier first orders the tile's ordinary
-// stores before these.
+// or whose weight row has a non-finite scale, recomputed by exact_dot (then
+// GELU with act).  Every thread of the workgroup calls; a barrier first
+// orders the tile's ordinary stores before these.
 __device__ __attribute__((noinline)) void exact_tile(const float* __restrict__ x, const int8_t* __restrict__ qs,
                                                      const uint16_t* __restrict__ dsc, const int8_t* __restrict__ rexp,
                                                      const uint8_t* __restrict__ xbad, const float* __restrict__ bias,
                                                      float* __restrict__ y, int m, int n, int k, int i0, int j0,
-                                                     int bm, int bn) {
+                                                     int bm, int bn, int act) {
     __syncthreads();
     for (int o = threadIdx.x; o < bm * bn; o += blockDim.x) {
         const int i = i0 + o / bn, j = j0 + o % bn;
         if (i >= m || j >= n || !((xbad && xbad[i]) || rexp[j] == kFhBadRowExp)) continue;
         const float s = exact_dot(x + static_cast<size_t>(i) * k, k, qs + static_cast<size_t>(j) * k,
                                   dsc + static_cast<size_t>(j) * (k >> 5));
-        y[static_cast<size_t>(i) * n + j] = bias ? s + bias[j] : s;
+        const float v = bias ? s + bias[j] : s;
+        y[static_cast<size_t>(i) * n + j] = act == FH_ACT_GELU ? gelu_unfused(v) : v;
     }
 }
 
@@ -405,7 +414,7 @@ __global__ void __launch_bounds__(64 * WM * WN * KW)
     // reference's own arithmetic (inf/NaN activations propagate exactly here).
     bool flagged = false;
     for (int t = tid; t < BN; t += NT) flagged |= j0 + t < n && rexp[j0 + t] == kFhBadRowExp;
-    if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, nullptr, bias, y, m, n, k, i0, j0, BM, BN);
+    if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, nullptr, bias, y, m, n, k, i0, j0, BM, BN, FH_ACT_NONE);
 }
 
 // ---- large m: both operands split, block scales folded into the weights ----------
@@ -432,7 +441,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
     k_gemm_wsplit(const uint4* __restrict__ panel, const float* __restrict__ xinv, const uint8_t* __restrict__ xbad,
                   const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
                   const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
-                  int k, int tiles_n) {
+                  int k, int tiles_n, int act) {
     constexpr int NW = WM * WN, NTH = 64 * NW;
     constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
     static_assert(TM * 32 * WM == BM && TN * 32 * WN == BN, "tile shape");
@@ -629,7 +638,8 @@ __global__ void __launch_bounds__(64 * WM * WN)
                 const int il = (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4), i = i0 + il;
                 if (i >= m) continue;
                 const float s = acc[r][c][v] * s_inv[il] * winv;
-                y[static_cast<size_t>(i) * n + j] = bias ? s + bj : s;
+                const float o = bias ? s + bj : s;
+                y[static_cast<size_t>(i) * n + j] = act == FH_ACT_GELU ? gelu_unfused(o) : o;
             }
     }
     // Rare: rows with inf/NaN activations or weight rows with a non-finite
@@ -637,7 +647,7 @@ __global__ void __launch_bounds__(64 * WM * WN)
     bool flagged = false;
     for (int t = tid; t < BM || t < BN; t += NTH)
         flagged |= (t < BM && s_bad[t]) || (t < BN && j0 + t < n && rexp[j0 + t] == kFhBadRowExp);
-    if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, xbad, bias, y, m, n, k, i0, j0, BM, BN);
+    if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, xbad, bias, y, m, n, k, i0, j0, BM, BN, act);
 }
 
 // ---- W8A8 on the int8 matrix cores ---------------------------------------------------
@@ -821,13 +831,6 @@ __device__ __forceinline__ int block_exponent(float mx) {
 
 }  // namespace
 
-// activation::gelu (activation.rs:9-12) with every product and sum rounded
-// (the kernels here are built with contraction on), so the skinny GEMM's
-// epilogue gives k_gelu's values bit for bit.
-__device__ __forceinline__ float gelu_unfused(float v) {
-#pragma clang fp contract(off)
-    return 0.5f * v * (1.0f + tanhf(0.7978846f * (v + 0.044715f * v * v * v)));
-}
 
 // FeedForward's gate (llm.rs:415-421), (g / (1 + exp(-g))) * u, rounded as
 // k_swiglu rounds it.
@@ -1383,7 +1386,7 @@ namespace {
 // The weight-split GEMM fed straight from x: row scales first (one read of
 // x), then the GEMM, which splits the activations while staging them.
 template <int BM, int BN, int WM, int WN>
-int launch_wsplit_x(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+int launch_wsplit_x(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y, int act) {
     const size_t m_pad = (m + BM - 1) / BM * BM;
     const size_t ibytes = fh_align256(m_pad * 4), fbytes = fh_align256(m_pad);
     void* ws = nullptr;
@@ -1398,7 +1401,7 @@ int launch_wsplit_x(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
     hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN, true>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN),
                        0, ctx->stream, nullptr, xinv, xbad, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
-                       static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n));
+                       static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n), act);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -1421,7 +1424,7 @@ int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const f
     if constexpr (KW == 0)  // the weight-split kernel
         hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN, false>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN), 0,
                            ctx->stream, panel, xinv, xbad, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
-                           static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n));
+                           static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n), FH_ACT_NONE);
     else
         hipLaunchKernelGGL((k_gemm_mfma<BM, BN, WM, WN, KW>), dim3(static_cast<unsigned>(tiles)),
                            dim3(64 * WM * WN * KW), 0, ctx->stream, panel, xinv, x, w->qs, w->d, w->rexp, bias, y,
@@ -1643,7 +1646,8 @@ int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m
     const size_t cus = static_cast<size_t>(ctx->num_cus);
     if (m <= 64) return launch_skinny(ctx, w, x, m, bias, y, nullptr, act);  // GELU in its epilogue
     int rc;
-    if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus) rc = launch_wsplit_x<256, 256, 2, 4>(ctx, w, x, m, bias, y);
+    if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus)
+        return launch_wsplit_x<256, 256, 2, 4>(ctx, w, x, m, bias, y, act);  // GELU in its epilogue
     else if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) rc = launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
     else if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) rc = launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
     else rc = launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);

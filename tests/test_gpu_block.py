@@ -272,6 +272,40 @@ def test_linear_with_gelu_equals_linear_then_gelu(fh, orc, m, n, k):
         ferrum_hip.linear_act_async(fh, w, tx, m, k, tb, n, fused, 7)
 
 
+def test_prefill_gemm_gelu_equals_gemm_then_gelu(fh, orc):
+    """At prefill depth (the weight-split MFMA GEMM, one tile per CU or more)
+    GELU runs in the GEMM's epilogue: bit for bit the GEMM followed by the
+    GELU kernel, including the rows recomputed by the reference's own
+    arithmetic (a weight row with an infinite block scale, an activation row
+    holding inf)."""
+    import torch
+
+    import ferrum_hip
+
+    m, n, k = 4096, 4096, 256
+    raw = np.array(orc.quantize_weight(n, k, 17, 0.05)).reshape(n, k // 32 * 34)
+    raw[5, 34:36] = np.frombuffer(np.float16(np.inf).tobytes(), np.uint8)  # row 5, block 1: scale inf
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw.ravel(), n, k)
+    x = np.random.default_rng(3).standard_normal((m, k)).astype(np.float32)
+    x[7, 3] = np.inf
+    b = (np.random.default_rng(4).standard_normal(n) * 0.1).astype(np.float32)
+    tx, tb = dev(x), dev(b)
+    fused, plain = (torch.empty((m, n), device="cuda") for _ in range(2))
+    ready()
+    ferrum_hip.linear_act_async(fh, w, tx, m, k, tb, n, fused, ferrum_hip.ACT_GELU)
+    ferrum_hip.linear_forward_async(fh, w, tx, m, k, tb, n, plain)
+    ferrum_hip.gelu_async(fh, plain, m * n)
+    got, sep = host(fh, fused), host(fh, plain)
+    w.free()
+    assert np.array_equal(got, sep, equal_nan=True)
+    assert not np.isfinite(got[:, 5]).all() and not np.isfinite(got[7]).all()
+    rows = [0, 7, 4095]
+    want = orc.gelu(orc.q8_0_linear(x[rows], raw.ravel(), n, b))
+    assert np.array_equal(got[rows], want, equal_nan=True) or np.allclose(got[rows][np.isfinite(want)],
+                                                                          want[np.isfinite(want)], rtol=2e-5,
+                                                                          atol=2e-5)
+
+
 @pytest.mark.parametrize(
     "m,n,k,res,act,numerics",
     [(1, 2304, 768, True, 0, 0), (1, 3072, 768, True, 1, 0), (1, 50257, 768, True, 0, 0),  # GPT-2 shapes (G = 16)
