@@ -510,6 +510,190 @@ __global__ void __launch_bounds__(kThreads) k_attn_group(AttnArgs a) {
     if (tid == 0) __hip_atomic_store(a.counters + rg, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Many rows at once (a batched decode): one workgroup per (row, kv head,
+// part of its query-head group) takes up to QS query heads of the kv head's
+// group over all of the row's positions and merges them itself, so nothing
+// goes through memory between workgroups and each K / V row is read from HBM
+// once (the parts of a group read it again from the caches).  Grid (kv heads
+// x parts, rows), kRowsThreads threads; head width 64.  A round covers
+// kRowsWaves * 32 positions, 32 per wave: lane pair (2 jj, 2 jj + 1) holds
+// position jj's k row (32 dims each) and lane (g, c) holds dims 4 c .. 4 c + 3
+// of positions g, g + 4, .. of the wave's 32 v rows.  Each wave keeps an
+// online softmax over its rounds (running max, rescaled sums); the waves'
+// (max, sum, weighted v sums) then merge through LDS.  Position pos (and the
+// masked positions past it) reads the new k / v rows from qkv; part 0 writes
+// them to the cache at row pos.  Scores and sums use FMA and sum in another
+// order than the reference (position order, one global max): the same value
+// up to rounding.  A query head's arithmetic does not depend on QS or on the
+// group.  A row past the cache or past max_len gives NaN and writes nothing.
+constexpr int kRowsThreads = 512;
+constexpr int kRowsWaves = kRowsThreads / 64;
+constexpr int kRowsPos = 32;  // positions per wave and round
+constexpr size_t kRowsMinGroups = 128;  // workgroups a launch needs to take k_attn_rows (timed at Qwen2-0.5B shapes)
+
+// Max over the 64 lanes of a wave, the same in every lane: DPP within 16-lane
+// rows (quad_perm [1,0,3,2], [2,3,0,1], row_half_mirror, row_mirror), then
+// the four rows by readlane.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, fh::dpp<0xB1>(v));
+    v = fmaxf(v, fh::dpp<0x4E>(v));
+    v = fmaxf(v, fh::dpp<0x141>(v));
+    v = fmaxf(v, fh::dpp<0x140>(v));
+    return fmaxf(fmaxf(fh::rdlane(v, 0), fh::rdlane(v, 16)), fmaxf(fh::rdlane(v, 32), fh::rdlane(v, 48)));
+}
+
+struct RowsFrag {
+    float4 k[8];  // 32 dims of position jj's k row
+    float4 v[8];  // dims c4 .. c4 + 3 of positions g, g + 4, .., g + 28 of the wave's 32
+};
+
+template <int QS>
+__global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, int max_len) {
+    constexpr int HD = 64, R = kRowsWaves * kRowsPos;
+    __shared__ __align__(16) float qs[QS][2][36];  // q halves, padded onto other banks
+    __shared__ __align__(16) float ps[kRowsWaves][QS][kRowsPos];  // position g + 4 q at g * 8 + q
+    __shared__ float wm[kRowsWaves][QS], wl[kRowsWaves][QS];
+    __shared__ __align__(16) float wo[kRowsWaves][QS][4][HD];  // each lane group's weighted v sums
+    const int parts = (a.group + QS - 1) / QS;
+    const int kvh = blockIdx.x / parts, hs = (blockIdx.x % parts) * QS, qn = min(QS, a.group - hs);
+    const int row = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int h0 = kvh * a.group + hs;  // this workgroup's first query head
+    const int pos = a.dpos ? static_cast<int>(min(a.dpos[row], 0x7FFFFFFFu)) : a.pos + a.pos_step * row;
+    float* out = a.out + static_cast<size_t>(row) * a.out_ld + static_cast<size_t>(h0) * HD;
+    if (pos >= a.cap || pos >= max_len) {  // a position the cache or the launch cannot hold
+        for (int i = tid; i < qn * HD; i += kRowsThreads) out[i] = __builtin_nanf("");
+        return;
+    }
+    const int len = pos + 1, d = a.kv_dim, kvs = kvh * HD;
+    const float* qkv = a.qkv + static_cast<size_t>(row) * a.ld;
+    float* kc = a.kc + row * a.seq_stride + kvs;
+    float* vc = a.vc + row * a.seq_stride + kvs;
+    const float* knew = qkv + a.k_off + kvs;
+    const float* vnew = qkv + a.v_off + kvs;
+    // k: lane pair (2 jj, 2 jj + 1) takes position jj, 32 dims each (rows at
+    // or past pos from qkv); v: lane (g, c) takes dims 4 c .. 4 c + 3 of
+    // positions g + 4 q, from the cache only, clamped below pos (rows at or
+    // past pos are replaced by the new row where they are used)
+    const int jj = lane >> 1, half = lane & 1, g = lane >> 4, c4 = (lane & 15) * 4, pm1 = max(pos - 1, 0);
+    auto load = [&](RowsFrag& f, int jb) __attribute__((always_inline)) {
+        const int jk = jb + jj;
+        const float4* kr =
+            reinterpret_cast<const float4*>((jk >= pos ? knew : kc + static_cast<size_t>(jk) * d) + half * 32);
+#pragma unroll
+        for (int i = 0; i < 8; i++) f.k[i] = kr[i];
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            f.v[q] = *reinterpret_cast<const float4*>(vc + static_cast<size_t>(min(jb + g + 4 * q, pm1)) * d + c4);
+    };
+    RowsFrag cur;
+    int jb = w * kRowsPos;
+    if (jb < len) load(cur, jb);
+    const float4 vn = *reinterpret_cast<const float4*>(vnew + c4);
+    for (int i = tid; i < qn * HD; i += kRowsThreads) qs[i / HD][(i % HD) / 32][i % 32] = qkv[h0 * HD + i];
+    if (hs == 0 && tid < HD) {
+        kc[static_cast<size_t>(pos) * d + tid] = knew[tid];
+        vc[static_cast<size_t>(pos) * d + tid] = vnew[tid];
+    }
+    float m[QS], l[QS];
+    float4 o[QS];
+#pragma unroll
+    for (int h = 0; h < QS; h++) {
+        m[h] = -INFINITY;
+        l[h] = 0.0f;
+        o[h] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    }
+    __syncthreads();
+    while (jb < len) {  // (wave-uniform)
+        // (q is read from LDS each round: held in registers across rounds it
+        // would take 32 per query head)
+        asm volatile("" ::: "memory");
+        const bool valid = jb + jj < len;
+        float s[QS];
+#pragma unroll
+        for (int h = 0; h < QS; h++) {
+            if (h >= qn) break;  // (wave-uniform)
+            asm volatile("" ::: "memory");  // (one head's q in registers at a time)
+            const float4* q4 = reinterpret_cast<const float4*>(&qs[h][half][0]);
+            float p = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float4 q = q4[i];
+                p = fmaf(q.x, cur.k[i].x, p);
+                p = fmaf(q.y, cur.k[i].y, p);
+                p = fmaf(q.z, cur.k[i].z, p);
+                p = fmaf(q.w, cur.k[i].w, p);
+            }
+            p = fh::group_sum<2>(p);  // the lane pair's two halves
+            s[h] = valid ? p * a.scale : -INFINITY;
+        }
+#pragma unroll
+        for (int h = 0; h < QS; h++) {
+            if (h >= qn) break;
+            const float mn = fmaxf(m[h], wave_max(s[h]));  // finite: position jb is in range
+            const float alpha = expf(m[h] - mn);           // 0 on the wave's first round
+            const float e = valid ? expf(s[h] - mn) : 0.0f;
+            l[h] = l[h] * alpha + (half == 0 ? e : 0.0f);
+            o[h].x *= alpha;
+            o[h].y *= alpha;
+            o[h].z *= alpha;
+            o[h].w *= alpha;
+            m[h] = mn;
+            if (half == 0) ps[w][h][(jj & 3) * 8 + (jj >> 2)] = e;
+        }
+        // rows at or past pos: the new v row
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (jb + g + 4 * q >= pos) cur.v[q] = vn;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int h = 0; h < QS; h++) {
+            if (h >= qn) break;
+            const float4* p4 = reinterpret_cast<const float4*>(&ps[w][h][g * 8]);
+            const float4 pa = p4[0], pb = p4[1];
+            const float pq[8] = {pa.x, pa.y, pa.z, pa.w, pb.x, pb.y, pb.z, pb.w};
+            float4 acc = o[h];
+#pragma unroll
+            for (int q = 0; q < 8; q++) {
+                acc.x = fmaf(pq[q], cur.v[q].x, acc.x);
+                acc.y = fmaf(pq[q], cur.v[q].y, acc.y);
+                acc.z = fmaf(pq[q], cur.v[q].z, acc.z);
+                acc.w = fmaf(pq[q], cur.v[q].w, acc.w);
+            }
+            o[h] = acc;
+        }
+        __builtin_amdgcn_wave_barrier();
+        jb += R;
+        if (jb < len) load(cur, jb);
+    }
+#pragma unroll
+    for (int h = 0; h < QS; h++) {
+        if (h >= qn) break;
+        const float lt = fh::group_total<64>(l[h]);
+        if (lane == 0) {
+            wm[w][h] = m[h];
+            wl[w][h] = lt;
+        }
+        *reinterpret_cast<float4*>(&wo[w][h][g][c4]) = o[h];
+    }
+    __syncthreads();
+    for (int i = tid; i < qn * HD; i += kRowsThreads) {
+        const int h = i / HD, dd = i % HD;
+        float M = -INFINITY;
+#pragma unroll
+        for (int v = 0; v < kRowsWaves; v++) M = fmaxf(M, wm[v][h]);
+        float S = 0.0f, O = 0.0f;
+#pragma unroll
+        for (int v = 0; v < kRowsWaves; v++) {
+            const float f = expf(wm[v][h] - M);  // 0 for a wave with no positions
+            S = fmaf(wl[v][h], f, S);
+            const float ov = (wo[v][h][0][dd] + wo[v][h][1][dd]) + (wo[v][h][2][dd] + wo[v][h][3][dd]);
+            O = fmaf(ov, f, O);
+        }
+        out[i] = O / S;
+    }
+}
+
 // x += y, then LayerNorm of the sum into ln (the residual add of
 // forward_with_cache followed by the next LayerNorm), one workgroup per row.
 // v = x (+ y); s (nullable, may alias x) receives v; ln = LayerNorm(v).
@@ -718,10 +902,46 @@ size_t attn_sub(size_t len) {
     return need <= 2 ? need : len > 768 ? 4 : 2;
 }
 
+// Query heads per k_attn_rows workgroup for a group size: up to four (a
+// group of seven takes two workgroups, four heads and three).
+int rows_heads(int group) { return group >= 5 ? 4 : group >= 2 ? 2 : 1; }
+
+// k_attn_rows for a launch of `rows` rows (batched decode only): grouped
+// query heads of width 64, float4-aligned k and v rows, and enough
+// workgroups to fill the part.  Timings at Qwen2-0.5B shapes (14 heads over 2
+// kv heads of 64), 64 rows at positions 63 / 127 / 255 / 511 / 1023: 6.1 /
+// 7.5 / 10.4 / 15.0 / 25.4 us against 6.7 / 10.6 / 15.9 / 19.3 / 48.9 for the
+// chunked kernels; 32 rows at 255 (128 workgroups) 8.7 against 9.9, 16 rows
+// (64) 8.3 against 8.0.  Multi-head rows (group 1, one workgroup per row and
+// head) ran slower than the chunked kernel: 32 rows of GPT-2 at 255, 15.4
+// against 14.6 us.
+bool rows_kernel_fits(const AttnArgs& a, size_t rows, size_t heads, size_t hd) {
+    const int g = a.group;
+    if (hd != 64 || g < 2) return false;
+    const size_t parts = (g + rows_heads(g) - 1) / rows_heads(g);
+    if (rows * (heads / g) * parts < kRowsMinGroups) return false;
+    const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+    return al(a.qkv) && al(a.kc) && al(a.vc) && a.ld % 4 == 0 && a.k_off % 4 == 0 && a.v_off % 4 == 0 &&
+           a.kv_dim % 4 == 0 && a.seq_stride % 4 == 0;
+}
+
 // max_len: the longest row (positions + 1) the launch may see.
-int launch_attention(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t hd, size_t max_len) {
+int launch_attention(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t hd, size_t max_len,
+                     bool batched = false) {
     if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
         return fh_fail(ctx, FH_ERR_LIMIT, "attention: head width must be 8, 16, 32, 64 or 128");
+    if (batched && rows_kernel_fits(a, rows, heads, hd)) {
+        a.scale = 1.0f / sqrtf(static_cast<float>(hd));
+        const int qs = rows_heads(a.group), parts = (a.group + qs - 1) / qs;
+        const dim3 grid(static_cast<unsigned>(heads / a.group * parts), static_cast<unsigned>(rows));
+        const int ml = static_cast<int>(max_len);
+        switch (qs) {
+            case 4: hipLaunchKernelGGL(k_attn_rows<4>, grid, dim3(kRowsThreads), 0, ctx->stream, a, ml); break;
+            default: hipLaunchKernelGGL(k_attn_rows<2>, grid, dim3(kRowsThreads), 0, ctx->stream, a, ml); break;
+        }
+        FH_HIP(ctx, hipGetLastError());
+        return FH_OK;
+    }
     const size_t sub = attn_sub(max_len);
     const size_t chunks = (max_len + sub * kChunk - 1) / (sub * kChunk);
     void* ws = nullptr;
@@ -853,5 +1073,5 @@ int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, siz
     a.cap = static_cast<int>(cap);
     a.out = out;
     a.out_ld = static_cast<int>(n_heads * hd);
-    return launch_attention(ctx, a, rows, n_heads, hd, (max_pos < cap ? max_pos : cap - 1) + 1);
+    return launch_attention(ctx, a, rows, n_heads, hd, (max_pos < cap ? max_pos : cap - 1) + 1, true);
 }

@@ -126,6 +126,53 @@ def test_gqa_attention_matches_oracle(fh, orc, nh, nkv, hd, T):
         assert np.array_equal(kh[r], ko[r]) and np.array_equal(vh[r], vo[r])
 
 
+@pytest.mark.parametrize("nh,nkv,rows", [(14, 2, 40), (32, 8, 10), (16, 2, 40), (6, 2, 40)])
+def test_batched_gqa_attention_matches_oracle(fh, orc, nh, nkv, rows):
+    """Launches with many (row, kv head) workgroups take the batched kernel
+    (one workgroup per row, kv head and up to four query heads, every position
+    merged inside it): groups of 7 (split 4 + 3), 4, 8 and 3 (split 2 + 1).
+    Positions span the wave (32) and round (256) edges, 0 and the last cache
+    row; two rows sit past max_pos and one at capacity (NaN, cache untouched).
+    Cache rows from pos on hold NaN, so a row read past the position shows."""
+    import torch
+
+    import ferrum_hip
+
+    hd, cap, max_pos = 64, 600, 580
+    qd, kvd = nh * hd, nkv * hd
+    ld = qd + 2 * kvd
+    rng = np.random.default_rng(nh * 10 + nkv + rows)
+    edges = [0, 1, 2, 30, 31, 32, 33, 63, 64, 255, 256, 257, 300, 511, 512, 513, 579, 580]
+    pos = np.array([edges[r] if r < len(edges) else int(rng.integers(0, max_pos + 1)) for r in range(rows)], np.uint32)
+    pos[rows - 3], pos[rows - 2], pos[rows - 1] = max_pos + 1, 599, cap  # past max_pos (twice), at capacity
+    qkv = (rng.standard_normal((rows, ld)) * 1.5).astype(np.float32)
+    kc0 = rng.standard_normal((rows, cap, kvd)).astype(np.float32)
+    vc0 = rng.standard_normal((rows, cap, kvd)).astype(np.float32)
+    for r in range(rows):
+        kc0[r, min(int(pos[r]), cap):] = np.nan
+        vc0[r, min(int(pos[r]), cap):] = np.nan
+    kc, vc = dev(kc0.ravel()), dev(vc0.ravel())
+    out = torch.empty((rows, qd), device="cuda")
+    ready()
+    ferrum_hip.gqa_attention_decode_async(fh, dev(qkv), ld, rows, nh, nkv, hd, kc, vc, cap, dev(pos.view(np.int32)),
+                                          max_pos, out)
+    got = host(fh, out)
+    kh, vh = host(fh, kc).reshape(rows, cap, kvd), host(fh, vc).reshape(rows, cap, kvd)
+    for r in range(rows):
+        p = int(pos[r])
+        if p > max_pos:
+            assert np.isnan(got[r]).all()
+            assert np.array_equal(kh[r].view(np.uint32), kc0[r].view(np.uint32))
+            assert np.array_equal(vh[r].view(np.uint32), vc0[r].view(np.uint32))
+            continue
+        ko, vo = kc0[r].copy(), vc0[r].copy()
+        want = orc.gqa_attention_decode(qkv[r], ko, vo, nh, nkv, hd, p)
+        close(got[r], want, 1e-5)
+        assert np.array_equal(kh[r, p], qkv[r, qd:qd + kvd]) and np.array_equal(vh[r, p], qkv[r, qd + kvd:])
+        keep = np.arange(cap) != p
+        assert np.array_equal(kh[r, keep].view(np.uint32), kc0[r, keep].view(np.uint32))
+
+
 @pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (32, 8, 128), (4, 2, 32), (12, 2, 64), (16, 2, 32)])
 def test_grouped_attention_equals_the_per_head_kernel(fh, orc, nh, nkv, hd):
     """The grouped-query kernel (one workgroup per kv head's query heads, K
