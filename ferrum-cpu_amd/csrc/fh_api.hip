@@ -956,6 +956,39 @@ int fh_gqa_attention_decode_async(fh_ctx* ctx, const float* d_qkv, size_t ld, si
                                           capacity, d_pos, max_pos, d_out);
 }
 
+int fh_gqa_attention_rope_decode_async(fh_ctx* ctx, float* d_qkv, size_t ld, size_t rows, size_t n_heads,
+                                       size_t n_kv, size_t head_dim, float* d_k_cache, float* d_v_cache,
+                                       size_t capacity, const uint32_t* d_pos, size_t max_pos, size_t rope_dim,
+                                       float base, int rope_type, const float* d_freq_factors, float linear_factor,
+                                       float* d_out) {
+    if (!ctx) return FH_ERR_INVALID;
+    ctx->err.clear();
+    if (rope_dim > head_dim || rope_dim % 2 != 0)
+        return fh_fail(ctx, FH_ERR_DIM, "rope_dim " + std::to_string(rope_dim) + " must be even and \u2264 head_dim " +
+                                            std::to_string(head_dim));
+    if (!(linear_factor > 0.0f) || !std::isfinite(linear_factor))
+        return fh_fail(ctx, FH_ERR_DIM, "RoPE scaling factors must be finite and > 0");
+    if (rope_type != FH_ROPE_NORM && rope_type != FH_ROPE_NEOX)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_gqa_attention_rope_decode: unknown rope_type " +
+                                                std::to_string(rope_type));
+    if (n_kv == 0 || n_heads % n_kv != 0)
+        return fh_fail(ctx, FH_ERR_DIM, "n_heads " + std::to_string(n_heads) + " must be a multiple of n_kv_heads " +
+                                            std::to_string(n_kv));
+    if (rows == 0 || n_heads == 0) return FH_OK;
+    if (!d_qkv || !d_k_cache || !d_v_cache || !d_pos || !d_out)
+        return fh_fail(ctx, FH_ERR_INVALID, "fh_gqa_attention_rope_decode: a pointer is NULL");
+    if (capacity == 0) return fh_fail(ctx, FH_ERR_INVALID, "fh_gqa_attention_rope_decode: capacity is 0");
+    if (ld < (n_heads + 2 * n_kv) * head_dim)
+        return fh_fail(ctx, FH_ERR_DIM, "fh_gqa_attention_rope_decode: ld is below (n_heads + 2 n_kv) * head_dim");
+    if (rows > 65535 || n_heads > 65535 || ld * rows > 0x7FFFFFFFu || capacity > 0x7FFFFFFFu ||
+        rows * capacity * n_kv * head_dim > (size_t(1) << 40))
+        return fh_fail(ctx, FH_ERR_LIMIT, "fh_gqa_attention_rope_decode: a dimension is too large");
+    FH_ON_DEVICE(ctx);
+    return fh_launch_gqa_attention_rope_decode(ctx, d_qkv, ld, rows, n_heads, n_kv, head_dim, d_k_cache, d_v_cache,
+                                               capacity, d_pos, max_pos, rope_dim, base, rope_type, d_freq_factors,
+                                               linear_factor, d_out);
+}
+
 int fh_swiglu_async(fh_ctx* ctx, const float* d_g, const float* d_u, size_t rows, size_t n, size_t ld, float* d_out) {
     if (!ctx) return FH_ERR_INVALID;
     ctx->err.clear();

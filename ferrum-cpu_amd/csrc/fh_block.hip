@@ -122,7 +122,8 @@ __global__ void __launch_bounds__(kThreads) k_kv_store(const float* __restrict__
 // kc / vc + r * seq_stride, one kv_dim-wide row per position; query head h
 // reads kv head h / group (group 1: multi-head, GPT-2).  Row r's position is
 // dpos[r] (device) or pos; chunks past it exit at once, and a position at or
-// past cap gives a NaN output and writes nothing.
+// past cap, or past the launch's max_len - 1, gives a NaN output and writes
+// nothing.
 // Every K, V and q element a thread needs is loaded at entry, so one memory
 // latency covers the whole chunk.  With one chunk the workgroup writes the
 // head's output itself; otherwise part: [rows][heads][chunks][2 + hd] (max,
@@ -138,6 +139,7 @@ struct AttnArgs {
     const uint32_t* dpos;
     int pos, cap;
     int pos_step;  // without dpos, row r's position is pos + pos_step * r
+    int max_len;   // rows at positions past max_len - 1 get NaN and write nothing
     float scale;
     float* part;
     unsigned* counters;
@@ -165,7 +167,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_chunk(AttnArgs a) {
         return;
     }
     const int len = pos + 1, chunks = (len + kPos - 1) / kPos;
-    if (chunks > static_cast<int>(gridDim.x)) {  // a position past the launch's max_pos
+    if (len > a.max_len) {  // a position past the launch's max_pos
         if (chunk == 0 && tid < hd) out[tid] = __builtin_nanf("");
         return;
     }
@@ -341,7 +343,7 @@ __global__ void __launch_bounds__(kThreads) k_attn_group(AttnArgs a) {
     const int pos = a.dpos ? static_cast<int>(min(a.dpos[row], 0x7FFFFFFFu)) : a.pos + a.pos_step * row;
     float* out = a.out + static_cast<size_t>(row) * a.out_ld + static_cast<size_t>(h0) * hd;
     const int len = pos + 1, chunks = (len + kPos - 1) / kPos;
-    if (pos >= a.cap || chunks > static_cast<int>(gridDim.x)) {  // a position the cache or the launch cannot hold
+    if (pos >= a.cap || len > a.max_len) {  // a position the cache or the launch cannot hold
         if (chunk == 0)
             for (int i = tid; i < QG * hd; i += kThreads) out[i] = __builtin_nanf("");
         return;
@@ -542,15 +544,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(fh::rdlane(v, 0), fh::rdlane(v, 16)), fmaxf(fh::rdlane(v, 32), fh::rdlane(v, 48)));
 }
 
+// apply_rope's parameters for k_attn_rows's own rotation of q and k.
+struct RopeArgs {
+    int rope_dim, neox;
+    float base, linear_factor;
+    const float* freq_factors;
+};
+
 struct RowsFrag {
     float4 k[8];  // 32 dims of position jj's k row
     float4 v[8];  // dims c4 .. c4 + 3 of positions g, g + 4, .., g + 28 of the wave's 32
 };
 
-template <int QS>
-__global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, int max_len) {
+// With ROPE, q and the new k row are rotated here (fh::rope_rotate, as
+// k_rope) as they are read from qkv, which is left as it is.
+template <int QS, bool ROPE>
+__global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, RopeArgs ra) {
     constexpr int HD = 64, R = kRowsWaves * kRowsPos;
     __shared__ __align__(16) float qs[QS][2][36];  // q halves, padded onto other banks
+    __shared__ __align__(16) float kn[HD];         // the new k row (rotated with ROPE)
     __shared__ __align__(16) float ps[kRowsWaves][QS][kRowsPos];  // position g + 4 q at g * 8 + q
     __shared__ float wm[kRowsWaves][QS], wl[kRowsWaves][QS];
     __shared__ __align__(16) float wo[kRowsWaves][QS][4][HD];  // each lane group's weighted v sums
@@ -561,7 +573,7 @@ __global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, int max_
     const int h0 = kvh * a.group + hs;  // this workgroup's first query head
     const int pos = a.dpos ? static_cast<int>(min(a.dpos[row], 0x7FFFFFFFu)) : a.pos + a.pos_step * row;
     float* out = a.out + static_cast<size_t>(row) * a.out_ld + static_cast<size_t>(h0) * HD;
-    if (pos >= a.cap || pos >= max_len) {  // a position the cache or the launch cannot hold
+    if (pos >= a.cap || pos >= a.max_len) {  // a position the cache or the launch cannot hold
         for (int i = tid; i < qn * HD; i += kRowsThreads) out[i] = __builtin_nanf("");
         return;
     }
@@ -591,8 +603,34 @@ __global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, int max_
     if (jb < len) load(cur, jb);
     const float4 vn = *reinterpret_cast<const float4*>(vnew + c4);
     for (int i = tid; i < qn * HD; i += kRowsThreads) qs[i / HD][(i % HD) / 32][i % 32] = qkv[h0 * HD + i];
+    if (tid < HD) kn[tid] = knew[tid];
+    if constexpr (ROPE) {
+        // pair i of query head h (h == qn: the new k row), in LDS
+        __syncthreads();
+        const int hr = ra.rope_dim / 2;
+        for (int t = tid; t < (qn + 1) * hr; t += kRowsThreads) {
+            const int h = t / hr, i = t % hr;
+            const int ia = ra.neox ? i : 2 * i, ib = ra.neox ? i + hr : 2 * i + 1;
+            float* pa = h < qn ? &qs[h][ia / 32][ia % 32] : &kn[ia];
+            float* pb = h < qn ? &qs[h][ib / 32][ib % 32] : &kn[ib];
+            float x = *pa, y = *pb;
+            fh::rope_rotate(x, y, pos, i, ra.rope_dim, ra.base, ra.freq_factors, ra.linear_factor);
+            *pa = x;
+            *pb = y;
+        }
+        __syncthreads();
+    }
+    // the loads take row pos's k from qkv: with ROPE the rotated row instead
+    auto rotated_new_k = [&]() __attribute__((always_inline)) {
+        if (ROPE && jb + jj == pos) {
+            const float4* k4 = reinterpret_cast<const float4*>(&kn[half * 32]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) cur.k[i] = k4[i];
+        }
+    };
+    rotated_new_k();
     if (hs == 0 && tid < HD) {
-        kc[static_cast<size_t>(pos) * d + tid] = knew[tid];
+        kc[static_cast<size_t>(pos) * d + tid] = kn[tid];
         vc[static_cast<size_t>(pos) * d + tid] = vnew[tid];
     }
     float m[QS], l[QS];
@@ -664,7 +702,10 @@ __global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, int max_
         }
         __builtin_amdgcn_wave_barrier();
         jb += R;
-        if (jb < len) load(cur, jb);
+        if (jb < len) {
+            load(cur, jb);
+            rotated_new_k();
+        }
     }
 #pragma unroll
     for (int h = 0; h < QS; h++) {
@@ -925,23 +966,32 @@ bool rows_kernel_fits(const AttnArgs& a, size_t rows, size_t heads, size_t hd) {
            a.kv_dim % 4 == 0 && a.seq_stride % 4 == 0;
 }
 
+// k_attn_rows over `rows` rows (rows_kernel_fits holds), with the rotation
+// of q and the new k rows when rope is set.
+int launch_rows(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t max_len, const RopeArgs* rope) {
+    a.scale = 1.0f / sqrtf(64.0f);
+    const int qs = rows_heads(a.group), parts = (a.group + qs - 1) / qs;
+    const dim3 grid(static_cast<unsigned>(heads / a.group * parts), static_cast<unsigned>(rows)), block(kRowsThreads);
+    a.max_len = static_cast<int>(max_len);
+    const RopeArgs ra = rope ? *rope : RopeArgs{};
+    if (rope) {
+        if (qs == 4) hipLaunchKernelGGL((k_attn_rows<4, true>), grid, block, 0, ctx->stream, a, ra);
+        else hipLaunchKernelGGL((k_attn_rows<2, true>), grid, block, 0, ctx->stream, a, ra);
+    } else {
+        if (qs == 4) hipLaunchKernelGGL((k_attn_rows<4, false>), grid, block, 0, ctx->stream, a, ra);
+        else hipLaunchKernelGGL((k_attn_rows<2, false>), grid, block, 0, ctx->stream, a, ra);
+    }
+    FH_HIP(ctx, hipGetLastError());
+    return FH_OK;
+}
+
 // max_len: the longest row (positions + 1) the launch may see.
 int launch_attention(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t hd, size_t max_len,
                      bool batched = false) {
     if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
         return fh_fail(ctx, FH_ERR_LIMIT, "attention: head width must be 8, 16, 32, 64 or 128");
-    if (batched && rows_kernel_fits(a, rows, heads, hd)) {
-        a.scale = 1.0f / sqrtf(static_cast<float>(hd));
-        const int qs = rows_heads(a.group), parts = (a.group + qs - 1) / qs;
-        const dim3 grid(static_cast<unsigned>(heads / a.group * parts), static_cast<unsigned>(rows));
-        const int ml = static_cast<int>(max_len);
-        switch (qs) {
-            case 4: hipLaunchKernelGGL(k_attn_rows<4>, grid, dim3(kRowsThreads), 0, ctx->stream, a, ml); break;
-            default: hipLaunchKernelGGL(k_attn_rows<2>, grid, dim3(kRowsThreads), 0, ctx->stream, a, ml); break;
-        }
-        FH_HIP(ctx, hipGetLastError());
-        return FH_OK;
-    }
+    if (batched && rows_kernel_fits(a, rows, heads, hd)) return launch_rows(ctx, a, rows, heads, max_len, nullptr);
+    a.max_len = static_cast<int>(max_len);
     const size_t sub = attn_sub(max_len);
     const size_t chunks = (max_len + sub * kChunk - 1) / (sub * kChunk);
     void* ws = nullptr;
@@ -1055,9 +1105,10 @@ int fh_launch_attention_prefill(fh_ctx* ctx, const float* qkv, float* kc, float*
     return launch_attention(ctx, a, rows, heads, d / heads, pos0 + rows);
 }
 
-int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,
-                                   size_t hd, float* kc, float* vc, size_t cap, const uint32_t* dpos, size_t max_pos,
-                                   float* out) {
+namespace {
+
+AttnArgs gqa_args(const float* qkv, size_t ld, size_t n_heads, size_t n_kv, size_t hd, float* kc, float* vc,
+                  size_t cap, const uint32_t* dpos, float* out) {
     AttnArgs a{};
     a.qkv = qkv;
     a.ld = static_cast<int>(ld);
@@ -1073,5 +1124,31 @@ int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, siz
     a.cap = static_cast<int>(cap);
     a.out = out;
     a.out_ld = static_cast<int>(n_heads * hd);
+    return a;
+}
+
+}  // namespace
+
+int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,
+                                   size_t hd, float* kc, float* vc, size_t cap, const uint32_t* dpos, size_t max_pos,
+                                   float* out) {
+    const AttnArgs a = gqa_args(qkv, ld, n_heads, n_kv, hd, kc, vc, cap, dpos, out);
     return launch_attention(ctx, a, rows, n_heads, hd, (max_pos < cap ? max_pos : cap - 1) + 1, true);
+}
+
+int fh_launch_gqa_attention_rope_decode(fh_ctx* ctx, float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,
+                                        size_t hd, float* kc, float* vc, size_t cap, const uint32_t* dpos,
+                                        size_t max_pos, size_t rope_dim, float base, int rope_type,
+                                        const float* freq_factors, float linear_factor, float* out) {
+    const AttnArgs a = gqa_args(qkv, ld, n_heads, n_kv, hd, kc, vc, cap, dpos, out);
+    const size_t max_len = (max_pos < cap ? max_pos : cap - 1) + 1;
+    if (rows_kernel_fits(a, rows, n_heads, hd)) {
+        const RopeArgs ra{static_cast<int>(rope_dim), rope_type == FH_ROPE_NEOX ? 1 : 0, base, linear_factor,
+                          freq_factors};
+        return launch_rows(ctx, a, rows, n_heads, max_len, &ra);
+    }
+    const int rc = fh_launch_rope(ctx, qkv, rows, ld, n_heads + n_kv, hd, rope_dim, dpos, base, rope_type,
+                                  freq_factors, linear_factor);
+    if (rc) return rc;
+    return launch_attention(ctx, a, rows, n_heads, hd, max_len, true);
 }

@@ -206,6 +206,13 @@ int fh_launch_attention_decode(fh_ctx* ctx, const float* qkv, float* kc, float* 
 int fh_launch_gqa_attention_decode(fh_ctx* ctx, const float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,
                                    size_t hd, float* kc, float* vc, size_t cap, const uint32_t* dpos, size_t max_pos,
                                    float* out);
+// The same with apply_rope on each row's q and k first (fh_launch_rope's
+// rotation, inside the attention kernel for batched launches, else
+// fh_launch_rope in place on qkv's q and k heads before the attention).
+int fh_launch_gqa_attention_rope_decode(fh_ctx* ctx, float* qkv, size_t ld, size_t rows, size_t n_heads, size_t n_kv,
+                                        size_t hd, float* kc, float* vc, size_t cap, const uint32_t* dpos,
+                                        size_t max_pos, size_t rope_dim, float base, int rope_type,
+                                        const float* freq_factors, float linear_factor, float* out);
 int fh_launch_rmsnorm(fh_ctx* ctx, const float* x, const float* r, float* s, size_t rows, size_t d, const float* w,
                       float eps, float* out);
 int fh_launch_rope(fh_ctx* ctx, float* x, size_t rows, size_t ld, size_t n_heads, size_t hd, size_t rope_dim,
@@ -229,6 +236,22 @@ __device__ __forceinline__ float fh_h2f(uint16_t h) {
 }
 
 namespace fh {
+// apply_rope's rotation of one pair (llm.rs:146-175, the angle of
+// RopeScaling::angle, llm.rs:118-121): pair i of rope_dim / 2 at position
+// pos, the frequency in float64 then rounded, as the reference computes it;
+// one definition for every kernel that rotates, so they give the same bits.
+__device__ __forceinline__ void rope_rotate(float& a, float& b, int pos, int i, int rope_dim, float base,
+                                            const float* ff, float linear_factor) {
+#pragma clang fp contract(off)
+    const float freq = static_cast<float>(pow(static_cast<double>(base), -2.0 * i / static_cast<double>(rope_dim)));
+    const float f = ff ? ff[i] : 1.0f;
+    const float theta = static_cast<float>(pos) * freq / f * (1.0f / linear_factor);
+    const float sn = sinf(theta), cs = cosf(theta);
+    const float x = a, y = b;
+    a = x * cs - y * sn;
+    b = x * sn + y * cs;
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);

@@ -62,16 +62,12 @@ __global__ void __launch_bounds__(kThreads) k_rope(float* __restrict__ x, int ro
     const int i = static_cast<int>(id % half);
     const int h = static_cast<int>((id / half) % n_heads);
     const int r = static_cast<int>(id / (static_cast<size_t>(half) * n_heads));
-    // freq in float64 then rounded, as the reference computes it
-    const float freq = static_cast<float>(pow(static_cast<double>(base), -2.0 * i / static_cast<double>(rope_dim)));
-    const float f = ff ? ff[i] : 1.0f;
-    const float theta = static_cast<float>(dpos[r]) * freq / f * (1.0f / linear_factor);
-    const float sn = sinf(theta), cs = cosf(theta);
     float* xh = x + static_cast<size_t>(r) * ld + static_cast<size_t>(h) * hd;
     const int ia = neox ? i : 2 * i, ib = neox ? i + half : 2 * i + 1;
-    const float a = xh[ia], b = xh[ib];
-    xh[ia] = a * cs - b * sn;
-    xh[ib] = a * sn + b * cs;
+    float a = xh[ia], b = xh[ib];
+    fh::rope_rotate(a, b, static_cast<int>(dpos[r]), i, rope_dim, base, ff, linear_factor);
+    xh[ia] = a;
+    xh[ib] = b;
 }
 
 __global__ void __launch_bounds__(kThreads) k_swiglu(const float* __restrict__ g, const float* __restrict__ u, int rows,

@@ -50,7 +50,8 @@ EXPORTS = (
     "fh_q8_0_linear_act_async", "fh_add_layernorm_async", "fh_q8_0_linear_ln_async",
     "fh_q8_0_linear_residual_async", "fh_q8_0_linear_normed_async",
     "fh_gpt2_stack_create", "fh_gpt2_stack_free", "fh_gpt2_stack_forward_async",
-    "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_swiglu_async", "fh_embed_rows_async",
+    "fh_rmsnorm_async", "fh_rope_async", "fh_gqa_attention_decode_async", "fh_gqa_attention_rope_decode_async",
+    "fh_swiglu_async", "fh_embed_rows_async",
     "fh_embed_rows_pos_async",
     "fh_gguf_open", "fh_gguf_close", "fh_gguf_error", "fh_gguf_version", "fh_gguf_tensor_count", "fh_gguf_find_tensor",
     "fh_gguf_tensor_info", "fh_gguf_tensor_data", "fh_gguf_meta_type", "fh_gguf_meta_u64", "fh_gguf_meta_f64",
@@ -201,6 +202,8 @@ def lib():
         L.fh_rmsnorm_async.argtypes = [vp, vp, vp, vp, sz, sz, vp, f32, vp]
         L.fh_rope_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, f32, i32, vp, f32]
         L.fh_gqa_attention_decode_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, sz, vp, sz, vp]
+        L.fh_gqa_attention_rope_decode_async.argtypes = [vp, vp, sz, sz, sz, sz, sz, vp, vp, sz, vp, sz, sz, f32, i32,
+                                                         vp, f32, vp]
         L.fh_swiglu_async.argtypes = [vp, vp, vp, sz, sz, sz, vp]
         L.fh_embed_rows_async.argtypes = [vp, vp, sz, sz, vp, sz, vp]
         L.fh_embed_rows_pos_async.argtypes = [vp, vp, vp, sz, sz, sz, vp, vp, sz, vp, sz, vp]
@@ -1091,6 +1094,18 @@ def gqa_attention_decode_async(ctx: Context, qkv, ld: int, rows: int, n_heads: i
                                                   _ptr(v_cache), capacity, _ptr(pos), max_pos, _ptr(out)))
 
 
+def gqa_attention_rope_decode_async(ctx: Context, qkv, ld: int, rows: int, n_heads: int, n_kv: int, head_dim: int,
+                                    k_cache, v_cache, capacity: int, pos, max_pos: int, rope_dim: int, base: float,
+                                    rope_type: int, freq_factors, linear_factor: float, out):
+    """rope_async on each row's q and k heads, then gqa_attention_decode_async,
+    in one call (one launch for many rows at head width 64); qkv's q and k
+    values are scratch afterwards."""
+    ctx.check(lib().fh_gqa_attention_rope_decode_async(ctx.h, _ptr(qkv), ld, rows, n_heads, n_kv, head_dim,
+                                                       _ptr(k_cache), _ptr(v_cache), capacity, _ptr(pos), max_pos,
+                                                       rope_dim, base, rope_type, _ptr(freq_factors), linear_factor,
+                                                       _ptr(out)))
+
+
 def swiglu_async(ctx: Context, g, u, rows: int, n: int, ld: int, out):
     """(g / (1 + exp(-g))) * u per row (row r of g and u at r * ld)."""
     ctx.check(lib().fh_swiglu_async(ctx.h, _ptr(g), _ptr(u), rows, n, ld, _ptr(out)))
@@ -1321,10 +1336,23 @@ class LlamaDevice:
         rows the o and down projections add themselves to the residual stream
         and leave its row statistics, and the q|k|v and gate|up GEMMs form the
         RmsNorm from them as they stage their inputs (seven launches per
-        block, six with SwiGLU in the gate|up GEMM); otherwise each RmsNorm is
-        a launch of its own (nine)."""
+        block, six with SwiGLU in the gate|up GEMM, one fewer again where the
+        attention rotates q and k itself); otherwise each RmsNorm is a launch
+        of its own (nine).  The head counts as one call (a wide head at more
+        than 32 rows takes one launch per 32 rows)."""
         per = (6 if all(b.get("glu") for b in self.blocks) else 7) if self.fused else 9
+        if self.fused and self._rope_in_attention():
+            per -= 1
         return 1 + per * self.layers + 2 + (1 if self.fused else 0)
+
+    def _rope_in_attention(self) -> bool:
+        """Whether fh_gqa_attention_rope_decode_async rotates inside its one
+        attention launch here (the library's rule for its batched kernel: head
+        width 64, grouped heads, at least 128 workgroups of up to four query
+        heads), rather than launching fh_rope first."""
+        g = self.nh // self.nkv
+        per = 4 if g >= 5 else 2
+        return self.hd == 64 and g >= 2 and self.rows * self.nkv * -(-g // per) >= 128
 
     def forward_one(self, token: int):
         """LlamaModel::forward_one (llm.rs:606-616) for a single sequence (rows
@@ -1365,10 +1393,9 @@ class LlamaDevice:
                 else:
                     linear_normed_async(ctx, b["qkv"], x, B, d, st, b["attn_norm"], None, self.eps, True, qkv_b,
                                         0 if qkv_b is None else self.qkv_dim, self.qkv)
-                rope_async(ctx, self.qkv, B, self.qkv_dim, self.nh + self.nkv, self.hd, self.rope_dim, self.pos,
-                           self.rope_base, self.rope_type, self.rope_freqs, self.rope_linear)
-                gqa_attention_decode_async(ctx, self.qkv, self.qkv_dim, B, self.nh, self.nkv, self.hd, b["k"], b["v"],
-                                           self.cap, self.pos, max_pos, self.att)
+                gqa_attention_rope_decode_async(ctx, self.qkv, self.qkv_dim, B, self.nh, self.nkv, self.hd, b["k"],
+                                                b["v"], self.cap, self.pos, max_pos, self.rope_dim, self.rope_base,
+                                                self.rope_type, self.rope_freqs, self.rope_linear, self.att)
                 linear_residual_async(ctx, b["o"], self.att, B, self.q_dim, None, 0, x, x, st)
                 if b.get("glu"):
                     linear_normed_async(ctx, b["gate_up"], x, B, d, st, b["ffn_norm"], None, self.eps, True, None, 0,

@@ -143,6 +143,7 @@ pub mod sys {
         pub fn fh_rmsnorm_async(ctx: *mut fh_ctx, d_x: *const f32, d_r: *const f32, d_s: *mut f32, rows: usize, d: usize, d_w: *const f32, eps: f32, d_out: *mut f32) -> c_int;
         pub fn fh_rope_async(ctx: *mut fh_ctx, d_x: *mut f32, rows: usize, ld: usize, n_heads: usize, head_dim: usize, rope_dim: usize, d_pos: *const u32, base: f32, rope_type: c_int, d_freq_factors: *const f32, linear_factor: f32) -> c_int;
         pub fn fh_gqa_attention_decode_async(ctx: *mut fh_ctx, d_qkv: *const f32, ld: usize, rows: usize, n_heads: usize, n_kv: usize, head_dim: usize, d_k_cache: *mut f32, d_v_cache: *mut f32, capacity: usize, d_pos: *const u32, max_pos: usize, d_out: *mut f32) -> c_int;
+        pub fn fh_gqa_attention_rope_decode_async(ctx: *mut fh_ctx, d_qkv: *mut f32, ld: usize, rows: usize, n_heads: usize, n_kv: usize, head_dim: usize, d_k_cache: *mut f32, d_v_cache: *mut f32, capacity: usize, d_pos: *const u32, max_pos: usize, rope_dim: usize, base: f32, rope_type: c_int, d_freq_factors: *const f32, linear_factor: f32, d_out: *mut f32) -> c_int;
         pub fn fh_swiglu_async(ctx: *mut fh_ctx, d_g: *const f32, d_u: *const f32, rows: usize, n: usize, ld: usize, d_out: *mut f32) -> c_int;
         pub fn fh_embed_rows_async(ctx: *mut fh_ctx, d_tok_w: *const f32, vocab: usize, d: usize, d_tokens: *const u32, rows: usize, d_out: *mut f32) -> c_int;
         pub fn fh_embed_rows_pos_async(ctx: *mut fh_ctx, d_token_w: *const f32, d_pos_w: *const f32, vocab: usize, max_seq: usize, d: usize, d_tokens: *const u32, d_pos: *const u32, rows: usize, d_hist: *mut u32, hist_stride: usize, d_out: *mut f32) -> c_int;

@@ -373,6 +373,18 @@ int fh_rope_async(fh_ctx* ctx, float* d_x, size_t rows, size_t ld, size_t n_head
 int fh_gqa_attention_decode_async(fh_ctx* ctx, const float* d_qkv, size_t ld, size_t rows, size_t n_heads,
                                   size_t n_kv, size_t head_dim, float* d_k_cache, float* d_v_cache, size_t capacity,
                                   const uint32_t* d_pos, size_t max_pos, float* d_out);
+/* fh_rope_async on each row's q and k heads (n_heads + n_kv heads from d_qkv
+ * + r * ld), then fh_gqa_attention_decode_async: Attention::forward_one with
+ * its apply_rope calls (llm.rs:285-358, 146-175) in one call.  The outputs
+ * and caches are those of the two calls, bit for bit.  Many rows at head
+ * width 64 take one launch that rotates q and the new k row as it reads them;
+ * otherwise the two launches run.  d_qkv's q and k values are scratch: on
+ * return they hold the input or its rotation.  Errors as the two calls. */
+int fh_gqa_attention_rope_decode_async(fh_ctx* ctx, float* d_qkv, size_t ld, size_t rows, size_t n_heads,
+                                       size_t n_kv, size_t head_dim, float* d_k_cache, float* d_v_cache,
+                                       size_t capacity, const uint32_t* d_pos, size_t max_pos, size_t rope_dim,
+                                       float base, int rope_type, const float* d_freq_factors, float linear_factor,
+                                       float* d_out);
 /* FeedForward::forward's gate (llm.rs:415-421): out[r, j] = (g / (1 +
  * exp(-g))) * u, g = d_g[r * ld + j], u = d_u[r * ld + j], j < n. */
 int fh_swiglu_async(fh_ctx* ctx, const float* d_g, const float* d_u, size_t rows, size_t n, size_t ld, float* d_out);

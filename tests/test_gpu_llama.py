@@ -173,6 +173,77 @@ def test_batched_gqa_attention_matches_oracle(fh, orc, nh, nkv, rows):
         assert np.array_equal(kh[r, keep].view(np.uint32), kc0[r, keep].view(np.uint32))
 
 
+@pytest.mark.parametrize("nh,nkv,hd,rows,rt,rope_dim,ff,lf", [
+    (14, 2, 64, 40, 1, 64, False, 1.0),   # one launch, rotation inside (group 7: 4 + 3 heads)
+    (32, 8, 64, 10, 0, 48, True, 2.0),    # one launch, NORM pairs, partial rotary, factors, scaling
+    (6, 2, 64, 40, 0, 64, False, 1.0),    # one launch, group 3 (2 + 1 heads)
+    (14, 2, 64, 3, 1, 64, False, 1.0),    # few rows: fh_rope, then the attention
+    (8, 2, 32, 50, 1, 32, False, 1.0),    # head width 32: fh_rope, then the attention
+])
+def test_attention_with_rope_equals_rope_then_attention(fh, orc, nh, nkv, hd, rows, rt, rope_dim, ff, lf):
+    """fh_gqa_attention_rope_decode_async gives the bits of fh_rope_async on
+    the q and k heads followed by fh_gqa_attention_decode_async, outputs and
+    caches, whichever form it takes; a row past max_pos is NaN in both and
+    leaves its cache alone."""
+    import torch
+
+    import ferrum_hip
+
+    cap, max_pos = 600, 560
+    qd, kvd = nh * hd, nkv * hd
+    ld = qd + 2 * kvd + 8  # rows of a wider buffer
+    rng = np.random.default_rng(nh + rows * 3 + rt)
+    edges = [0, 1, 31, 32, 255, 256, 300, 511, 512, 560]
+    pos = np.array([edges[r] if r < len(edges) else int(rng.integers(0, max_pos + 1)) for r in range(rows)], np.uint32)
+    pos[-1] = max_pos + 3
+    qkv = (rng.standard_normal((rows, ld)) * 1.5).astype(np.float32)
+    kc0 = rng.standard_normal(rows * cap * kvd).astype(np.float32)
+    vc0 = rng.standard_normal(rows * cap * kvd).astype(np.float32)
+    fac = dev(rng.uniform(0.5, 8.0, rope_dim // 2).astype(np.float32)) if ff else None
+    dpos = dev(pos.view(np.int32))
+    outs, caches = [], []
+    for fused in (False, True):
+        x, kc, vc = dev(qkv), dev(kc0), dev(vc0)
+        out = torch.empty((rows, qd), device="cuda")
+        ready()
+        if fused:
+            ferrum_hip.gqa_attention_rope_decode_async(fh, x, ld, rows, nh, nkv, hd, kc, vc, cap, dpos, max_pos,
+                                                       rope_dim, 1e6, rt, fac, lf, out)
+        else:
+            ferrum_hip.rope_async(fh, x, rows, ld, nh + nkv, hd, rope_dim, dpos, 1e6, rt, fac, lf)
+            ferrum_hip.gqa_attention_decode_async(fh, x, ld, rows, nh, nkv, hd, kc, vc, cap, dpos, max_pos, out)
+        outs.append(host(fh, out))
+        caches.append((host(fh, kc), host(fh, vc)))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    for a, b in zip(caches[0], caches[1]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert np.isnan(outs[1][-1]).all() and not np.isnan(outs[1][:-1]).any()
+    kh = caches[1][0].reshape(rows, cap, kvd)
+    assert np.array_equal(kh[-1], kc0.reshape(rows, cap, kvd)[-1])
+    # row 1 against the oracle: RoPE'd q|k, then the attention
+    q = qkv[1, :qd + 2 * kvd].copy()
+    f = None if fac is None else host(fh, fac)
+    q[:qd + kvd] = orc.rope(q[:qd + kvd], nh + nkv, hd, rope_dim, int(pos[1]), 1e6, rt, f, lf)
+    ko, vo = kc0.reshape(rows, cap, kvd)[1].copy(), vc0.reshape(rows, cap, kvd)[1].copy()
+    close(outs[1][1], orc.gqa_attention_decode(q, ko, vo, nh, nkv, hd, int(pos[1])), 1e-5)
+
+
+def test_attention_with_rope_errors(fh):
+    import ferrum_hip
+
+    x, c, p, o = (dev(np.zeros(n, np.float32)) for n in (256, 4096, 1, 256))
+    ready()
+    call = ferrum_hip.gqa_attention_rope_decode_async
+    with pytest.raises(ferrum_hip.DimMismatch, match="must be even"):
+        call(fh, x, 192, 1, 2, 1, 64, c, c, 8, p, 0, 63, 1e4, 0, None, 1.0, o)
+    with pytest.raises(ferrum_hip.DimMismatch, match="finite and > 0"):
+        call(fh, x, 192, 1, 2, 1, 64, c, c, 8, p, 0, 64, 1e4, 0, None, float("inf"), o)
+    with pytest.raises(ferrum_hip.DimMismatch, match="multiple of n_kv_heads"):
+        call(fh, x, 192, 1, 3, 2, 32, c, c, 8, p, 0, 32, 1e4, 0, None, 1.0, o)
+    with pytest.raises(ferrum_hip.FerrumHipError, match="rope_type"):
+        call(fh, x, 192, 1, 2, 1, 64, c, c, 8, p, 0, 64, 1e4, 5, None, 1.0, o)
+
+
 @pytest.mark.parametrize("nh,nkv,hd", [(14, 2, 64), (32, 8, 128), (4, 2, 32), (12, 2, 64), (16, 2, 32)])
 def test_grouped_attention_equals_the_per_head_kernel(fh, orc, nh, nkv, hd):
     """The grouped-query kernel (one workgroup per kv head's query heads, K
