@@ -541,8 +541,7 @@ __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
     __shared__ __align__(16) float hq[3 * HD];
     __shared__ float sc[kPos], esc[kWaves * kPos], acc[kT], red[2 * kWaves];
     static_assert(kPos == 64, "the softmax maps lane j to position j");
-    extern __shared__ __align__(16) float part[];  // polled attention partials [H][nch][HD + 2], then [H][nch] factors
-    float* fac = part + H * a.nch_max * kAttnSlots;
+    extern __shared__ __align__(16) float part[];  // polled attention partials [H][nch][HD + 2]
 
     const int tid = threadIdx.x, w = blockIdx.x, gw = w * kWaves + (tid >> 6);
     if (w >= G) {  // a prefetch workgroup (its own epoch counter, like every workgroup)
@@ -638,25 +637,41 @@ __global__ void __launch_bounds__(kT) k_gpt2_stack(DecArgs a) {
         wup.issue(B.q[2], B.d[2], B.b[2], gw);
         ln2.issue(B.ln2_g, B.ln2_b);
         poll_into<8>(s_att, items * kAttnSlots, tag, part, wt);  // item (h, c) at (h * nch + c) * (HD + 2)
-        // Per item (h, c): f = exp(m_c - M_h) / S_h, S_h = sum_c l_c exp(m_c - M_h)
-        // (M_h the head's largest chunk max), so att[h, d] = sum_c acc_c[d] f_c.
-        // (one thread per item: each forms its head's M and S itself)
-        for (int it = tid; it < items; it += kT) {
-            const float* hp = part + (it / nch) * nch * kAttnSlots;
-            float M = -INFINITY;
-            for (int c = 0; c < nch; c++) M = fmaxf(M, hp[c * kAttnSlots]);
-            float S = 0.0f;
-            for (int c = 0; c < nch; c++) S += hp[c * kAttnSlots + 1] * expf(hp[c * kAttnSlots] - M);
-            fac[it] = expf(part[it * kAttnSlots] - M) / S;
-        }
-        __syncthreads();
+        // att[h, d] = (sum_c acc_c[d] e_c) / S_h, e_c = exp(m_c - M_h), S_h =
+        // sum_c l_c e_c (M_h the head's largest chunk max).  Each output's
+        // thread forms its head's M, e and S itself, four chunks' values
+        // loaded at a time, so the merge costs one barrier and a few LDS
+        // round trips.
         for (int o = tid; o < D; o += kT) {
             const int h = o / HD, dd = o % HD;
-            const float* hp = part + h * nch * kAttnSlots + 2 + dd;
-            const float* hf = fac + h * nch;
-            float r = 0.0f;
-            for (int c = 0; c < nch; c++) r += hp[c * kAttnSlots] * hf[c];
-            hbuf[o] = r;
+            const float* hp = part + h * nch * kAttnSlots;
+            float M = -INFINITY;
+            for (int c0 = 0; c0 < nch; c0 += 4) {
+                float mv[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) mv[i] = hp[min(c0 + i, nch - 1) * kAttnSlots];  // (repeats: same max)
+#pragma unroll
+                for (int i = 0; i < 4; i++) M = fmaxf(M, mv[i]);
+            }
+            float S = 0.0f, r = 0.0f;
+            for (int c0 = 0; c0 < nch; c0 += 4) {
+                float mv[4], lv[4], av[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    const float* cp = hp + min(c0 + i, nch - 1) * kAttnSlots;
+                    mv[i] = cp[0];
+                    lv[i] = cp[1];
+                    av[i] = cp[2 + dd];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (c0 + i < nch) {
+                        const float e = expf(mv[i] - M);
+                        S += lv[i] * e;
+                        r += av[i] * e;
+                    }
+            }
+            hbuf[o] = r / S;
         }
         __syncthreads();
         wout.template compute<false>(hbuf, s_proj, tag, gw, pub);
@@ -776,7 +791,7 @@ int fh_gpt2_stack_create(fh_ctx* ctx, const fh_gpt2_block* blocks, size_t layers
     int cur = -1;
     if (hipGetDevice(&cur) != hipSuccess || cur != ctx->device) FH_HIP(ctx, hipSetDevice(ctx->device));
     const int nch = static_cast<int>((capacity + kPos - 1) / kPos);
-    const size_t dyn = static_cast<size_t>(heads) * nch * (hd + 3) * sizeof(float);
+    const size_t dyn = static_cast<size_t>(heads) * nch * (hd + 2) * sizeof(float);
     const int grid = grid_for(static_cast<int>(d));
     int per_cu = 0;
     FH_HIP(ctx, hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kern, kT, dyn));
