@@ -1448,8 +1448,14 @@ __global__ void k_zero_counters(unsigned* __restrict__ c, int n) {
 template <int MT, int NT, int BPW>
 int launch_skinny_t(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
                     const fh_scratch* scratch, int act, const fh_edge* edge = nullptr, int mode = kSkinnyPlain) {
-    constexpr size_t kMaxWaves = 16 / (MT * NT) < 8 ? 16 / (MT * NT) : 8;
     const size_t kb = w->k / 32, tiles = (w->n + 32 * NT - 1) / (32 * NT);
+    // Waves per workgroup: eight, except that a tile of more than two 32 x 32
+    // output groups keeps 16 KB of wave sums per wave in LDS, so where the
+    // tiles outnumber the CUs it takes four and two workgroups share a CU.
+    // (Qwen2-0.5B gate|up at m = 64, 152 tiles: seven blocks per wave with
+    // four waves, three or four with eight.)
+    const size_t kMaxWaves =
+        MT * NT > 2 && tiles > static_cast<size_t>(ctx->num_cus) ? (16 / (MT * NT) < 8 ? 16 / (MT * NT) : 8) : 8;
     size_t splits = 1;
     if (tiles < static_cast<size_t>(ctx->num_cus) / 2) splits = (kb + kMaxWaves * BPW - 1) / (kMaxWaves * BPW);
     if (splits > static_cast<size_t>(kMaxSplits)) splits = kMaxSplits;
