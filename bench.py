@@ -267,9 +267,16 @@ def main():
         t0 = time.perf_counter()
         m3.generate(prompt, 1, params, fh.Rng(2))
         t_prime = time.perf_counter() - t0
+        # (the wall clock at the end of the prime and of each 32-step chunk is
+        # recorded, and the run is repeated: some processes have run it at
+        # about half speed, so the record shows where such a run loses time)
+        chunks, chunks2 = [], []
         t0 = time.perf_counter()
-        run_ids = m3.generate(prompt, 256, params, fh.Rng(3))
+        run_ids = m3.generate(prompt, 256, params, fh.Rng(3), timings=chunks)
         t_run = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        m3.generate(prompt, 256, params, fh.Rng(3), timings=chunks2)
+        t_run2 = time.perf_counter() - t0
         # the same run with the prompt primed in one pass (prefill=True: its
         # 127 positions as rows of GEMMs and one attention launch per block)
         m3.generate(prompt, 8, params, fh.Rng(1), prefill=True)
@@ -281,6 +288,7 @@ def main():
         t_run_pf = time.perf_counter() - t0
         result["config3_run"] = {
             "prompt": 128, "steps": len(run_ids), "run_ms": round(t_run * 1e3, 2), "prime_ms": round(t_prime * 1e3, 2),
+            "run_marks_ms": chunks, "repeat_run_ms": round(t_run2 * 1e3, 2), "repeat_marks_ms": chunks2,
             "decode_tok_s": round(255 / max(t_run - t_prime, 1e-9), 1), "run_tok_s": round(len(run_ids) / t_run, 1),
             "prefill": {"run_ms": round(t_run_pf * 1e3, 2), "prime_ms": round(t_prime_pf * 1e3, 2),
                         "run_tok_s": round(len(run_ids_pf) / t_run_pf, 1),

@@ -1708,7 +1708,7 @@ class GPT2Device:
         self._keep = (x, x2, h, qkv, att, proj, mid)  # alive until the stream has used them
 
     def generate(self, prompt, max_tokens: int, params: SamplingParams, rng: Rng, eos=None, bos: int = 0,
-                 prefill: bool = False, cancel=None, chunk: int = 32):
+                 prefill: bool = False, cancel=None, chunk: int = 32, timings=None):
         """GenerativeSLM::token_stream + stream_next (slm/token_stream.rs:66-190)
         with every step on the device: the prompt is primed, then each step
         runs the block stack, the head and the fused sampler, which writes its
@@ -1732,9 +1732,15 @@ class GPT2Device:
         prefill=True primes the prompt in one pass (prefill_async: its
         positions as rows of GEMMs) instead of position by position: much
         faster for long prompts, and the same run within the 1e-5 rule
-        rather than bit for bit."""
+        rather than bit for bit.
+
+        timings (a list, optional) receives the wall-clock milliseconds from
+        the call's start to the end of the prime and of each chunk."""
+        import time
+
         import torch
 
+        t_start = time.perf_counter()
         win = GPT2Window(self.cap, prompt, bos)
         n0 = len(win.ids)
         if n0 + max_tokens > self.cap or self.stack is None or not self.fused:
@@ -1746,7 +1752,11 @@ class GPT2Device:
         greedy = params.temperature <= 0.0
         hist = torch.zeros(n0 + max_tokens, dtype=torch.int32, device=dev)
         hist[:n0] = torch.tensor(win.ids, dtype=torch.int32, device=dev)
-        offs = torch.tensor([[0, n0 + k] for k in range(max_tokens)], dtype=torch.int32, device=dev)
+        # step j's penalty window is hist[0 : n0 + j], built on the device (a
+        # nested Python list of max_tokens pairs can set off a full garbage
+        # collection of the host process, tens of ms, inside the run)
+        offs = torch.zeros((max_tokens, 2), dtype=torch.int32, device=dev)
+        offs[:, 1] = torch.arange(n0, n0 + max_tokens, dtype=torch.int32, device=dev)
         draws = None
         if not greedy:
             probe = Rng.from_state(rng.state)
@@ -1761,6 +1771,9 @@ class GPT2Device:
             for p in range(n0 - 1):
                 ctx.check(lib().fh_gpt2_stack_forward_async(ctx.h, self.stack, hist.data_ptr() + 4 * p, p,
                                                             _ptr(self.x)))
+        if timings is not None:
+            ctx.sync()
+            timings.append(round((time.perf_counter() - t_start) * 1e3, 3))
         out, used, k = [], 0, 0
         while k < max_tokens:
             if k > 0 and cancelled(cancel):
@@ -1772,6 +1785,8 @@ class GPT2Device:
                 sample_rows_async(ctx, self.z, 1, self.vocab, params, hist, offs[j], None if greedy else draws[j:],
                                   hist.data_ptr() + 4 * (n0 + j), LOGITS_GPT2_SOFTMAX)
             ctx.sync()
+            if timings is not None:
+                timings.append(round((time.perf_counter() - t_start) * 1e3, 3))
             got = [int(t) for t in hist[n0 + k:n0 + k + c].cpu().numpy()]
             k += c
             stop = False
@@ -2014,7 +2029,10 @@ class GPT2Batch:
         draws = None
         if not greedy:
             probes = [Rng.from_state(r.state) for r in rngs]
-            dr = np.array([[probes[r].next_u64() for r in range(B)] for _ in range(max_tokens)], dtype=np.uint64)
+            dr = np.empty((max_tokens, B), dtype=np.uint64)  # (filled in place: no per-step Python lists)
+            for t in range(max_tokens):
+                for r in range(B):
+                    dr[t, r] = probes[r].next_u64()
             draws = torch.from_numpy(dr.view(np.int64)).to(dev)
         toks = hist[:, :n0 - 1].contiguous()
         torch.cuda.synchronize()
