@@ -752,6 +752,131 @@ __global__ void __launch_bounds__(256)
     }
 }
 
+// W8A8 for large m (a prompt's linears), the same arithmetic as k_gemm_w8a8
+// (every output the same bits) with the operands staged through LDS: a
+// workgroup owns a 256 x 256 output tile (eight waves of 128 x 64, 4 x 2
+// MFMA tiles) and stages one Q8_0 block of it at a time, 18 KiB: the eight
+// 32-row activation fragments (already in MFMA lane order in the panel), the
+// 256 weight half-rows as [half][column] (a fragment read is 64 consecutive
+// 16-byte pieces), the rows' activation scales and the columns' weight
+// scales.  Each operand byte then crosses from memory once per workgroup
+// instead of once per wave.  Two LDS stages: block b + 1 is loaded into
+// registers while block b's MFMAs and epilogue run, and stored into the other
+// stage between the two halves of them.  Workgroups are dealt to XCDs in
+// contiguous runs of tiles.  The panel covers whole 256-row tiles.
+constexpr int kW8Rows = 256, kW8Cols = 256, kW8Threads = 512;
+constexpr int kW8StageBytes = 8 * 1024 + 8 * 1024 + 256 * 4 + 256 * 4;
+constexpr size_t kW8LdsMinRows = 1024;  // m from which W8A8 takes the staged kernel
+
+__global__ void __launch_bounds__(kW8Threads)
+    k_gemm_w8a8_lds(const uint4* __restrict__ qp, const float* __restrict__ dp, const int8_t* __restrict__ qs,
+                    const uint16_t* __restrict__ dsc, const float* __restrict__ bias, float* __restrict__ y, int m,
+                    int n, int k, int tiles_n) {
+    typedef int i4 __attribute__((ext_vector_type(4)));
+    typedef int i16 __attribute__((ext_vector_type(16)));
+    constexpr int TM = 4, TN = 2;
+    __shared__ __attribute__((aligned(16))) char lds[2 * kW8StageBytes];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+    const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves
+    const int tiles = static_cast<int>(gridDim.x), per_xcd = tiles / 8, rem = tiles % 8;
+    const int xcd = static_cast<int>(blockIdx.x) % 8, slot = static_cast<int>(blockIdx.x) / 8;
+    const int tile = xcd * per_xcd + min(xcd, rem) + slot;
+    const int tile_m = tile / tiles_n, tile_n = tile % tiles_n;
+    const int j0 = tile_n * kW8Cols, kb = k >> 5;
+    // This thread's staging pieces: activation fragment (row tile tid / 64,
+    // lane tid % 64), weight half-row (column tid / 2, half tid % 2), and
+    // one scale: the row scale of row tid (tid < 256) or the weight scale of
+    // column tid - 256.  Columns past n repeat column n - 1 (never stored).
+    const int art = tid >> 6, alane = tid & 63;
+    const size_t a_base = static_cast<size_t>(tile_m * 8 + art) * kb;
+    const int bcol = tid >> 1, bhalf = tid & 1;
+    const int8_t* wsrc = qs + static_cast<size_t>(min(j0 + bcol, n - 1)) * k + bhalf * 16;
+    const bool row_scale = tid < 256;
+    const int sc_i = tid & 255;
+    const float* dsrc_x = dp + static_cast<size_t>(tile_m * 8 + (sc_i >> 5)) * kb * 32 + (sc_i & 31);
+    const uint16_t* dsrc_w = dsc + static_cast<size_t>(min(j0 + sc_i, n - 1)) * kb;
+    uint4 ra, rb;
+    float rs;
+    auto load = [&](int b) __attribute__((always_inline)) {
+        ra = qp[(a_base + b) * 64 + alane];
+        rb = *reinterpret_cast<const uint4*>(wsrc + b * 32);
+        rs = row_scale ? dsrc_x[static_cast<size_t>(b) * 32] : fh_h2f(dsrc_w[b]);
+    };
+    auto store = [&](int buf) __attribute__((always_inline)) {
+        char* st = lds + buf * kW8StageBytes;
+        reinterpret_cast<uint4*>(st)[art * 64 + alane] = ra;
+        reinterpret_cast<uint4*>(st + 8192)[bhalf * 256 + bcol] = rb;
+        reinterpret_cast<float*>(st + 16384)[tid] = rs;  // [0, 256): row scales, [256, 512): weight scales
+    };
+    float acc[TM][TN][16];
+#pragma unroll
+    for (int r = 0; r < TM; r++)
+#pragma unroll
+        for (int c = 0; c < TN; c++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[r][c][v] = 0.0f;
+
+    load(0);
+    store(0);
+    __syncthreads();
+    for (int b = 0; b < kb; b++) {
+        const int buf = b & 1;
+        if (b + 1 < kb) load(b + 1);
+        const char* st = lds + buf * kW8StageBytes;
+        const uint4* As = reinterpret_cast<const uint4*>(st);
+        const uint4* Bs = reinterpret_cast<const uint4*>(st + 8192);
+        const float* Ss = reinterpret_cast<const float*>(st + 16384);
+        i4 bf[TN];
+        float dw[TN];
+#pragma unroll
+        for (int c = 0; c < TN; c++) {
+            const int col = (wn * TN + c) * 32 + l32;
+            bf[c] = __builtin_bit_cast(i4, Bs[g * 256 + col]);
+            dw[c] = Ss[256 + col];
+        }
+        auto rows = [&](int r0, int r1) __attribute__((always_inline)) {
+#pragma clang fp contract(off)  // plain operators: separately rounded products and sums
+#pragma unroll
+            for (int r = r0; r < r1; r++) {
+                const int rt = wm * TM + r;
+                const i4 af = __builtin_bit_cast(i4, As[rt * 64 + lane]);
+                // output v of this lane is row (v / 4) * 8 + g * 4 + v % 4 of the row tile
+                f4 dx[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) dx[q] = *reinterpret_cast<const f4*>(Ss + rt * 32 + q * 8 + g * 4);
+#pragma unroll
+                for (int c = 0; c < TN; c++) {
+                    const i16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[c], i16{}, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        const float dd = dw[c] * dx[v >> 2][v & 3];
+                        acc[r][c][v] = acc[r][c][v] + static_cast<float>(d[v]) * dd;
+                    }
+                }
+            }
+        };
+        rows(0, TM / 2);
+        // (the other stage is free since the last barrier; at the last block
+        // it is rewritten with this block's pieces, never read again)
+        store(buf ^ 1);
+        rows(TM / 2, TM);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int c = 0; c < TN; c++) {
+        const int j = j0 + (wn * TN + c) * 32 + l32;
+        if (j >= n) continue;
+        const float bj = bias ? bias[j] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < TM; r++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) {
+                const int i = tile_m * kW8Rows + (wm * TM + r) * 32 + (v >> 2) * 8 + g * 4 + (v & 3);
+                if (i < m) y[static_cast<size_t>(i) * n + j] = bias ? acc[r][c][v] + bj : acc[r][c][v];
+            }
+    }
+}
+
 // ---- skinny m (batched decode): m <= 32 * MT ------------------------------------
 // Grid: 32-wide weight-row tiles x S splits of the Q8_0 blocks.  A workgroup's
 // waves divide its split's blocks and issue every load of a batch of up to BPW
@@ -1599,7 +1724,9 @@ __global__ void fh_k_encode_panel(const float* __restrict__ x, int m, int m_pad,
 // W8A8 through the int8 matrix cores: the activations are encoded into the
 // lane-order panel, then one wave per (32 TM) x 64 output tile.
 int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
-    const int tm_rows = m >= 64 ? 64 : 32;
+    // (a prompt's m takes the LDS-staged kernel: its panel covers whole 256-row tiles)
+    const bool staged = m >= kW8LdsMinRows;
+    const int tm_rows = staged ? kW8Rows : m >= 64 ? 64 : 32;
     const size_t kb = w->k / 32, m_pad = (m + tm_rows - 1) / tm_rows * tm_rows;
     const size_t qbytes = fh_align256(m_pad * w->k), dbytes = fh_align256(m_pad * kb * 4);
     void* ws = nullptr;
@@ -1611,6 +1738,15 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
     hipLaunchKernelGGL(fh_k_encode_panel, dim3(static_cast<unsigned>((nb + 255) / 256)), dim3(256), 0, ctx->stream, x,
                        static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(kb), qp, dp);
     FH_HIP(ctx, hipGetLastError());
+    if (staged) {
+        const size_t tn = (w->n + kW8Cols - 1) / kW8Cols, tl = tn * (m_pad / kW8Rows);
+        if (tl > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
+        hipLaunchKernelGGL(k_gemm_w8a8_lds, dim3(static_cast<unsigned>(tl)), dim3(kW8Threads), 0, ctx->stream, qp,
+                           dp, w->qs, w->d, bias, y, static_cast<int>(m), static_cast<int>(w->n),
+                           static_cast<int>(w->k), static_cast<int>(tn));
+        FH_HIP(ctx, hipGetLastError());
+        return FH_OK;
+    }
     const size_t tiles_n = (w->n + 63) / 64, tiles = tiles_n * (m_pad / tm_rows);
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
     const dim3 grid(static_cast<unsigned>((tiles + 3) / 4)), block(256);

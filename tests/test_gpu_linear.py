@@ -519,13 +519,16 @@ def test_w8a8_matches_oracle(fh, orc, m, n, k):
 
 
 @pytest.mark.parametrize("m,n,k,has_bias", [(32, 6144, 32, True), (40, 6200, 96, False), (64, 6144, 64, True),
-                                            (100, 3100, 768, True), (257, 2304, 768, False), (1000, 1024, 1024, True)])
+                                            (100, 3100, 768, True), (257, 2304, 768, False), (1000, 1024, 1024, True),
+                                            (1030, 700, 96, True), (2048, 512, 1024, False), (1024, 256, 32, True)])
 def test_w8a8_matrix_cores_are_bit_exact(fh, orc, m, n, k, has_bias):
     """With >= 96 output tiles of (32 or 64) x 64, W8A8 runs on the int8
     matrix cores (one v_mfma_i32_32x32x32_i8 per Q8_0 block of a 32 x 32
     tile) and adds the scaled block dots in the reference's order without FMA:
     equal to the reference bit for bit, non-finite rows, ragged shapes and
-    odd block counts included."""
+    odd block counts included.  From m = 1024 the operands go through LDS
+    (256 x 256 workgroup tiles): rows and columns past a tile edge, one
+    block and an odd number of blocks."""
     import ferrum_hip
 
     raw = weight(orc, n, k, 7 * m + n + k)
