@@ -753,27 +753,41 @@ __global__ void __launch_bounds__(256)
 }
 
 // W8A8 for large m (a prompt's linears), the same arithmetic as k_gemm_w8a8
-// (every output the same bits) with the operands staged through LDS: a
+// (every output the same bits), with the operands staged through LDS: a
 // workgroup owns a 256 x 256 output tile (eight waves of 128 x 64, 4 x 2
-// MFMA tiles) and stages one Q8_0 block of it at a time, 18 KiB: the eight
-// 32-row activation fragments (already in MFMA lane order in the panel), the
-// 256 weight half-rows as [half][column] (a fragment read is 64 consecutive
-// 16-byte pieces), the rows' activation scales and the columns' weight
-// scales.  Each operand byte then crosses from memory once per workgroup
-// instead of once per wave.  Two LDS stages: block b + 1 is loaded into
-// registers while block b's MFMAs and epilogue run, and stored into the other
-// stage between the two halves of them.  Workgroups are dealt to XCDs in
-// contiguous runs of tiles.  The panel covers whole 256-row tiles.
+// 32 x 32 tiles) and stages one Q8_0 block of it at a time.  Each operand byte
+// crosses from memory once per workgroup instead of once per wave.
+// The block terms are formed on the matrix cores, leaving two VALU
+// operations per output and block (the product and the sum):
+//  * the int8 quants are staged as f16 (exact), and two
+//    v_mfma_f32_32x32x16_f16 give the block dot as an f32 that is the exact
+//    integer (|dot| <= 32 * 128 * 128 < 2^24, so every partial sum is
+//    exact whatever the order inside the MFMA);
+//  * d_w * d_x is the product of two f16 values, exact in f32, so one
+//    v_mfma_f32_32x32x1_2b_f32 outer product (32 row scales x 64 column
+//    scales, no other term) gives it for both 32 x 32 tiles of a row tile, in
+//    the accumulators' own register layout; inf and NaN scales propagate as
+//    in the scalar product, and a zero's sign cannot reach a sum that
+//    starts at +0.
+// Then acc = acc + dot * dd with the product and the sum rounded separately,
+// in ascending b, as the reference does.  A stage (34 KiB): the eight 32-row
+// activation fragments as [row tile][MFMA half][lane] (the panel is in MFMA
+// lane order already), the 256 weight half-rows as [MFMA half][lane half]
+// [column] (a fragment read is 32 consecutive 16-byte pieces), the rows'
+// activation scales and the columns' weight scales.  Two stages: block b + 1
+// is loaded into registers while block b's MFMAs and epilogue run, and
+// converted and stored into the other stage between the two halves of them.
+// Workgroups are dealt to XCDs in contiguous runs of tiles.  The panel covers
+// whole 256-row tiles.
 constexpr int kW8Rows = 256, kW8Cols = 256, kW8Threads = 512;
-constexpr int kW8StageBytes = 8 * 1024 + 8 * 1024 + 256 * 4 + 256 * 4;
+constexpr int kW8StageBytes = 16 * 1024 + 16 * 1024 + 256 * 4 + 256 * 4;
 constexpr size_t kW8LdsMinRows = 1024;  // m from which W8A8 takes the staged kernel
 
 __global__ void __launch_bounds__(kW8Threads)
     k_gemm_w8a8_lds(const uint4* __restrict__ qp, const float* __restrict__ dp, const int8_t* __restrict__ qs,
                     const uint16_t* __restrict__ dsc, const float* __restrict__ bias, float* __restrict__ y, int m,
                     int n, int k, int tiles_n) {
-    typedef int i4 __attribute__((ext_vector_type(4)));
-    typedef int i16 __attribute__((ext_vector_type(16)));
+    typedef float f32x __attribute__((ext_vector_type(32)));
     constexpr int TM = 4, TN = 2;
     __shared__ __attribute__((aligned(16))) char lds[2 * kW8StageBytes];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
@@ -791,22 +805,34 @@ __global__ void __launch_bounds__(kW8Threads)
     const size_t a_base = static_cast<size_t>(tile_m * 8 + art) * kb;
     const int bcol = tid >> 1, bhalf = tid & 1;
     const int8_t* wsrc = qs + static_cast<size_t>(min(j0 + bcol, n - 1)) * k + bhalf * 16;
-    const bool row_scale = tid < 256;
+    // (waves 0-3 hold row scales, 4-7 weight scales: a wave-uniform branch,
+    // and the f16 weight scale is widened at the store, so that no wave waits
+    // for its loads where it issues them)
+    const bool row_scale = __builtin_amdgcn_readfirstlane(wave) < 4;
     const int sc_i = tid & 255;
     const float* dsrc_x = dp + static_cast<size_t>(tile_m * 8 + (sc_i >> 5)) * kb * 32 + (sc_i & 31);
     const uint16_t* dsrc_w = dsc + static_cast<size_t>(min(j0 + sc_i, n - 1)) * kb;
     uint4 ra, rb;
-    float rs;
+    uint32_t rs;  // the scale's bits: f32 (row scale) or f16 (weight scale)
     auto load = [&](int b) __attribute__((always_inline)) {
         ra = qp[(a_base + b) * 64 + alane];
         rb = *reinterpret_cast<const uint4*>(wsrc + b * 32);
-        rs = row_scale ? dsrc_x[static_cast<size_t>(b) * 32] : fh_h2f(dsrc_w[b]);
+        if (row_scale) rs = __builtin_bit_cast(uint32_t, dsrc_x[static_cast<size_t>(b) * 32]);
+        else rs = dsrc_w[b];
     };
     auto store = [&](int buf) __attribute__((always_inline)) {
         char* st = lds + buf * kW8StageBytes;
-        reinterpret_cast<uint4*>(st)[art * 64 + alane] = ra;
-        reinterpret_cast<uint4*>(st + 8192)[bhalf * 256 + bcol] = rb;
-        reinterpret_cast<float*>(st + 16384)[tid] = rs;  // [0, 256): row scales, [256, 512): weight scales
+        uint4* As = reinterpret_cast<uint4*>(st);
+        uint4* Bs = reinterpret_cast<uint4*>(st + 16384);
+        uint2 q0 = quants_to_f16(ra.x), q1 = quants_to_f16(ra.y), q2 = quants_to_f16(ra.z), q3 = quants_to_f16(ra.w);
+        As[(art * 2) * 64 + alane] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        As[(art * 2 + 1) * 64 + alane] = make_uint4(q2.x, q2.y, q3.x, q3.y);
+        q0 = quants_to_f16(rb.x), q1 = quants_to_f16(rb.y), q2 = quants_to_f16(rb.z), q3 = quants_to_f16(rb.w);
+        Bs[bhalf * 256 + bcol] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        Bs[(2 + bhalf) * 256 + bcol] = make_uint4(q2.x, q2.y, q3.x, q3.y);
+        // [0, 256): row scales, [256, 512): weight scales
+        reinterpret_cast<float*>(st + 32768)[tid] =
+            row_scale ? __builtin_bit_cast(float, rs) : fh_h2f(static_cast<uint16_t>(rs));
     };
     float acc[TM][TN][16];
 #pragma unroll
@@ -823,35 +849,31 @@ __global__ void __launch_bounds__(kW8Threads)
         const int buf = b & 1;
         if (b + 1 < kb) load(b + 1);
         const char* st = lds + buf * kW8StageBytes;
-        const uint4* As = reinterpret_cast<const uint4*>(st);
-        const uint4* Bs = reinterpret_cast<const uint4*>(st + 8192);
-        const float* Ss = reinterpret_cast<const float*>(st + 16384);
-        i4 bf[TN];
-        float dw[TN];
+        const h8* As = reinterpret_cast<const h8*>(st);
+        const h8* Bs = reinterpret_cast<const h8*>(st + 16384);
+        const float* Ss = reinterpret_cast<const float*>(st + 32768);
+        h8 bf[TN][2];
 #pragma unroll
         for (int c = 0; c < TN; c++) {
             const int col = (wn * TN + c) * 32 + l32;
-            bf[c] = __builtin_bit_cast(i4, Bs[g * 256 + col]);
-            dw[c] = Ss[256 + col];
+            bf[c][0] = Bs[g * 256 + col];
+            bf[c][1] = Bs[(2 + g) * 256 + col];
         }
+        const float dw = Ss[256 + wn * 64 + lane];  // lane half c: column tile c of this wave
         auto rows = [&](int r0, int r1) __attribute__((always_inline)) {
 #pragma clang fp contract(off)  // plain operators: separately rounded products and sums
 #pragma unroll
             for (int r = r0; r < r1; r++) {
                 const int rt = wm * TM + r;
-                const i4 af = __builtin_bit_cast(i4, As[rt * 64 + lane]);
-                // output v of this lane is row (v / 4) * 8 + g * 4 + v % 4 of the row tile
-                f4 dx[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) dx[q] = *reinterpret_cast<const f4*>(Ss + rt * 32 + q * 8 + g * 4);
+                const h8 a0 = As[(rt * 2) * 64 + lane], a1 = As[(rt * 2 + 1) * 64 + lane];
+                // dd[16 c + v]: d_w * d_x of output v of this lane in column tile c
+                const f32x dd = __builtin_amdgcn_mfma_f32_32x32x1f32(Ss[rt * 32 + l32], dw, f32x{}, 0, 0, 0);
 #pragma unroll
                 for (int c = 0; c < TN; c++) {
-                    const i16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(af, bf[c], i16{}, 0, 0, 0);
+                    f16x d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[c][0], f16x{}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[c][1], d, 0, 0, 0);
 #pragma unroll
-                    for (int v = 0; v < 16; v++) {
-                        const float dd = dw[c] * dx[v >> 2][v & 3];
-                        acc[r][c][v] = acc[r][c][v] + static_cast<float>(d[v]) * dd;
-                    }
+                    for (int v = 0; v < 16; v++) acc[r][c][v] = acc[r][c][v] + d[v] * dd[c * 16 + v];
                 }
             }
         };

@@ -527,8 +527,9 @@ def test_w8a8_matrix_cores_are_bit_exact(fh, orc, m, n, k, has_bias):
     tile) and adds the scaled block dots in the reference's order without FMA:
     equal to the reference bit for bit, non-finite rows, ragged shapes and
     odd block counts included.  From m = 1024 the operands go through LDS
-    (256 x 256 workgroup tiles): rows and columns past a tile edge, one
-    block and an odd number of blocks."""
+    (256 x 256 workgroup tiles) as f16, the block dot is two f16 MFMAs (an
+    exact integer in f32) and d_w * d_x one f32 outer-product MFMA: rows and
+    columns past a tile edge, one block and an odd number of blocks."""
     import ferrum_hip
 
     raw = weight(orc, n, k, 7 * m + n + k)
