@@ -1740,6 +1740,7 @@ int launch_skinny(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const
 
 }  // namespace
 
+template <bool V4>
 __global__ void fh_k_encode_panel(const float* __restrict__ x, int m, int m_pad, int kb, uint4* __restrict__ qp,
                                   float* __restrict__ dp);
 
@@ -1756,9 +1757,14 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
     if (rc) return rc;
     uint4* qp = static_cast<uint4*>(ws);
     float* dp = reinterpret_cast<float*>(static_cast<char*>(ws) + qbytes);
-    const size_t nb = m_pad * kb;
-    hipLaunchKernelGGL(fh_k_encode_panel, dim3(static_cast<unsigned>((nb + 255) / 256)), dim3(256), 0, ctx->stream, x,
-                       static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(kb), qp, dp);
+    const size_t frags = m_pad / 32 * kb;  // one wave each
+    const dim3 egrid(static_cast<unsigned>((frags + 3) / 4));
+    if (reinterpret_cast<uintptr_t>(x) & 15)
+        hipLaunchKernelGGL(fh_k_encode_panel<false>, egrid, dim3(256), 0, ctx->stream, x, static_cast<int>(m),
+                           static_cast<int>(m_pad), static_cast<int>(kb), qp, dp);
+    else
+        hipLaunchKernelGGL(fh_k_encode_panel<true>, egrid, dim3(256), 0, ctx->stream, x, static_cast<int>(m),
+                           static_cast<int>(m_pad), static_cast<int>(kb), qp, dp);
     FH_HIP(ctx, hipGetLastError());
     if (staged) {
         const size_t tn = (w->n + kW8Cols - 1) / kW8Cols, tl = tn * (m_pad / kW8Rows);

@@ -171,23 +171,59 @@ __global__ void __launch_bounds__(256) fh_k_encode_split(const float* __restrict
 }
 
 // f32 [m, k] -> Q8_0 activations in the W8A8 matrix-core panel: per 32-row
-// tile and block b, 1 KiB of quants in MFMA lane order (lane g * 32 + r holds
-// row r's quants 16 g .. 16 g + 15) and the 32 row scales as f32.  Rows m ..
-// m_pad - 1 are zero.  Same per-block arithmetic as the GGUF encoder.
+// tile and block b (a fragment), 1 KiB of quants in MFMA lane order (lane
+// g * 32 + r holds row r's quants 16 g .. 16 g + 15) and the 32 row scales
+// as f32.  Rows m .. m_pad - 1 are zero.  Same per-block arithmetic as the
+// GGUF encoder.  One wave per fragment: lane g * 32 + r reads row r's
+// elements 16 g .. 16 g + 15 and writes exactly their 16 panel bytes (the
+// wave's stores are one contiguous KiB); the block's maximum is the larger
+// of the two halves' (fmaxf drops NaN in any order, so it is the same value).
+// V4: x is 16-byte aligned (float4 loads); otherwise 4-byte loads.
+template <bool V4>
 __global__ void __launch_bounds__(256) fh_k_encode_panel(const float* __restrict__ x, int m, int m_pad, int kb,
                                                          uint4* __restrict__ qp, float* __restrict__ dp) {
-    const size_t t = blockIdx.x * static_cast<size_t>(256) + threadIdx.x;
-    if (t >= static_cast<size_t>(m_pad) * kb) return;
-    const int row = static_cast<int>(t / kb), b = static_cast<int>(t % kb);
-    uint32_t q[8] = {};
-    uint16_t d16 = 0;
-    if (row < m) d16 = encode_block(x + (static_cast<size_t>(row) * kb + b) * 32, q);
-    const size_t tile = (static_cast<size_t>(row >> 5) * kb + b);
-    uint4* dst = qp + tile * 64 + (row & 31);
-    dst[0] = make_uint4(q[0], q[1], q[2], q[3]);
-    dst[32] = make_uint4(q[4], q[5], q[6], q[7]);
-    dp[tile * 32 + (row & 31)] = fh_h2f(d16);
+    const int lane = threadIdx.x & 63;
+    const size_t frag = blockIdx.x * static_cast<size_t>(4) + (threadIdx.x >> 6);  // tile * kb + b
+    if (frag >= static_cast<size_t>(m_pad / 32) * kb) return;  // (the whole wave)
+    const int tile = static_cast<int>(frag / kb), b = static_cast<int>(frag % kb);
+    const int r = lane & 31, g = lane >> 5, row = tile * 32 + r;
+    float v[16];
+    if (row < m) {
+        const float* src = x + (static_cast<size_t>(row) * kb + b) * 32 + g * 16;
+        if (V4) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const float4 f = reinterpret_cast<const float4*>(src)[i];
+                v[4 * i] = f.x; v[4 * i + 1] = f.y; v[4 * i + 2] = f.z; v[4 * i + 3] = f.w;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 16; i++) v[i] = src[i];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 16; i++) v[i] = 0.0f;
+    }
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; i++) amax = fmaxf(amax, fabsf(v[i]));
+    amax = fmaxf(amax, __shfl_xor(amax, 32));
+    const float d = amax / 127.0f;
+    const float id = d != 0.0f ? 1.0f / d : 0.0f;
+    uint32_t q[4];
+#pragma unroll
+    for (int w = 0; w < 4; w++) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) word |= (static_cast<uint32_t>(round_sat_i8(v[w * 4 + e] * id)) & 0xFFu) << (8 * e);
+        q[w] = word;
+    }
+    qp[frag * 64 + lane] = make_uint4(q[0], q[1], q[2], q[3]);
+    if (g == 0) dp[frag * 32 + r] = fh_h2f(f32_to_f16_bits(d));
 }
+
+template __global__ void fh_k_encode_panel<true>(const float*, int, int, int, uint4*, float*);
+template __global__ void fh_k_encode_panel<false>(const float*, int, int, int, uint4*, float*);
 
 int fh_launch_repack(fh_ctx* ctx, const uint8_t* d_raw, size_t n, size_t k, int8_t* qs, uint16_t* d) {
     if (reinterpret_cast<uintptr_t>(d_raw) & 1)

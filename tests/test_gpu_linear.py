@@ -520,7 +520,7 @@ def test_w8a8_matches_oracle(fh, orc, m, n, k):
 
 @pytest.mark.parametrize("m,n,k,has_bias", [(32, 6144, 32, True), (40, 6200, 96, False), (64, 6144, 64, True),
                                             (100, 3100, 768, True), (257, 2304, 768, False), (1000, 1024, 1024, True),
-                                            (1030, 700, 96, True), (2048, 512, 1024, False), (1024, 256, 32, True)])
+                                            (1030, 700, 96, True), (2048, 512, 1024, False), (1024, 384, 32, True)])
 def test_w8a8_matrix_cores_are_bit_exact(fh, orc, m, n, k, has_bias):
     """With >= 96 output tiles of (32 or 64) x 64, W8A8 runs on the int8
     matrix cores (one v_mfma_i32_32x32x32_i8 per Q8_0 block of a 32 x 32
@@ -546,6 +546,31 @@ def test_w8a8_matrix_cores_are_bit_exact(fh, orc, m, n, k, has_bias):
     ref = orc.q8_0_linear_w8a8(x, raw, n, b)
     assert np.array_equal(got, ref, equal_nan=True)
     assert np.isnan(got[1]).all() and np.isfinite(got[5:m - 1]).all()
+
+
+@pytest.mark.parametrize("m,n,k", [(64, 6144, 64), (1030, 700, 96)])
+def test_w8a8_takes_rows_at_a_4_byte_offset(fh, orc, m, n, k):
+    """x need only be 4-byte aligned: from a torch view one float into its
+    buffer the panel encoder reads it with 4-byte loads, and the outputs still
+    equal the reference bit for bit (the matrix-core path and the staged one)."""
+    import torch
+
+    import ferrum_hip
+
+    raw = weight(orc, n, k, m + n)
+    x = acts(m, k, m + n)
+    x[2, 7] = np.nan
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    buf = torch.zeros(m * k + 1, device="cuda")
+    dx = buf[1:]
+    dx.copy_(torch.from_numpy(x.ravel()))
+    assert dx.data_ptr() % 16 == 4
+    dy = torch.full((m, n), float("nan"), device="cuda")
+    torch.cuda.synchronize()
+    ferrum_hip.linear_forward_async(fh, w, dx, m, k, None, 0, dy, numerics=ferrum_hip.W8A8)
+    fh.sync()
+    w.free()
+    assert np.array_equal(dy.cpu().numpy(), orc.q8_0_linear_w8a8(x, raw, n, None), equal_nan=True)
 
 
 def test_int32_block_dots_are_bit_exact(fh, orc):
