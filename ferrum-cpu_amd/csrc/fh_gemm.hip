@@ -23,9 +23,9 @@
 // Work split: for the mid-size tiles k_split_rows writes the h/l terms once
 // per call into a panel laid out for the GEMM's staging ([row tile][block]
 // [row][h 32 | l 32], 128 B per row and block, so a stage is one contiguous
-// read); the large-m weight-split kernel instead takes only the row scales
-// (k_row_scales, one read of x) and splits the activations while staging
-// them, which saves the panel's write and re-read.  k_gemm_mfma stages
+// read); the large-m block-scaled kernel (k_gemm_bscale) instead takes only
+// the row scales (k_row_scales, one read of x) and splits the activations
+// while staging them, which saves the panel's write and re-read.  k_gemm_mfma stages
 // KW Q8_0 blocks of the activation panel and of the weight rows per step into
 // LDS (double buffered, one barrier per step), converting the int8 quants to
 // f16 on the way in; each wave owns TM x TN 32x32 output tiles, and with
@@ -196,8 +196,8 @@ __global__ void __launch_bounds__(256)
     }
 }
 
-// The row scales and flags of k_split_rows without the panel: the weight-split
-// GEMM splits the activations itself while staging them (one read of x here
+// The row scales and flags of k_split_rows without the panel: the
+// block-scaled GEMM splits the activations itself while staging them (one read of x here
 // instead of a read and a write of the whole panel).  Rows m .. m_pad - 1 get
 // scale 1 and no flag.
 __global__ void __launch_bounds__(256)
@@ -417,233 +417,184 @@ __global__ void __launch_bounds__(64 * WM * WN * KW)
     if (__syncthreads_or(flagged)) exact_tile(x, qs, dsc, rexp, nullptr, bias, y, m, n, k, i0, j0, BM, BN, FH_ACT_NONE);
 }
 
-// ---- large m: both operands split, block scales folded into the weights ----------
-// For the big tiles the per-block weight-scale FMA would need every output sum
-// in VGPRs; instead the weight operand carries its scale: per weight row j,
-//   2^e_j * f16(d_jb) * q   (e_j from the row's largest scale, at upload)
-// has at most 18 significant bits and is split exactly into f16 hi + lo.  The
-// products then accumulate across all Q8_0 blocks in the matrix core's
-// accumulators (AGPRs):  x_h W_h + x_h W_l + x_l W_h  (three MFMAs per K = 16;
-// the dropped x_l W_l is 2^-22 of a product), and the output is
-// acc * 2^-e_i * 2^-e_j (+ bias).  The dequantised weight is used exactly; the
-// only rounding beyond the f32 sums is the activations' 22-bit split.
-// Workgroup tile 256 x 256, eight waves of 128 x 64 (4 x 2 MFMA tiles), one
-// Q8_0 block per stage, two LDS stages of 72 KiB.
-// Activation staging pieces (4 values of a row's 32-value block) for the
-// large-m GEMM: each 64-piece group covers 8 rows x 8 pieces, 16 consecutive
-// lanes taking 8 rows x 2 adjacent pieces, so their 8-byte LDS stores (the
-// 144-byte row pitch) fall on disjoint banks of the 32.
-__device__ __forceinline__ int piece_row(int q) { return (q >> 6) * 8 + ((q & 15) >> 1); }
-__device__ __forceinline__ int piece_col(int q) { return ((q & 63) >> 4) * 2 + (q & 1); }
+// ---- large m, block-scaled: the quants as the weight operand -------------------------
+// W8A32 for a prompt's linears without folding the block scales into the
+// weights: the weight operand is the int8 quants themselves (exact in f16),
+// so a Q8_0 block of a 32 x 32 tile is four MFMAs (the activation's h and l
+// terms, two K halves) giving the block's partial sum sum_p (h + l) q in f32,
+// and one FMA per output adds it times the block scale d_jb to the running
+// f32 sum.  Folding the scales into the weights instead (d * q has up to 19
+// significant bits: two f16 terms, x_h w_h + x_h w_l + x_l w_h, six MFMAs per
+// block) costs half as much again on the matrix cores and a costlier weight
+// staging; here the price is 16 FMAs per tile and block on the VALU.  The
+// activations are split as in k_gemm_mfma (row scale 2^e_i from
+// k_row_scales, h = f16(x 2^e_i), l = f16(x 2^e_i - h)); the sum is scaled by
+// 2^-e_i at the end (exact), then the bias is added and GELU applied.  Rows
+// with inf/NaN activations and weight rows with a non-finite scale are
+// recomputed with the reference's own arithmetic (exact_tile).
+// Workgroup tile 256 x 256, eight waves of 128 x 64 (4 x 2 tiles), one Q8_0
+// block per stage, two stages of 49 KiB: the activations as [row tile][term
+// h|l][MFMA half][lane] (16-byte fragments: lane g * 32 + r holds row r's
+// elements 16 g + 8 half .. + 7), the quants as [MFMA half][lane half]
+// [column] and the 256 columns' block scales.  Block b + 1 is loaded into
+// registers while block b's MFMAs run and is split and stored into the other
+// stage between their two halves.
+constexpr int kBsStage = 32 * 1024 + 16 * 1024 + 256 * 4;
 
-template <int BM, int BN, int WM, int WN, bool FROM_X>
-__global__ void __launch_bounds__(64 * WM * WN)
-    k_gemm_wsplit(const uint4* __restrict__ panel, const float* __restrict__ xinv, const uint8_t* __restrict__ xbad,
-                  const float* __restrict__ x, const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc,
-                  const int8_t* __restrict__ rexp, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
-                  int k, int tiles_n, int act) {
-    constexpr int NW = WM * WN, NTH = 64 * NW;
-    constexpr int TM = BM / (32 * WM), TN = BN / (32 * WN);
-    static_assert(TM * 32 * WM == BM && TN * 32 * WN == BN, "tile shape");
-    constexpr int A_BYTES = BM * kArow * 2, B_BYTES = BN * kArow * 2, STAGE = A_BYTES + B_BYTES;
-    constexpr int AP = BM * 8 / NTH;  // 16-byte activation pieces per thread
-    static_assert(AP * NTH == BM * 8 && BN * 2 == NTH, "staging split: one weight half-row per thread");
-    __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int wm = wave / WN, wn = wave % WN;
+__global__ void __launch_bounds__(512)
+    k_gemm_bscale(const float* __restrict__ xinv, const uint8_t* __restrict__ xbad, const float* __restrict__ x,
+                  const int8_t* __restrict__ qs, const uint16_t* __restrict__ dsc, const int8_t* __restrict__ rexp,
+                  const float* __restrict__ bias, float* __restrict__ y, int m, int n, int k, int tiles_n, int act) {
+    constexpr int TM = 4, TN = 2, BM = 256, BN = 256, NTH = 512;
+    __shared__ __attribute__((aligned(16))) char lds[2 * kBsStage];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 5, l32 = lane & 31;
+    const int wm = wave >> 2, wn = wave & 3;  // 2 x 4 waves
     const int tiles = static_cast<int>(gridDim.x), per_xcd = tiles / 8, rem = tiles % 8;
     const int xcd = static_cast<int>(blockIdx.x) % 8, slot = static_cast<int>(blockIdx.x) / 8;
     const int tile = xcd * per_xcd + min(xcd, rem) + slot;
     const int tile_m = tile / tiles_n, tile_n = tile % tiles_n;
-    const int j0 = tile_n * BN;
-    const int kb = k >> 5;
-    const uint4* pan = panel + static_cast<size_t>(tile_m) * kb * BM * 8;
-
-    // This thread's weight half-row (rows past n repeat row n - 1: their
-    // output columns are never stored, and a column depends only on its row).
-    // (lanes 8t .. 8t + 7 take eight consecutive rows, one half each: their
-    // 16-byte LDS stores fall on disjoint banks)
-    const int jr = ((tid >> 4) << 3) | (tid & 7), jhalf = (tid >> 3) & 1;
-    const int jw = min(j0 + jr, n - 1);
-    const int8_t* wsrc = qs + static_cast<size_t>(jw) * k + jhalf * 16;
-    const uint16_t* dsrc = dsc + static_cast<size_t>(jw) * kb;
-    const int ejw = rexp[jw] == kFhBadRowExp ? 0 : rexp[jw];  // flagged rows: recomputed at the end
-    const float wscale = __builtin_bit_cast(float, static_cast<uint32_t>(ejw + 127) << 23);
-
-    // FROM_X: the activations come straight from x (f32, row-major) and are
-    // split here, with the row scales of k_row_scales: each thread stages
-    // four 4-value pieces (rows piece / 8, values 4 * (piece % 8) of the
-    // block) as the h and l terms k_split_rows writes to the panel.
-    constexpr int XP = BM * 8 / NTH;  // (also AP) pieces per thread
-    float xsc[FROM_X ? XP : 1];
-    const float* xrow[FROM_X ? XP : 1];
-    if constexpr (FROM_X) {
-        const int i0x = (tile / tiles_n) * BM;
-#pragma unroll
-        for (int p = 0; p < XP; p++) {
-            const int r = piece_row(tid + NTH * p), i = min(i0x + r, m - 1);  // rows past m: clamped, never stored
-            // 2^e from the stored 2^-e (both exact powers of two)
-            xsc[p] = __builtin_bit_cast(float, (254u << 23) - __builtin_bit_cast(uint32_t, xinv[i0x + r]));
-            xrow[p] = x + static_cast<size_t>(i) * k + piece_col(tid + NTH * p) * 4;
-        }
-    }
-    u4 ra[AP], rq;
-    uint16_t rd;
-    auto load = [&](int b) __attribute__((always_inline)) {
-        if constexpr (FROM_X) {
-#pragma unroll
-            for (int p = 0; p < AP; p++) ra[p] = *reinterpret_cast<const u4*>(xrow[p] + b * 32);
-        } else {
-#pragma unroll
-            for (int p = 0; p < AP; p++)
-                ra[p] = reinterpret_cast<const u4*>(pan)[static_cast<size_t>(b) * BM * 8 + tid + NTH * p];
-        }
-        rq = *reinterpret_cast<const u4*>(wsrc + b * 32);
-        rd = dsrc[b];
+    const int i0 = tile_m * BM, j0 = tile_n * BN, kb = k >> 5;
+    // This thread's activation pieces: row wave * 32 + lane / 2 of the tile,
+    // elements 16 s + 8 (lane % 2) .. + 7 for s = 0, 1 (two lanes read 64
+    // contiguous bytes of a row).  Rows past m repeat row m - 1 (never stored).
+    const int ar = lane >> 1, ahf = lane & 1;
+    const float* xsrc = x + static_cast<size_t>(min(i0 + wave * 32 + ar, m - 1)) * k + ahf * 8;
+    // 2^e from the stored 2^-e (both exact powers of two)
+    const float xsc = __builtin_bit_cast(float, (254u << 23) - __builtin_bit_cast(uint32_t, xinv[i0 + wave * 32 + ar]));
+    // Weight half-row (column tid / 2, half tid % 2); waves 0-3 also load the
+    // block scale of column tid.  Columns past n repeat column n - 1.
+    const int bcol = tid >> 1, bhalf = tid & 1;
+    const int8_t* wsrc = qs + static_cast<size_t>(min(j0 + bcol, n - 1)) * k + bhalf * 16;
+    const bool scale_loader = __builtin_amdgcn_readfirstlane(wave) < 4;
+    const uint16_t* dsrc = dsc + static_cast<size_t>(min(j0 + (tid & 255), n - 1)) * kb;
+    u4 ra[2], rb;  // one activation piece in flight at a time
+    uint16_t rd = 0;
+    auto load_a = [&](int b, int s2) __attribute__((always_inline)) {
+        ra[0] = *reinterpret_cast<const u4*>(xsrc + b * 32 + s2 * 16);
+        ra[1] = *reinterpret_cast<const u4*>(xsrc + b * 32 + s2 * 16 + 4);
     };
-    auto store = [&](int buf) __attribute__((always_inline)) {
-        char* st = lds + buf * STAGE;
-#pragma unroll
-        for (int p = 0; p < AP; p++) {
-            const int piece = tid + NTH * p;
-            if constexpr (FROM_X) {
-                const f4 sv = __builtin_bit_cast(f4, ra[p]) * xsc[p];  // exact (power of two)
-                const f2 s01 = {sv.x, sv.y}, s23 = {sv.z, sv.w};
-                const h2 h01 = __builtin_convertvector(s01, h2), h23 = __builtin_convertvector(s23, h2);
-                // (no guard for inf / NaN: such a row's outputs are
-                // recomputed at the end, and an MFMA output row depends only
-                // on its own activation row)
-                const f2 r01 = {sv.x - static_cast<float>(h01.x), sv.y - static_cast<float>(h01.y)};
-                const f2 r23 = {sv.z - static_cast<float>(h23.x), sv.w - static_cast<float>(h23.y)};
-                char* rowp = st + piece_row(piece) * kArow * 2 + piece_col(piece) * 8;
-                *reinterpret_cast<uint2*>(rowp) =
-                    make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
-                *reinterpret_cast<uint2*>(rowp + 64) =
-                    make_uint2(__builtin_bit_cast(uint32_t, __builtin_convertvector(r01, h2)),
-                               __builtin_bit_cast(uint32_t, __builtin_convertvector(r23, h2)));
-            } else {
-                *reinterpret_cast<u4*>(st + (piece / 8) * kArow * 2 + (piece % 8) * 16) = ra[p];
-            }
-        }
-        const float ds = fh_h2f(rd) * wscale;  // exact (power of two)
-        uint32_t hi[8], lo[8];
-#pragma unroll
-        for (int t = 0; t < 8; t++) {
-            const uint32_t word = t < 2 ? rq.x : t < 4 ? rq.y : t < 6 ? rq.z : rq.w;
-            const int sh = (t & 1) * 16;
-            const f2 w = {static_cast<float>(static_cast<int8_t>((word >> sh) & 0xFF)) * ds,
-                          static_cast<float>(static_cast<int8_t>((word >> (sh + 8)) & 0xFF)) * ds};
-            const h2 h = __builtin_convertvector(w, h2);
-            // (no guard: a weight row with a non-finite scale is flagged at
-            // upload and its output column recomputed at the end)
-            const f2 r = {w.x - static_cast<float>(h.x), w.y - static_cast<float>(h.y)};
-            hi[t] = __builtin_bit_cast(uint32_t, h);
-            lo[t] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r, h2));
-        }
-        char* dst = st + A_BYTES + jr * kArow * 2 + jhalf * 32;
-        *reinterpret_cast<u4*>(dst) = u4{hi[0], hi[1], hi[2], hi[3]};
-        *reinterpret_cast<u4*>(dst + 16) = u4{hi[4], hi[5], hi[6], hi[7]};
-        *reinterpret_cast<u4*>(dst + 64) = u4{lo[0], lo[1], lo[2], lo[3]};
-        *reinterpret_cast<u4*>(dst + 80) = u4{lo[4], lo[5], lo[6], lo[7]};
+    auto load_b = [&](int b) __attribute__((always_inline)) {
+        rb = *reinterpret_cast<const u4*>(wsrc + b * 32);
+        if (scale_loader) rd = dsrc[b];
     };
-
-    f16x acc[TM][TN];
+    auto store_a = [&](int buf, int s2) __attribute__((always_inline)) {
+        uint4* As = reinterpret_cast<uint4*>(lds + buf * kBsStage);
+        uint32_t hw[4], lw[4];
+#pragma unroll
+        for (int p2 = 0; p2 < 2; p2++) {
+            const f4 sv = __builtin_bit_cast(f4, ra[p2]) * xsc;  // exact (power of two)
+            const f2 s01 = {sv.x, sv.y}, s23 = {sv.z, sv.w};
+            const h2 h01 = __builtin_convertvector(s01, h2), h23 = __builtin_convertvector(s23, h2);
+            // (no guard for inf / NaN: such a row's outputs are recomputed)
+            const f2 r01 = {sv.x - static_cast<float>(h01.x), sv.y - static_cast<float>(h01.y)};
+            const f2 r23 = {sv.z - static_cast<float>(h23.x), sv.w - static_cast<float>(h23.y)};
+            hw[2 * p2] = __builtin_bit_cast(uint32_t, h01);
+            hw[2 * p2 + 1] = __builtin_bit_cast(uint32_t, h23);
+            lw[2 * p2] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r01, h2));
+            lw[2 * p2 + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r23, h2));
+        }
+        const int frag = s2 * 32 + ar;  // lane g * 32 + r of the fragment
+        As[((wave * 2) * 2 + ahf) * 64 + frag] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        As[((wave * 2 + 1) * 2 + ahf) * 64 + frag] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    };
+    auto store_b = [&](int buf) __attribute__((always_inline)) {
+        char* st = lds + buf * kBsStage;
+        uint4* Bs = reinterpret_cast<uint4*>(st + 32768);
+        const uint2 q0 = quants_to_f16(rb[0]), q1 = quants_to_f16(rb[1]), q2 = quants_to_f16(rb[2]),
+                    q3 = quants_to_f16(rb[3]);
+        Bs[bhalf * 256 + bcol] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        Bs[(2 + bhalf) * 256 + bcol] = make_uint4(q2.x, q2.y, q3.x, q3.y);
+        if (scale_loader) reinterpret_cast<float*>(st + 49152)[tid] = fh_h2f(rd);
+    };
+    float acc[TM][TN][16];
 #pragma unroll
     for (int r = 0; r < TM; r++)
 #pragma unroll
-        for (int c = 0; c < TN; c++) acc[r][c] = f16x{};
+        for (int c = 0; c < TN; c++)
+#pragma unroll
+            for (int v = 0; v < 16; v++) acc[r][c][v] = 0.0f;
 
-    load(0);
-    store(0);
+    load_a(0, 0);
+    store_a(0, 0);
+    load_a(0, 1);
+    load_b(0);
+    store_a(0, 1);
+    store_b(0);
     __syncthreads();
-    const int arow = lane % 32, koff = (lane / 32) * 8;
     for (int b = 0; b < kb; b++) {
         const int buf = b & 1;
-        if (b + 1 < kb) load(b + 1);
-        const char* sb = lds + buf * STAGE;
-        const _Float16* As = reinterpret_cast<const _Float16*>(sb);
-        const _Float16* Bs = reinterpret_cast<const _Float16*>(sb + A_BYTES);
-        h8 wh[TN][2], wl[TN][2];
+        const int bn = b + 1 < kb ? b + 1 : b;  // (at the last block: this block again, into the unused stage)
+        load_a(bn, 0);
+        load_b(bn);
+        const char* st = lds + buf * kBsStage;
+        const h8* As = reinterpret_cast<const h8*>(st);
+        const h8* Bs = reinterpret_cast<const h8*>(st + 32768);
+        const float* Sw = reinterpret_cast<const float*>(st + 49152);
+        h8 bf[TN][2];
+        float dw[TN];
 #pragma unroll
         for (int c = 0; c < TN; c++) {
-            const _Float16* q = Bs + ((wn * TN + c) * 32 + arow) * kArow + koff;
-            wh[c][0] = *reinterpret_cast<const h8*>(q);
-            wh[c][1] = *reinterpret_cast<const h8*>(q + 16);
-            wl[c][0] = *reinterpret_cast<const h8*>(q + 32);
-            wl[c][1] = *reinterpret_cast<const h8*>(q + 48);
+            const int col = (wn * TN + c) * 32 + l32;
+            bf[c][0] = Bs[g * 256 + col];
+            bf[c][1] = Bs[(2 + g) * 256 + col];
+            dw[c] = Sw[col];
         }
-        auto mfma_rows = [&](int r0, int r1) __attribute__((always_inline)) {
+        auto rows = [&](int r0, int r1) __attribute__((always_inline)) {
 #pragma unroll
             for (int r = r0; r < r1; r++) {
-                const _Float16* a = As + ((wm * TM + r) * 32 + arow) * kArow + koff;
-                const h8 ah0 = *reinterpret_cast<const h8*>(a), ah1 = *reinterpret_cast<const h8*>(a + 16);
-                const h8 al0 = *reinterpret_cast<const h8*>(a + 32), al1 = *reinterpret_cast<const h8*>(a + 48);
+                const int rt = wm * TM + r;
+                const h8 ah0 = As[((rt * 2) * 2) * 64 + lane], ah1 = As[((rt * 2) * 2 + 1) * 64 + lane];
+                const h8 al0 = As[((rt * 2 + 1) * 2) * 64 + lane], al1 = As[((rt * 2 + 1) * 2 + 1) * 64 + lane];
 #pragma unroll
                 for (int c = 0; c < TN; c++) {
-                    f16x p = acc[r][c];
-                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wh[c][0], p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, wl[c][0], p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, wh[c][0], p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wh[c][1], p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, wl[c][1], p, 0, 0, 0);
-                    p = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, wh[c][1], p, 0, 0, 0);
-                    acc[r][c] = p;
+                    f16x d = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, bf[c][0], f16x{}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah1, bf[c][1], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(al0, bf[c][0], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_32x32x16_f16(al1, bf[c][1], d, 0, 0, 0);
+#pragma unroll
+                    for (int v = 0; v < 16; v++) {
+                        acc[r][c][v] = __builtin_fmaf(d[v], dw[c], acc[r][c][v]);
+                        asm volatile("" : "+v"(acc[r][c][v]));  // (keeps the sum before the fence below)
+                    }
                 }
+                __builtin_amdgcn_sched_barrier(0);  // row tiles in order: bounds the live partial sums
             }
         };
-        // The next block's split and stores go between the two halves of
-        // this block's MFMAs (its loads have landed by then; the other LDS
-        // buffer is free since the last barrier), unconditionally, so they
-        // share a scheduling region with the MFMAs (at the last block they
-        // rewrite the unused buffer with the same block, before the barrier
-        // that precedes the epilogue's use of the LDS), and the scheduler
-        // interleaves them with the second half: per MFMA eight VALU
-        // operations, every other MFMA one LDS store.  (Measured: 31.8 ->
-        // 30.7 ms for the GPT-2-medium prefill; the same order without the
-        // interleave, 32.1 ms.)
-        mfma_rows(0, TM / 2);
-        store(buf ^ 1);
-        mfma_rows(TM / 2, TM);
-#pragma unroll
-        for (int i = 0; i < TM / 2 * TN * 6; i++) {
-            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-            __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);  // VALU
-            if (i % 2 == 1) __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-        }
+        // (the other stage is free since the last barrier)
+        rows(0, 1);
+        store_a(buf ^ 1, 0);
+        load_a(bn, 1);
+        rows(1, 3);
+        store_a(buf ^ 1, 1);
+        store_b(buf ^ 1);
+        rows(3, TM);
         __syncthreads();
     }
 
-    // Row scales and flags of this tile through LDS (one load each, not one
-    // dependent global load per output).
-    const int i0 = tile_m * BM;
+    // Row scales and flags of this tile through LDS.
     float* s_inv = reinterpret_cast<float*>(lds);
     uint8_t* s_bad = reinterpret_cast<uint8_t*>(lds + BM * 4);
-    for (int t = tid; t < BM; t += NTH) {  // rows < m_pad: the panel arrays cover them
+    for (int t = tid; t < BM; t += NTH) {  // rows < m_pad: the arrays cover them
         s_inv[t] = xinv[i0 + t];
         s_bad[t] = xbad[i0 + t];
     }
     __syncthreads();
 #pragma unroll
     for (int c = 0; c < TN; c++) {
-        const int j = j0 + (wn * TN + c) * 32 + arow;
+        const int j = j0 + (wn * TN + c) * 32 + l32;
         if (j >= n) continue;
-        const float winv = __builtin_bit_cast(
-            float, static_cast<uint32_t>(127 - (rexp[j] == kFhBadRowExp ? 0 : rexp[j])) << 23);
         const float bj = bias ? bias[j] : 0.0f;
 #pragma unroll
         for (int r = 0; r < TM; r++)
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                const int il = (wm * TM + r) * 32 + (v / 4) * 8 + (lane / 32) * 4 + (v % 4), i = i0 + il;
+                const int il = (wm * TM + r) * 32 + (v >> 2) * 8 + g * 4 + (v & 3), i = i0 + il;
                 if (i >= m) continue;
-                const float s = acc[r][c][v] * s_inv[il] * winv;
-                const float o = bias ? s + bj : s;
+                const float sv = acc[r][c][v] * s_inv[il];
+                const float o = bias ? sv + bj : sv;
                 y[static_cast<size_t>(i) * n + j] = act == FH_ACT_GELU ? gelu_unfused(o) : o;
             }
     }
-    // Rare: rows with inf/NaN activations or weight rows with a non-finite
-    // scale are rewritten with the reference's own arithmetic.
     bool flagged = false;
     for (int t = tid; t < BM || t < BN; t += NTH)
         flagged |= (t < BM && s_bad[t]) || (t < BN && j0 + t < n && rexp[j0 + t] == kFhBadRowExp);
@@ -1530,11 +1481,9 @@ __global__ void __launch_bounds__(64 * kWideWaves)
 
 namespace {
 
-// The weight-split GEMM fed straight from x: row scales first (one read of
-// x), then the GEMM, which splits the activations while staging them.
-template <int BM, int BN, int WM, int WN>
-int launch_wsplit_x(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y, int act) {
-    const size_t m_pad = (m + BM - 1) / BM * BM;
+// The block-scaled GEMM (k_gemm_bscale): row scales first, then the GEMM.
+int launch_bscale(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y, int act) {
+    const size_t m_pad = (m + 255) / 256 * 256;
     const size_t ibytes = fh_align256(m_pad * 4), fbytes = fh_align256(m_pad);
     void* ws = nullptr;
     int rc = fh_workspace(ctx, ibytes + fbytes, &ws);
@@ -1544,11 +1493,11 @@ int launch_wsplit_x(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, con
     hipLaunchKernelGGL(k_row_scales, dim3(static_cast<unsigned>((m_pad + 3) / 4)), dim3(256), 0, ctx->stream, x,
                        static_cast<int>(m), static_cast<int>(m_pad), static_cast<int>(w->k), xinv, xbad);
     FH_HIP(ctx, hipGetLastError());
-    const size_t tiles_n = (w->n + BN - 1) / BN, tiles = tiles_n * (m_pad / BM);
+    const size_t tiles_n = (w->n + 255) / 256, tiles = tiles_n * (m_pad / 256);
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
-    hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN, true>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN),
-                       0, ctx->stream, nullptr, xinv, xbad, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
-                       static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n), act);
+    hipLaunchKernelGGL(k_gemm_bscale, dim3(static_cast<unsigned>(tiles)), dim3(512), 0, ctx->stream, xinv, xbad, x,
+                       w->qs, w->d, w->rexp, bias, y, static_cast<int>(m), static_cast<int>(w->n),
+                       static_cast<int>(w->k), static_cast<int>(tiles_n), act);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }
@@ -1568,12 +1517,7 @@ int launch_gemm(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const f
     FH_HIP(ctx, hipGetLastError());
     const size_t tiles_n = (w->n + BN - 1) / BN, tiles = tiles_n * (m_pad / BM);
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
-    if constexpr (KW == 0)  // the weight-split kernel
-        hipLaunchKernelGGL((k_gemm_wsplit<BM, BN, WM, WN, false>), dim3(static_cast<unsigned>(tiles)), dim3(64 * WM * WN), 0,
-                           ctx->stream, panel, xinv, xbad, x, w->qs, w->d, w->rexp, bias, y, static_cast<int>(m),
-                           static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n), FH_ACT_NONE);
-    else
-        hipLaunchKernelGGL((k_gemm_mfma<BM, BN, WM, WN, KW>), dim3(static_cast<unsigned>(tiles)),
+    hipLaunchKernelGGL((k_gemm_mfma<BM, BN, WM, WN, KW>), dim3(static_cast<unsigned>(tiles)),
                            dim3(64 * WM * WN * KW), 0, ctx->stream, panel, xinv, x, w->qs, w->d, w->rexp, bias, y,
                            static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k),
                            static_cast<int>(tiles_n));
@@ -1809,7 +1753,7 @@ int fh_launch_skinny_scratch(fh_ctx* ctx, const fh_q8_0* w, const float* x, size
 }
 
 // Tile choice: m <= 64 takes the skinny kernel; otherwise the 256 x 256
-// weight-split tile (eight waves) once it still yields a tile per CU, the 128 x 128 tile at two
+// block-scaled tile (eight waves) once it still yields a tile per CU, the 128 x 128 tile at two
 // tiles per CU, else 64 x 64, else 32 x 32 outputs with four waves splitting K.
 int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
                          int act) {
@@ -1817,7 +1761,7 @@ int fh_launch_gemm_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m
     if (m <= 64) return launch_skinny(ctx, w, x, m, bias, y, nullptr, act);  // GELU in its epilogue
     int rc;
     if (((m + 255) / 256) * ((w->n + 255) / 256) >= cus)
-        return launch_wsplit_x<256, 256, 2, 4>(ctx, w, x, m, bias, y, act);  // GELU in its epilogue
+        return launch_bscale(ctx, w, x, m, bias, y, act);  // GELU in its epilogue
     else if (((m + 127) / 128) * ((w->n + 127) / 128) >= 2 * cus) rc = launch_gemm<128, 128, 2, 2, 1>(ctx, w, x, m, bias, y);
     else if (((m + 63) / 64) * ((w->n + 63) / 64) >= 2 * cus) rc = launch_gemm<64, 64, 2, 2, 1>(ctx, w, x, m, bias, y);
     else rc = launch_gemm<32, 32, 1, 1, 4>(ctx, w, x, m, bias, y);

@@ -85,9 +85,9 @@ struct fh_q8_0 {
     uint16_t* d = nullptr;
     // Per row j, e_j with 127 * max_b |d_jb| * 2^e_j in [2^14, 2^15) (0 for a
     // row without non-zero scales, kFhBadRowExp for a row with a non-finite
-    // scale): the large-m GEMM splits 2^e_j * d * q exactly into two f16
-    // terms, and every GEMM recomputes the flagged rows' outputs exactly.
-    // Derived from d at upload.
+    // scale): every GEMM recomputes the flagged rows' outputs exactly (the
+    // kernels read only the flag; e_j is the exponent an exact two-term f16
+    // split of 2^e_j * d * q would take).  Derived from d at upload.
     int8_t* rexp = nullptr;
     void* base = nullptr;  // the one allocation holding all planes
 };

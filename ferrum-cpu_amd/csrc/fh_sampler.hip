@@ -212,7 +212,6 @@ __device__ __forceinline__ float block_exclusive_scan(Shared& s, float v, float*
 // base + t + j * kT < n, j < ITEMS (n is the end of the ids held here).
 template <int ITEMS>
 struct RegRow {
-    static constexpr bool kRegs = true;
     float v[ITEMS];
     int n;
     int base = 0;
@@ -244,7 +243,6 @@ struct RegRow {
 // Global-buffer row for vocabularies beyond the register file: same id-to-thread
 // mapping, streamed eight ids per thread at a time.
 struct GlobalRow {
-    static constexpr bool kRegs = false;
     static constexpr int U = 8;
     float* w;
     int n;

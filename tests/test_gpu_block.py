@@ -273,7 +273,7 @@ def test_linear_with_gelu_equals_linear_then_gelu(fh, orc, m, n, k):
 
 
 def test_prefill_gemm_gelu_equals_gemm_then_gelu(fh, orc):
-    """At prefill depth (the weight-split MFMA GEMM, one tile per CU or more)
+    """At prefill depth (the block-scaled MFMA GEMM, one tile per CU or more)
     GELU runs in the GEMM's epilogue: bit for bit the GEMM followed by the
     GELU kernel, including the rows recomputed by the reference's own
     arithmetic (a weight row with an infinite block scale, an activation row

@@ -353,9 +353,10 @@ def test_gemm_propagates_inf_and_nan_like_the_reference(fh, orc):
 @pytest.mark.parametrize("m,n,k", [(4096, 4096, 64), (4100, 4095, 96), (4096, 4352, 128), (4000, 4100, 256),
                                    (4352, 4096, 192)])
 def test_gemm_weight_split_tiles_match(fh, orc, m, n, k):
-    """Shapes with >= 256 tiles of 256 x 256 take the kernel that folds the
-    block scales into an exact two-term f16 weight split (2 to 8 Q8_0 blocks
-    per row, ragged m and n); against the float64 product of the same weights
+    """Shapes with >= 256 tiles of 256 x 256 take the block-scaled kernel
+    (quants as the f16 weight operand, the activation as two f16 terms, one
+    FMA per output and block for the block scale; 2 to 8 Q8_0 blocks per row,
+    ragged m and n); against the float64 product of the same weights
     (finite rows) and against the oracle on rows with special values.  Weight
     rows of very different scale share tiles."""
     import ferrum_hip
@@ -401,7 +402,7 @@ def test_config4_prefill_at_its_own_depth(fh, orc, n, k):
     m = 16,384 activation rows through each layer shape (QKV 3072 x 1024, out
     1024 x 1024, up 4096 x 1024, down 1024 x 4096; ops.rs:233-256 reached
     through layer/transformer.rs:352-354 at m = B * ctx).  These run the
-    weight-split 256 x 256 MFMA kernel over 32 and 128 Q8_0 blocks of K, its
+    block-scaled 256 x 256 MFMA kernel over 32 and 128 Q8_0 blocks of K, its
     whole double-buffered K loop and epilogue.  N(0, 0.02) weights and N(0, 1)
     activations as the config draws them; a seeded sample of 265 rows against
     the oracle and against the float64 product."""
@@ -425,7 +426,7 @@ def test_non_finite_block_scales_match_the_reference(fh, orc, m, n, k):
     """GGUF block scales of inf or NaN (f16 0x7C00 / 0x7E00), with zero and
     non-zero quants in the block: inf * 0 = NaN and inf * q = +-inf per weight,
     as the reference's f32 expansion has it.  Every path (GEMV, skinny, tiled,
-    weight-split) must reproduce the inf/NaN pattern and the finite values."""
+    block-scaled) must reproduce the inf/NaN pattern and the finite values."""
     import ferrum_hip
 
     raw = orc.quantize_weight(n, k, 77 + m, 0.05).reshape(n, k // 32, 34).copy()
