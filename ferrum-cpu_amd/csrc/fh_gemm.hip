@@ -433,13 +433,18 @@ __global__ void __launch_bounds__(64 * WM * WN * KW)
 // with inf/NaN activations and weight rows with a non-finite scale are
 // recomputed with the reference's own arithmetic (exact_tile).
 // Workgroup tile 256 x 256, eight waves of 128 x 64 (4 x 2 tiles), one Q8_0
-// block per stage, two stages of 49 KiB: the activations as [row tile][term
+// block per stage, two stages of 51 KiB: the activations as [row tile][term
 // h|l][MFMA half][lane] (16-byte fragments: lane g * 32 + r holds row r's
 // elements 16 g + 8 half .. + 7), the quants as [MFMA half][lane half]
 // [column] and the 256 columns' block scales.  Block b + 1 is loaded into
 // registers while block b's MFMAs run and is split and stored into the other
 // stage between their two halves.
-constexpr int kBsStage = 32 * 1024 + 16 * 1024 + 256 * 4;
+// (each 16-byte-fragment plane is padded by 64 bytes: the two lanes of a
+// staging pair write the same slot of neighbouring planes, which then fall on
+// different banks)
+constexpr int kBsAPlane = 68, kBsBPlane = 260;  // 16-byte entries
+constexpr int kBsAOff = 0, kBsBOff = 32 * kBsAPlane * 16, kBsSOff = kBsBOff + 4 * kBsBPlane * 16;
+constexpr int kBsStage = kBsSOff + 256 * 4;
 
 __global__ void __launch_bounds__(512)
     k_gemm_bscale(const float* __restrict__ xinv, const uint8_t* __restrict__ xbad, const float* __restrict__ x,
@@ -478,7 +483,7 @@ __global__ void __launch_bounds__(512)
         if (scale_loader) rd = dsrc[b];
     };
     auto store_a = [&](int buf, int s2) __attribute__((always_inline)) {
-        uint4* As = reinterpret_cast<uint4*>(lds + buf * kBsStage);
+        uint4* As = reinterpret_cast<uint4*>(lds + buf * kBsStage + kBsAOff);
         uint32_t hw[4], lw[4];
 #pragma unroll
         for (int p2 = 0; p2 < 2; p2++) {
@@ -494,17 +499,17 @@ __global__ void __launch_bounds__(512)
             lw[2 * p2 + 1] = __builtin_bit_cast(uint32_t, __builtin_convertvector(r23, h2));
         }
         const int frag = s2 * 32 + ar;  // lane g * 32 + r of the fragment
-        As[((wave * 2) * 2 + ahf) * 64 + frag] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-        As[((wave * 2 + 1) * 2 + ahf) * 64 + frag] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+        As[((wave * 2) * 2 + ahf) * kBsAPlane + frag] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+        As[((wave * 2 + 1) * 2 + ahf) * kBsAPlane + frag] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
     };
     auto store_b = [&](int buf) __attribute__((always_inline)) {
         char* st = lds + buf * kBsStage;
-        uint4* Bs = reinterpret_cast<uint4*>(st + 32768);
+        uint4* Bs = reinterpret_cast<uint4*>(st + kBsBOff);
         const uint2 q0 = quants_to_f16(rb[0]), q1 = quants_to_f16(rb[1]), q2 = quants_to_f16(rb[2]),
                     q3 = quants_to_f16(rb[3]);
-        Bs[bhalf * 256 + bcol] = make_uint4(q0.x, q0.y, q1.x, q1.y);
-        Bs[(2 + bhalf) * 256 + bcol] = make_uint4(q2.x, q2.y, q3.x, q3.y);
-        if (scale_loader) reinterpret_cast<float*>(st + 49152)[tid] = fh_h2f(rd);
+        Bs[bhalf * kBsBPlane + bcol] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        Bs[(2 + bhalf) * kBsBPlane + bcol] = make_uint4(q2.x, q2.y, q3.x, q3.y);
+        if (scale_loader) reinterpret_cast<float*>(st + kBsSOff)[tid] = fh_h2f(rd);
     };
     float acc[TM][TN][16];
 #pragma unroll
@@ -527,24 +532,25 @@ __global__ void __launch_bounds__(512)
         load_a(bn, 0);
         load_b(bn);
         const char* st = lds + buf * kBsStage;
-        const h8* As = reinterpret_cast<const h8*>(st);
-        const h8* Bs = reinterpret_cast<const h8*>(st + 32768);
-        const float* Sw = reinterpret_cast<const float*>(st + 49152);
+        const h8* As = reinterpret_cast<const h8*>(st + kBsAOff);
+        const h8* Bs = reinterpret_cast<const h8*>(st + kBsBOff);
+        const float* Sw = reinterpret_cast<const float*>(st + kBsSOff);
         h8 bf[TN][2];
         float dw[TN];
 #pragma unroll
         for (int c = 0; c < TN; c++) {
             const int col = (wn * TN + c) * 32 + l32;
-            bf[c][0] = Bs[g * 256 + col];
-            bf[c][1] = Bs[(2 + g) * 256 + col];
+            bf[c][0] = Bs[g * kBsBPlane + col];
+            bf[c][1] = Bs[(2 + g) * kBsBPlane + col];
             dw[c] = Sw[col];
         }
         auto rows = [&](int r0, int r1) __attribute__((always_inline)) {
 #pragma unroll
             for (int r = r0; r < r1; r++) {
                 const int rt = wm * TM + r;
-                const h8 ah0 = As[((rt * 2) * 2) * 64 + lane], ah1 = As[((rt * 2) * 2 + 1) * 64 + lane];
-                const h8 al0 = As[((rt * 2 + 1) * 2) * 64 + lane], al1 = As[((rt * 2 + 1) * 2 + 1) * 64 + lane];
+                const h8 ah0 = As[((rt * 2) * 2) * kBsAPlane + lane], ah1 = As[((rt * 2) * 2 + 1) * kBsAPlane + lane];
+                const h8 al0 = As[((rt * 2 + 1) * 2) * kBsAPlane + lane],
+                         al1 = As[((rt * 2 + 1) * 2 + 1) * kBsAPlane + lane];
 #pragma unroll
                 for (int c = 0; c < TN; c++) {
                     f16x d = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah0, bf[c][0], f16x{}, 0, 0, 0);
@@ -721,7 +727,7 @@ __global__ void __launch_bounds__(256)
 //    in the scalar product, and a zero's sign cannot reach a sum that
 //    starts at +0.
 // Then acc = acc + dot * dd with the product and the sum rounded separately,
-// in ascending b, as the reference does.  A stage (34 KiB): the eight 32-row
+// in ascending b, as the reference does.  A stage (35 KiB): the eight 32-row
 // activation fragments as [row tile][MFMA half][lane] (the panel is in MFMA
 // lane order already), the 256 weight half-rows as [MFMA half][lane half]
 // [column] (a fragment read is 32 consecutive 16-byte pieces), the rows'
@@ -731,7 +737,9 @@ __global__ void __launch_bounds__(256)
 // Workgroups are dealt to XCDs in contiguous runs of tiles.  The panel covers
 // whole 256-row tiles.
 constexpr int kW8Rows = 256, kW8Cols = 256, kW8Threads = 512;
-constexpr int kW8StageBytes = 16 * 1024 + 16 * 1024 + 256 * 4 + 256 * 4;
+constexpr int kW8BPlane = 260;  // 16-byte entries (padded: see the block-scaled kernel)
+constexpr int kW8BOff = 16 * 1024, kW8SOff = kW8BOff + 4 * kW8BPlane * 16;
+constexpr int kW8StageBytes = kW8SOff + 256 * 4 + 256 * 4;
 constexpr size_t kW8LdsMinRows = 1024;  // m from which W8A8 takes the staged kernel
 
 __global__ void __launch_bounds__(kW8Threads)
@@ -774,15 +782,15 @@ __global__ void __launch_bounds__(kW8Threads)
     auto store = [&](int buf) __attribute__((always_inline)) {
         char* st = lds + buf * kW8StageBytes;
         uint4* As = reinterpret_cast<uint4*>(st);
-        uint4* Bs = reinterpret_cast<uint4*>(st + 16384);
+        uint4* Bs = reinterpret_cast<uint4*>(st + kW8BOff);
         uint2 q0 = quants_to_f16(ra.x), q1 = quants_to_f16(ra.y), q2 = quants_to_f16(ra.z), q3 = quants_to_f16(ra.w);
         As[(art * 2) * 64 + alane] = make_uint4(q0.x, q0.y, q1.x, q1.y);
         As[(art * 2 + 1) * 64 + alane] = make_uint4(q2.x, q2.y, q3.x, q3.y);
         q0 = quants_to_f16(rb.x), q1 = quants_to_f16(rb.y), q2 = quants_to_f16(rb.z), q3 = quants_to_f16(rb.w);
-        Bs[bhalf * 256 + bcol] = make_uint4(q0.x, q0.y, q1.x, q1.y);
-        Bs[(2 + bhalf) * 256 + bcol] = make_uint4(q2.x, q2.y, q3.x, q3.y);
+        Bs[bhalf * kW8BPlane + bcol] = make_uint4(q0.x, q0.y, q1.x, q1.y);
+        Bs[(2 + bhalf) * kW8BPlane + bcol] = make_uint4(q2.x, q2.y, q3.x, q3.y);
         // [0, 256): row scales, [256, 512): weight scales
-        reinterpret_cast<float*>(st + 32768)[tid] =
+        reinterpret_cast<float*>(st + kW8SOff)[tid] =
             row_scale ? __builtin_bit_cast(float, rs) : fh_h2f(static_cast<uint16_t>(rs));
     };
     float acc[TM][TN][16];
@@ -801,14 +809,14 @@ __global__ void __launch_bounds__(kW8Threads)
         if (b + 1 < kb) load(b + 1);
         const char* st = lds + buf * kW8StageBytes;
         const h8* As = reinterpret_cast<const h8*>(st);
-        const h8* Bs = reinterpret_cast<const h8*>(st + 16384);
-        const float* Ss = reinterpret_cast<const float*>(st + 32768);
+        const h8* Bs = reinterpret_cast<const h8*>(st + kW8BOff);
+        const float* Ss = reinterpret_cast<const float*>(st + kW8SOff);
         h8 bf[TN][2];
 #pragma unroll
         for (int c = 0; c < TN; c++) {
             const int col = (wn * TN + c) * 32 + l32;
-            bf[c][0] = Bs[g * 256 + col];
-            bf[c][1] = Bs[(2 + g) * 256 + col];
+            bf[c][0] = Bs[g * kW8BPlane + col];
+            bf[c][1] = Bs[(2 + g) * kW8BPlane + col];
         }
         const float dw = Ss[256 + wn * 64 + lane];  // lane half c: column tile c of this wave
         auto rows = [&](int r0, int r1) __attribute__((always_inline)) {
