@@ -391,11 +391,11 @@ void fh_q8_0_free(fh_q8_0* w) {
 static int check_linear(fh_ctx* ctx, const fh_q8_0* w, size_t k, const void* bias, size_t bias_len,
                         int numerics) {
     if (!w) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight is NULL");
-    if (numerics != FH_W8A32 && numerics != FH_W8A8 && numerics != FH_W8A32_EXACT)
+    if (numerics != FH_W8A32 && numerics != FH_W8A8 && numerics != FH_W8A32_EXACT && numerics != FH_W8A8_FAST)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: unknown numerics " + std::to_string(numerics));
     if (w->device != ctx->device)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight lives on another device");
-    if (w->kind == FH_WEIGHT_F32 && numerics == FH_W8A8)
+    if (w->kind == FH_WEIGHT_F32 && (numerics == FH_W8A8 || numerics == FH_W8A8_FAST))
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: FH_W8A8 needs a Q8_0 weight (this one is F32)");
     if (k != w->k)
         return fh_fail(ctx, FH_ERR_DIM, "linear_forward: input width " + std::to_string(k) +
@@ -414,8 +414,9 @@ static int launch_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m
                          int numerics, int act = FH_ACT_NONE) {
     if (w->kind == FH_WEIGHT_F32) numerics = FH_W8A32_EXACT;
     if (numerics == FH_W8A32) return fh_launch_linear_w8a32(ctx, w, x, m, bias, y, act);
-    int rc = numerics == FH_W8A8 ? fh_launch_linear_w8a8(ctx, w, x, m, bias, y)
-                                 : fh_launch_linear_exact(ctx, w, x, m, bias, y);
+    int rc = numerics == FH_W8A8 || numerics == FH_W8A8_FAST
+                 ? fh_launch_linear_w8a8(ctx, w, x, m, bias, y, numerics == FH_W8A8_FAST)
+                 : fh_launch_linear_exact(ctx, w, x, m, bias, y);
     if (rc == FH_OK && act == FH_ACT_GELU) rc = fh_launch_gelu(ctx, y, m * w->n);
     return rc;
 }

@@ -620,7 +620,7 @@ __global__ void __launch_bounds__(512)
 // (fh_k_encode_panel) in MFMA lane order, 1 KiB contiguous per fragment; the
 // weight rows 16 bytes per lane.  The next block's operands are loaded while
 // the current one is finished.
-template <int TM>
+template <int TM, bool FAST>
 __global__ void __launch_bounds__(256)
     k_gemm_w8a8(const uint4* __restrict__ qp, const float* __restrict__ dp, const int8_t* __restrict__ qs,
                 const uint16_t* __restrict__ dsc, const float* __restrict__ bias, float* __restrict__ y, int m, int n,
@@ -680,7 +680,8 @@ __global__ void __launch_bounds__(256)
                 for (int v = 0; v < 16; v++) {
                     // acc row (v / 4) * 8 + g * 4 + v % 4: its scale is dx[v / 4][v % 4]
                     const float dd = dw * o.dx[r][v >> 2][v & 3];
-                    acc[r][c][v] = acc[r][c][v] + static_cast<float>(d[v]) * dd;
+                    if (FAST) acc[r][c][v] = __builtin_fmaf(static_cast<float>(d[v]), dd, acc[r][c][v]);
+                    else acc[r][c][v] = acc[r][c][v] + static_cast<float>(d[v]) * dd;
                 }
             }
         }
@@ -742,6 +743,7 @@ constexpr int kW8BOff = 16 * 1024, kW8SOff = kW8BOff + 4 * kW8BPlane * 16;
 constexpr int kW8StageBytes = kW8SOff + 256 * 4 + 256 * 4;
 constexpr size_t kW8LdsMinRows = 1024;  // m from which W8A8 takes the staged kernel
 
+template <bool FAST>
 __global__ void __launch_bounds__(kW8Threads)
     k_gemm_w8a8_lds(const uint4* __restrict__ qp, const float* __restrict__ dp, const int8_t* __restrict__ qs,
                     const uint16_t* __restrict__ dsc, const float* __restrict__ bias, float* __restrict__ y, int m,
@@ -832,7 +834,10 @@ __global__ void __launch_bounds__(kW8Threads)
                     f16x d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a0, bf[c][0], f16x{}, 0, 0, 0);
                     d = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, bf[c][1], d, 0, 0, 0);
 #pragma unroll
-                    for (int v = 0; v < 16; v++) acc[r][c][v] = acc[r][c][v] + d[v] * dd[c * 16 + v];
+                    for (int v = 0; v < 16; v++) {
+                        if (FAST) acc[r][c][v] = __builtin_fmaf(d[v], dd[c * 16 + v], acc[r][c][v]);
+                        else acc[r][c][v] = acc[r][c][v] + d[v] * dd[c * 16 + v];
+                    }
                 }
             }
         };
@@ -1698,7 +1703,8 @@ __global__ void fh_k_encode_panel(const float* __restrict__ x, int m, int m_pad,
 
 // W8A8 through the int8 matrix cores: the activations are encoded into the
 // lane-order panel, then one wave per (32 TM) x 64 output tile.
-int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                        bool fast) {
     // (a prompt's m takes the LDS-staged kernel: its panel covers whole 256-row tiles)
     const bool staged = m >= kW8LdsMinRows;
     const int tm_rows = staged ? kW8Rows : m >= 64 ? 64 : 32;
@@ -1721,23 +1727,27 @@ int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
     if (staged) {
         const size_t tn = (w->n + kW8Cols - 1) / kW8Cols, tl = tn * (m_pad / kW8Rows);
         if (tl > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
-        hipLaunchKernelGGL(k_gemm_w8a8_lds, dim3(static_cast<unsigned>(tl)), dim3(kW8Threads), 0, ctx->stream, qp,
-                           dp, w->qs, w->d, bias, y, static_cast<int>(m), static_cast<int>(w->n),
-                           static_cast<int>(w->k), static_cast<int>(tn));
+        if (fast)
+            hipLaunchKernelGGL(k_gemm_w8a8_lds<true>, dim3(static_cast<unsigned>(tl)), dim3(kW8Threads), 0,
+                               ctx->stream, qp, dp, w->qs, w->d, bias, y, static_cast<int>(m),
+                               static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tn));
+        else
+            hipLaunchKernelGGL(k_gemm_w8a8_lds<false>, dim3(static_cast<unsigned>(tl)), dim3(kW8Threads), 0,
+                               ctx->stream, qp, dp, w->qs, w->d, bias, y, static_cast<int>(m),
+                               static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tn));
         FH_HIP(ctx, hipGetLastError());
         return FH_OK;
     }
     const size_t tiles_n = (w->n + 63) / 64, tiles = tiles_n * (m_pad / tm_rows);
     if (tiles > 0x7FFFFFFFu) return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: output above 2^31 tiles");
     const dim3 grid(static_cast<unsigned>((tiles + 3) / 4)), block(256);
-    if (tm_rows == 64)
-        hipLaunchKernelGGL(k_gemm_w8a8<2>, grid, block, 0, ctx->stream, qp, dp, w->qs, w->d, bias, y,
-                           static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k),
-                           static_cast<int>(tiles_n), static_cast<int>(tiles));
-    else
-        hipLaunchKernelGGL(k_gemm_w8a8<1>, grid, block, 0, ctx->stream, qp, dp, w->qs, w->d, bias, y,
-                           static_cast<int>(m), static_cast<int>(w->n), static_cast<int>(w->k),
-                           static_cast<int>(tiles_n), static_cast<int>(tiles));
+    auto go = [&](auto kern) {
+        hipLaunchKernelGGL(kern, grid, block, 0, ctx->stream, qp, dp, w->qs, w->d, bias, y, static_cast<int>(m),
+                           static_cast<int>(w->n), static_cast<int>(w->k), static_cast<int>(tiles_n),
+                           static_cast<int>(tiles));
+    };
+    if (tm_rows == 64) fast ? go(k_gemm_w8a8<2, true>) : go(k_gemm_w8a8<2, false>);
+    else fast ? go(k_gemm_w8a8<1, true>) : go(k_gemm_w8a8<1, false>);
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
 }

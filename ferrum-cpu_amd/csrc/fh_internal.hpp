@@ -172,10 +172,11 @@ struct fh_scratch {
 // the shape needs more than scratch.bytes.
 int fh_launch_skinny_scratch(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
                              const fh_scratch& scratch);
+// W8A8 (fast: FH_W8A8_FAST, each block term fused into the sum by one FMA).
 int fh_launch_gemm_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
-                        const float* bias, float* y);
+                        const float* bias, float* y, bool fast);
 int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m,
-                          const float* bias, float* y);
+                          const float* bias, float* y, bool fast);
 // FH_W8A32_EXACT: ferrum_core's sequential sums, bit for bit (no K split).
 int fh_launch_linear_exact(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y);
 int fh_launch_encode(fh_ctx* ctx, const float* x, size_t n, uint8_t* out);

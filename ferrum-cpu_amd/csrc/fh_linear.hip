@@ -449,14 +449,17 @@ int fh_launch_linear_ln_w8a32(fh_ctx* ctx, const fh_q8_0* w, const float* x, siz
     return fh_launch_linear_w8a32(ctx, w, static_cast<float*>(h), m, bias, y, act);
 }
 
-int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y) {
+// (fast: the matrix-core kernels fuse each block term into the sum; the
+// block-parallel kernel below sums blocks in parallel in either mode)
+int fh_launch_linear_w8a8(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, const float* bias, float* y,
+                          bool fast) {
     if (reinterpret_cast<uintptr_t>(x) & 3)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: x must be 4-byte aligned");
     if (w->n > 0x7FFFFFFFu || w->k > 0x7FFFFFFFu || m * w->n > 0x7FFFFFFFu * size_t(64))
         return fh_fail(ctx, FH_ERR_LIMIT, "fh_q8_0_linear: problem too large for the W8A8 kernel");
     const size_t tile_rows = m >= 64 ? 64 : 32;
     if (m >= 32 && (m + tile_rows - 1) / tile_rows * ((w->n + 63) / 64) >= kW8a8MfmaTiles)
-        return fh_launch_gemm_w8a8(ctx, w, x, m, bias, y);
+        return fh_launch_gemm_w8a8(ctx, w, x, m, bias, y, fast);
     const size_t kb = w->k / 32;
     const size_t qbytes = fh_align256(m * w->k), dbytes = fh_align256(m * kb * 2);
     void* ws = nullptr;

@@ -58,7 +58,7 @@ extern "C" int fh_q8_0_linear_noalloc_async(fh_ctx* ctx, const fh_q8_0* w, const
     if (!ctx) return FH_ERR_INVALID;
     ctx->err.clear();
     if (!w) return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight is NULL");
-    if (numerics != FH_W8A32 && numerics != FH_W8A8 && numerics != FH_W8A32_EXACT)
+    if (numerics != FH_W8A32 && numerics != FH_W8A8 && numerics != FH_W8A32_EXACT && numerics != FH_W8A8_FAST)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: unknown numerics " + std::to_string(numerics));
     if (w->device != ctx->device)
         return fh_fail(ctx, FH_ERR_INVALID, "fh_q8_0_linear: weight lives on another device");

@@ -34,7 +34,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "lib", "libferrum_hip.so")
 
 FH_OK, FH_ERR_DIM, FH_ERR_INVALID, FH_ERR_OOM, FH_ERR_HIP, FH_ERR_LIMIT, FH_ERR_FORMAT, FH_ERR_EXCHANGE = range(8)
-W8A32, W8A8, W8A32_EXACT = 0, 1, 2
+W8A32, W8A8, W8A32_EXACT, W8A8_FAST = 0, 1, 2, 3  # FH_W8A32 ... (W8A8_FAST: W8A8 with each block term fused, 1e-5)
 LOGITS_RAW, LOGITS_GPT2_SOFTMAX = 0, 1
 RECENT_RANGES = 0x100  # OR'd into the logits kind: recent offsets as (begin, end) pairs per row
 

@@ -94,6 +94,7 @@ pub mod sys {
     pub const FH_W8A32: c_int = 0;
     pub const FH_W8A8: c_int = 1;
     pub const FH_W8A32_EXACT: c_int = 2;
+    pub const FH_W8A8_FAST: c_int = 3;
     pub const FH_LOGITS_RAW: c_int = 0;
     pub const FH_LOGITS_GPT2_SOFTMAX: c_int = 1;
     pub const FH_RECENT_RANGES: c_int = 0x100;
@@ -237,6 +238,9 @@ pub enum Numerics {
     W8A8,
     /// ferrum_core's sums bit for bit (ascending k, no FMA, bias last).
     W8A32Exact,
+    /// `W8A8` with each block's term fused into the sum (one rounding),
+    /// within the 1e-5 rule of `W8A8`'s outputs: the prefill speed mode.
+    W8A8Fast,
 }
 
 /// The drop-in default is the bit-exact mode: `ops::linear_forward`'s bits on
@@ -255,6 +259,7 @@ impl Numerics {
             Numerics::W8A32 => sys::FH_W8A32,
             Numerics::W8A8 => sys::FH_W8A8,
             Numerics::W8A32Exact => sys::FH_W8A32_EXACT,
+            Numerics::W8A8Fast => sys::FH_W8A8_FAST,
         }
     }
 }

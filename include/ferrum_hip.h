@@ -80,8 +80,14 @@ enum {
  *            in ascending k, every product and add rounded (no FMA), then
  *            + bias (ops.rs:29-148, 233-256) — the contract the reference's
  *            roadmap names q8_0_packed_forward_equals_expanded.  K is never
- *            split, so it runs at a fraction of FH_W8A32's speed; opt-in. */
-enum { FH_W8A32 = 0, FH_W8A8 = 1, FH_W8A32_EXACT = 2 };
+ *            split, so it runs at a fraction of FH_W8A32's speed; opt-in.
+ *  FH_W8A8_FAST: FH_W8A8's quantisation and exact int32 block dots, with each
+ *            block's term fused into the running sum (one rounding for
+ *            f32(dot_b) * (d_w * d_x) + s instead of two): within 1e-5 of
+ *            FH_W8A8's outputs (componentwise, relative to the sum of the
+ *            terms' magnitudes), not bit-identical to them.  The prefill
+ *            speed mode of the W8A8 semantics; no reference counterpart. */
+enum { FH_W8A32 = 0, FH_W8A8 = 1, FH_W8A32_EXACT = 2, FH_W8A8_FAST = 3 };
 
 /* What fh_sample_* receives in `logits`.
  *  FH_LOGITS_RAW:          the sampler input itself (the Llama/Qwen path,
@@ -167,7 +173,7 @@ void fh_q8_0_free(fh_q8_0* w);
  * bias_len 0) on a Q8_0-backed Linear (layer/linear.rs:191-194).
  * k != W's k, or bias_len not in {0 (with bias NULL), n} -> FH_ERR_DIM, with the
  * reference's message.  m == 0 is a valid empty call.  numerics: FH_W8A32,
- * FH_W8A8 or FH_W8A32_EXACT.  Host pointers; blocks until y is written. */
+ * FH_W8A8, FH_W8A32_EXACT or FH_W8A8_FAST.  Host pointers; blocks until y is written. */
 int fh_q8_0_linear(fh_ctx* ctx, const fh_q8_0* w, const float* x, size_t m, size_t k,
                    const float* bias, size_t bias_len, float* y, int numerics);
 /* Device-pointer form of fh_q8_0_linear, enqueued on the context stream. */

@@ -66,3 +66,16 @@ def test_sampling_params_layout_matches_the_header():
     assert ctypes.sizeof(ferrum_hip.SamplingParams) == 16
     p = ferrum_hip.SamplingParams(0.8, 40, 0.95, 1.1)
     assert (p.top_k, round(p.temperature, 6)) == (40, 0.8)
+
+
+def test_numerics_constants_match_the_header():
+    """The Python and Rust numerics codes are the header's enum."""
+    import ferrum_hip
+
+    text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    enum = dict((k, int(v)) for k, v in re.findall(r"\bFH_(W8A32_EXACT|W8A8_FAST|W8A32|W8A8)\s*=\s*(\d+)", text))
+    assert enum == {"W8A32": ferrum_hip.W8A32, "W8A8": ferrum_hip.W8A8, "W8A32_EXACT": ferrum_hip.W8A32_EXACT,
+                    "W8A8_FAST": ferrum_hip.W8A8_FAST}
+    rust = open(os.path.join(ROOT, "ferrum-cpu_amd", "rust", "ferrum_hip", "src", "lib.rs")).read()
+    for name, code in enum.items():
+        assert re.search(rf"pub const FH_{name}: c_int = {code};", rust), name

@@ -574,6 +574,40 @@ def test_w8a8_takes_rows_at_a_4_byte_offset(fh, orc, m, n, k):
     assert np.array_equal(dy.cpu().numpy(), orc.q8_0_linear_w8a8(x, raw, n, None), equal_nan=True)
 
 
+@pytest.mark.parametrize("m,n,k,has_bias", [(64, 6144, 64, True), (257, 2304, 768, False), (1030, 700, 96, True),
+                                            (2048, 512, 1024, False), (40, 300, 96, True)])
+def test_w8a8_fast_is_within_the_rule_of_w8a8(fh, orc, m, n, k, has_bias):
+    """FH_W8A8_FAST: FH_W8A8's quantisation and exact block dots with each
+    block's term fused into the sum (one FMA): within 1e-5 of the reference's
+    W8A8 outputs relative to the magnitudes of the block terms summed, the same
+    inf/NaN pattern, and at least as accurate as W8A8 against the float64 sum
+    of the same terms.  The matrix-core kernel (from 96 output tiles), the
+    staged one (m >= 1024) and the block-parallel kernel (below 96 tiles)."""
+    import ferrum_hip
+
+    raw = weight(orc, n, k, 5 * m + n + k)
+    x = acts(m, k, m + 5)
+    x[1, 5] = np.inf
+    x[2, :] = 0.0
+    x[m - 1, k - 1] = np.nan
+    b = bias_for(n, k) if has_bias else None
+    w = ferrum_hip.Q8_0Weight.upload(fh, raw, n, k)
+    got = ferrum_hip.linear_forward(fh, x, w, b, numerics=ferrum_hip.W8A8_FAST)
+    w.free()
+    ref = orc.q8_0_linear_w8a8(x, raw, n, b)
+    assert np.array_equal(np.isnan(got), np.isnan(ref))
+    assert np.array_equal(np.isposinf(got), np.isposinf(ref)) and np.array_equal(np.isneginf(got), np.isneginf(ref))
+    d16, q = orc.q8_0_quantize_rows(x)
+    xq = (q.astype(np.float64).reshape(m, k // 32, 32)
+          * d16.view(np.float16).astype(np.float64)[:, :, None]).reshape(m, k)
+    wf = orc.q8_0_to_ferrum_weight(raw, n, k).astype(np.float64)
+    fin = np.isfinite(ref).all(axis=1)
+    mass = np.abs(xq[fin]) @ np.abs(wf)
+    assert_close(got[fin], ref[fin], mass)
+    exact = xq[fin] @ wf + (0.0 if b is None else b.astype(np.float64))
+    assert_as_accurate(got[fin], ref[fin], exact)
+
+
 def test_int32_block_dots_are_bit_exact(fh, orc):
     import torch
 
