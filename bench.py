@@ -854,6 +854,13 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
             "frac_i8_dense_peak": round(tflops / I8_DENSE_TOPS, 4),
             "mfma_f16_tflops": round(2 * tflops, 1), "mfma_frac_f16_dense_peak": round(2 * tflops / F16_DENSE_TFLOPS, 4),
             "library_f16_same_accuracy_ms": round(lib_ms, 3), "vs_library": round(lib_ms / ms, 3),
+            "roofline": {"bound": "mfma", "achieved": round(2 * tflops, 1), "peak": F16_DENSE_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(2 * tflops / F16_DENSE_TFLOPS, 4), "traffic": None,
+                         "kernel": "k_gemm_bscale (+ k_row_scales): f16 MFMA work of two f16 products per "
+                                   "activation-weight pair (the h and l terms against the quants), per step of "
+                                   "the 96 linears",
+                         "note": "the per-block FMA step bounds it with the MFMA work: MFMA busy 34 % "
+                                 "(profiles/prefill_gemm_gpt2_medium_kernels.md)"},
             "config4_run": config4, "prompt_attention": prompt_attention,
             "decode_b32": {"ms_per_step": round(dms, 4), "tok_s": round(B32 * 1000.0 / dms, 1),
                            "weight_bytes": dbytes, "weight_GBps": round(dbytes / (dms * 1e-3) / 1e9, 1),
@@ -861,7 +868,13 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
                                    "unchained inputs"},
             "w8a8_int8_mfma": {"ms": round(ms8, 3), "tops": round(tops8, 1),
                                "frac_i8_dense_peak": round(tops8 / I8_DENSE_TOPS, 4),
-                               "numerics": "W8A8 (activations re-quantised to Q8_0), bit-exact with the reference"},
+                               "numerics": "W8A8 (activations re-quantised to Q8_0), bit-exact with the reference",
+                               "roofline": {"bound": "mfma", "achieved": round(tops8, 1), "peak": I8_DENSE_TOPS,
+                                            "unit": "TOP/s", "frac": round(tops8 / I8_DENSE_TOPS, 4), "traffic": None,
+                                            "kernel": "k_gemm_w8a8_lds (+ fh_k_encode_panel): 2 m n k ops of "
+                                                      "the int8 product per step of the 96 linears",
+                                            "note": "bound by the reference's per-block rounding (a product and "
+                                                    "a sum per output and block on the VALU): MFMA busy 29 %"}},
             "w8a8_fast": {"ms": round(ms8f, 3), "tops": round(tops8f, 1),
                           "frac_i8_dense_peak": round(tops8f / I8_DENSE_TOPS, 4),
                           "numerics": "FH_W8A8_FAST: W8A8's exact block dots, each block term fused into the sum "
