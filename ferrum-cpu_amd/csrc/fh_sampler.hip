@@ -1630,7 +1630,7 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
     if (ctx->split_per_cu < 0) {  // the least over the instances below
         const void* ks[] = {reinterpret_cast<const void*>(k_sample_split<2>), reinterpret_cast<const void*>(k_sample_split<4>),
                             reinterpret_cast<const void*>(k_sample_split<8>), reinterpret_cast<const void*>(k_sample_split<16>),
-                            reinterpret_cast<const void*>(k_sample_split<32>)};
+                            reinterpret_cast<const void*>(k_sample_split<32>), reinterpret_cast<const void*>(k_sample_split<40>)};
         int least = 1 << 30;
         for (const void* k : ks) {
             int per = 0;
@@ -1640,7 +1640,8 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
         ctx->split_per_cu = least;
     }
     if (vocab >= 8192 && rows <= 1024 && ctx->split_per_cu > 0) {
-        static const int kOpts[] = {2, 4, 8, 16, 32};
+        // (40: a 151936-id row in four segments, so that 64 rows take one launch)
+        static const int kOpts[] = {2, 4, 8, 16, 32, 40};
         const size_t cus = static_cast<size_t>(ctx->num_cus) * static_cast<size_t>(ctx->split_per_cu);
         int pick = 0;
         size_t pick_rows = 0, pick_launches = 9;
@@ -1674,7 +1675,8 @@ int fh_launch_sample(fh_ctx* ctx, const float* logits, size_t rows, size_t vocab
                     case 4: rc = launch_split<4>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
                     case 8: rc = launch_split<8>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
                     case 16: rc = launch_split<16>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
-                    default: rc = launch_split<32>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
+                    case 32: rc = launch_split<32>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
+                    default: rc = launch_split<40>(ctx, nr, s32, lg, P, recent, of, dr, out + r0, sy, pb); break;
                 }
                 if (rc) return rc;
             }

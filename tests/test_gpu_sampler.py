@@ -176,8 +176,8 @@ def test_flat_top_p_takes_the_general_path(fh, orc):
 def test_qwen_config5_rows(fh, orc, rows):
     """Config 5: 151936-wide logits ~N(0,3) plus 5 planted peaks (+12), top-k 50,
     top-p 0.9, repetition penalty 1.05 over a 1024-token random history.  At 64
-    rows the split sampler runs as consecutive launches of the rows that fit
-    the CUs together."""
+    rows the split sampler takes four segments of 40 ids per thread, so every
+    row fits the CUs together in one launch."""
     vocab = 151936
     rng = np.random.default_rng(55)
     lg = (rng.standard_normal((rows, vocab)) * 3).astype(np.float32)
