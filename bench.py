@@ -56,7 +56,7 @@ B32 = 32
 # of 32 prompts x 512 tokens = 16,384 activation rows per linear.
 MED_D, MED_L, MED_FFN, MED_M = 1024, 24, 4096, 32 * 512
 MED_SHAPES = [(3 * MED_D, MED_D), (MED_D, MED_D), (MED_FFN, MED_D), (MED_D, MED_FFN)]
-F16_DENSE_TFLOPS, I8_DENSE_TOPS, F32_MATRIX_TFLOPS = 2500.0, 5000.0, 157.3
+F16_DENSE_TFLOPS, I8_DENSE_TOPS = 2500.0, 5000.0
 HEADS, CTX, FULL_POS = 12, 1024, 255  # GPT-2-124M attention; the whole-step leg's position
 
 COPY_BYTES = 256 << 20
@@ -798,9 +798,11 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
     pa_flops = MED_L * B32 * 16 * (pa_rows * (pa_rows + 1) / 2) * 64 * 4
     pa_tflops = pa_flops / (pa_ms * 1e-3) / 1e12
     prompt_attention = {"ms": round(pa_ms, 3), "tflops": round(pa_tflops, 1),
-                        "frac_fp32_matrix_peak": round(pa_tflops / F32_MATRIX_TFLOPS, 4),
+                        "mfma_f16_tflops": round(3 * pa_tflops, 1),
+                        "mfma_frac_f16_dense_peak": round(3 * pa_tflops / F16_DENSE_TFLOPS, 4),
                         "what": "configs[3]'s prompt attention: 24 blocks x 32 prompts x 511 positions x 16 heads of "
-                                "64, causal, one launch per block (k/v store + fp32-MFMA flash attention); useful "
+                                "64, causal, one launch per block (k/v store + flash attention on the f16 matrix "
+                                "cores, each f32 operand as two f16 terms: three f16 products per product); useful "
                                 "flops of the causal triangle"}
     del ga, pa_qkv, pa_k, pa_v, pa_out
     # Config 4 as a run: GPT-2-medium (N(0, 0.02) Q8_0 weights), 32 prompts

@@ -1,4 +1,4 @@
-// fh_attn_prefill.hip — the attention of a prompt block on the fp32 matrix cores.
+// fh_attn_prefill.hip — the attention of a prompt block on the matrix cores.
 //
 // What it computes: the attention of TransformerBlock::forward_with_cache
 // (layer/transformer.rs:242-279) for every row of a prompt block at once.
@@ -13,24 +13,12 @@
 // Each of its four waves owns 32 query rows and walks 32-key tiles of the
 // sequence's cache up to its last row's position; the tiles are staged in LDS
 // once for the four waves (double-buffered, the next tile's loads in flight
-// while the current one is used).  Per tile, flash style:
-//   S^T = K Q^T   32 v_mfma_f32_32x32x2_f32 (32 keys x 32 queries, K = 64
-//                 dims, two dims per step: half h of the wave supplies dim
-//                 s + 32 h, so each lane reads one contiguous half row);
-//   softmax       lane j of each half holds query j's scores for 16 keys: the
-//                 masked max, exp(s - max) and the row sums per query, and the
-//                 running max / sum with exact rescaling between tiles;
-//   O += P V      32 v_mfma_f32_32x32x2_f32 (32 queries x 2 x 32 dims): the
-//                 keys of step s are the ones lane half h holds in accumulator
-//                 s, so P goes into the matrix cores straight from the S^T
-//                 accumulators, and the outputs come out one query row per
-//                 accumulator (coalesced stores).
-// All products and sums are f32 (the matrix cores' fp32 path), so the result
-// is the reference's within the 1e-5 rule: the same dot products scaled after
-// the sum, exp(s - max), a blockwise order of the sums.  A tile holding a
-// non-finite v value is finished on the vector units with only the attended
-// keys (0 * inf would otherwise turn a masked key's v into NaN); non-finite k
-// values of masked keys never reach a score (the mask selects -inf).
+// while the current one is used).  Per tile, flash style: S^T = K Q^T on the
+// matrix cores, the masked softmax with a running max and sum per query
+// (exact rescaling between tiles), then O += P V on the matrix cores, P
+// going in straight from the S^T accumulators and the outputs coming out one
+// query row per accumulator (coalesced stores).  The f32 operands ride on the
+// f16 matrix cores as two terms each (k_attn_prefill_f16 below).
 #include "fh_internal.hpp"
 
 #pragma clang fp contract(off)
@@ -43,7 +31,6 @@ constexpr int kPT = 256;       // threads: four waves of 32 query rows
 constexpr int kQRows = 128;    // query rows per workgroup
 constexpr int kKeys = 32;      // keys per tile
 constexpr int kHd = 64;        // head width
-constexpr int kKPitch = kHd + 4;  // K tile row pitch (floats): 16-byte reads of 8 rows hit distinct banks
 
 struct PrefillArgs {
     const float* qkv;   // row s * rows + r; head h's q at column h * 64
@@ -58,51 +45,118 @@ struct PrefillArgs {
     int out_ld;
 };
 
-__device__ __forceinline__ bool finite4(float4 v) {
-    return __builtin_isfinite(v.x) && __builtin_isfinite(v.y) && __builtin_isfinite(v.z) && __builtin_isfinite(v.w);
-}
-
 // Query row of accumulator v in a lane of half `half` (the 32 x 32 MFMA
 // output layout: rows 8 (v / 4) + 4 half + v % 4).
 __device__ __forceinline__ int acc_row(int v, int half) { return (v >> 2) * 8 + half * 4 + (v & 3); }
 
-__global__ void __launch_bounds__(kPT, 2) k_attn_prefill_mfma(PrefillArgs a) {
-    __shared__ __align__(16) float ks[2][kKeys * kKPitch];
-    __shared__ __align__(16) float vs[2][kKeys * kHd];     // row kk: position 2 c + t holds v[kk][c + 32 t]
-    __shared__ __align__(16) float cx[4][32];               // per wave: one factor per query row
-    __shared__ __align__(16) float pt[4][kKeys * 33];       // per wave: P of a tile with non-finite v ([key][query])
+// The products on the f16 matrix cores: every f32 operand is carried as two
+// f16 terms, x = h + l with l = f16(x - h) (22 significant bits), and a
+// product of two such operands as the three f16 products h h' + h l' + l h'
+// (the dropped l l' is 2^-22 of it), summed in f32 by v_mfma_f32_32x32x16_f16:
+// 12 MFMAs per 32-key tile for S^T = K Q^T and 12 for O += P V, against 32 +
+// 32 v_mfma_f32_32x32x2_f32 on the fp32 path, each of which takes twice an
+// f16 one's cycles (measured on the configs[3] prime: 10.6 -> 6.8 ms).
+//   q, k: each query row and each key row is scaled by its own power of two
+//     (its largest finite |value| into [2^14, 2^15)) before the split, and
+//     the score is unscaled exactly afterwards with the 1/sqrt(64) of the
+//     reference: s = S' * 2^-eq * 2^-ek / 8.  Non-finite values keep l = 0,
+//     so inf and NaN reach the score as the f32 product gives them.
+//   P V: P (in [0, 1]) is split as it leaves the score accumulators; a lane's
+//     16 keys of its query are the A operand's two K16 steps as they stand
+//     (keys 8 a + 4 half + (0..3)), and the v tile is staged transposed,
+//     [dim][key] with the keys in that same order, as the B operand.  A tile
+//     whose v values are not all finite and below 2^15 in magnitude is
+//     finished on the vector units with only the attended keys (0 * inf would
+//     otherwise turn a masked key's v into NaN), v read from the cache.
+// The error is that of the 22-bit operands, ~2^-22 relative per product,
+// well inside the 1e-5 rule.
+constexpr int kHPitch = kHd + 8;   // K tile row pitch (halves): 144-byte rows
+constexpr int kVPitch = kKeys + 8;  // V tile (transposed) row pitch (halves): 80-byte rows
+
+typedef _Float16 h8f __attribute__((ext_vector_type(8)));
+typedef _Float16 h2f __attribute__((ext_vector_type(2)));
+
+// Position of key kk of a tile in the transposed V rows: K16 step s holds,
+// per lane half g, the keys 8 (2 s) + 4 g + (0..3) then 8 (2 s + 1) + 4 g + (0..3).
+__device__ __forceinline__ int vkey_pos(int kk) {
+    const int a = kk >> 3, g = (kk >> 2) & 1, b = kk & 3;
+    return 16 * (a >> 1) + 8 * g + 4 * (a & 1) + b;
+}
+
+// 2^e with |x| 2^e in [2^14, 2^15) for the largest finite |x| (mx; 0 -> e = 0).
+__device__ __forceinline__ int pow2_exponent(float mx) {
+    if (!(mx > 0.0f)) return 0;
+    const int E = static_cast<int>((__builtin_bit_cast(uint32_t, mx) >> 23) & 0xFF) - 126;
+    return min(max(15 - E, -126), 126);
+}
+__device__ __forceinline__ float pow2f(int e) { return __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23); }
+
+// Two scaled f32 values as f16 h and l terms (l = 0 for a non-finite value).
+__device__ __forceinline__ void split2(float x0, float x1, float sc, h2f& h, h2f& l) {
+    const float s0 = x0 * sc, s1 = x1 * sc;
+    h = h2f{static_cast<_Float16>(s0), static_cast<_Float16>(s1)};
+    const float r0 = __builtin_isfinite(s0) ? s0 - static_cast<float>(h.x) : 0.0f;
+    const float r1 = __builtin_isfinite(s1) ? s1 - static_cast<float>(h.y) : 0.0f;
+    l = h2f{static_cast<_Float16>(r0), static_cast<_Float16>(r1)};
+}
+
+__global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
+    __shared__ __align__(16) _Float16 kh[2][kKeys * kHPitch], kl[2][kKeys * kHPitch];
+    __shared__ __align__(16) _Float16 vh[2][kHd * kVPitch], vl[2][kHd * kVPitch];
+    __shared__ __align__(16) float kinv[2][kKeys];           // 2^-ek per key row
+    __shared__ __align__(16) float cx[4][32];                // per wave: one factor per query row
+    __shared__ __align__(16) float pt[4][kKeys * 33];        // per wave: P of a tile with unsafe v ([key][query])
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, half = lane >> 5, col = lane & 31;
     const int g = a.groups - 1 - static_cast<int>(blockIdx.x);  // the longest rows first
     const int h = blockIdx.y, s = blockIdx.z;
     const int r0 = g * kQRows + wave * 32;
     const int last_row = min(a.rows - 1, g * kQRows + kQRows - 1);
-    const int kmax = a.pos0 + last_row;                         // the last cache row this workgroup reads
+    const int kmax = a.pos0 + last_row;
     const int ntiles = kmax / kKeys + 1;
     const int my_tiles = r0 < a.rows ? (a.pos0 + min(a.rows - 1, r0 + 31)) / kKeys + 1 : 0;
     const size_t sbase = static_cast<size_t>(s) * a.seq_stride + static_cast<size_t>(h) * kHd;
     const float* kc = a.kc + sbase;
     const float* vc = a.vc + sbase;
 
-    // This lane's half of its query row (rows past the block repeat the last one).
-    float q[32];
+    // This lane's query: dims 16 i + 8 half + (0..7), i = 0..3 (the B
+    // operand of step i), scaled by the row's power of two and split.
+    h8f qh[4], ql[4];
+    float qscale;
     {
         const int row = min(r0 + col, a.rows - 1);
-        const float4* qp = reinterpret_cast<const float4*>(a.qkv + (static_cast<size_t>(s) * a.rows + row) * a.ld +
-                                                           h * kHd + half * 32);
+        const float* qp = a.qkv + (static_cast<size_t>(s) * a.rows + row) * a.ld + h * kHd + half * 8;
+        float qv[32];
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            const float4 v = qp[i];
-            q[4 * i] = v.x;
-            q[4 * i + 1] = v.y;
-            q[4 * i + 2] = v.z;
-            q[4 * i + 3] = v.w;
+        for (int i = 0; i < 4; i++) {
+            const float4 u = *reinterpret_cast<const float4*>(qp + 16 * i);
+            const float4 w = *reinterpret_cast<const float4*>(qp + 16 * i + 4);
+            qv[8 * i] = u.x; qv[8 * i + 1] = u.y; qv[8 * i + 2] = u.z; qv[8 * i + 3] = u.w;
+            qv[8 * i + 4] = w.x; qv[8 * i + 5] = w.y; qv[8 * i + 6] = w.z; qv[8 * i + 7] = w.w;
         }
+        float mx = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 32; i++)
+            if (__builtin_isfinite(qv[i])) mx = fmaxf(mx, fabsf(qv[i]));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));  // the other half of the row
+        const int eq = pow2_exponent(mx);
+        const float sc = pow2f(eq);
+        qscale = pow2f(-eq) * a.scale;  // (a.scale = 1/8: the product stays exact)
+#pragma unroll
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+            for (int j = 0; j < 8; j += 2) {
+                h2f hh, ll;
+                split2(qv[8 * i + j], qv[8 * i + j + 1], sc, hh, ll);
+                qh[i][j] = hh.x; qh[i][j + 1] = hh.y;
+                ql[i][j] = ll.x; ql[i][j + 1] = ll.y;
+            }
     }
-    const int qpos = a.pos0 + r0 + col;  // the position of this lane's query row
+    const int qpos = a.pos0 + r0 + col;
 
-    // Tile staging: 512 float4 of k rows and 512 of v rows; thread t takes
-    // float4s t and t + 256 of each (row idx / 16, dims 4 (idx % 16) ...).
+    // Tile staging: thread t takes float4s t and t + 256 of the k and of the v
+    // rows (row idx / 16, dims 4 (idx % 16) ...); the 16 threads of a key row
+    // are consecutive lanes, so its exponent is a 16-lane reduction.
     float4 pk[2], pv[2];
     auto fetch = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
@@ -113,17 +167,43 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_mfma(PrefillArgs a) {
             pv[i] = *reinterpret_cast<const float4*>(vc + key * a.kv_dim + c4 * 4);
         }
     };
-    auto stash = [&](int buf) __attribute__((always_inline)) {
+    // returns whether this thread's v values are unsafe for the f16 split
+    auto stash = [&](int buf) __attribute__((always_inline)) -> bool {
+        bool bad = false;
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int idx = tid + i * kPT, row = idx >> 4, c0 = (idx & 15) * 4;
-            *reinterpret_cast<float4*>(&ks[buf][row * kKPitch + c0]) = pk[i];
-            float* vr = &vs[buf][row * kHd + 2 * (c0 & 31) + (c0 >> 5)];
-            vr[0] = pv[i].x;
-            vr[2] = pv[i].y;
-            vr[4] = pv[i].z;
-            vr[6] = pv[i].w;
+            const float4 k4 = pk[i];
+            float mx = 0.0f;
+            if (__builtin_isfinite(k4.x)) mx = fmaxf(mx, fabsf(k4.x));
+            if (__builtin_isfinite(k4.y)) mx = fmaxf(mx, fabsf(k4.y));
+            if (__builtin_isfinite(k4.z)) mx = fmaxf(mx, fabsf(k4.z));
+            if (__builtin_isfinite(k4.w)) mx = fmaxf(mx, fabsf(k4.w));
+            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 4, 64));
+            mx = fmaxf(mx, __shfl_xor(mx, 8, 64));
+            const int ek = pow2_exponent(mx);
+            h2f h01, l01, h23, l23;
+            split2(k4.x, k4.y, pow2f(ek), h01, l01);
+            split2(k4.z, k4.w, pow2f(ek), h23, l23);
+            *reinterpret_cast<uint2*>(&kh[buf][row * kHPitch + c0]) =
+                make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+            *reinterpret_cast<uint2*>(&kl[buf][row * kHPitch + c0]) =
+                make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
+            if (c0 == 0) kinv[buf][row] = pow2f(-ek);
+            const float4 v4 = pv[i];
+            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
+            const int kp = vkey_pos(row);
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                bad |= !(fabsf(vv[j]) < 32768.0f);  // (also NaN)
+                const _Float16 hv = static_cast<_Float16>(vv[j]);
+                vh[buf][(c0 + j) * kVPitch + kp] = hv;
+                vl[buf][(c0 + j) * kVPitch + kp] = static_cast<_Float16>(vv[j] - static_cast<float>(hv));
+            }
         }
+        return bad;
     };
 
     float m_run = -INFINITY, l_run = 0.0f;
@@ -134,32 +214,38 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_mfma(PrefillArgs a) {
         o1[v] = 0.0f;
     }
     fetch(0);
-    stash(0);
-    bool vbad = __syncthreads_or(!finite4(pv[0]) || !finite4(pv[1]));
+    bool vbad = __syncthreads_or(stash(0));
     for (int t = 0; t < ntiles; t++) {
         const int buf = t & 1, k0 = t * kKeys;
         if (t + 1 < ntiles) fetch(t + 1);
         if (t < my_tiles) {
-            // ---- S^T = K Q^T: accumulator v of lane (half, col) is key acc_row(v, half), query col
+            // ---- S'^T = K Q^T (scaled terms): accumulator v of lane (half, col) is key acc_row(v, half), query col
             f32x16 sacc;
 #pragma unroll
             for (int v = 0; v < 16; v++) sacc[v] = 0.0f;
-            const float* krow = &ks[buf][col * kKPitch + half * 32];
+            const _Float16* khr = &kh[buf][col * kHPitch + half * 8];
+            const _Float16* klr = &kl[buf][col * kHPitch + half * 8];
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const float4 kv = *reinterpret_cast<const float4*>(krow + 4 * i);
-                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.x, q[4 * i], sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.y, q[4 * i + 1], sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.z, q[4 * i + 2], sacc, 0, 0, 0);
-                sacc = __builtin_amdgcn_mfma_f32_32x32x2f32(kv.w, q[4 * i + 3], sacc, 0, 0, 0);
+            for (int i = 0; i < 4; i++) {
+                const h8f a_h = *reinterpret_cast<const h8f*>(khr + 16 * i);
+                const h8f a_l = *reinterpret_cast<const h8f*>(klr + 16 * i);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, qh[i], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_h, ql[i], sacc, 0, 0, 0);
+                sacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(a_l, qh[i], sacc, 0, 0, 0);
             }
-            // ---- scores (scaled after the sum, as the reference), masked past the query's position
+            // ---- scores, unscaled exactly, masked past the query's position
             float sv[16];
             float mt = -INFINITY;
 #pragma unroll
-            for (int v = 0; v < 16; v++) {
-                sv[v] = k0 + acc_row(v, half) <= qpos ? sacc[v] * a.scale : -INFINITY;
-                mt = fmaxf(mt, sv[v]);
+            for (int a4 = 0; a4 < 4; a4++) {
+                const float4 ki = *reinterpret_cast<const float4*>(&kinv[buf][a4 * 8 + half * 4]);
+                const float kv4[4] = {ki.x, ki.y, ki.z, ki.w};
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int v = 4 * a4 + j;
+                    sv[v] = k0 + acc_row(v, half) <= qpos ? sacc[v] * qscale * kv4[j] : -INFINITY;
+                    mt = fmaxf(mt, sv[v]);
+                }
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
             const float m_new = fmaxf(m_run, mt);
@@ -173,7 +259,6 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_mfma(PrefillArgs a) {
             ps += __shfl_xor(ps, 32, 64);
             l_run = l_run * corr + ps;
             m_run = m_new;
-            // ---- rescale the output rows (query acc_row(v, half)) by their query's factor
             if (half == 0) cx[wave][col] = corr;
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -189,17 +274,31 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_mfma(PrefillArgs a) {
                 o1[4 * a4 + 3] *= c.w;
             }
             __builtin_amdgcn_wave_barrier();
-            const float* vt = vs[buf];
             if (!vbad) {
-                // ---- O += P V: step st takes key acc_row(st, half) in half `half`
+                // ---- O += P V: step st takes this lane's keys acc_row(8 st + j, half)
 #pragma unroll
-                for (int st = 0; st < 16; st++) {
-                    const float2 vv = *reinterpret_cast<const float2*>(vt + acc_row(st, half) * kHd + 2 * col);
-                    o0 = __builtin_amdgcn_mfma_f32_32x32x2f32(sv[st], vv.x, o0, 0, 0, 0);
-                    o1 = __builtin_amdgcn_mfma_f32_32x32x2f32(sv[st], vv.y, o1, 0, 0, 0);
+                for (int st = 0; st < 2; st++) {
+                    h8f ph, pl;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        const float p = sv[8 * st + j];
+                        ph[j] = static_cast<_Float16>(p);
+                        pl[j] = static_cast<_Float16>(p - static_cast<float>(ph[j]));
+                    }
+                    const int off = 16 * st + 8 * half;
+                    const h8f v0h = *reinterpret_cast<const h8f*>(&vh[buf][col * kVPitch + off]);
+                    const h8f v0l = *reinterpret_cast<const h8f*>(&vl[buf][col * kVPitch + off]);
+                    const h8f v1h = *reinterpret_cast<const h8f*>(&vh[buf][(32 + col) * kVPitch + off]);
+                    const h8f v1l = *reinterpret_cast<const h8f*>(&vl[buf][(32 + col) * kVPitch + off]);
+                    o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, v0h, o0, 0, 0, 0);
+                    o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, v0l, o0, 0, 0, 0);
+                    o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, v0h, o0, 0, 0, 0);
+                    o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, v1h, o1, 0, 0, 0);
+                    o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, v1l, o1, 0, 0, 0);
+                    o1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, v1h, o1, 0, 0, 0);
                 }
             } else {
-                // ---- a non-finite v in this tile: only the attended keys, on the vector units
+                // ---- v not safe for the split: only the attended keys, on the vector units
                 float* pw = pt[wave];
 #pragma unroll
                 for (int v = 0; v < 16; v++) pw[acc_row(v, half) * 33 + col] = sv[v];
@@ -210,8 +309,9 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_mfma(PrefillArgs a) {
                     float s0 = o0[v], s1 = o1[v];
                     for (int kk = 0; kk < kKeys && k0 + kk <= qp; kk++) {
                         const float p = pw[kk * 33 + qr];
-                        s0 += p * vt[kk * kHd + 2 * col];
-                        s1 += p * vt[kk * kHd + 2 * col + 1];
+                        const float* vrow = vc + static_cast<size_t>(k0 + kk) * a.kv_dim;
+                        s0 += p * vrow[col];
+                        s1 += p * vrow[32 + col];
                     }
                     o0[v] = s0;
                     o1[v] = s1;
@@ -220,10 +320,7 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_mfma(PrefillArgs a) {
             }
         }
         bool vbad_next = false;
-        if (t + 1 < ntiles) {
-            stash(buf ^ 1);
-            vbad_next = !finite4(pv[0]) || !finite4(pv[1]);
-        }
+        if (t + 1 < ntiles) vbad_next = stash(buf ^ 1);
         vbad = __syncthreads_or(vbad_next);
     }
 
@@ -294,7 +391,7 @@ int fh_launch_attention_prefill_seqs(fh_ctx* ctx, const float* qkv, float* kc, f
     a.scale = 1.0f / sqrtf(static_cast<float>(hd));
     a.out = out;
     a.out_ld = static_cast<int>(d);
-    hipLaunchKernelGGL(k_attn_prefill_mfma,
+    hipLaunchKernelGGL(k_attn_prefill_f16,
                        dim3(static_cast<unsigned>(a.groups), static_cast<unsigned>(heads), static_cast<unsigned>(seqs)),
                        dim3(kPT), 0, ctx->stream, a);
     FH_HIP(ctx, hipGetLastError());

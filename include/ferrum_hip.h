@@ -427,7 +427,8 @@ int fh_attention_prefill_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache
  * rows s * rows .. s * rows + rows - 1 of d_qkv ([seqs * rows, 3d]) and d_out
  * ([seqs * rows, d]); its caches start at d_k_cache / d_v_cache + s *
  * seq_stride (floats; seq_stride >= capacity * d when seqs > 1).  Head width
- * 64 runs on the fp32 matrix cores; within the 1e-5 rule of the reference.
+ * 64 runs on the f16 matrix cores with every f32 operand as two f16 terms
+ * (three f16 products per product); within the 1e-5 rule of the reference.
  * Errors as fh_attention_prefill_async; seqs <= 65535. */
 int fh_attention_prefill_seqs_async(fh_ctx* ctx, const float* d_qkv, float* d_k_cache, float* d_v_cache,
                                     size_t seq_stride, size_t capacity, size_t d, size_t heads, size_t pos0,
