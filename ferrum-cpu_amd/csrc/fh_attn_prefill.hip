@@ -5,9 +5,9 @@
 // CachedTransformer's prime (slm/cached.rs:129-136) feeds a prompt position by
 // position; here row r of sequence s is position pos0 + r and attends over
 // cache positions 0 .. pos0 + r of its own sequence, with the scores
-// (q . k) * 1/sqrt(hd), their softmax and the weighted sum of v rows.  The
-// block's k / v rows go into the caches first (k_kv_store_seqs), so every key
-// and value comes from the cache.
+// (q . k) * 1/sqrt(hd), their softmax and the weighted sum of v rows.  Keys
+// before the block come from the caches, the block's own from its q|k|v rows;
+// the same launch writes the block's k / v rows into the caches.
 //
 // How (head width 64): one workgroup per (128 query rows, head, sequence).
 // Each of its four waves owns 32 query rows and walks 32-key tiles of the
@@ -35,8 +35,8 @@ constexpr int kHd = 64;        // head width
 struct PrefillArgs {
     const float* qkv;   // row s * rows + r; head h's q at column h * 64
     int ld;             // qkv row stride (floats)
-    const float* kc;    // sequence s's caches at kc / vc + s * seq_stride, rows of kv_dim floats
-    const float* vc;
+    float* kc;          // sequence s's caches at kc / vc + s * seq_stride, rows of kv_dim floats
+    float* vc;
     size_t seq_stride;
     int kv_dim;
     int rows, pos0, groups;
@@ -116,8 +116,8 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
     const int ntiles = kmax / kKeys + 1;
     const int my_tiles = r0 < a.rows ? (a.pos0 + min(a.rows - 1, r0 + 31)) / kKeys + 1 : 0;
     const size_t sbase = static_cast<size_t>(s) * a.seq_stride + static_cast<size_t>(h) * kHd;
-    const float* kc = a.kc + sbase;
-    const float* vc = a.vc + sbase;
+    float* kc = a.kc + sbase;
+    float* vc = a.vc + sbase;
 
     // This lane's query: dims 16 i + 8 half + (0..7), i = 0..3 (the B
     // operand of step i), scaled by the row's power of two and split.
@@ -156,15 +156,35 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
 
     // Tile staging: thread t takes float4s t and t + 256 of the k and of the v
     // rows (row idx / 16, dims 4 (idx % 16) ...); the 16 threads of a key row
-    // are consecutive lanes, so its exponent is a 16-lane reduction.
+    // are consecutive lanes, so its exponent is a 16-lane reduction.  Keys of
+    // the block itself (pos0 on) come from its q|k|v rows, earlier ones from
+    // the cache; workgroup 0 of each (sequence, head), which walks every tile,
+    // also writes the block's k and v rows into the cache as it stages them
+    // (no other workgroup of the launch reads those cache rows).
+    const bool writer = blockIdx.x == 0;
+    const float* bq = a.qkv + static_cast<size_t>(s) * a.rows * a.ld + h * kHd;  // this sequence's block rows
     float4 pk[2], pv[2];
     auto fetch = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
             const int idx = tid + i * kPT, row = idx >> 4, c4 = idx & 15;
-            const size_t key = static_cast<size_t>(min(t * kKeys + row, kmax));
-            pk[i] = *reinterpret_cast<const float4*>(kc + key * a.kv_dim + c4 * 4);
-            pv[i] = *reinterpret_cast<const float4*>(vc + key * a.kv_dim + c4 * 4);
+            const int key = min(t * kKeys + row, kmax);
+            const float* kp = key >= a.pos0 ? bq + static_cast<size_t>(key - a.pos0) * a.ld + a.kv_dim
+                                            : kc + static_cast<size_t>(key) * a.kv_dim;
+            const float* vp = key >= a.pos0 ? bq + static_cast<size_t>(key - a.pos0) * a.ld + 2 * a.kv_dim
+                                            : vc + static_cast<size_t>(key) * a.kv_dim;
+            pk[i] = *reinterpret_cast<const float4*>(kp + c4 * 4);
+            pv[i] = *reinterpret_cast<const float4*>(vp + c4 * 4);
+        }
+    };
+    auto store_block_rows = [&](int t) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int idx = tid + i * kPT, row = idx >> 4, c4 = idx & 15, key = t * kKeys + row;
+            if (key >= a.pos0 && key <= kmax) {
+                *reinterpret_cast<float4*>(kc + static_cast<size_t>(key) * a.kv_dim + c4 * 4) = pk[i];
+                *reinterpret_cast<float4*>(vc + static_cast<size_t>(key) * a.kv_dim + c4 * 4) = pv[i];
+            }
         }
     };
     // returns whether this thread's v values are unsafe for the f16 split
@@ -214,6 +234,7 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
         o1[v] = 0.0f;
     }
     fetch(0);
+    if (writer) store_block_rows(0);
     bool vbad = __syncthreads_or(stash(0));
     for (int t = 0; t < ntiles; t++) {
         const int buf = t & 1, k0 = t * kKeys;
@@ -309,7 +330,9 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
                     float s0 = o0[v], s1 = o1[v];
                     for (int kk = 0; kk < kKeys && k0 + kk <= qp; kk++) {
                         const float p = pw[kk * 33 + qr];
-                        const float* vrow = vc + static_cast<size_t>(k0 + kk) * a.kv_dim;
+                        const int key = k0 + kk;
+                        const float* vrow = key >= a.pos0 ? bq + static_cast<size_t>(key - a.pos0) * a.ld + 2 * a.kv_dim
+                                                          : vc + static_cast<size_t>(key) * a.kv_dim;
                         s0 += p * vrow[col];
                         s1 += p * vrow[32 + col];
                     }
@@ -320,7 +343,10 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
             }
         }
         bool vbad_next = false;
-        if (t + 1 < ntiles) vbad_next = stash(buf ^ 1);
+        if (t + 1 < ntiles) {
+            if (writer) store_block_rows(t + 1);
+            vbad_next = stash(buf ^ 1);
+        }
         vbad = __syncthreads_or(vbad_next);
     }
 
@@ -337,20 +363,6 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
             op[col] = o0[v] / l;
             op[32 + col] = o1[v] / l;
         }
-    }
-}
-
-// Rows r of each sequence's block: their k and v slices into cache rows
-// pos0 + r of that sequence (grid: (column chunks, rows, sequences)).
-__global__ void __launch_bounds__(kPT) k_kv_store_seqs(const float* __restrict__ qkv, int ld, int k_off, int v_off,
-                                                      int kv_dim, int rows, int pos0, size_t seq_stride,
-                                                      float* __restrict__ kc, float* __restrict__ vc) {
-    const int r = blockIdx.y, s = blockIdx.z;
-    const float* src = qkv + (static_cast<size_t>(s) * rows + r) * ld;
-    const size_t dst = static_cast<size_t>(s) * seq_stride + static_cast<size_t>(pos0 + r) * kv_dim;
-    for (int c = blockIdx.x * kPT + threadIdx.x; c < kv_dim; c += gridDim.x * kPT) {
-        kc[dst + c] = src[k_off + c];
-        vc[dst + c] = src[v_off + c];
     }
 }
 
@@ -372,12 +384,6 @@ int fh_launch_attention_prefill_seqs(fh_ctx* ctx, const float* qkv, float* kc, f
         }
         return FH_OK;
     }
-    const unsigned gx = static_cast<unsigned>((d + kPT - 1) / kPT);
-    hipLaunchKernelGGL(k_kv_store_seqs, dim3(gx, static_cast<unsigned>(rows), static_cast<unsigned>(seqs)),
-                       dim3(kPT), 0, ctx->stream, qkv, static_cast<int>(3 * d), static_cast<int>(d),
-                       static_cast<int>(2 * d), static_cast<int>(d), static_cast<int>(rows), static_cast<int>(pos0),
-                       seq_stride, kc, vc);
-    FH_HIP(ctx, hipGetLastError());
     PrefillArgs a{};
     a.qkv = qkv;
     a.ld = static_cast<int>(3 * d);
