@@ -83,6 +83,14 @@ __device__ __forceinline__ int vkey_pos(int kk) {
     return 16 * (a >> 1) + 8 * g + 4 * (a & 1) + b;
 }
 
+// Offset of (dim, key position kp) in a transposed V tile: the 8-key chunks
+// of dim row d are permuted by (d / 16) % 4, so the pair stores of one wave
+// (16 dims 4 apart) spread over the banks; a chunk's 8 keys stay contiguous
+// for the 16-byte operand loads.
+__device__ __forceinline__ int vt_pos(int d, int kp) {
+    return d * kVPitch + 8 * ((kp >> 3) ^ ((d >> 4) & 3)) + (kp & 7);
+}
+
 // 2^e with |x| 2^e in [2^14, 2^15) for the largest finite |x| (mx; 0 -> e = 0).
 __device__ __forceinline__ int pow2_exponent(float mx) {
     if (!(mx > 0.0f)) return 0;
@@ -90,6 +98,11 @@ __device__ __forceinline__ int pow2_exponent(float mx) {
     return min(max(15 - E, -126), 126);
 }
 __device__ __forceinline__ float pow2f(int e) { return __builtin_bit_cast(float, static_cast<uint32_t>(e + 127) << 23); }
+
+// e^x for x <= 0 as 2^(x log2 e) on the hardware's exp2 (v_exp_f32, 1 ulp):
+// the product's rounding adds |x| 2^-24 relative, ~1e-6 for the x that carry
+// weight in a softmax, far inside the 1e-5 rule; -inf gives 0, NaN stays NaN.
+__device__ __forceinline__ float exp_approx(float x) { return __builtin_amdgcn_exp2f(x * 1.44269504088896341f); }
 
 // Two scaled f32 values as f16 h and l terms (l = 0 for a non-finite value).
 __device__ __forceinline__ void split2(float x0, float x1, float sc, h2f& h, h2f& l) {
@@ -163,28 +176,33 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
     // (no other workgroup of the launch reads those cache rows).
     const bool writer = blockIdx.x == 0;
     const float* bq = a.qkv + static_cast<size_t>(s) * a.rows * a.ld + h * kHd;  // this sequence's block rows
+    // The v rows go by pairs instead: thread t takes keys 2 (t / 16) and
+    // 2 (t / 16) + 1, dims 4 (t % 16) ..., which sit side by side in the
+    // transposed tile, so each dim is one 4-byte store per term.
     float4 pk[2], pv[2];
+    auto key_row = [&](int key, int off, const float* cache) __attribute__((always_inline)) {
+        return key >= a.pos0 ? bq + static_cast<size_t>(key - a.pos0) * a.ld + off
+                             : cache + static_cast<size_t>(key) * a.kv_dim;
+    };
     auto fetch = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int idx = tid + i * kPT, row = idx >> 4, c4 = idx & 15;
-            const int key = min(t * kKeys + row, kmax);
-            const float* kp = key >= a.pos0 ? bq + static_cast<size_t>(key - a.pos0) * a.ld + a.kv_dim
-                                            : kc + static_cast<size_t>(key) * a.kv_dim;
-            const float* vp = key >= a.pos0 ? bq + static_cast<size_t>(key - a.pos0) * a.ld + 2 * a.kv_dim
-                                            : vc + static_cast<size_t>(key) * a.kv_dim;
-            pk[i] = *reinterpret_cast<const float4*>(kp + c4 * 4);
-            pv[i] = *reinterpret_cast<const float4*>(vp + c4 * 4);
+            const int idx = tid + i * kPT, c4 = idx & 15;
+            const int key = min(t * kKeys + (idx >> 4), kmax);
+            const int vkey = min(t * kKeys + 2 * (tid >> 4) + i, kmax);
+            pk[i] = *reinterpret_cast<const float4*>(key_row(key, a.kv_dim, kc) + c4 * 4);
+            pv[i] = *reinterpret_cast<const float4*>(key_row(vkey, 2 * a.kv_dim, vc) + c4 * 4);
         }
     };
     auto store_block_rows = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
         for (int i = 0; i < 2; i++) {
-            const int idx = tid + i * kPT, row = idx >> 4, c4 = idx & 15, key = t * kKeys + row;
-            if (key >= a.pos0 && key <= kmax) {
+            const int idx = tid + i * kPT, c4 = idx & 15;
+            const int key = t * kKeys + (idx >> 4), vkey = t * kKeys + 2 * (tid >> 4) + i;
+            if (key >= a.pos0 && key <= kmax)
                 *reinterpret_cast<float4*>(kc + static_cast<size_t>(key) * a.kv_dim + c4 * 4) = pk[i];
-                *reinterpret_cast<float4*>(vc + static_cast<size_t>(key) * a.kv_dim + c4 * 4) = pv[i];
-            }
+            if (vkey >= a.pos0 && vkey <= kmax)
+                *reinterpret_cast<float4*>(vc + static_cast<size_t>(vkey) * a.kv_dim + c4 * 4) = pv[i];
         }
     };
     // returns whether this thread's v values are unsafe for the f16 split
@@ -212,16 +230,19 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
             *reinterpret_cast<uint2*>(&kl[buf][row * kHPitch + c0]) =
                 make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
             if (c0 == 0) kinv[buf][row] = pow2f(-ek);
-            const float4 v4 = pv[i];
-            const float vv[4] = {v4.x, v4.y, v4.z, v4.w};
-            const int kp = vkey_pos(row);
+        }
+        const int c0 = (tid & 15) * 4, kp = vkey_pos(2 * (tid >> 4));  // even; the pair's second key at kp + 1
+        const float va[4] = {pv[0].x, pv[0].y, pv[0].z, pv[0].w};
+        const float vb[4] = {pv[1].x, pv[1].y, pv[1].z, pv[1].w};
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                bad |= !(fabsf(vv[j]) < 32768.0f);  // (also NaN)
-                const _Float16 hv = static_cast<_Float16>(vv[j]);
-                vh[buf][(c0 + j) * kVPitch + kp] = hv;
-                vl[buf][(c0 + j) * kVPitch + kp] = static_cast<_Float16>(vv[j] - static_cast<float>(hv));
-            }
+        for (int j = 0; j < 4; j++) {
+            bad |= !(fabsf(va[j]) < 32768.0f) || !(fabsf(vb[j]) < 32768.0f);  // (also NaN)
+            const h2f hv = h2f{static_cast<_Float16>(va[j]), static_cast<_Float16>(vb[j])};
+            const h2f lv = h2f{static_cast<_Float16>(va[j] - static_cast<float>(hv.x)),
+                               static_cast<_Float16>(vb[j] - static_cast<float>(hv.y))};
+            const int at = vt_pos(c0 + j, kp);
+            *reinterpret_cast<uint32_t*>(&vh[buf][at]) = __builtin_bit_cast(uint32_t, hv);
+            *reinterpret_cast<uint32_t*>(&vl[buf][at]) = __builtin_bit_cast(uint32_t, lv);
         }
         return bad;
     };
@@ -270,11 +291,11 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
             }
             mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
             const float m_new = fmaxf(m_run, mt);
-            const float corr = expf(m_run - m_new);  // 0 on the first tile (m_run = -inf)
+            const float corr = exp_approx(m_run - m_new);  // 0 on the first tile (m_run = -inf)
             float ps = 0.0f;
 #pragma unroll
             for (int v = 0; v < 16; v++) {
-                sv[v] = expf(sv[v] - m_new);
+                sv[v] = exp_approx(sv[v] - m_new);
                 ps += sv[v];
             }
             ps += __shfl_xor(ps, 32, 64);
@@ -306,11 +327,11 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
                         ph[j] = static_cast<_Float16>(p);
                         pl[j] = static_cast<_Float16>(p - static_cast<float>(ph[j]));
                     }
-                    const int off = 16 * st + 8 * half;
-                    const h8f v0h = *reinterpret_cast<const h8f*>(&vh[buf][col * kVPitch + off]);
-                    const h8f v0l = *reinterpret_cast<const h8f*>(&vl[buf][col * kVPitch + off]);
-                    const h8f v1h = *reinterpret_cast<const h8f*>(&vh[buf][(32 + col) * kVPitch + off]);
-                    const h8f v1l = *reinterpret_cast<const h8f*>(&vl[buf][(32 + col) * kVPitch + off]);
+                    const int off = 16 * st + 8 * half, at0 = vt_pos(col, off), at1 = vt_pos(32 + col, off);
+                    const h8f v0h = *reinterpret_cast<const h8f*>(&vh[buf][at0]);
+                    const h8f v0l = *reinterpret_cast<const h8f*>(&vl[buf][at0]);
+                    const h8f v1h = *reinterpret_cast<const h8f*>(&vh[buf][at1]);
+                    const h8f v1l = *reinterpret_cast<const h8f*>(&vl[buf][at1]);
                     o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, v0h, o0, 0, 0, 0);
                     o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(ph, v0l, o0, 0, 0, 0);
                     o0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(pl, v0h, o0, 0, 0, 0);
@@ -331,8 +352,7 @@ __global__ void __launch_bounds__(kPT, 2) k_attn_prefill_f16(PrefillArgs a) {
                     for (int kk = 0; kk < kKeys && k0 + kk <= qp; kk++) {
                         const float p = pw[kk * 33 + qr];
                         const int key = k0 + kk;
-                        const float* vrow = key >= a.pos0 ? bq + static_cast<size_t>(key - a.pos0) * a.ld + 2 * a.kv_dim
-                                                          : vc + static_cast<size_t>(key) * a.kv_dim;
+                        const float* vrow = key_row(key, 2 * a.kv_dim, vc);
                         s0 += p * vrow[col];
                         s1 += p * vrow[32 + col];
                     }
