@@ -801,9 +801,10 @@ def prefill_leg(ctx, fh, torch, gen, dev, steps):
                         "mfma_f16_tflops": round(3 * pa_tflops, 1),
                         "mfma_frac_f16_dense_peak": round(3 * pa_tflops / F16_DENSE_TFLOPS, 4),
                         "what": "configs[3]'s prompt attention: 24 blocks x 32 prompts x 511 positions x 16 heads of "
-                                "64, causal, one launch per block (k/v store + flash attention on the f16 matrix "
-                                "cores, each f32 operand as two f16 terms: three f16 products per product); useful "
-                                "flops of the causal triangle"}
+                                "64, causal, one launch per block (flash attention on the f16 matrix cores, each "
+                                "f32 operand as two f16 terms: three f16 products per product; the block's k / v rows "
+                                "read from q|k|v and written into the caches by the same launch); useful flops of "
+                                "the causal triangle"}
     del ga, pa_qkv, pa_k, pa_v, pa_out
     # Config 4 as a run: GPT-2-medium (N(0, 0.02) Q8_0 weights), 32 prompts
     # of 512 random ids primed in one pass (GPT2Batch.prefill_async: the
