@@ -961,7 +961,7 @@ int rows_heads(int group) { return group >= 5 ? 4 : group >= 2 ? 2 : 1; }
 // against 14.6 us.
 bool rows_kernel_fits(const AttnArgs& a, size_t rows, size_t heads, size_t hd) {
     const int g = a.group;
-    if (hd != 64 || g < 2) return false;
+    if (hd != 64 || g < 1) return false;
     const size_t parts = (g + rows_heads(g) - 1) / rows_heads(g);
     if (rows * (heads / g) * parts < kRowsMinGroups) return false;
     const auto al = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
@@ -982,7 +982,8 @@ int launch_rows(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t max_l
         else hipLaunchKernelGGL((k_attn_rows<2, true>), grid, block, 0, ctx->stream, a, ra);
     } else {
         if (qs == 4) hipLaunchKernelGGL((k_attn_rows<4, false>), grid, block, 0, ctx->stream, a, ra);
-        else hipLaunchKernelGGL((k_attn_rows<2, false>), grid, block, 0, ctx->stream, a, ra);
+        else if (qs == 2) hipLaunchKernelGGL((k_attn_rows<2, false>), grid, block, 0, ctx->stream, a, ra);
+        else hipLaunchKernelGGL((k_attn_rows<1, false>), grid, block, 0, ctx->stream, a, ra);
     }
     FH_HIP(ctx, hipGetLastError());
     return FH_OK;
@@ -993,7 +994,12 @@ int launch_attention(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t 
                      bool batched = false) {
     if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
         return fh_fail(ctx, FH_ERR_LIMIT, "attention: head width must be 8, 16, 32, 64 or 128");
-    if (batched && rows_kernel_fits(a, rows, heads, hd)) return launch_rows(ctx, a, rows, heads, max_len, nullptr);
+    // One query head per kv head (GPT-2) takes the one-pass kernel from 384
+    // positions on: configs[3]'s batch-32 run (GPT-2-medium, 512-575
+    // positions) 151.0 -> 149.2 ms; at 256 positions (GPT-2-124M batch 32)
+    // the chunked kernel stays ahead, 0.665 against 0.668 ms a step.
+    if (batched && (a.group >= 2 || max_len >= 384) && rows_kernel_fits(a, rows, heads, hd))
+        return launch_rows(ctx, a, rows, heads, max_len, nullptr);
     a.max_len = static_cast<int>(max_len);
     const size_t sub = attn_sub(max_len);
     const size_t chunks = (max_len + sub * kChunk - 1) / (sub * kChunk);
@@ -1145,7 +1151,7 @@ int fh_launch_gqa_attention_rope_decode(fh_ctx* ctx, float* qkv, size_t ld, size
                                         const float* freq_factors, float linear_factor, float* out) {
     const AttnArgs a = gqa_args(qkv, ld, n_heads, n_kv, hd, kc, vc, cap, dpos, out);
     const size_t max_len = (max_pos < cap ? max_pos : cap - 1) + 1;
-    if (rows_kernel_fits(a, rows, n_heads, hd)) {
+    if (a.group >= 2 && rows_kernel_fits(a, rows, n_heads, hd)) {
         const RopeArgs ra{static_cast<int>(rope_dim), rope_type == FH_ROPE_NEOX ? 1 : 0, base, linear_factor,
                           freq_factors};
         return launch_rows(ctx, a, rows, n_heads, max_len, &ra);

@@ -126,11 +126,15 @@ def test_gqa_attention_matches_oracle(fh, orc, nh, nkv, hd, T):
         assert np.array_equal(kh[r], ko[r]) and np.array_equal(vh[r], vo[r])
 
 
-@pytest.mark.parametrize("nh,nkv,rows", [(14, 2, 40), (32, 8, 10), (16, 2, 40), (6, 2, 40)])
+@pytest.mark.parametrize("nh,nkv,rows", [(14, 2, 40), (32, 8, 10), (16, 2, 40), (6, 2, 40), (16, 16, 40),
+                                         (12, 12, 10)])
 def test_batched_gqa_attention_matches_oracle(fh, orc, nh, nkv, rows):
     """Launches with many (row, kv head) workgroups take the batched kernel
     (one workgroup per row, kv head and up to four query heads, every position
-    merged inside it): groups of 7 (split 4 + 3), 4, 8 and 3 (split 2 + 1).
+    merged inside it): groups of 7 (split 4 + 3), 4, 8 and 3 (split 2 + 1),
+    and one query head per kv head (GPT-2's batched decode, which takes it
+    for rows of 384 positions or more; 12 x 10 workgroups are too few and take
+    the chunked kernel).
     Positions span the wave (32) and round (256) edges, 0 and the last cache
     row; two rows sit past max_pos and one at capacity (NaN, cache untouched).
     Cache rows from pos on hold NaN, so a row read past the position shows."""
