@@ -518,9 +518,17 @@ __global__ void __launch_bounds__(kThreads) k_attn_group(AttnArgs a) {
 // goes through memory between workgroups and each K / V row is read from HBM
 // once (the parts of a group read it again from the caches).  Grid (kv heads
 // x parts, rows), kRowsThreads threads; head width 64.  A round covers
-// kRowsWaves * 32 positions, 32 per wave: lane pair (2 jj, 2 jj + 1) holds
-// position jj's k row (32 dims each) and lane (g, c) holds dims 4 c .. 4 c + 3
-// of positions g, g + 4, .. of the wave's 32 v rows.  Each wave keeps an
+// kRowsWaves * 32 positions, 32 per wave: lane (g, c) holds dims 4 c .. 4 c +
+// 3 of positions g, g + 4, .. of the wave's 32 v rows.  Its k rows: with
+// several query heads (QS > 1), lane pair (2 jj, 2 jj + 1) holds position
+// jj's k row (32 dims each), so a score is a two-lane sum and the weights go
+// to the v lanes through LDS; with one (QS = 1) the k rows are laid out as the
+// v rows (16 lanes per 256-byte row, four rows per load instead of 16-byte
+// pieces of 64), a score is a 16-lane sum, and every lane of row g then
+// holds the weights of exactly the v rows it multiplies (configs[3]'s
+// batch-32 run 148.9 -> 146.5 ms; with two or four heads the 16-lane sums per
+// head cost more than they save, the 64-row Qwen2-0.5B step 1.877 -> 1.953).
+// Each wave keeps an
 // online softmax over its rounds (running max, rescaled sums); the waves'
 // (max, sum, weighted v sums) then merge through LDS.  Position pos (and the
 // masked positions past it) reads the new k / v rows from qkv; part 0 writes
@@ -552,7 +560,7 @@ struct RopeArgs {
 };
 
 struct RowsFrag {
-    float4 k[8];  // 32 dims of position jj's k row
+    float4 k[8];  // QS > 1: 32 dims of position jj's k row; QS = 1: as v
     float4 v[8];  // dims c4 .. c4 + 3 of positions g, g + 4, .., g + 28 of the wave's 32
 };
 
@@ -589,11 +597,19 @@ __global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, RopeArgs
     // past pos are replaced by the new row where they are used)
     const int jj = lane >> 1, half = lane & 1, g = lane >> 4, c4 = (lane & 15) * 4, pm1 = max(pos - 1, 0);
     auto load = [&](RowsFrag& f, int jb) __attribute__((always_inline)) {
-        const int jk = jb + jj;
-        const float4* kr =
-            reinterpret_cast<const float4*>((jk >= pos ? knew : kc + static_cast<size_t>(jk) * d) + half * 32);
+        if constexpr (QS == 1) {
 #pragma unroll
-        for (int i = 0; i < 8; i++) f.k[i] = kr[i];
+            for (int q = 0; q < 8; q++) {
+                const int jk = jb + g + 4 * q;
+                f.k[q] = *reinterpret_cast<const float4*>((jk >= pos ? knew : kc + static_cast<size_t>(jk) * d) + c4);
+            }
+        } else {
+            const int jk = jb + jj;
+            const float4* kr =
+                reinterpret_cast<const float4*>((jk >= pos ? knew : kc + static_cast<size_t>(jk) * d) + half * 32);
+#pragma unroll
+            for (int i = 0; i < 8; i++) f.k[i] = kr[i];
+        }
 #pragma unroll
         for (int q = 0; q < 8; q++)
             f.v[q] = *reinterpret_cast<const float4*>(vc + static_cast<size_t>(min(jb + g + 4 * q, pm1)) * d + c4);
@@ -622,7 +638,11 @@ __global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, RopeArgs
     }
     // the loads take row pos's k from qkv: with ROPE the rotated row instead
     auto rotated_new_k = [&]() __attribute__((always_inline)) {
-        if (ROPE && jb + jj == pos) {
+        if constexpr (ROPE && QS == 1) {
+#pragma unroll
+            for (int q = 0; q < 8; q++)
+                if (jb + g + 4 * q == pos) cur.k[q] = *reinterpret_cast<const float4*>(&kn[c4]);
+        } else if (ROPE && jb + jj == pos) {
             const float4* k4 = reinterpret_cast<const float4*>(&kn[half * 32]);
 #pragma unroll
             for (int i = 0; i < 8; i++) cur.k[i] = k4[i];
@@ -643,6 +663,48 @@ __global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, RopeArgs
     }
     __syncthreads();
     while (jb < len) {  // (wave-uniform)
+      if constexpr (QS == 1) {
+        // rows at or past pos: the new v row
+#pragma unroll
+        for (int q = 0; q < 8; q++)
+            if (jb + g + 4 * q >= pos) cur.v[q] = vn;
+        asm volatile("" ::: "memory");  // (q from LDS each round)
+        const float4 q4 = *reinterpret_cast<const float4*>(&qs[0][c4 >> 5][c4 & 31]);
+        float sq[8];
+        float mr = -INFINITY;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            float p = q4.x * cur.k[q].x;
+            p = fmaf(q4.y, cur.k[q].y, p);
+            p = fmaf(q4.z, cur.k[q].z, p);
+            p = fmaf(q4.w, cur.k[q].w, p);
+            p = fh::group_sum<16>(p);  // every lane of row g: position jb + g + 4 q's score
+            sq[q] = jb + g + 4 * q < len ? p * a.scale : -INFINITY;
+            mr = fmaxf(mr, sq[q]);
+        }
+        const float wmx =
+            fmaxf(fmaxf(fh::rdlane(mr, 0), fh::rdlane(mr, 16)), fmaxf(fh::rdlane(mr, 32), fh::rdlane(mr, 48)));
+        const float mn = fmaxf(m[0], wmx);    // finite: position jb is in range
+        const float alpha = expf(m[0] - mn);  // 0 on the wave's first round
+        float4 acc = o[0];
+        acc.x *= alpha;
+        acc.y *= alpha;
+        acc.z *= alpha;
+        acc.w *= alpha;
+        float es = 0.0f;
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            const float e = jb + g + 4 * q < len ? expf(sq[q] - mn) : 0.0f;
+            es += e;
+            acc.x = fmaf(e, cur.v[q].x, acc.x);
+            acc.y = fmaf(e, cur.v[q].y, acc.y);
+            acc.z = fmaf(e, cur.v[q].z, acc.z);
+            acc.w = fmaf(e, cur.v[q].w, acc.w);
+        }
+        o[0] = acc;
+        l[0] = l[0] * alpha + ((lane & 15) == 0 ? es : 0.0f);  // one lane per row counts its positions
+        m[0] = mn;
+      } else {
         // (q is read from LDS each round: held in registers across rounds it
         // would take 32 per query head)
         asm volatile("" ::: "memory");
@@ -701,6 +763,7 @@ __global__ void __launch_bounds__(kRowsThreads) k_attn_rows(AttnArgs a, RopeArgs
             o[h] = acc;
         }
         __builtin_amdgcn_wave_barrier();
+      }
         jb += R;
         if (jb < len) {
             load(cur, jb);
