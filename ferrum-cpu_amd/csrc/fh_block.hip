@@ -1057,11 +1057,11 @@ int launch_attention(fh_ctx* ctx, AttnArgs a, size_t rows, size_t heads, size_t 
                      bool batched = false) {
     if (hd > static_cast<size_t>(kMaxHd) || hd % 8 != 0 || kThreads % hd != 0)
         return fh_fail(ctx, FH_ERR_LIMIT, "attention: head width must be 8, 16, 32, 64 or 128");
-    // One query head per kv head (GPT-2) takes the one-pass kernel from 384
+    // One query head per kv head (GPT-2) takes the one-pass kernel from 256
     // positions on: configs[3]'s batch-32 run (GPT-2-medium, 512-575
-    // positions) 151.0 -> 149.2 ms; at 256 positions (GPT-2-124M batch 32)
-    // the chunked kernel stays ahead, 0.665 against 0.668 ms a step.
-    if (batched && (a.group >= 2 || max_len >= 384) && rows_kernel_fits(a, rows, heads, hd))
+    // positions) 151.0 -> 145.0 ms, the GPT-2-124M batch-32 step at position
+    // 255 0.670 -> 0.648 ms (shorter rows are not measured: the chunked kernel).
+    if (batched && (a.group >= 2 || max_len >= 256) && rows_kernel_fits(a, rows, heads, hd))
         return launch_rows(ctx, a, rows, heads, max_len, nullptr);
     a.max_len = static_cast<int>(max_len);
     const size_t sub = attn_sub(max_len);

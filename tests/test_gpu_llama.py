@@ -133,7 +133,7 @@ def test_batched_gqa_attention_matches_oracle(fh, orc, nh, nkv, rows):
     (one workgroup per row, kv head and up to four query heads, every position
     merged inside it): groups of 7 (split 4 + 3), 4, 8 and 3 (split 2 + 1),
     and one query head per kv head (GPT-2's batched decode, which takes it
-    for rows of 384 positions or more; 12 x 10 workgroups are too few and take
+    for rows of 256 positions or more; 12 x 10 workgroups are too few and take
     the chunked kernel).
     Positions span the wave (32) and round (256) edges, 0 and the last cache
     row; two rows sit past max_pos and one at capacity (NaN, cache untouched).
